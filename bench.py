@@ -1,0 +1,325 @@
+"""Benchmark of the MI355X block-FP8 path (one GPU).
+
+Headline (BASELINE.json metric): block-FP8 GEMM 4096x4096x8192, e4m3fn
+operands with 1x128 activation / 128x128 weight fp32 scales, bf16 output.
+One step = one w8a8_block_fp8_matmul call on inputs already resident in HBM
+(the activations are quantised by act_quant once, before timing).
+
+Prints ONE JSON line on stdout; progress goes to stderr. The line carries:
+  roofline      the GEMM kernel's achieved TFLOP/s (algorithmic 2MNK per
+                launch / mean launch time from HIP events around back-to-back
+                launches on the launch stream) against dense FP8 MFMA peak;
+  cpu_baseline  the reference's PyTorch CPU dequantise-then-matmul path
+                (finegrained-fp8-helion/bench.py:11-14, restated in
+                oracle/torch_ref.py) on a row sample of the same workload;
+  secondary     act-quant, decode-shaped, medium, small and MLP-chain rows.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_FP8_TFLOPS = 5000.0   # MI355X dense FP8 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+METRIC = "TFLOP/s + % FP8 MFMA peak, block-FP8 GEMM 4096x4096x8192, 1 GPU"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-secondary", action="store_true")
+    p.add_argument("--only", default=None,
+                   help="profile helper: run only one workload (gemm|act_quant|decode|mlp|medium|small)"
+                        " for --steps steps and exit without JSON")
+    return p.parse_args()
+
+
+def time_events(fn, steps, warmup, torch):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(steps):
+        fn()
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps  # ms per call
+
+
+def gemm_launcher(A, B, As, Bs, out, torch):
+    """Direct C-ABI launch of the GEMM on the current stream (no Python-side
+    allocation or validation), used to time the kernel itself."""
+    from hf_kernels_helion_amd import _native
+    lib = _native.load()
+    M, K = A.shape
+    N = B.shape[0]
+    ws_bytes = lib.fp8b_gemm_workspace_size(M, N, K, 128, 128)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=A.device)
+    stream = torch.cuda.current_stream().cuda_stream
+    args = (A.data_ptr(), A.stride(0), B.data_ptr(), B.stride(0), As.data_ptr(), As.stride(0),
+            As.stride(1), Bs.data_ptr(), Bs.stride(0), Bs.stride(1), out.data_ptr(),
+            out.stride(0), _native.BF16, M, N, K, 128, 128,
+            ws.data_ptr() if ws_bytes else None, ws_bytes, stream)
+    fn = lib.fp8b_w8a8_block_matmul
+
+    def run():
+        st = fn(*args)
+        if st:
+            _native.check(st, "fp8b_w8a8_block_matmul")
+    return run, ws
+
+
+def cpu_baseline(A, B, As, Bs, torch):
+    from oracle import torch_ref
+    torch.set_num_threads(os.cpu_count() or 1)
+    R = 512
+    M, K = A.shape
+    N = B.shape[0]
+    a, a_s = A[:R].contiguous(), As[:R].contiguous()
+    torch_ref.dequant_matmul(a, B, a_s, Bs)  # warmup
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 20 and (time.perf_counter() - t_start) < 12.0:
+        t0 = time.perf_counter()
+        torch_ref.dequant_matmul(a, B, a_s, Bs)
+        times.append(time.perf_counter() - t0)
+    t = sum(times) / len(times)
+    return {
+        "value": 2.0 * R * N * K / t / 1e12,
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"{R} of {M} rows of the {M}x{N}x{K} workload: dequantise A rows and all of B "
+                   f"with their block scales, fp32 matmul, bf16 cast (bench.py:11-14 restated); "
+                   f"mean of {len(times)} iterations, {t * 1e3:.1f} ms each, "
+                   f"os.cpu_count()={os.cpu_count()}"),
+    }
+
+
+def load_traffic(key):
+    f = ROOT / "profiles" / "traffic.json"
+    if not f.exists():
+        return None
+    try:
+        return json.loads(f.read_text()).get(key)
+    except Exception:
+        return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
+              "(every GPU box in this build has a single MI355X; see DESIGN.md for how the "
+              "path would shard)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from hf_kernels_helion_amd import finegrained_fp8_helion as fp8
+    from hf_kernels_helion_amd.finegrained_fp8_helion import synthetic
+
+    assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    steps, warmup = args.steps, args.warmup
+
+    if args.only:
+        run_only(args.only, steps, warmup, torch, fp8, synthetic, dev)
+        return
+
+    # ---- headline: 4096x4096x8192 --------------------------------------
+    M, N, K = 4096, 4096, 8192
+    log(f"generating inputs {M}x{N}x{K}")
+    x = synthetic.activations(M, K)
+    W, Bs = synthetic.weights(N, K)
+    Ad, As = fp8.act_quant(x.to(dev), 128)
+    Bd, Bsd = W.to(dev), Bs.to(dev)
+    flops = 2.0 * M * N * K
+
+    def step():
+        return fp8.w8a8_block_fp8_matmul(Ad, Bd, As, Bsd, [128, 128], torch.bfloat16)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(st)
+    for _ in range(steps):
+        step()
+    e1.record(st)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / steps
+    value = flops / (ms * 1e-3) / 1e12
+    log(f"headline: {ms * 1e3:.1f} us/step, {value:.1f} TFLOP/s (wall {wall:.3f}s)")
+
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    run, _ws = gemm_launcher(Ad, Bd, As, Bsd, out, torch)
+    k_ms = time_events(run, steps, warmup, torch)
+    achieved = flops / (k_ms * 1e-3) / 1e12
+    log(f"kernel: {k_ms * 1e3:.1f} us/launch, {achieved:.1f} TFLOP/s "
+        f"({100 * achieved / PEAK_FP8_TFLOPS:.1f}% of FP8 peak)")
+    torch.testing.assert_close(out.float(), step().float(), rtol=0, atol=0)
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3fn x fp8_e4m3fn -> fp32 acc -> bf16",
+        "data": "synthetic: A~N(0,1) bf16 act-quantised per 1x128, W~N(0,0.02) quantised per "
+                "128x128 block, seeds 1234/5678",
+        "config": {"workload": "block-FP8 GEMM M=4096 N=4096 K=8192 (BASELINE configs[2])",
+                   "M": M, "N": N, "K": K, "block_size": [128, 128], "out_dtype": "bf16",
+                   "pct_fp8_peak": round(100 * value / PEAK_FP8_TFLOPS, 2)},
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_FP8_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_FP8_TFLOPS, 4),
+            "traffic": load_traffic("gemm_4096x4096x8192"),
+            "kernel": "gemm_bs128_kernel<256,256,64,128>",
+            "launch_us": round(k_ms * 1e3, 2),
+        },
+    }
+
+    if not args.no_secondary:
+        result["secondary"] = secondary(torch, fp8, synthetic, dev)
+
+    if not args.no_cpu_baseline:
+        log("cpu baseline ...")
+        result["cpu_baseline"] = cpu_baseline(Ad.cpu(), Bd.cpu(), As.cpu(), Bsd.cpu(), torch)
+        log(f"cpu baseline: {result['cpu_baseline']['value']:.3f} TFLOP/s")
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+def _gpu_weights(N, K, seed, dev, torch, synthetic):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    W = torch.randn(N, K, generator=g, device=dev) * 0.02
+    return synthetic.quantize_weight_blockwise(W)
+
+
+def _gpu_acts(M, K, seed, dev, torch):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+
+
+def secondary(torch, fp8, synthetic, dev):
+    res = {}
+    # act-quant 4096x8192; 4 input/output sets (384 MB) rotate past the 256 MB MALL
+    M, K = 4096, 8192
+    xs = [_gpu_acts(M, K, 10 + i, dev, torch) for i in range(4)]
+    it = [0]
+
+    def aq():
+        i = it[0] = (it[0] + 1) % 4
+        return fp8.act_quant(xs[i], 128)
+    ms = time_events(aq, 40, 5, torch)
+    byt = 3.0 * M * K + 4.0 * M * K / 128
+    res["act_quant_4096x8192"] = {"us": round(ms * 1e3, 2), "GB/s": round(byt / ms / 1e6, 1),
+                                  "pct_hbm_peak": round(100 * byt / ms / 1e6 / PEAK_HBM_GBS, 1)}
+    log(f"act_quant: {res['act_quant_4096x8192']}")
+    del xs
+
+    # decode 32x4096x14336 with act-quant in-op; 5 weight copies (294 MB)
+    M, N, K = 32, 4096, 14336
+    ws_ = [_gpu_weights(N, K, 20 + i, dev, torch, synthetic) for i in range(5)]
+    xd = _gpu_acts(M, K, 30, dev, torch)
+    it[0] = 0
+
+    def dec():
+        i = it[0] = (it[0] + 1) % 5
+        q, s = fp8.act_quant(xd, 128)
+        return fp8.w8a8_block_fp8_matmul(q, ws_[i][0], s, ws_[i][1], [128, 128], torch.bfloat16)
+    ms = time_events(dec, 50, 5, torch)
+    byt = 2.0 * M * K + N * K + 4.0 * (N // 128) * (K // 128) + 2.0 * M * N
+    res["decode_32x4096x14336"] = {"us": round(ms * 1e3, 2), "GB/s": round(byt / ms / 1e6, 1),
+                                   "pct_hbm_peak": round(100 * byt / ms / 1e6 / PEAK_HBM_GBS, 1),
+                                   "includes": "act_quant + gemm (+ split-K reduce)"}
+    log(f"decode: {res['decode_32x4096x14336']}")
+    del ws_
+
+    for name, (M, N, K) in {"medium_2048x2048x4096": (2048, 2048, 4096),
+                            "small_512x512x2048": (512, 512, 2048)}.items():
+        W, Bs = _gpu_weights(N, K, 40, dev, torch, synthetic)
+        q, s = fp8.act_quant(_gpu_acts(M, K, 41, dev, torch), 128)
+        ms = time_events(lambda: fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [128, 128],
+                                                           torch.bfloat16), 50, 10, torch)
+        tf = 2.0 * M * N * K / ms / 1e9
+        res[name] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
+                     "pct_fp8_peak": round(100 * tf / PEAK_FP8_TFLOPS, 1)}
+        log(f"{name}: {res[name]}")
+
+    # MLP chain M=3001, H=4096, I=14336
+    M, H, I = 3001, 4096, 14336
+    w13, s13 = _gpu_weights(2 * I, H, 50, dev, torch, synthetic)
+    w2, s2 = _gpu_weights(H, I, 51, dev, torch, synthetic)
+    x = _gpu_acts(M, H, 52, dev, torch)
+    ms = time_events(lambda: fp8.fp8_mlp(x, w13, s13, w2, s2), 10, 3, torch)
+    fl = 2.0 * M * (2 * I * H + H * I)
+    res["mlp_chain_3001"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(fl / ms / 1e9, 1),
+                             "pct_fp8_peak": round(100 * fl / ms / 1e9 / PEAK_FP8_TFLOPS, 1)}
+    log(f"mlp: {res['mlp_chain_3001']}")
+    return res
+
+
+def run_only(what, steps, warmup, torch, fp8, synthetic, dev):
+    """Run one workload for profiling (rocprofv3) without the other legs."""
+    shapes = {"gemm": (4096, 4096, 8192), "medium": (2048, 2048, 4096),
+              "small": (512, 512, 2048), "decode": (32, 4096, 14336)}
+    if what in shapes:
+        M, N, K = shapes[what]
+        W, Bs = _gpu_weights(N, K, 40, dev, torch, synthetic)
+        x = _gpu_acts(M, K, 41, dev, torch)
+        q, s = fp8.act_quant(x, 128)
+        if what == "decode":
+            def fn():
+                q2, s2 = fp8.act_quant(x, 128)
+                return fp8.w8a8_block_fp8_matmul(q2, W, s2, Bs, [128, 128], torch.bfloat16)
+        else:
+            fn = lambda: fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [128, 128], torch.bfloat16)
+    elif what == "act_quant":
+        x = _gpu_acts(4096, 8192, 10, dev, torch)
+        fn = lambda: fp8.act_quant(x, 128)
+    elif what == "mlp":
+        M, H, I = 3001, 4096, 14336
+        w13, s13 = _gpu_weights(2 * I, H, 50, dev, torch, synthetic)
+        w2, s2 = _gpu_weights(H, I, 51, dev, torch, synthetic)
+        x = _gpu_acts(M, H, 52, dev, torch)
+        fn = lambda: fp8.fp8_mlp(x, w13, s13, w2, s2)
+    else:
+        raise SystemExit(f"unknown --only {what}")
+    ms = time_events(fn, steps, warmup, torch)
+    log(f"{what}: {ms * 1e3:.2f} us/step over {steps} steps")
+
+
+if __name__ == "__main__":
+    main()

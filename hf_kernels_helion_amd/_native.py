@@ -1,0 +1,77 @@
+"""ctypes binding of libfp8_blockwise.so (the C ABI in include/fp8_blockwise.h).
+
+The library is built in-tree by ``hf_kernels_helion_amd.build``. There is no
+fallback: if the library is missing or fails to load, every op raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libfp8_blockwise.so"
+
+# fp8b_status codes (include/fp8_blockwise.h).
+STATUS_NAMES = {
+    0: "FP8B_OK",
+    1: "FP8B_ERR_NULL",
+    2: "FP8B_ERR_DIMS",
+    3: "FP8B_ERR_ALIGN",
+    4: "FP8B_ERR_BLOCK",
+    5: "FP8B_ERR_DTYPE",
+    6: "FP8B_ERR_WORKSPACE",
+    7: "FP8B_ERR_LAUNCH",
+}
+
+# fp8b_dtype codes.
+F32, BF16, F16 = 0, 1, 2
+
+_i64 = ctypes.c_int64
+_vp = ctypes.c_void_p
+_sz = ctypes.c_size_t
+
+# name -> (restype, argtypes); every symbol the header declares.
+SIGNATURES = {
+    "fp8b_version": (ctypes.c_int, []),
+    "fp8b_last_error": (ctypes.c_char_p, []),
+    "fp8b_act_quant": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _vp]),
+    "fp8b_w8a8_block_matmul": (
+        ctypes.c_int,
+        [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, ctypes.c_int,
+         _i64, _i64, _i64, _i64, _i64, _vp, _sz, _vp],
+    ),
+    "fp8b_gemm_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64]),
+    "fp8b_silu_and_mul": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _i64, _vp]),
+    "fp8b_silu_and_mul_quant": (
+        ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _vp]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load the HIP library once; raise RuntimeError if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"{LIB_PATH} is missing: build the HIP kernels first "
+                    "(python -m hf_kernels_helion_amd.build)")
+            lib = ctypes.CDLL(str(LIB_PATH))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    """Turn a non-zero fp8b_status into RuntimeError with the library's text."""
+    if status != 0:
+        msg = load().fp8b_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed: {STATUS_NAMES.get(status, status)}: {msg}")

@@ -1,0 +1,344 @@
+// Per-token-group float8_e4m3fn quantisation and gated SiLU for gfx950.
+//
+// Layout: x is bf16 row-major [M,K]; every row is cut into groups of `group`
+// consecutive elements. A group of 128 bf16 is 256 contiguous bytes, read by
+// 16 lanes (one DPP row) with one 16-byte load each, so a wavefront covers
+// four groups per load instruction and the whole wave's request is 1 KiB of
+// consecutive memory when the four groups sit in one row.
+//
+// Numerics (the contract written in include/fp8_blockwise.h):
+//   amax  = max |x| over the group, taken as the max of the 15-bit magnitude
+//           patterns of the bf16 inputs, so NaN (pattern > 0x7F80) wins;
+//   scale = max(amax, 1e-10) / 448 as one IEEE fp32 division;
+//   q     = e4m3fn(x / scale): IEEE fp32 division, then the gfx950 OCP fp8
+//           convert (round to nearest even). |x/scale| <= 448 * (1 + 2^-23)
+//           for finite groups, which the convert rounds into range.
+//   NaN group -> scale NaN, q = 0x7F; +inf group -> scale +inf, q = signed
+//   zero for finite x and 0x7F for +-inf.
+#include "common.h"
+
+namespace fp8b {
+
+// Quantise 8 values held by one lane of a 16-lane group of 128.
+// `mag` is the max over this lane's 8 bf16 magnitude patterns.
+__device__ __forceinline__ void quant_row16_8(const float v[8], uint32_t mag,
+                                              uint32_t& w0, uint32_t& w1,
+                                              float& scale) {
+  const uint32_t gmag = row16_max_u32(mag);
+  if (gmag < 0x7F80u) {
+    const float amax = fmaxf(bf16_to_f32(gmag), kAmaxFloor);
+    scale = amax / kFp8Max;
+    float y[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = v[i] / scale;
+    int p0 = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
+    p0 = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], p0, true);
+    int p1 = __builtin_amdgcn_cvt_pk_fp8_f32(y[4], y[5], 0, false);
+    p1 = __builtin_amdgcn_cvt_pk_fp8_f32(y[6], y[7], p1, true);
+    w0 = (uint32_t)p0;
+    w1 = (uint32_t)p1;
+  } else {
+    const bool is_nan = gmag > 0x7F80u;
+    scale = is_nan ? __uint_as_float(0x7FC00000u) : __uint_as_float(0x7F800000u);
+    uint32_t b[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t u = __float_as_uint(v[i]);
+      const bool nonfinite = (u & 0x7FFFFFFFu) >= 0x7F800000u;
+      b[i] = (is_nan || nonfinite) ? kFp8NaN : ((u >> 24) & 0x80u);
+    }
+    w0 = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+    w1 = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+  }
+}
+
+// Unpack 8 bf16 (one 16-byte load) into fp32 values and the max magnitude.
+__device__ __forceinline__ uint32_t unpack_bf16x8(const v4i raw, float v[8]) {
+  uint32_t mag = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t w = (uint32_t)raw[i];
+    const uint32_t lo = w & 0xFFFFu, hi = w >> 16;
+    v[2 * i] = bf16_to_f32(lo);
+    v[2 * i + 1] = bf16_to_f32(hi);
+    mag = max(mag, max(lo & 0x7FFFu, hi & 0x7FFFu));
+  }
+  return mag;
+}
+
+// Fast path: group = 128, K % 128 == 0, 16-byte aligned rows of x, 8-byte
+// aligned rows of q. 16 lanes per group, 16 groups per 256-thread block.
+__global__ void __launch_bounds__(256)
+act_quant_g128_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                      uint8_t* __restrict__ q, int64_t ldq,
+                      float* __restrict__ s, int64_t ssm, int64_t ssg,
+                      uint32_t groups, uint32_t groups_per_row) {
+  const uint32_t gi = (blockIdx.x * 256u + threadIdx.x) >> 4;
+  const uint32_t sub = threadIdx.x & 15u;
+  if (gi >= groups) return;  // uniform across the 16-lane group
+  const uint32_t m = gi / groups_per_row;
+  const uint32_t g = gi - m * groups_per_row;
+  const v4i raw = __builtin_nontemporal_load(
+      reinterpret_cast<const v4i*>(x + (int64_t)m * ldx + g * 128u + sub * 8u));
+  float v[8];
+  const uint32_t mag = unpack_bf16x8(raw, v);
+  uint32_t w0, w1;
+  float scale;
+  quant_row16_8(v, mag, w0, w1, scale);
+  v2i packed;
+  packed[0] = (int)w0;
+  packed[1] = (int)w1;
+  __builtin_nontemporal_store(
+      packed, reinterpret_cast<v2i*>(q + (int64_t)m * ldq + g * 128u + sub * 8u));
+  if (sub == 0) s[(int64_t)m * ssm + (int64_t)g * ssg] = scale;
+}
+
+// Scalar reference-shaped path for any group size, ragged K or unaligned
+// rows: one thread walks one group serially.
+__device__ __forceinline__ uint8_t quant_scalar(float xv, uint32_t gmag, float scale) {
+  if (gmag > 0x7F80u) return kFp8NaN;
+  if (gmag == 0x7F80u) {
+    const uint32_t u = __float_as_uint(xv);
+    if ((u & 0x7FFFFFFFu) >= 0x7F800000u) return kFp8NaN;
+    return (uint8_t)((u >> 24) & 0x80u);
+  }
+  const float y = xv / scale;
+  return (uint8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(y, 0.0f, 0, false) & 0xFF);
+}
+
+__device__ __forceinline__ float scale_from_mag(uint32_t gmag) {
+  if (gmag > 0x7F80u) return __uint_as_float(0x7FC00000u);
+  if (gmag == 0x7F80u) return __uint_as_float(0x7F800000u);
+  return fmaxf(bf16_to_f32(gmag), kAmaxFloor) / kFp8Max;
+}
+
+__global__ void __launch_bounds__(64)
+act_quant_generic_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                         uint8_t* __restrict__ q, int64_t ldq,
+                         float* __restrict__ s, int64_t ssm, int64_t ssg,
+                         int64_t M, int64_t K, int64_t group, int64_t groups_per_row) {
+  const int64_t gi = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  if (gi >= M * groups_per_row) return;
+  const int64_t m = gi / groups_per_row;
+  const int64_t g = gi - m * groups_per_row;
+  const int64_t k0 = g * group;
+  const int64_t k1 = min(k0 + group, K);
+  const uint16_t* xr = x + m * ldx;
+  uint32_t gmag = 0;
+  for (int64_t k = k0; k < k1; ++k) gmag = max(gmag, (uint32_t)(xr[k] & 0x7FFFu));
+  const float scale = scale_from_mag(gmag);
+  uint8_t* qr = q + m * ldq;
+  for (int64_t k = k0; k < k1; ++k) qr[k] = quant_scalar(bf16_to_f32(xr[k]), gmag, scale);
+  s[m * ssm + g * ssg] = scale;
+}
+
+// silu(a) * b with the reference's rounding points: silu in fp32, rounded to
+// bf16, multiplied by the bf16 `up` value in fp32, rounded to bf16.
+__device__ __forceinline__ uint32_t silu_mul_bits(uint32_t gate_bits, uint32_t up_bits) {
+  const float a = bf16_to_f32(gate_bits);
+  const float silu = a / (1.0f + expf(-a));
+  const float silu_b = bf16_to_f32(f32_to_bf16_bits(silu));
+  return f32_to_bf16_bits(silu_b * bf16_to_f32(up_bits));
+}
+
+// 8 outputs per thread; requires d % 8 == 0 and 16-byte aligned rows.
+__global__ void __launch_bounds__(256)
+silu_and_mul_vec_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                        uint16_t* __restrict__ out, int64_t ldo,
+                        uint32_t chunks, uint32_t chunks_per_row, int64_t d) {
+  const uint32_t ci = blockIdx.x * 256u + threadIdx.x;
+  if (ci >= chunks) return;
+  const uint32_t m = ci / chunks_per_row;
+  const uint32_t c = ci - m * chunks_per_row;
+  const uint16_t* xr = x + (int64_t)m * ldx + c * 8u;
+  const v4i g = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(xr));
+  const v4i u = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(xr + d));
+  v4i o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t gw = (uint32_t)g[i], uw = (uint32_t)u[i];
+    const uint32_t lo = silu_mul_bits(gw & 0xFFFFu, uw & 0xFFFFu);
+    const uint32_t hi = silu_mul_bits(gw >> 16, uw >> 16);
+    o[i] = (int)(lo | (hi << 16));
+  }
+  __builtin_nontemporal_store(o, reinterpret_cast<v4i*>(out + (int64_t)m * ldo + c * 8u));
+}
+
+__global__ void __launch_bounds__(256)
+silu_and_mul_generic_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                            uint16_t* __restrict__ out, int64_t ldo, int64_t M, int64_t d) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= M * d) return;
+  const int64_t m = i / d, j = i - m * d;
+  out[m * ldo + j] = (uint16_t)silu_mul_bits(x[m * ldx + j], x[m * ldx + d + j]);
+}
+
+// Fused silu_and_mul + group-128 quantisation: identical arithmetic to
+// silu_and_mul_vec_kernel followed by act_quant_g128_kernel, without the
+// bf16 round trip through memory. Requires d % 128 == 0.
+__global__ void __launch_bounds__(256)
+silu_mul_quant_g128_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                           uint8_t* __restrict__ q, int64_t ldq,
+                           float* __restrict__ s, int64_t ssm, int64_t ssg,
+                           uint32_t groups, uint32_t groups_per_row, int64_t d) {
+  const uint32_t gi = (blockIdx.x * 256u + threadIdx.x) >> 4;
+  const uint32_t sub = threadIdx.x & 15u;
+  if (gi >= groups) return;
+  const uint32_t m = gi / groups_per_row;
+  const uint32_t g = gi - m * groups_per_row;
+  const uint16_t* xr = x + (int64_t)m * ldx + g * 128u + sub * 8u;
+  const v4i gr = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(xr));
+  const v4i ur = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(xr + d));
+  float v[8];
+  uint32_t mag = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t gw = (uint32_t)gr[i], uw = (uint32_t)ur[i];
+    const uint32_t lo = silu_mul_bits(gw & 0xFFFFu, uw & 0xFFFFu);
+    const uint32_t hi = silu_mul_bits(gw >> 16, uw >> 16);
+    v[2 * i] = bf16_to_f32(lo);
+    v[2 * i + 1] = bf16_to_f32(hi);
+    mag = max(mag, max(lo & 0x7FFFu, hi & 0x7FFFu));
+  }
+  uint32_t w0, w1;
+  float scale;
+  quant_row16_8(v, mag, w0, w1, scale);
+  v2i packed;
+  packed[0] = (int)w0;
+  packed[1] = (int)w1;
+  __builtin_nontemporal_store(
+      packed, reinterpret_cast<v2i*>(q + (int64_t)m * ldq + g * 128u + sub * 8u));
+  if (sub == 0) s[(int64_t)m * ssm + (int64_t)g * ssg] = scale;
+}
+
+__global__ void __launch_bounds__(64)
+silu_mul_quant_generic_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                              uint8_t* __restrict__ q, int64_t ldq,
+                              float* __restrict__ s, int64_t ssm, int64_t ssg,
+                              int64_t M, int64_t d, int64_t group, int64_t groups_per_row) {
+  const int64_t gi = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  if (gi >= M * groups_per_row) return;
+  const int64_t m = gi / groups_per_row;
+  const int64_t g = gi - m * groups_per_row;
+  const int64_t j0 = g * group;
+  const int64_t j1 = min(j0 + group, d);
+  const uint16_t* xr = x + m * ldx;
+  uint32_t gmag = 0;
+  for (int64_t j = j0; j < j1; ++j)
+    gmag = max(gmag, silu_mul_bits(xr[j], xr[d + j]) & 0x7FFFu);
+  const float scale = scale_from_mag(gmag);
+  uint8_t* qr = q + m * ldq;
+  for (int64_t j = j0; j < j1; ++j)
+    qr[j] = quant_scalar(bf16_to_f32(silu_mul_bits(xr[j], xr[d + j])), gmag, scale);
+  s[m * ssm + g * ssg] = scale;
+}
+
+}  // namespace fp8b
+
+using namespace fp8b;
+
+static inline bool aligned(const void* p, uintptr_t a) {
+  return ((uintptr_t)p & (a - 1)) == 0;
+}
+
+static int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error(what);
+    return FP8B_ERR_LAUNCH;
+  }
+  return FP8B_OK;
+}
+
+extern "C" int fp8b_act_quant(const void* x, int64_t ldx, void* q, int64_t ldq,
+                              float* s, int64_t s_stride_m, int64_t s_stride_g,
+                              int64_t M, int64_t K, int64_t group, void* stream) {
+  if (M < 0 || K < 0 || ldx < K || ldq < K) {
+    set_error("fp8b_act_quant: bad dims (need M,K >= 0, ldx >= K, ldq >= K)");
+    return FP8B_ERR_DIMS;
+  }
+  if (group != 32 && group != 64 && group != 128 && group != 256) {
+    set_error("fp8b_act_quant: group must be 32, 64, 128 or 256");
+    return FP8B_ERR_BLOCK;
+  }
+  if (M == 0 || K == 0) return FP8B_OK;
+  if (!x || !q || !s) {
+    set_error("fp8b_act_quant: null pointer");
+    return FP8B_ERR_NULL;
+  }
+  const int64_t gpr = (K + group - 1) / group;
+  hipStream_t st = (hipStream_t)stream;
+  const bool fast = group == 128 && K % 128 == 0 && ldx % 8 == 0 && ldq % 8 == 0 &&
+                    aligned(x, 16) && aligned(q, 8) && M * gpr < (int64_t(1) << 31);
+  if (fast) {
+    const uint32_t groups = (uint32_t)(M * gpr);
+    const uint32_t blocks = (groups + 15u) / 16u;
+    act_quant_g128_kernel<<<blocks, 256, 0, st>>>((const uint16_t*)x, ldx, (uint8_t*)q, ldq, s,
+                                                  s_stride_m, s_stride_g, groups, (uint32_t)gpr);
+  } else {
+    const int64_t groups = M * gpr;
+    act_quant_generic_kernel<<<(unsigned)((groups + 63) / 64), 64, 0, st>>>(
+        (const uint16_t*)x, ldx, (uint8_t*)q, ldq, s, s_stride_m, s_stride_g, M, K, group, gpr);
+  }
+  return check_launch("fp8b_act_quant: kernel launch failed");
+}
+
+extern "C" int fp8b_silu_and_mul(const void* x, int64_t ldx, void* out, int64_t ldo,
+                                 int64_t M, int64_t d, void* stream) {
+  if (M < 0 || d < 0 || ldx < 2 * d || ldo < d) {
+    set_error("fp8b_silu_and_mul: bad dims (need ldx >= 2d, ldo >= d)");
+    return FP8B_ERR_DIMS;
+  }
+  if (M == 0 || d == 0) return FP8B_OK;
+  if (!x || !out) {
+    set_error("fp8b_silu_and_mul: null pointer");
+    return FP8B_ERR_NULL;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  const bool fast = d % 8 == 0 && ldx % 8 == 0 && ldo % 8 == 0 && aligned(x, 16) &&
+                    aligned(out, 16) && M * (d / 8) < (int64_t(1) << 31);
+  if (fast) {
+    const uint32_t cpr = (uint32_t)(d / 8);
+    const uint32_t chunks = (uint32_t)(M * cpr);
+    silu_and_mul_vec_kernel<<<(chunks + 255u) / 256u, 256, 0, st>>>(
+        (const uint16_t*)x, ldx, (uint16_t*)out, ldo, chunks, cpr, d);
+  } else {
+    const int64_t n = M * d;
+    silu_and_mul_generic_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(
+        (const uint16_t*)x, ldx, (uint16_t*)out, ldo, M, d);
+  }
+  return check_launch("fp8b_silu_and_mul: kernel launch failed");
+}
+
+extern "C" int fp8b_silu_and_mul_quant(const void* x, int64_t ldx, void* q, int64_t ldq,
+                                       float* s, int64_t s_stride_m, int64_t s_stride_g,
+                                       int64_t M, int64_t d, int64_t group, void* stream) {
+  if (M < 0 || d < 0 || ldx < 2 * d || ldq < d) {
+    set_error("fp8b_silu_and_mul_quant: bad dims (need ldx >= 2d, ldq >= d)");
+    return FP8B_ERR_DIMS;
+  }
+  if (group != 32 && group != 64 && group != 128 && group != 256) {
+    set_error("fp8b_silu_and_mul_quant: group must be 32, 64, 128 or 256");
+    return FP8B_ERR_BLOCK;
+  }
+  if (M == 0 || d == 0) return FP8B_OK;
+  if (!x || !q || !s) {
+    set_error("fp8b_silu_and_mul_quant: null pointer");
+    return FP8B_ERR_NULL;
+  }
+  const int64_t gpr = (d + group - 1) / group;
+  hipStream_t st = (hipStream_t)stream;
+  const bool fast = group == 128 && d % 128 == 0 && ldx % 8 == 0 && ldq % 8 == 0 &&
+                    aligned(x, 16) && aligned(q, 8) && M * gpr < (int64_t(1) << 31);
+  if (fast) {
+    const uint32_t groups = (uint32_t)(M * gpr);
+    silu_mul_quant_g128_kernel<<<(groups + 15u) / 16u, 256, 0, st>>>(
+        (const uint16_t*)x, ldx, (uint8_t*)q, ldq, s, s_stride_m, s_stride_g, groups,
+        (uint32_t)gpr, d);
+  } else {
+    const int64_t groups = M * gpr;
+    silu_mul_quant_generic_kernel<<<(unsigned)((groups + 63) / 64), 64, 0, st>>>(
+        (const uint16_t*)x, ldx, (uint8_t*)q, ldq, s, s_stride_m, s_stride_g, M, d, group, gpr);
+  }
+  return check_launch("fp8b_silu_and_mul_quant: kernel launch failed");
+}

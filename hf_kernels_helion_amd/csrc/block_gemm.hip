@@ -1,0 +1,520 @@
+// Block-scaled w8a8 GEMM for gfx950:  C[M,N] = A[M,K] . B[N,K]^T with
+//   C[m,n] = sum_kb dot_kb(m,n) * As[m,kb] * Bs[n/128,kb],
+// the arithmetic of the Helion kernel in
+// finegrained-fp8-helion/torch-ext/finegrained_fp8_helion/fp8.py:28-38.
+//
+// MFMA path (block_n = block_k = 128):
+//   * One K-block of 128 is exactly one v_mfma_f32_16x16x128_f8f6f4 per 16x16
+//     output sub-tile, issued with a zero accumulator; its fp32 result is
+//     folded into the running fp32 accumulator with one FMA by the product of
+//     the row's activation scale and the tile's weight scale. No second set of
+//     accumulators is needed.
+//   * The weight tile is the MFMA's A operand and the activation tile its B
+//     operand, so the 16x16 result holds one activation row per lane and four
+//     consecutive output columns: the activation scale is one register per
+//     lane and sub-tile row, the weight scale one scalar per wave.
+//   * Both operand tiles stream global -> LDS with global_load_lds_dwordx4
+//     (no VGPR staging) into two LDS stages. Each 128-byte tile row is kept as
+//     eight 16-byte chunks, chunk c of row r stored at slot c ^ (r & 7), which
+//     makes the per-lane fragment reads (16 rows x same chunk) hit distinct
+//     banks.
+//   * Ragged M/N: rows past the end are clamped to the last row when loading
+//     and masked when storing. K must be a multiple of 128.
+//   * Split-K writes fp32 partials to the caller's workspace; a second kernel
+//     sums them in split order and applies the output conversion.
+//
+// Generic path (any block_n/block_k, ragged K, unaligned operands): a SIMT
+// kernel with the same blockwise summation, used only where the MFMA path's
+// preconditions do not hold.
+#include "common.h"
+
+#include <algorithm>
+
+namespace fp8b {
+
+struct GemmArgs {
+  const uint8_t* A;
+  const uint8_t* B;
+  const float* As;
+  const float* Bs;
+  void* C;
+  float* ws;
+  int64_t lda, ldb, as_sm, as_sk, bs_sn, bs_sk, ldc;
+  int M, N, K;
+  int KB;            // number of 128-wide K-blocks
+  int kb_per_split;  // K-blocks per grid.z slice
+  int tiles_m, tiles_n;
+  int out_dtype;     // fp8b_dtype; ignored when writing split-K partials
+  int vec_store;     // 1 if 4 consecutive outputs can be stored as one vector
+};
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ void lds_dma16(const void* gsrc, uint8_t* ldst) {
+  __builtin_amdgcn_global_load_lds(gsrc, (lds_void*)ldst, 16, 0, 0);
+}
+
+// Store four consecutive outputs (columns n..n+3 of row m).
+__device__ __forceinline__ void store4(const GemmArgs& a, int m, int n, const v4f& v,
+                                       bool partial_ws, int split) {
+  if (m >= a.M || n >= a.N) return;
+  if (partial_ws) {
+    float* p = a.ws + ((int64_t)split * a.M + m) * a.N + n;
+    if (n + 3 < a.N && a.vec_store) {
+      *reinterpret_cast<v4f*>(p) = v;
+    } else {
+      for (int r = 0; r < 4 && n + r < a.N; ++r) p[r] = v[r];
+    }
+    return;
+  }
+  if (a.out_dtype == FP8B_F32) {
+    float* p = reinterpret_cast<float*>(a.C) + (int64_t)m * a.ldc + n;
+    if (n + 3 < a.N && a.vec_store) {
+      *reinterpret_cast<v4f*>(p) = v;
+    } else {
+      for (int r = 0; r < 4 && n + r < a.N; ++r) p[r] = v[r];
+    }
+  } else {
+    uint16_t* p = reinterpret_cast<uint16_t*>(a.C) + (int64_t)m * a.ldc + n;
+    const bool bf = a.out_dtype == FP8B_BF16;
+    const uint32_t lo = bf ? pack_bf16x2(v[0], v[1]) : pack_f16x2(v[0], v[1]);
+    const uint32_t hi = bf ? pack_bf16x2(v[2], v[3]) : pack_f16x2(v[2], v[3]);
+    if (n + 3 < a.N && a.vec_store) {
+      v2i w;
+      w[0] = (int)lo;
+      w[1] = (int)hi;
+      *reinterpret_cast<v2i*>(p) = w;
+    } else {
+      const uint16_t h[4] = {(uint16_t)lo, (uint16_t)(lo >> 16), (uint16_t)hi,
+                             (uint16_t)(hi >> 16)};
+      for (int r = 0; r < 4 && n + r < a.N; ++r) p[r] = h[r];
+    }
+  }
+}
+
+// BM x BN output tile per workgroup, WM x WN per wavefront.
+template <int BM, int BN, int WM, int WN>
+__global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64)
+gemm_bs128_kernel(GemmArgs a) {
+  constexpr int NWM = BM / WM, NWN = BN / WN, NW = NWM * NWN;
+  constexpr int FM = WM / 16, FN = WN / 16;
+  constexpr int ROWS = BM + BN;         // tile rows per stage (A rows then B rows)
+  constexpr int STAGE = ROWS * 128;     // bytes per LDS stage
+  constexpr int LOADS = ROWS / 8;       // 1 KiB wave-loads per stage
+  static_assert(LOADS % NW == 0, "stage loads must split evenly over waves");
+  static_assert(WN <= 128 && 128 % WN == 0, "a wave's columns must sit in one 128-block");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wid = tid >> 6;
+  const int wm = wid / NWN, wn = wid % NWN;
+
+  // Workgroup -> tile. Consecutive workgroup ids go round-robin over the 8
+  // XCDs; regroup so each XCD owns a contiguous run of tiles, then walk the
+  // run in column-major groups of 8 tile rows so neighbouring workgroups
+  // share A row-panels and B column-panels in their XCD's L2.
+  const int tiles = a.tiles_m * a.tiles_n;
+  int bid = blockIdx.x;
+  if (tiles % 8 == 0) bid = (bid & 7) * (tiles >> 3) + (bid >> 3);
+  constexpr int GROUP_M = 8;
+  const int group_size = GROUP_M * a.tiles_n;
+  const int first_m = (bid / group_size) * GROUP_M;
+  const int gm = min(a.tiles_m - first_m, GROUP_M);
+  const int tm = first_m + (bid % group_size) % gm;
+  const int tn = (bid % group_size) / gm;
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  const int split = blockIdx.z;
+  const int kb_begin = split * a.kb_per_split;
+  const int kb_end = min(kb_begin + a.kb_per_split, a.KB);
+
+  // Per-lane global source of each wave-load: row r of the stage, logical
+  // chunk (lane&7) ^ (r&7) so that it lands in LDS slot lane&7.
+  const uint8_t* src[LOADS / NW];
+#pragma unroll
+  for (int i = 0; i < LOADS / NW; ++i) {
+    const int L = wid + i * NW;
+    const int r = L * 8 + (lane >> 3);
+    const int chunk = (lane & 7) ^ (r & 7);
+    if (L * 8 < BM) {
+      const int gmr = min(m0 + r, a.M - 1);
+      src[i] = a.A + (int64_t)gmr * a.lda + chunk * 16;
+    } else {
+      const int gnr = min(n0 + r - BM, a.N - 1);
+      src[i] = a.B + (int64_t)gnr * a.ldb + chunk * 16;
+    }
+  }
+
+  // Activation-scale rows of this lane (one per 16-row fragment) and the
+  // weight-scale block row of this wave.
+  const float* sa_ptr[FM];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int m = min(m0 + wm * WM + i * 16 + (lane & 15), a.M - 1);
+    sa_ptr[i] = a.As + (int64_t)m * a.as_sm;
+  }
+  const int nb = min((n0 + wn * WN) >> 7, (a.N - 1) >> 7);
+  const float* sb_ptr = a.Bs + (int64_t)nb * a.bs_sn;
+
+  // LDS byte offsets of this lane's fragment rows; the two 16-byte chunks of
+  // a fragment are logical chunks 2*(lane>>4) and 2*(lane>>4)+1.
+  const int c0 = 2 * (lane >> 4);
+  int a_off[FM], b_off[FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) a_off[i] = (wm * WM + i * 16 + (lane & 15)) * 128;
+#pragma unroll
+  for (int j = 0; j < FN; ++j) b_off[j] = (BM + wn * WN + j * 16 + (lane & 15)) * 128;
+
+  v4f acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  auto issue = [&](int kb, int stage) {
+    uint8_t* base = smem + stage * STAGE;
+#pragma unroll
+    for (int i = 0; i < LOADS / NW; ++i) {
+      const int L = wid + i * NW;
+      lds_dma16(src[i] + (int64_t)kb * 128, base + L * 1024);
+    }
+  };
+
+  if (kb_begin < kb_end) issue(kb_begin, 0);
+  float sa_cur[FM], sb_cur = 0.f;
+  if (kb_begin < kb_end) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) sa_cur[i] = sa_ptr[i][(int64_t)kb_begin * a.as_sk];
+    sb_cur = sb_ptr[(int64_t)kb_begin * a.bs_sk];
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  for (int kb = kb_begin; kb < kb_end; ++kb) {
+    const int stage = (kb - kb_begin) & 1;
+    const bool more = kb + 1 < kb_end;
+    if (more) issue(kb + 1, stage ^ 1);
+    float sa_nxt[FM], sb_nxt = 0.f;
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i) sa_nxt[i] = sa_ptr[i][(int64_t)(kb + 1) * a.as_sk];
+      sb_nxt = sb_ptr[(int64_t)(kb + 1) * a.bs_sk];
+    }
+
+    const uint8_t* sbase = smem + stage * STAGE;
+    v8i xf[FM], wf[FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int r7 = (a_off[i] >> 7) & 7;
+      const v4i lo = *reinterpret_cast<const v4i*>(sbase + a_off[i] + ((c0 ^ r7) << 4));
+      const v4i hi = *reinterpret_cast<const v4i*>(sbase + a_off[i] + (((c0 + 1) ^ r7) << 4));
+      xf[i] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int r7 = (b_off[j] >> 7) & 7;
+      const v4i lo = *reinterpret_cast<const v4i*>(sbase + b_off[j] + ((c0 ^ r7) << 4));
+      const v4i hi = *reinterpret_cast<const v4i*>(sbase + b_off[j] + (((c0 + 1) ^ r7) << 4));
+      wf[j] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const float sc = sa_cur[i] * sb_cur;
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const v4f t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+            wf[j], xf[i], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[i][j][r] = fmaf(t[r], sc, acc[i][j][r]);
+      }
+    }
+
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i) sa_cur[i] = sa_nxt[i];
+      sb_cur = sb_nxt;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
+
+  // Epilogue: lane holds row m = ... + (lane & 15) and columns 4*(lane>>4)+0..3
+  // of each 16x16 sub-tile.
+  const bool to_ws = gridDim.z > 1;
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int m = m0 + wm * WM + i * 16 + (lane & 15);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int n = n0 + wn * WN + j * 16 + 4 * (lane >> 4);
+      store4(a, m, n, acc[i][j], to_ws, split);
+    }
+  }
+}
+
+// Sum split-K partials in split order and convert: 4 outputs per thread.
+__global__ void __launch_bounds__(256)
+splitk_reduce_kernel(GemmArgs a, int splits) {
+  const int64_t quads_per_row = (a.N + 3) / 4;
+  const int64_t qi = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (qi >= (int64_t)a.M * quads_per_row) return;
+  const int m = (int)(qi / quads_per_row);
+  const int n = (int)(qi - (int64_t)m * quads_per_row) * 4;
+  v4f s = {0.f, 0.f, 0.f, 0.f};
+  const int64_t plane = (int64_t)a.M * a.N;
+  const float* p = a.ws + (int64_t)m * a.N + n;
+  for (int z = 0; z < splits; ++z) {
+    v4f v;
+    if (n + 3 < a.N && a.vec_store) {
+      v = *reinterpret_cast<const v4f*>(p + z * plane);
+    } else {
+      for (int r = 0; r < 4; ++r) v[r] = (n + r < a.N) ? p[z * plane + r] : 0.f;
+    }
+    s += v;
+  }
+  store4(a, m, n, s, false, 0);
+}
+
+// Generic SIMT kernel: 32x32 outputs per 256-thread block, 2x2 per thread.
+// For each K-block: part = sum_k A*B over the block (fp32 FMA chain in k
+// order), then acc += part * As * Bs, as in fp8.py:31-37.
+struct GenericArgs {
+  const uint8_t* A;
+  const uint8_t* B;
+  const float* As;
+  const float* Bs;
+  void* C;
+  int64_t lda, ldb, as_sm, as_sk, bs_sn, bs_sk, ldc;
+  int64_t M, N, K, block_n, block_k;
+  int out_dtype;
+};
+
+__global__ void __launch_bounds__(256) gemm_generic_kernel(GenericArgs g) {
+  __shared__ float sA[32][33];
+  __shared__ float sB[32][33];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int64_t mb = (int64_t)blockIdx.y * 32, nbase = (int64_t)blockIdx.x * 32;
+  float acc[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+  const int64_t KB = (g.K + g.block_k - 1) / g.block_k;
+  for (int64_t kb = 0; kb < KB; ++kb) {
+    float part[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+    const int64_t kbeg = kb * g.block_k, kend = min(kbeg + g.block_k, g.K);
+    for (int64_t k0 = kbeg; k0 < kend; k0 += 32) {
+      for (int e = threadIdx.x; e < 32 * 32; e += 256) {
+        const int r = e >> 5, c = e & 31;
+        const int64_t k = k0 + c;
+        const int64_t m = mb + r, n = nbase + r;
+        sA[r][c] = (m < g.M && k < kend) ? fp8e4m3_to_f32(g.A[m * g.lda + k]) : 0.f;
+        sB[r][c] = (n < g.N && k < kend) ? fp8e4m3_to_f32(g.B[n * g.ldb + k]) : 0.f;
+      }
+      __syncthreads();
+      for (int c = 0; c < 32; ++c) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            part[i][j] = fmaf(sA[ty * 2 + i][c], sB[tx * 2 + j][c], part[i][j]);
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int64_t m = min(mb + ty * 2 + i, g.M - 1);
+      const float sa = g.As[m * g.as_sm + kb * g.as_sk];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int64_t n = min(nbase + tx * 2 + j, g.N - 1);
+        const float sb = g.Bs[(n / g.block_n) * g.bs_sn + kb * g.bs_sk];
+        acc[i][j] = acc[i][j] + part[i][j] * sa * sb;
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int64_t m = mb + ty * 2 + i;
+    if (m >= g.M) continue;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t n = nbase + tx * 2 + j;
+      if (n >= g.N) continue;
+      const float v = acc[i][j];
+      if (g.out_dtype == FP8B_F32) {
+        reinterpret_cast<float*>(g.C)[m * g.ldc + n] = v;
+      } else if (g.out_dtype == FP8B_BF16) {
+        reinterpret_cast<uint16_t*>(g.C)[m * g.ldc + n] = f32_to_bf16_bits(v);
+      } else {
+        _Float16 h = (_Float16)v;
+        reinterpret_cast<uint16_t*>(g.C)[m * g.ldc + n] = __builtin_bit_cast(uint16_t, h);
+      }
+    }
+  }
+}
+
+}  // namespace fp8b
+
+using namespace fp8b;
+
+namespace {
+
+// Tile configurations of the MFMA path.
+enum TileCfg { CFG_256x256 = 0, CFG_128x128 = 1, CFG_64x128 = 2, CFG_32x128 = 3, CFG_COUNT };
+
+struct Plan {
+  int cfg;
+  int bm, bn;
+  int splits;
+  int kb_per_split;
+};
+
+int device_cu_count() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    return 256;
+  return cus;
+}
+
+Plan make_plan(int64_t M, int64_t N, int64_t K) {
+  const int KB = (int)(K / 128);
+  const int cus = device_cu_count();
+  Plan p;
+  auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+  if (M <= 32) {
+    p.cfg = CFG_32x128; p.bm = 32; p.bn = 128;
+  } else if (M <= 64) {
+    p.cfg = CFG_64x128; p.bm = 64; p.bn = 128;
+  } else if (tiles(256, 256) >= cus) {
+    p.cfg = CFG_256x256; p.bm = 256; p.bn = 256;
+  } else {
+    p.cfg = CFG_128x128; p.bm = 128; p.bn = 128;
+  }
+  const int64_t t = tiles(p.bm, p.bn);
+  // Grids with fewer tiles than CUs split K until there are about two
+  // workgroups per CU, keeping at least four K-blocks per split. Grids that
+  // already cover the CUs are not split: the fp32 partials would cost more
+  // HBM traffic than the extra occupancy recovers.
+  int splits = 1;
+  if (t < cus)
+    while (t * splits < 2 * cus && KB / (splits * 2) >= 4) splits *= 2;
+  p.kb_per_split = (KB + splits - 1) / splits;
+  p.splits = (KB + p.kb_per_split - 1) / p.kb_per_split;
+  if (p.splits < 1) p.splits = 1;
+  return p;
+}
+
+bool mfma_path_ok(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N,
+                  int64_t K, int64_t block_n, int64_t block_k) {
+  return block_n == 128 && block_k == 128 && K % 128 == 0 && K > 0 && lda % 16 == 0 &&
+         ldb % 16 == 0 && ((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0 &&
+         M < (int64_t(1) << 30) && N < (int64_t(1) << 30) && K < (int64_t(1) << 30);
+}
+
+template <int BM, int BN, int WM, int WN>
+void launch_cfg(const GemmArgs& a, int splits, hipStream_t st) {
+  dim3 grid(a.tiles_m * a.tiles_n, 1, splits);
+  gemm_bs128_kernel<BM, BN, WM, WN><<<grid, (BM / WM) * (BN / WN) * 64, 0, st>>>(a);
+}
+
+}  // namespace
+
+extern "C" size_t fp8b_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int64_t block_n,
+                                           int64_t block_k) {
+  if (M <= 0 || N <= 0 || K <= 0 || block_n != 128 || block_k != 128 || K % 128 != 0) return 0;
+  const Plan p = make_plan(M, N, K);
+  if (p.splits <= 1) return 0;
+  return (size_t)p.splits * (size_t)M * (size_t)N * sizeof(float);
+}
+
+extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B, int64_t ldb,
+                                      const float* As, int64_t as_sm, int64_t as_sk,
+                                      const float* Bs, int64_t bs_sn, int64_t bs_sk, void* C,
+                                      int64_t ldc, int out_dtype, int64_t M, int64_t N,
+                                      int64_t K, int64_t block_n, int64_t block_k,
+                                      void* workspace, size_t workspace_bytes, void* stream) {
+  if (M < 0 || N < 0 || K < 0 || lda < K || ldb < K || ldc < N) {
+    set_error("fp8b_w8a8_block_matmul: bad dims (need M,N,K >= 0, lda,ldb >= K, ldc >= N)");
+    return FP8B_ERR_DIMS;
+  }
+  if (block_n <= 0 || block_k <= 0) {
+    set_error("fp8b_w8a8_block_matmul: block_n and block_k must be positive");
+    return FP8B_ERR_BLOCK;
+  }
+  if (out_dtype != FP8B_F32 && out_dtype != FP8B_BF16 && out_dtype != FP8B_F16) {
+    set_error("fp8b_w8a8_block_matmul: out_dtype must be FP8B_F32, FP8B_BF16 or FP8B_F16");
+    return FP8B_ERR_DTYPE;
+  }
+  if (M == 0 || N == 0) return FP8B_OK;
+  if (!C || (K > 0 && (!A || !B || !As || !Bs))) {
+    set_error("fp8b_w8a8_block_matmul: null pointer");
+    return FP8B_ERR_NULL;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  const size_t esz = out_dtype == FP8B_F32 ? 4 : 2;
+
+  if (!mfma_path_ok(A, lda, B, ldb, M, N, K, block_n, block_k)) {
+    GenericArgs g;
+    g.A = (const uint8_t*)A; g.B = (const uint8_t*)B; g.As = As; g.Bs = Bs; g.C = C;
+    g.lda = lda; g.ldb = ldb; g.as_sm = as_sm; g.as_sk = as_sk; g.bs_sn = bs_sn;
+    g.bs_sk = bs_sk; g.ldc = ldc; g.M = M; g.N = N; g.K = K; g.block_n = block_n;
+    g.block_k = block_k; g.out_dtype = out_dtype;
+    dim3 grid((unsigned)((N + 31) / 32), (unsigned)((M + 31) / 32));
+    if (grid.y > 65535) {
+      set_error("fp8b_w8a8_block_matmul: M too large for the generic kernel");
+      return FP8B_ERR_DIMS;
+    }
+    gemm_generic_kernel<<<grid, 256, 0, st>>>(g);
+    if (hipGetLastError() != hipSuccess) {
+      set_error("fp8b_w8a8_block_matmul: generic kernel launch failed");
+      return FP8B_ERR_LAUNCH;
+    }
+    return FP8B_OK;
+  }
+
+  const Plan p = make_plan(M, N, K);
+  const size_t need = p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
+    set_error("fp8b_w8a8_block_matmul: workspace smaller than fp8b_gemm_workspace_size()");
+    return FP8B_ERR_WORKSPACE;
+  }
+  if (need > 0 && ((uintptr_t)workspace & 15) != 0) {
+    set_error("fp8b_w8a8_block_matmul: workspace must be 16-byte aligned");
+    return FP8B_ERR_ALIGN;
+  }
+  GemmArgs a;
+  a.A = (const uint8_t*)A; a.B = (const uint8_t*)B; a.As = As; a.Bs = Bs; a.C = C;
+  a.ws = (float*)workspace;
+  a.lda = lda; a.ldb = ldb; a.as_sm = as_sm; a.as_sk = as_sk; a.bs_sn = bs_sn; a.bs_sk = bs_sk;
+  a.ldc = ldc; a.M = (int)M; a.N = (int)N; a.K = (int)K; a.KB = (int)(K / 128);
+  a.kb_per_split = p.kb_per_split;
+  a.tiles_m = (int)((M + p.bm - 1) / p.bm);
+  a.tiles_n = (int)((N + p.bn - 1) / p.bn);
+  a.out_dtype = out_dtype;
+  const bool c_vec = (ldc % 4 == 0) && (((uintptr_t)C & (4 * esz - 1)) == 0);
+  const bool ws_vec = (N % 4 == 0);
+  a.vec_store = (p.splits > 1) ? (ws_vec ? 1 : 0) : (c_vec ? 1 : 0);
+
+  switch (p.cfg) {
+    case CFG_256x256: launch_cfg<256, 256, 64, 128>(a, p.splits, st); break;
+    case CFG_128x128: launch_cfg<128, 128, 64, 64>(a, p.splits, st); break;
+    case CFG_64x128: launch_cfg<64, 128, 32, 64>(a, p.splits, st); break;
+    default: launch_cfg<32, 128, 32, 32>(a, p.splits, st); break;
+  }
+  if (hipGetLastError() != hipSuccess) {
+    set_error("fp8b_w8a8_block_matmul: MFMA kernel launch failed");
+    return FP8B_ERR_LAUNCH;
+  }
+  if (p.splits > 1) {
+    GemmArgs r = a;
+    r.vec_store = (ws_vec && c_vec) ? 1 : 0;
+    const int64_t quads = M * ((N + 3) / 4);
+    splitk_reduce_kernel<<<(unsigned)((quads + 255) / 256), 256, 0, st>>>(r, p.splits);
+    if (hipGetLastError() != hipSuccess) {
+      set_error("fp8b_w8a8_block_matmul: split-K reduce launch failed");
+      return FP8B_ERR_LAUNCH;
+    }
+  }
+  return FP8B_OK;
+}

@@ -1,0 +1,69 @@
+"""MI355X-native drop-in for the finegrained-fp8-helion package.
+
+Public surface of finegrained-fp8-helion/torch-ext/finegrained_fp8_helion/
+__init__.py:7-17 (``w8a8_block_fp8_matmul`` with the same signature, block_size
+unpacking and output_dtype default) plus the activation quantiser that feeds
+it, the gated SiLU of the FP8 MLP chain and their fused form.
+"""
+from __future__ import annotations
+
+import torch
+
+from ._ops import ops
+from . import op as _op  # registers the custom ops
+from .mlp import fp8_mlp
+
+_DIRECT_OUT = (torch.float32, torch.bfloat16, torch.float16)
+
+
+def w8a8_block_fp8_matmul(A: torch.Tensor, B: torch.Tensor, As: torch.Tensor,
+                          Bs: torch.Tensor, block_size, output_dtype=torch.float32):
+    """C = A @ B.T with blockwise scales (reference __init__.py:7-14).
+
+    A: [M,K] float8_e4m3fn, B: [N,K] float8_e4m3fn, As: [M, K//bk] fp32,
+    Bs: [N//bn, K//bk] fp32, block_size = [block_n, block_k].
+    Returns [M,N] in output_dtype. float32/bfloat16/float16 are written by the
+    kernel's epilogue; other dtypes are cast from the fp32 result.
+    """
+    block_n, block_k = int(block_size[0]), int(block_size[1])
+    if output_dtype in _DIRECT_OUT:
+        return ops.w8a8_block_fp8_matmul_dtype(A, B, As, Bs, block_n, block_k, output_dtype)
+    out = ops.w8a8_block_fp8_matmul(A, B, As, Bs, block_n, block_k)
+    return out.to(output_dtype)
+
+
+def act_quant(x: torch.Tensor, block_size: int = 128):
+    """Quantise bf16 activations per 1 x block_size group to float8_e4m3fn.
+
+    Returns (q, s): q has x's shape, s is fp32 [..., ceil(K/block_size)] with
+    s = max(amax, 1e-10) / 448 and q = e4m3fn(x / s). The pair is the (A, As)
+    operand of w8a8_block_fp8_matmul.
+    """
+    return ops.act_quant(x, int(block_size))
+
+
+def per_token_group_quant_fp8(x: torch.Tensor, group_size: int = 128):
+    """Alias of act_quant under the name serving stacks use for it."""
+    return act_quant(x, group_size)
+
+
+def silu_and_mul(out: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """out = silu(x[..., :d]) * x[..., d:] (bf16), written into ``out``
+    (activation-helion/activation-helion/torch-ext/activation_helion/__init__.py:7-10)."""
+    ops.silu_and_mul(out, x)
+    return out
+
+
+def silu_and_mul_quant(x: torch.Tensor, block_size: int = 128):
+    """act_quant(silu_and_mul(x)) in one pass; returns (q, s)."""
+    return ops.silu_and_mul_quant(x, int(block_size))
+
+
+__all__ = [
+    "w8a8_block_fp8_matmul",
+    "act_quant",
+    "per_token_group_quant_fp8",
+    "silu_and_mul",
+    "silu_and_mul_quant",
+    "fp8_mlp",
+]

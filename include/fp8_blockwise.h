@@ -1,0 +1,142 @@
+/*
+ * fp8_blockwise.h -- C ABI of the MI355X (gfx950) block-FP8 linear path.
+ *
+ * Two stages, each a hand-written HIP kernel family in libfp8_blockwise.so:
+ *   1. per-token-group activation quantisation: bf16 [M,K] -> float8_e4m3fn
+ *      [M,K] plus fp32 scales [M, ceil(K/group)], scale = amax/448;
+ *   2. w8a8 GEMM  C[M,N] = A[M,K] . B[N,K]^T  with A carrying per-(row, K-block)
+ *      fp32 scales As and B carrying per-(N-block, K-block) fp32 scales Bs,
+ *      accumulated in fp32 and stored as fp32, bf16 or fp16.
+ *
+ * Conventions shared by every entry point:
+ *   - all data pointers are DEVICE pointers; the library never allocates,
+ *     frees or copies on the host; it only reads/writes the caller's buffers;
+ *   - strides are in ELEMENTS, the innermost (K or N) stride of matrices is 1;
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream);
+ *     launches are asynchronous on it; the functions are stateless and
+ *     re-entrant (concurrent calls on different streams are safe);
+ *   - the return value is an fp8b_status; no C++ exception crosses the ABI.
+ *     fp8b_last_error() returns a static text describing the last failure of
+ *     the calling thread.
+ */
+#ifndef FP8_BLOCKWISE_H
+#define FP8_BLOCKWISE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum fp8b_status {
+  FP8B_OK = 0,
+  FP8B_ERR_NULL = 1,       /* a required pointer is NULL                         */
+  FP8B_ERR_DIMS = 2,       /* negative/overflowing size or stride                */
+  FP8B_ERR_ALIGN = 3,      /* pointer or leading dimension misaligned             */
+  FP8B_ERR_BLOCK = 4,      /* unsupported block_n / block_k / group size          */
+  FP8B_ERR_DTYPE = 5,      /* unsupported output dtype code                       */
+  FP8B_ERR_WORKSPACE = 6,  /* workspace too small for the chosen plan             */
+  FP8B_ERR_LAUNCH = 7      /* a HIP launch or runtime call failed                 */
+} fp8b_status;
+
+/* Output element type codes for the GEMM epilogue. */
+typedef enum fp8b_dtype {
+  FP8B_F32 = 0,
+  FP8B_BF16 = 1,
+  FP8B_F16 = 2
+} fp8b_dtype;
+
+/* Library version, e.g. 0x000100 = 0.1.0. */
+int fp8b_version(void);
+
+/* Text of the calling thread's most recent error (never NULL). */
+const char* fp8b_last_error(void);
+
+/*
+ * Per-token-group fp8 quantisation.
+ *
+ * No counterpart exists in the reference: finegrained-fp8-helion consumes
+ * already-quantised A/As (torch-ext/finegrained_fp8_helion/fp8.py:5,24) and
+ * ships no quantiser. The contract is the one its callers feed it with:
+ *   for each row m and group g = [g*group, min((g+1)*group, K)):
+ *     amax   = max |x[m,k]|          (NaN if any element is NaN)
+ *     amax'  = max(amax, 1e-10)
+ *     s[m,g] = amax' / 448            (fp32, IEEE division)
+ *     q[m,k] = float8_e4m3fn(x[m,k] / s[m,g])   (IEEE division, RNE)
+ *   non-finite groups: amax NaN -> s = NaN, every q = 0x7F;
+ *                      amax +inf -> s = +inf, q = signed zero for finite x,
+ *                      0x7F for +-inf.
+ *
+ * x : bf16 [M,K] with row stride ldx; q : e4m3fn [M,K] row stride ldq;
+ * s : fp32, element (m,g) at s[m*s_stride_m + g*s_stride_g].
+ * group must be 32, 64, 128 or 256.
+ */
+int fp8b_act_quant(const void* x, int64_t ldx,
+                   void* q, int64_t ldq,
+                   float* s, int64_t s_stride_m, int64_t s_stride_g,
+                   int64_t M, int64_t K, int64_t group,
+                   void* stream);
+
+/*
+ * Block-scaled w8a8 GEMM: C = A . B^T.
+ *
+ * Replaces the Helion kernel _w8a8_block_fp8_matmul
+ * (finegrained-fp8-helion/torch-ext/finegrained_fp8_helion/fp8.py:19-39)
+ * behind the custom op of op.py:8-11:
+ *   C[m,n] = sum_kb ( sum_{k in kb} A[m,k] B[n,k] ) * As[m,kb] * Bs[n/block_n, kb]
+ *
+ * A  : e4m3fn [M,K], row stride lda      B  : e4m3fn [N,K], row stride ldb
+ * As : fp32, (m,kb) at As[m*as_sm + kb*as_sk]
+ * Bs : fp32, (nb,kb) at Bs[nb*bs_sn + kb*bs_sk]
+ * C  : out_dtype [M,N], row stride ldc
+ * kb runs over ceil(K/block_k) K-blocks; nb over ceil(N/block_n).
+ *
+ * block_n = block_k = 128, K % 128 == 0, 16-byte aligned A/B with lda, ldb
+ * multiples of 16 take the MFMA path; any other positive block sizes take a
+ * generic (slower) GPU kernel with the same semantics.
+ * workspace may be NULL when fp8b_gemm_workspace_size() returns 0 for the
+ * same arguments; otherwise it must hold at least that many bytes.
+ */
+int fp8b_w8a8_block_matmul(const void* A, int64_t lda,
+                           const void* B, int64_t ldb,
+                           const float* As, int64_t as_sm, int64_t as_sk,
+                           const float* Bs, int64_t bs_sn, int64_t bs_sk,
+                           void* C, int64_t ldc, int out_dtype,
+                           int64_t M, int64_t N, int64_t K,
+                           int64_t block_n, int64_t block_k,
+                           void* workspace, size_t workspace_bytes,
+                           void* stream);
+
+/* Bytes of device workspace fp8b_w8a8_block_matmul needs for these sizes. */
+size_t fp8b_gemm_workspace_size(int64_t M, int64_t N, int64_t K,
+                                int64_t block_n, int64_t block_k);
+
+/*
+ * Gated SiLU: out[m,j] = bf16( bf16(silu(fp32 x[m,j])) * x[m,d+j] ), j < d,
+ * for bf16 x [M,2d] (row stride ldx) and out [M,d] (row stride ldo).
+ * Replaces _silu_and_mul of
+ * activation-helion/activation-helion/torch-ext/activation_helion/act.py:20-28
+ * (the SiLU(gate)*up step between the two GEMMs of an FP8 MLP).
+ */
+int fp8b_silu_and_mul(const void* x, int64_t ldx, void* out, int64_t ldo,
+                      int64_t M, int64_t d, void* stream);
+
+/*
+ * silu_and_mul fused with per-token-group fp8 quantisation of its result:
+ * q/s as fp8b_act_quant would produce from the bf16 output of
+ * fp8b_silu_and_mul, without writing that bf16 tensor to memory.
+ * No single counterpart in the reference: it composes act.py:20-28 with the
+ * quantiser above.
+ */
+int fp8b_silu_and_mul_quant(const void* x, int64_t ldx,
+                            void* q, int64_t ldq,
+                            float* s, int64_t s_stride_m, int64_t s_stride_g,
+                            int64_t M, int64_t d, int64_t group,
+                            void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FP8_BLOCKWISE_H */

@@ -1,0 +1,87 @@
+"""CPU checks of the C ABI: the library loads, exports every symbol that
+include/fp8_blockwise.h declares, and rejects bad arguments before touching
+the GPU."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from hf_kernels_helion_amd import _native
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "fp8_blockwise.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fp8b_\w+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    for n in ("fp8b_act_quant", "fp8b_w8a8_block_matmul", "fp8b_gemm_workspace_size",
+              "fp8b_silu_and_mul", "fp8b_silu_and_mul_quant", "fp8b_version", "fp8b_last_error"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.load()
+    for n in declared_functions():
+        assert hasattr(lib, n), n
+        assert n in _native.SIGNATURES, f"{n} missing from the ctypes signature table"
+
+
+def test_version_and_error_text():
+    lib = _native.load()
+    assert lib.fp8b_version() == 0x000100
+    assert isinstance(lib.fp8b_last_error(), bytes)
+
+
+def test_gemm_rejects_bad_args_without_gpu():
+    lib = _native.load()
+    # negative M
+    st = lib.fp8b_w8a8_block_matmul(None, 128, None, 128, None, 1, 1, None, 1, 1, None, 128,
+                                    _native.BF16, -1, 128, 128, 128, 128, None, 0, None)
+    assert st == 2 and b"bad dims" in lib.fp8b_last_error()
+    # lda < K
+    st = lib.fp8b_w8a8_block_matmul(None, 64, None, 128, None, 1, 1, None, 1, 1, None, 128,
+                                    _native.BF16, 4, 128, 128, 128, 128, None, 0, None)
+    assert st == 2
+    # bad block size
+    st = lib.fp8b_w8a8_block_matmul(None, 128, None, 128, None, 1, 1, None, 1, 1, None, 128,
+                                    _native.BF16, 4, 128, 128, 0, 128, None, 0, None)
+    assert st == 4
+    # bad out dtype
+    st = lib.fp8b_w8a8_block_matmul(None, 128, None, 128, None, 1, 1, None, 1, 1, None, 128,
+                                    9, 4, 128, 128, 128, 128, None, 0, None)
+    assert st == 5
+    # null pointers with non-empty sizes
+    st = lib.fp8b_w8a8_block_matmul(None, 128, None, 128, None, 1, 1, None, 1, 1, None, 128,
+                                    _native.BF16, 4, 128, 128, 128, 128, None, 0, None)
+    assert st == 1
+    # empty problem is a no-op success
+    st = lib.fp8b_w8a8_block_matmul(None, 128, None, 128, None, 1, 1, None, 1, 1, None, 128,
+                                    _native.BF16, 0, 128, 128, 128, 128, None, 0, None)
+    assert st == 0
+
+
+def test_act_quant_rejects_bad_args_without_gpu():
+    lib = _native.load()
+    assert lib.fp8b_act_quant(None, 128, None, 128, None, 1, 1, 4, 128, 100, None) == 4
+    assert lib.fp8b_act_quant(None, 64, None, 128, None, 1, 1, 4, 128, 128, None) == 2
+    assert lib.fp8b_act_quant(None, 128, None, 128, None, 1, 1, 4, 128, 128, None) == 1
+    assert lib.fp8b_act_quant(None, 128, None, 128, None, 1, 1, 0, 128, 128, None) == 0
+    assert lib.fp8b_silu_and_mul(None, 10, None, 8, 2, 8, None) == 2
+    assert lib.fp8b_silu_and_mul_quant(None, 256, None, 128, None, 1, 1, 2, 128, 48, None) == 4
+
+
+def test_workspace_size_zero_for_unsupported_blocks():
+    lib = _native.load()
+    assert lib.fp8b_gemm_workspace_size(32, 4096, 14336, 64, 128) == 0
+    assert lib.fp8b_gemm_workspace_size(0, 4096, 14336, 128, 128) == 0
+
+
+def test_status_to_runtime_error():
+    with pytest.raises(RuntimeError, match="FP8B_ERR_DIMS"):
+        _native.check(2, "probe")

@@ -1,0 +1,148 @@
+"""GPU parity of the act-quant kernels against the CPU oracle: bit-exact fp8
+codes and fp32 scales (bits compared, NaN included)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from hf_kernels_helion_amd import finegrained_fp8_helion as fp8
+from hf_kernels_helion_amd.finegrained_fp8_helion import synthetic
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(x_bf16: torch.Tensor) -> np.ndarray:
+    return x_bf16.cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _run(x_cpu: torch.Tensor, group: int, dev):
+    q, s = fp8.act_quant(x_cpu.to(dev), group)
+    torch.cuda.synchronize()
+    return q.cpu().view(torch.uint8).numpy(), s.cpu().numpy()
+
+
+def _assert_exact(x_cpu, group, dev):
+    q, s = _run(x_cpu, group, dev)
+    x2 = _bits(x_cpu).reshape(-1, x_cpu.shape[-1])
+    qo, so = oracle.act_quant(x2, group)
+    np.testing.assert_array_equal(q.reshape(qo.shape), qo)
+    np.testing.assert_array_equal(s.reshape(so.shape).view(np.uint32), so.view(np.uint32))
+
+
+@pytest.mark.parametrize("M,K", [(1, 128), (4, 512), (32, 14336), (57, 4096), (3001, 1024),
+                                 (512, 2048)])
+def test_act_quant_g128_exact(M, K, dev):
+    print(f"act_quant g128 M={M} K={K}", flush=True)
+    x = synthetic.activations(M, K, seed=M * 7 + K)
+    _assert_exact(x, 128, dev)
+
+
+def test_act_quant_outliers_exact(dev):
+    print("act_quant outliers", flush=True)
+    x = synthetic.activations(256, 4096, seed=99, outlier_frac=0.01)
+    _assert_exact(x, 128, dev)
+
+
+@pytest.mark.parametrize("group", [32, 64, 128, 256])
+@pytest.mark.parametrize("K", [100, 300, 1000])
+def test_act_quant_generic_exact(group, K, dev):
+    print(f"act_quant generic group={group} K={K}", flush=True)
+    x = synthetic.activations(9, K, seed=group + K)
+    _assert_exact(x, group, dev)
+
+
+def test_act_quant_every_bf16_through_cvt(dev):
+    """Groups whose amax is exactly 448 have scale 1.0, so q = e4m3fn(x) for
+    every bf16 x with |x| <= 448: the hardware convert is checked on all of
+    them. Each 128-group holds one 448 and 127 test values."""
+    print("act_quant exhaustive bf16 cvt", flush=True)
+    bits = np.arange(65536, dtype=np.uint32)
+    f = (bits << 16).view(np.float32)
+    vals = f[np.isfinite(f) & (np.abs(f) <= 448.0)]
+    per = 127
+    G = -(-vals.size // per)
+    padded = np.zeros(G * per, dtype=np.float32)
+    padded[: vals.size] = vals
+    grid = np.full((G, 128), 448.0, dtype=np.float32)
+    grid[:, 1:] = padded.reshape(G, per)
+    x = torch.from_numpy(grid.reshape(-1, 1024 if G % 8 == 0 else 128)).to(torch.bfloat16)
+    _assert_exact(x, 128, dev)
+    q, s = _run(x, 128, dev)
+    assert np.all(s == 1.0)
+
+
+def test_act_quant_scales_sweep_exact(dev):
+    """Same values under many amax values: exercises the IEEE division."""
+    print("act_quant scale sweep", flush=True)
+    g = torch.Generator().manual_seed(7)
+    rows = []
+    for e in range(-30, 30, 3):
+        r = torch.randn(1, 4096, generator=g) * (2.0 ** e)
+        rows.append(r)
+    x = torch.cat(rows).to(torch.bfloat16)
+    _assert_exact(x, 128, dev)
+
+
+def test_act_quant_nonfinite_and_zero_groups(dev):
+    print("act_quant nonfinite", flush=True)
+    x = torch.randn(4, 512).to(torch.bfloat16)
+    x[0, 0:128] = 0.0
+    x[0, 5] = -0.0
+    x[1, 130] = float("nan")
+    x[2, 300] = float("inf")
+    x[2, 301] = -float("inf")
+    x[3, 400] = 1e-39  # bf16 subnormal
+    x[3, 384:512] = 1e-30
+    _assert_exact(x, 128, dev)
+    _assert_exact(x, 64, dev)
+
+
+def test_act_quant_strided_and_3d(dev):
+    print("act_quant strided/3d", flush=True)
+    x = synthetic.activations(64, 1024, seed=3)
+    xs = x[:, :512]  # row stride 1024
+    q, s = fp8.act_quant(xs.to(dev), 128)
+    qo, so = oracle.act_quant(_bits(xs.contiguous()), 128)
+    np.testing.assert_array_equal(q.cpu().view(torch.uint8).numpy(), qo)
+    np.testing.assert_array_equal(s.cpu().numpy(), so)
+    x3 = x.view(4, 16, 1024)
+    q3, s3 = fp8.act_quant(x3.to(dev), 128)
+    assert q3.shape == (4, 16, 1024) and s3.shape == (4, 16, 8)
+    qo, so = oracle.act_quant(_bits(x), 128)
+    np.testing.assert_array_equal(q3.cpu().view(torch.uint8).numpy().reshape(64, 1024), qo)
+
+
+def test_act_quant_empty(dev):
+    q, s = fp8.act_quant(torch.empty(0, 256, dtype=torch.bfloat16, device=dev), 128)
+    assert q.shape == (0, 256) and s.shape == (0, 2)
+
+
+def test_act_quant_full_size_properties(dev):
+    """At the 4096x8192 benchmark size: check a sample of rows bit-exactly and
+    the size-independent properties on all rows (amax element -> +-448,
+    s == amax/448 exactly, |dequant - x| within half an fp8 step)."""
+    print("act_quant 4096x8192 properties", flush=True)
+    M, K = 4096, 8192
+    x = synthetic.activations(M, K, seed=11)
+    xd = x.to(dev)
+    q, s = fp8.act_quant(xd, 128)
+    xf = xd.float().view(M, K // 128, 128)
+    amax = xf.abs().amax(-1)
+    # IEEE fp32 division on the host (torch's GPU scalar division multiplies
+    # by the reciprocal, which is not the contract)
+    s_expect = np.maximum(amax.cpu().numpy(), np.float32(1e-10)) / np.float32(448.0)
+    np.testing.assert_array_equal(s.cpu().numpy(), s_expect)
+    qf = q.float().view(M, K // 128, 128)
+    assert torch.all(qf.abs().amax(-1) == 448.0)
+    # |q*s - x| <= half an e4m3 step at x/s, in float64 on the host.
+    # e4m3 spacing at |v| in [2^e, 2^(e+1)) is 2^(e-3) (2^-9 below 2^-6).
+    q64 = qf.cpu().double()
+    s64 = torch.from_numpy(s_expect).double().unsqueeze(-1)
+    x64 = xf.cpu().double()
+    y = (x64 / s64).abs().clamp_min(2.0 ** -6)
+    half_step = torch.exp2(torch.floor(torch.log2(y)) - 4)
+    assert torch.all((q64 - x64 / s64).abs() <= half_step * (1 + 1e-9))
+    rows = torch.randperm(M, generator=torch.Generator().manual_seed(5))[:64]
+    qo, so = oracle.act_quant(_bits(x[rows]), 128)
+    np.testing.assert_array_equal(q[rows.to(dev)].cpu().view(torch.uint8).numpy(), qo)
+    np.testing.assert_array_equal(s[rows.to(dev)].cpu().numpy(), so)

@@ -1,0 +1,184 @@
+"""GPU parity of the block-FP8 GEMM against the CPU oracle.
+
+Tolerance: the bf16 output within 1e-2 relative /
+1e-3 absolute of the oracle's result of the reference formula
+(finegrained-fp8-helion/torch-ext/finegrained_fp8_helion/fp8.py:28-38),
+itself checked against the fp32 dequant-matmul oracle.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from hf_kernels_helion_amd import finegrained_fp8_helion as fp8
+from hf_kernels_helion_amd.finegrained_fp8_helion import synthetic
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-2, 1e-3
+
+
+def _u8(t: torch.Tensor) -> np.ndarray:
+    return t.cpu().contiguous().view(torch.uint8).numpy()
+
+
+def _operands(M, N, K, seed, kind="model", outliers=0.0):
+    if kind == "harness":
+        return synthetic.harness_operands(M, N, K, seed=seed)
+    x = synthetic.activations(M, K, seed=seed, outlier_frac=outliers)
+    xg = x.cuda()
+    q, s = fp8.act_quant(xg, 128)
+    W, Bs = synthetic.weights(N, K, seed=seed + 1)
+    return q.cpu(), W, s.cpu(), Bs
+
+
+def _check(out_gpu, A, B, As, Bs, block=(128, 128), rows=None):
+    ref = oracle.block_gemm(_u8(A), _u8(B), As.numpy(), Bs.numpy(), block)
+    got = out_gpu.float().cpu()
+    if rows is not None:
+        got = got[rows]
+    ref_t = torch.from_numpy(ref)
+    if out_gpu.dtype != torch.float32:
+        ref_t = ref_t.to(out_gpu.dtype).float()
+    torch.testing.assert_close(got, ref_t, rtol=RTOL, atol=ATOL)
+    return ref
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 512, 2048), (128, 256, 1024), (57, 200, 384),
+                                   (1, 128, 128), (300, 640, 512), (32, 4096, 1024),
+                                   (64, 512, 2048), (257, 384, 256)])
+@pytest.mark.parametrize("kind", ["model", "harness"])
+def test_gemm_bf16_vs_oracle(M, N, K, kind, dev):
+    print(f"gemm bf16 {kind} M={M} N={N} K={K}", flush=True)
+    A, B, As, Bs = _operands(M, N, K, seed=M + N + K, kind=kind)
+    out = fp8.w8a8_block_fp8_matmul(A.to(dev), B.to(dev), As.to(dev), Bs.to(dev), [128, 128],
+                                    torch.bfloat16)
+    assert out.dtype == torch.bfloat16 and out.shape == (M, N)
+    _check(out, A, B, As, Bs)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.float64])
+def test_gemm_output_dtypes(dtype, dev):
+    print(f"gemm out dtype {dtype}", flush=True)
+    M, N, K = 96, 384, 1024
+    A, B, As, Bs = _operands(M, N, K, seed=5)
+    out = fp8.w8a8_block_fp8_matmul(A.to(dev), B.to(dev), As.to(dev), Bs.to(dev), [128, 128],
+                                    dtype)
+    assert out.dtype == dtype
+    _check(out.float() if dtype == torch.float64 else out, A, B, As, Bs)
+
+
+def test_gemm_default_output_is_fp32(dev):
+    A, B, As, Bs = _operands(64, 128, 256, seed=1)
+    out = fp8.w8a8_block_fp8_matmul(A.to(dev), B.to(dev), As.to(dev), Bs.to(dev), (128, 128))
+    assert out.dtype == torch.float32
+
+
+def test_gemm_bf16_is_rne_of_fp32(dev):
+    """The bf16 epilogue equals the fp32 op's result rounded by torch."""
+    M, N, K = 200, 512, 2048
+    A, B, As, Bs = [t.to(dev) for t in _operands(M, N, K, seed=8)]
+    f32 = fp8.w8a8_block_fp8_matmul(A, B, As, Bs, [128, 128], torch.float32)
+    b16 = fp8.w8a8_block_fp8_matmul(A, B, As, Bs, [128, 128], torch.bfloat16)
+    assert torch.equal(f32.to(torch.bfloat16), b16)
+
+
+def test_gemm_exact_small_integers(dev):
+    """As = Bs = 1 and small-integer fp8 operands: every partial sum is an
+    integer below 2^24, so the result is exact and must match bit for bit."""
+    print("gemm exact integers", flush=True)
+    g = torch.Generator().manual_seed(3)
+    M, N, K = 160, 256, 1024
+    A = torch.randint(-4, 5, (M, K), generator=g).float().to(torch.float8_e4m3fn)
+    B = torch.randint(-4, 5, (N, K), generator=g).float().to(torch.float8_e4m3fn)
+    As = torch.ones(M, K // 128)
+    Bs = torch.ones(N // 128, K // 128)
+    out = fp8.w8a8_block_fp8_matmul(A.to(dev), B.to(dev), As.to(dev), Bs.to(dev), [128, 128])
+    exact = A.double() @ B.double().T
+    assert torch.equal(out.cpu().double(), exact)
+
+
+def test_gemm_one_hot_rows_select_weight_rows(dev):
+    M, N, K = 64, 256, 512
+    A = torch.zeros(M, K)
+    cols = torch.arange(M) * 7 % K
+    A[torch.arange(M), cols] = 1.0
+    A = A.to(torch.float8_e4m3fn)
+    W, Bs = synthetic.weights(N, K, seed=4)
+    As = torch.full((M, K // 128), 2.0)
+    out = fp8.w8a8_block_fp8_matmul(A.to(dev), W.to(dev), As.to(dev), Bs.to(dev), [128, 128])
+    sbf = Bs.repeat_interleave(128, 0)[:N].repeat_interleave(128, 1)[:, :K]
+    expect = (W.float() * sbf)[:, cols].T * 2.0
+    assert torch.equal(out.cpu(), expect)
+
+
+def test_gemm_generic_block_sizes(dev):
+    """Block sizes other than 128x128 and ragged K run the generic kernel."""
+    for (M, N, K, bn, bk) in [(33, 70, 200, 64, 64), (16, 96, 256, 32, 128), (40, 130, 300, 128, 128)]:
+        print(f"gemm generic M={M} N={N} K={K} bn={bn} bk={bk}", flush=True)
+        A, B, As, Bs = synthetic.harness_operands(M, N, K, seed=M, block_n=bn, block_k=bk)
+        out = fp8.w8a8_block_fp8_matmul(A.to(dev), B.to(dev), As.to(dev), Bs.to(dev), [bn, bk],
+                                        torch.float32)
+        _check(out, A, B, As, Bs, block=(bn, bk))
+
+
+def test_gemm_strided_scales_and_operands(dev):
+    """Non-contiguous A (row stride > K) and transposed-storage As."""
+    M, N, K = 100, 256, 1024
+    A, B, As, Bs = _operands(M, N, K, seed=12)
+    Abig = torch.zeros(M, K + 256, dtype=torch.uint8)
+    Abig[:, :K] = A.view(torch.uint8)
+    Av = Abig.to(dev).view(torch.float8_e4m3fn)[:, :K]
+    As_t = As.T.contiguous().to(dev).T  # column-major storage
+    out = fp8.w8a8_block_fp8_matmul(Av, B.to(dev), As_t, Bs.to(dev), [128, 128], torch.bfloat16)
+    _check(out, A, B, As, Bs)
+
+
+def test_gemm_empty_shapes(dev):
+    A = torch.empty(0, 256, dtype=torch.float8_e4m3fn, device=dev)
+    B = torch.zeros(128, 256, dtype=torch.float8_e4m3fn, device=dev)
+    out = fp8.w8a8_block_fp8_matmul(A, B, torch.ones(0, 2, device=dev),
+                                    torch.ones(1, 2, device=dev), [128, 128], torch.bfloat16)
+    assert out.shape == (0, 128)
+
+
+def test_gemm_decode_shape_splitk(dev):
+    """M=32, N=4096, K=14336 (split-K path) against the oracle on all rows."""
+    print("gemm decode 32x4096x14336", flush=True)
+    A, B, As, Bs = _operands(32, 4096, 14336, seed=21)
+    out = fp8.w8a8_block_fp8_matmul(A.to(dev), B.to(dev), As.to(dev), Bs.to(dev), [128, 128],
+                                    torch.bfloat16)
+    _check(out, A, B, As, Bs)
+
+
+@pytest.mark.parametrize("M,N,K,outliers", [(2048, 2048, 4096, 0.01), (4096, 4096, 8192, 0.0)])
+def test_gemm_large_sampled_rows(M, N, K, outliers, dev):
+    """Benchmark sizes: every row checked against torch's fp32 dequant-matmul
+    on the GPU; a seeded sample of rows checked against the oracle."""
+    print(f"gemm large M={M} N={N} K={K}", flush=True)
+    A, B, As, Bs = _operands(M, N, K, seed=M, outliers=outliers)
+    Ad, Bd, Asd, Bsd = A.to(dev), B.to(dev), As.to(dev), Bs.to(dev)
+    out = fp8.w8a8_block_fp8_matmul(Ad, Bd, Asd, Bsd, [128, 128], torch.bfloat16)
+    rows = torch.randperm(M, generator=torch.Generator().manual_seed(1))[:8]
+    ref = oracle.block_gemm(_u8(A[rows]), _u8(B), As[rows].numpy(), Bs.numpy())
+    torch.testing.assert_close(out[rows.to(dev)].float().cpu(),
+                               torch.from_numpy(ref).to(torch.bfloat16).float(),
+                               rtol=RTOL, atol=ATOL)
+    saf = Asd.repeat_interleave(128, 1)[:, :K]
+    sbf = Bsd.repeat_interleave(128, 0)[:N].repeat_interleave(128, 1)[:, :K]
+    full = (Ad.float() * saf) @ (Bd.float() * sbf).T
+    torch.testing.assert_close(out.float(), full.to(torch.bfloat16).float(), rtol=RTOL, atol=ATOL)
+
+
+def test_gemm_golden_fixture(dev):
+    """Float64 golden output; the fp8 MFMA sums a 128-long K-block with less
+    than fp32 precision (measured ~2^-15 relative to the block's dot), so the
+    bound is 1e-4 absolute on outputs of magnitude ~1."""
+    import pathlib
+    z = np.load(pathlib.Path(__file__).parent / "golden" / "gemm_fp64_small.npz")
+    A = torch.from_numpy(z["A"]).view(torch.float8_e4m3fn)
+    B = torch.from_numpy(z["B"]).view(torch.float8_e4m3fn)
+    As, Bs = torch.from_numpy(z["As"]), torch.from_numpy(z["Bs"])
+    out = fp8.w8a8_block_fp8_matmul(A.to(dev), B.to(dev), As.to(dev), Bs.to(dev),
+                                    z["block"].tolist(), torch.float32)
+    np.testing.assert_allclose(out.cpu().numpy(), z["C"], rtol=1e-3, atol=1e-4)

@@ -1,0 +1,83 @@
+"""GPU parity of silu_and_mul, its fused quantiser and the FP8 MLP chain."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import torch_ref
+from hf_kernels_helion_amd import finegrained_fp8_helion as fp8
+from hf_kernels_helion_amd.finegrained_fp8_helion import synthetic
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(t):
+    return t.cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("M,d", [(1, 8), (7, 1000), (64, 14336), (3001, 256)])
+def test_silu_and_mul_vs_oracle(M, d, dev):
+    """silu goes through expf on both sides; results agree to 1 bf16 ulp."""
+    print(f"silu_and_mul M={M} d={d}", flush=True)
+    x = synthetic.activations(M, 2 * d, seed=d) * 3
+    out = torch.empty(M, d, dtype=torch.bfloat16, device=dev)
+    fp8.silu_and_mul(out, x.to(dev))
+    ref = torch.from_numpy(oracle.silu_and_mul(_bits(x)).view(np.int16)).view(torch.bfloat16)
+    torch.testing.assert_close(out.cpu().float(), ref.float(), rtol=2 ** -7, atol=1e-6)
+    exact = (out.cpu() == ref).float().mean().item()
+    assert exact > 0.99, exact
+
+
+def test_silu_and_mul_3d(dev):
+    x = synthetic.activations(24, 512, seed=2).view(2, 12, 512)
+    out = torch.empty(2, 12, 256, dtype=torch.bfloat16, device=dev)
+    fp8.silu_and_mul(out, x.to(dev))
+    ref = torch_ref.silu_and_mul(x)
+    torch.testing.assert_close(out.cpu().float(), ref.float(), rtol=2 ** -7, atol=1e-6)
+
+
+@pytest.mark.parametrize("M,d,group", [(3001, 14336, 128), (5, 384, 128), (9, 200, 64),
+                                       (4, 256, 256)])
+def test_silu_and_mul_quant_equals_two_ops(M, d, group, dev):
+    """Fused kernel == silu_and_mul then act_quant, bit for bit."""
+    print(f"silu_and_mul_quant M={M} d={d} group={group}", flush=True)
+    x = (synthetic.activations(M, 2 * d, seed=M + d) * 2).to(dev)
+    q, s = fp8.silu_and_mul_quant(x, group)
+    h = torch.empty(M, d, dtype=torch.bfloat16, device=dev)
+    fp8.silu_and_mul(h, x)
+    q2, s2 = fp8.act_quant(h, group)
+    assert torch.equal(q.view(torch.uint8), q2.view(torch.uint8))
+    assert torch.equal(s.view(torch.int32), s2.view(torch.int32))
+    # and act_quant of the GPU bf16 intermediate is the oracle's, bit for bit
+    qo, so = oracle.act_quant(_bits(h), group)
+    np.testing.assert_array_equal(q.cpu().view(torch.uint8).numpy(), qo)
+
+
+def test_fp8_mlp_chain_ragged(dev):
+    """Config-5 structure at reduced width: M=3001 (57-row tail), I=1024, H=512."""
+    print("fp8 mlp chain M=3001", flush=True)
+    M, H, I = 3001, 512, 1024
+    x = synthetic.activations(M, H, seed=31)
+    w13, s13 = synthetic.weights(2 * I, H, seed=32)
+    w2, s2 = synthetic.weights(H, I, seed=33)
+    y = fp8.fp8_mlp(x.to(dev), w13.to(dev), s13.to(dev), w2.to(dev), s2.to(dev))
+    y2 = fp8.fp8_mlp(x.to(dev), w13.to(dev), s13.to(dev), w2.to(dev), s2.to(dev),
+                     fuse_quant=False)
+    assert torch.equal(y, y2)
+    assert y.shape == (M, H) and y.dtype == torch.bfloat16
+    # The chain through the oracle, step by step from the GPU's own
+    # intermediates (h rounding can flip fp8 codes, so compare per stage).
+    xq, xs = fp8.act_quant(x.to(dev), 128)
+    qo, so = oracle.act_quant(_bits(x), 128)
+    np.testing.assert_array_equal(xq.cpu().view(torch.uint8).numpy(), qo)
+    h = fp8.w8a8_block_fp8_matmul(xq, w13.to(dev), xs, s13.to(dev), [128, 128], torch.bfloat16)
+    ho = oracle.block_gemm(qo, w13.view(torch.uint8).numpy(), so, s13.numpy())
+    torch.testing.assert_close(h.float().cpu(), torch.from_numpy(ho).to(torch.bfloat16).float(),
+                               rtol=1e-2, atol=1e-3)
+    hq, hs = fp8.silu_and_mul_quant(h, 128)
+    y3 = fp8.w8a8_block_fp8_matmul(hq, w2.to(dev), hs, s2.to(dev), [128, 128], torch.bfloat16)
+    assert torch.equal(y3, y)
+    yo = oracle.block_gemm(hq.cpu().view(torch.uint8).numpy(), w2.view(torch.uint8).numpy(),
+                           hs.cpu().numpy(), s2.numpy())
+    torch.testing.assert_close(y.float().cpu(), torch.from_numpy(yo).to(torch.bfloat16).float(),
+                               rtol=1e-2, atol=1e-3)

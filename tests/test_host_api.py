@@ -1,0 +1,65 @@
+"""CPU checks of the Python op surface: signature parity with the reference
+package, op registration, fake (meta) shapes, and loud failure instead of a
+CPU fallback."""
+import inspect
+
+import pytest
+import torch
+
+from hf_kernels_helion_amd import finegrained_fp8_helion as fp8
+from hf_kernels_helion_amd.finegrained_fp8_helion import _ops
+
+
+def test_public_signature_matches_reference():
+    # finegrained-fp8-helion/torch-ext/finegrained_fp8_helion/__init__.py:7-8
+    sig = inspect.signature(fp8.w8a8_block_fp8_matmul)
+    assert list(sig.parameters) == ["A", "B", "As", "Bs", "block_size", "output_dtype"]
+    assert sig.parameters["output_dtype"].default is torch.float32
+    assert "w8a8_block_fp8_matmul" in fp8.__all__
+
+
+def test_namespace_follows_kernel_builder_scheme():
+    assert _ops._OPS_NAME == "_finegrained_fp8_helion_rocm_mi355x"
+    assert _ops.add_op_namespace_prefix("x") == "_finegrained_fp8_helion_rocm_mi355x::x"
+    for name in ("w8a8_block_fp8_matmul", "w8a8_block_fp8_matmul_dtype", "act_quant",
+                 "silu_and_mul", "silu_and_mul_quant"):
+        assert hasattr(_ops.ops, name)
+
+
+def _fp8(*shape, device="cpu"):
+    return torch.zeros(*shape, dtype=torch.float8_e4m3fn, device=device)
+
+
+def test_cpu_tensors_raise_not_fallback():
+    A, B = _fp8(4, 256), _fp8(128, 256)
+    As, Bs = torch.ones(4, 2), torch.ones(1, 2)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        fp8.w8a8_block_fp8_matmul(A, B, As, Bs, [128, 128], torch.bfloat16)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        fp8.act_quant(torch.zeros(4, 256, dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        fp8.silu_and_mul(torch.empty(2, 8, dtype=torch.bfloat16),
+                         torch.zeros(2, 16, dtype=torch.bfloat16))
+
+
+def test_fake_impls_give_reference_shapes():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    with FakeTensorMode():
+        A, B = _fp8(7, 384), _fp8(200, 384)
+        As, Bs = torch.ones(7, 3), torch.ones(2, 3)
+        out = _ops.ops.w8a8_block_fp8_matmul(A, B, As, Bs, 128, 128)
+        assert out.shape == (7, 200) and out.dtype == torch.float32  # reference op.py:14-16
+        out = _ops.ops.w8a8_block_fp8_matmul_dtype(A, B, As, Bs, 128, 128, torch.bfloat16)
+        assert out.dtype == torch.bfloat16
+        q, s = _ops.ops.act_quant(torch.zeros(3, 5, 300, dtype=torch.bfloat16), 128)
+        assert q.shape == (3, 5, 300) and q.dtype == torch.float8_e4m3fn
+        assert s.shape == (3, 5, 3) and s.dtype == torch.float32
+        q, s = _ops.ops.silu_and_mul_quant(torch.zeros(4, 512, dtype=torch.bfloat16), 128)
+        assert q.shape == (4, 256) and s.shape == (4, 2)
+
+
+def test_argument_validation_messages():
+    # validation happens before any device work; use meta-device-free checks
+    from hf_kernels_helion_amd.finegrained_fp8_helion import op
+    with pytest.raises(RuntimeError, match="group size"):
+        op._check_group(100)
