@@ -43,7 +43,7 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--only", default=None,
-                   help="profile helper: run only one workload (gemm|act_quant|decode|mlp|medium|small)"
+                   help="profile helper: run only one workload (gemm|act_quant|decode|mlp|medium|small|copy)"
                         " for --steps steps and exit without JSON")
     return p.parse_args()
 
@@ -306,6 +306,12 @@ def run_only(what, steps, warmup, torch, fp8, synthetic, dev):
                 return fp8.w8a8_block_fp8_matmul(q2, W, s2, Bs, [128, 128], torch.bfloat16)
         else:
             fn = lambda: fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [128, 128], torch.bfloat16)
+    elif what == "copy":
+        # calibration for the rocprofv3 FETCH_SIZE/WRITE_SIZE counters: a
+        # plain 256 MiB device-to-device copy
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        fn = lambda: dst.copy_(src)
     elif what == "act_quant":
         x = _gpu_acts(4096, 8192, 10, dev, torch)
         fn = lambda: fp8.act_quant(x, 128)

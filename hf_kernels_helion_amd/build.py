@@ -15,6 +15,7 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_DIR = PKG_DIR / "_lib"
 LIB_NAME = "libfp8_blockwise.so"
+TORCH_LIB_NAME = "libfp8_torch_ops.so"
 SOURCES = ["capi.cpp", "act_quant.hip", "block_gemm.hip"]
 ARCH = "gfx950"
 
@@ -39,13 +40,7 @@ def compile_flags() -> list:
     ]
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every source into LIB_DIR/LIB_NAME; returns the library path."""
-    LIB_DIR.mkdir(exist_ok=True)
-    out = LIB_DIR / LIB_NAME
-    tmp = LIB_DIR / (LIB_NAME + ".tmp")
-    cmd = [hipcc(), *compile_flags(), "-shared", "-o", str(tmp)]
-    cmd += [str(CSRC / s) for s in SOURCES]
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -53,10 +48,45 @@ def build(verbose: bool = False) -> Path:
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
     if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
+        raise RuntimeError(f"{cmd[0]} failed ({res.returncode}):\n{err}")
     if verbose and err.strip():
         print(err, file=sys.stderr)
+
+
+def build_torch_ops(verbose: bool = False) -> Path:
+    """Compile the torch custom-op library (host C++ only) against torch's
+    headers; it links libfp8_blockwise.so from the same directory."""
+    import torch
+    from torch.utils import cpp_extension as ce
+    out = LIB_DIR / TORCH_LIB_NAME
+    tmp = LIB_DIR / (TORCH_LIB_NAME + ".tmp")
+    torch_lib = Path(torch.__file__).resolve().parent / "lib"
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           "-DTORCH_EXTENSION_NAME=fp8_torch_ops", "-Wno-deprecated-declarations"]
+    for inc in ce.include_paths(device_type="cuda"):
+        cmd += ["-isystem", inc]
+    cmd += [str(CSRC / "torch_ops.cpp"), "-o", str(tmp),
+            f"-L{LIB_DIR}", "-lfp8_blockwise", f"-L{torch_lib}", "-lc10", "-lc10_hip",
+            "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-Wl,-rpath,$ORIGIN",
+            f"-Wl,-rpath,{torch_lib}"]
+    _run(cmd, verbose)
     os.replace(tmp, out)
+    return out
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile the HIP kernels into LIB_DIR/LIB_NAME and the torch op library
+    beside it; returns the kernel library path."""
+    LIB_DIR.mkdir(exist_ok=True)
+    out = LIB_DIR / LIB_NAME
+    tmp = LIB_DIR / (LIB_NAME + ".tmp")
+    cmd = [hipcc(), *compile_flags(), "-shared", "-o", str(tmp)]
+    cmd += [str(CSRC / s) for s in SOURCES]
+    _run(cmd, verbose)
+    os.replace(tmp, out)
+    build_torch_ops(verbose)
     return out
 
 

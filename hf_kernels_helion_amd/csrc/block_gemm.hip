@@ -29,6 +29,7 @@
 #include "common.h"
 
 #include <algorithm>
+#include <atomic>
 
 namespace fp8b {
 
@@ -92,18 +93,45 @@ __device__ __forceinline__ void store4(const GemmArgs& a, int m, int n, const v4
   }
 }
 
+__device__ __forceinline__ void lds_dma4(const void* gsrc, uint8_t* ldst) {
+  __builtin_amdgcn_global_load_lds(gsrc, (lds_void*)ldst, 4, 0, 0);
+}
+
+__device__ __forceinline__ v8i lds_frag(const uint8_t* row, int c0, int r7) {
+  const v4i lo = *reinterpret_cast<const v4i*>(row + ((c0 ^ r7) << 4));
+  const v4i hi = *reinterpret_cast<const v4i*>(row + (((c0 + 1) ^ r7) << 4));
+  return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
 // BM x BN output tile per workgroup, WM x WN per wavefront.
+//
+// LDS stage layout (two stages):
+//   [0, (BM+BN)*128)        A rows then B rows, 128 bytes each, chunk-swizzled
+//   [SA_OFF, +max(BM,64)*4) As[m0+r, kb] for r < BM (gathered by lane DMA)
+//   [SB_OFF, +256)          Bs[n0/128 + j, kb] for the tile's 128-column blocks
+// Every operand and scale of a K-block arrives by global_load_lds, so the
+// only wait on vector memory in the main loop is the one per K-block that
+// also guards the double buffer.
 template <int BM, int BN, int WM, int WN>
 __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64)
 gemm_bs128_kernel(GemmArgs a) {
   constexpr int NWM = BM / WM, NWN = BN / WN, NW = NWM * NWN;
   constexpr int FM = WM / 16, FN = WN / 16;
-  constexpr int ROWS = BM + BN;         // tile rows per stage (A rows then B rows)
-  constexpr int STAGE = ROWS * 128;     // bytes per LDS stage
-  constexpr int LOADS = ROWS / 8;       // 1 KiB wave-loads per stage
+  constexpr int ROWS = BM + BN;
+  constexpr int SA_OFF = ROWS * 128;
+  constexpr int SA_LOADS = (BM + 63) / 64;
+  constexpr int SB_OFF = SA_OFF + SA_LOADS * 256;
+  constexpr int STAGE = SB_OFF + 256;
+  constexpr int LOADS = ROWS / 8;  // 1 KiB wave-loads of operand rows per stage
+  constexpr int NB_TILE = BN / 128;
+  constexpr int EPI_PITCH = WN * 2 + 16;  // bf16 epilogue row pitch (conflict-free)
+  constexpr int EPI = NW * WM * EPI_PITCH;
+  constexpr int SMEM = (2 * STAGE > EPI) ? 2 * STAGE : EPI;
   static_assert(LOADS % NW == 0, "stage loads must split evenly over waves");
-  static_assert(WN <= 128 && 128 % WN == 0, "a wave's columns must sit in one 128-block");
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+  static_assert(BN % 128 == 0 && WN <= 128 && 128 % WN == 0,
+                "a wave's columns must sit in one 128-column scale block");
+  static_assert(FN % 2 == 0, "weight fragments are consumed in two halves");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -129,8 +157,8 @@ gemm_bs128_kernel(GemmArgs a) {
   const int kb_begin = split * a.kb_per_split;
   const int kb_end = min(kb_begin + a.kb_per_split, a.KB);
 
-  // Per-lane global source of each wave-load: row r of the stage, logical
-  // chunk (lane&7) ^ (r&7) so that it lands in LDS slot lane&7.
+  // Per-lane global source of each operand wave-load: row r of the stage,
+  // logical chunk (lane&7) ^ (r&7) so that it lands in LDS slot lane&7.
   const uint8_t* src[LOADS / NW];
 #pragma unroll
   for (int i = 0; i < LOADS / NW; ++i) {
@@ -145,32 +173,13 @@ gemm_bs128_kernel(GemmArgs a) {
       src[i] = a.B + (int64_t)gnr * a.ldb + chunk * 16;
     }
   }
-
-  // Activation-scale rows of this lane (one per 16-row fragment) and the
-  // weight-scale block row of this wave.
-  const float* sa_ptr[FM];
-#pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    const int m = min(m0 + wm * WM + i * 16 + (lane & 15), a.M - 1);
-    sa_ptr[i] = a.As + (int64_t)m * a.as_sm;
-  }
-  const int nb = min((n0 + wn * WN) >> 7, (a.N - 1) >> 7);
-  const float* sb_ptr = a.Bs + (int64_t)nb * a.bs_sn;
-
-  // LDS byte offsets of this lane's fragment rows; the two 16-byte chunks of
-  // a fragment are logical chunks 2*(lane>>4) and 2*(lane>>4)+1.
-  const int c0 = 2 * (lane >> 4);
-  int a_off[FM], b_off[FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i) a_off[i] = (wm * WM + i * 16 + (lane & 15)) * 128;
-#pragma unroll
-  for (int j = 0; j < FN; ++j) b_off[j] = (BM + wn * WN + j * 16 + (lane & 15)) * 128;
-
-  v4f acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+  // Scale gathers: waves 0..SA_LOADS-1 fetch 64 activation-scale rows each,
+  // the last wave fetches the tile's weight-scale blocks (rows and blocks past
+  // the matrix edge are clamped; their values only reach masked outputs).
+  const float* sa_src =
+      a.As + (int64_t)min(m0 + min(wid * 64 + lane, BM - 1), a.M - 1) * a.as_sm;
+  const float* sb_src =
+      a.Bs + (int64_t)min((n0 >> 7) + min(lane, NB_TILE - 1), (a.N - 1) >> 7) * a.bs_sn;
 
   auto issue = [&](int kb, int stage) {
     uint8_t* base = smem + stage * STAGE;
@@ -179,76 +188,119 @@ gemm_bs128_kernel(GemmArgs a) {
       const int L = wid + i * NW;
       lds_dma16(src[i] + (int64_t)kb * 128, base + L * 1024);
     }
+    if (wid < SA_LOADS) lds_dma4(sa_src + (int64_t)kb * a.as_sk, base + SA_OFF + wid * 256);
+    if (wid == NW - 1) lds_dma4(sb_src + (int64_t)kb * a.bs_sk, base + SB_OFF);
   };
 
-  if (kb_begin < kb_end) issue(kb_begin, 0);
-  float sa_cur[FM], sb_cur = 0.f;
-  if (kb_begin < kb_end) {
+  // LDS byte offsets of this lane's fragment rows; the two 16-byte chunks of
+  // a fragment are logical chunks 2*(lane>>4) and 2*(lane>>4)+1.
+  const int c0 = 2 * (lane >> 4);
+  const int r7 = lane & 7;  // fragment rows start at multiples of 16
+  const int a_row = (wm * WM + (lane & 15)) * 128;
+  const int b_row = (BM + wn * WN + (lane & 15)) * 128;
+  const int sa_row = SA_OFF + (wm * WM + (lane & 15)) * 4;
+  const int sb_slot = SB_OFF + ((wn * WN) >> 7) * 4;
+
+  v4f acc[FM][FN];
 #pragma unroll
-    for (int i = 0; i < FM; ++i) sa_cur[i] = sa_ptr[i][(int64_t)kb_begin * a.as_sk];
-    sb_cur = sb_ptr[(int64_t)kb_begin * a.bs_sk];
-  }
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  if (kb_begin < kb_end) issue(kb_begin, 0);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
   for (int kb = kb_begin; kb < kb_end; ++kb) {
     const int stage = (kb - kb_begin) & 1;
-    const bool more = kb + 1 < kb_end;
-    if (more) issue(kb + 1, stage ^ 1);
-    float sa_nxt[FM], sb_nxt = 0.f;
-    if (more) {
-#pragma unroll
-      for (int i = 0; i < FM; ++i) sa_nxt[i] = sa_ptr[i][(int64_t)(kb + 1) * a.as_sk];
-      sb_nxt = sb_ptr[(int64_t)(kb + 1) * a.bs_sk];
-    }
+    if (kb + 1 < kb_end) issue(kb + 1, stage ^ 1);
 
     const uint8_t* sbase = smem + stage * STAGE;
-    v8i xf[FM], wf[FN];
+    const float sbv = *reinterpret_cast<const float*>(sbase + sb_slot);
+    float sc[FM];
+    v8i xf[FM];
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
-      const int r7 = (a_off[i] >> 7) & 7;
-      const v4i lo = *reinterpret_cast<const v4i*>(sbase + a_off[i] + ((c0 ^ r7) << 4));
-      const v4i hi = *reinterpret_cast<const v4i*>(sbase + a_off[i] + (((c0 + 1) ^ r7) << 4));
-      xf[i] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      sc[i] = *reinterpret_cast<const float*>(sbase + sa_row + i * 64) * sbv;
+      xf[i] = lds_frag(sbase + a_row + i * 16 * 128, c0, r7);
     }
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int r7 = (b_off[j] >> 7) & 7;
-      const v4i lo = *reinterpret_cast<const v4i*>(sbase + b_off[j] + ((c0 ^ r7) << 4));
-      const v4i hi = *reinterpret_cast<const v4i*>(sbase + b_off[j] + (((c0 + 1) ^ r7) << 4));
-      wf[j] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-    }
+    for (int h = 0; h < 2; ++h) {
+      v8i wf[FN / 2];
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      const float sc = sa_cur[i] * sb_cur;
+      for (int j = 0; j < FN / 2; ++j)
+        wf[j] = lds_frag(sbase + b_row + (h * FN / 2 + j) * 16 * 128, c0, r7);
+      // Software pipeline: the FMAs of one sub-tile run under the next MFMA.
+      v4f prev = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+          wf[0], xf[0], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const v4f t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-            wf[j], xf[i], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
+      for (int t = 1; t <= FM * (FN / 2); ++t) {
+        v4f cur = prev;
+        if (t < FM * (FN / 2)) {
+          const int i = t / (FN / 2), j = t % (FN / 2);
+          cur = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              wf[j], xf[i], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
+        }
+        const int pi = (t - 1) / (FN / 2), pj = h * (FN / 2) + (t - 1) % (FN / 2);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[i][j][r] = fmaf(t[r], sc, acc[i][j][r]);
+        for (int r = 0; r < 4; ++r) acc[pi][pj][r] = fmaf(prev[r], sc[pi], acc[pi][pj][r]);
+        prev = cur;
       }
-    }
-
-    if (more) {
-#pragma unroll
-      for (int i = 0; i < FM; ++i) sa_cur[i] = sa_nxt[i];
-      sb_cur = sb_nxt;
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
   }
 
-  // Epilogue: lane holds row m = ... + (lane & 15) and columns 4*(lane>>4)+0..3
-  // of each 16x16 sub-tile.
+  // Epilogue: lane holds row (lane & 15) and columns 4*(lane>>4)+0..3 of each
+  // 16x16 sub-tile.
   const bool to_ws = gridDim.z > 1;
+  if (to_ws || a.out_dtype == FP8B_F32) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int m = m0 + wm * WM + i * 16 + (lane & 15);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int n = n0 + wn * WN + j * 16 + 4 * (lane >> 4);
+        store4(a, m, n, acc[i][j], to_ws, split);
+      }
+    }
+    return;
+  }
+  // 16-bit outputs: stage the wave's WM x WN tile in LDS (the operand stages
+  // are dead after the loop's last barrier), then write whole 16-byte runs of
+  // each output row.
+  const bool bf = a.out_dtype == FP8B_BF16;
+  uint8_t* wbase = smem + wid * WM * EPI_PITCH;
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
-    const int m = m0 + wm * WM + i * 16 + (lane & 15);
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-      const int n = n0 + wn * WN + j * 16 + 4 * (lane >> 4);
-      store4(a, m, n, acc[i][j], to_ws, split);
+      const v4f v = acc[i][j];
+      v2i w;
+      w[0] = (int)(bf ? pack_bf16x2(v[0], v[1]) : pack_f16x2(v[0], v[1]));
+      w[1] = (int)(bf ? pack_bf16x2(v[2], v[3]) : pack_f16x2(v[2], v[3]));
+      *reinterpret_cast<v2i*>(wbase + (i * 16 + (lane & 15)) * EPI_PITCH +
+                              (j * 16 + 4 * (lane >> 4)) * 2) = w;
+    }
+  }
+  __syncthreads();
+  constexpr int CPR = WN / 8;   // 16-byte chunks per wave row
+  constexpr int RPP = 64 / CPR; // rows per pass
+  const int c = lane % CPR;
+  const int n = n0 + wn * WN + c * 8;
+  uint16_t* C = reinterpret_cast<uint16_t*>(a.C);
+#pragma unroll
+  for (int p = 0; p < WM / RPP; ++p) {
+    const int r = p * RPP + lane / CPR;
+    const int m = m0 + wm * WM + r;
+    const v4i v = *reinterpret_cast<const v4i*>(wbase + r * EPI_PITCH + c * 16);
+    if (m >= a.M || n >= a.N) continue;
+    uint16_t* dst = C + (int64_t)m * a.ldc + n;
+    if (n + 8 <= a.N && a.vec_store) {
+      *reinterpret_cast<v4i*>(dst) = v;
+    } else {
+      for (int e = 0; e < 8 && n + e < a.N; ++e)
+        dst[e] = (uint16_t)(((uint32_t)v[e >> 1]) >> ((e & 1) * 16));
     }
   }
 }
@@ -367,13 +419,20 @@ struct Plan {
   int kb_per_split;
 };
 
+// CU count of the current device, queried once per device.
 int device_cu_count() {
+  static std::atomic<int> cache[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (dev >= 0 && dev < 64) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
       cus <= 0)
     return 256;
+  if (dev >= 0 && dev < 64) cache[dev].store(cus, std::memory_order_relaxed);
   return cus;
 }
 
@@ -492,7 +551,10 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
   a.tiles_m = (int)((M + p.bm - 1) / p.bm);
   a.tiles_n = (int)((N + p.bn - 1) / p.bn);
   a.out_dtype = out_dtype;
-  const bool c_vec = (ldc % 4 == 0) && (((uintptr_t)C & (4 * esz - 1)) == 0);
+  // Vector stores: 4 fp32 (16 B) for fp32 C and split-K partials, 8 x 16-bit
+  // (16 B) for bf16/fp16 C.
+  const bool c_vec = esz == 4 ? (ldc % 4 == 0 && ((uintptr_t)C & 15) == 0)
+                              : (ldc % 8 == 0 && ((uintptr_t)C & 15) == 0);
   const bool ws_vec = (N % 4 == 0);
   a.vec_store = (p.splits > 1) ? (ws_vec ? 1 : 0) : (c_vec ? 1 : 0);
 

@@ -1,0 +1,226 @@
+// PyTorch-ROCm custom ops over the C ABI of libfp8_blockwise.so.
+//
+// Registers, in the namespace _finegrained_fp8_helion_rocm_mi355x (the
+// kernel-builder scheme of finegrained-fp8-helion/build/torch-cuda/_ops.py:21-30):
+//   w8a8_block_fp8_matmul(A, B, As, Bs, block_n, block_k) -> fp32 Tensor
+//       (schema of finegrained-fp8-helion/torch-ext/finegrained_fp8_helion/op.py:8-11)
+//   w8a8_block_fp8_matmul_dtype(..., ScalarType output_dtype) -> Tensor
+//   act_quant(x, block_size) -> (q, s)
+//   silu_and_mul(Tensor(a!) out, x) -> ()
+//       (schema of activation-helion/.../torch-ext/activation_helion/op.py:15-18)
+//   silu_and_mul_quant(x, block_size) -> (q, s)
+// Each op validates its tensors (TORCH_CHECK -> RuntimeError), allocates its
+// outputs and any split-K workspace from torch's caching allocator, and calls
+// one C-ABI entry point on torch's current HIP stream. CPU tensors raise: the
+// path has no CPU implementation.
+#include <ATen/ATen.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+#include <torch/library.h>
+
+#include "../../include/fp8_blockwise.h"
+
+namespace {
+
+using at::Tensor;
+
+void* current_stream(const Tensor& t) {
+  return (void*)at::hip::getCurrentHIPStreamMasqueradingAsCUDA(t.device().index()).stream();
+}
+
+void check_status(int st, const char* what) {
+  TORCH_CHECK(st == FP8B_OK, what, " failed (status ", st, "): ", fp8b_last_error());
+}
+
+void check_gpu(const Tensor& t, const char* name) {
+  TORCH_CHECK(t.is_cuda(), name, " must be a tensor on a ROCm GPU (got ", t.device(),
+              "); this package has no CPU implementation");
+}
+
+int out_code(at::ScalarType t) {
+  switch (t) {
+    case at::kFloat: return FP8B_F32;
+    case at::kBFloat16: return FP8B_BF16;
+    case at::kHalf: return FP8B_F16;
+    default: TORCH_CHECK(false, "unsupported output_dtype ", t, " (float32, bfloat16, float16)");
+  }
+  return -1;
+}
+
+Tensor matmul_impl(const Tensor& A, const Tensor& B, const Tensor& As, const Tensor& Bs,
+                   int64_t block_n, int64_t block_k, at::ScalarType out_dtype) {
+  check_gpu(A, "A");
+  check_gpu(B, "B");
+  check_gpu(As, "As");
+  check_gpu(Bs, "Bs");
+  TORCH_CHECK(A.dim() == 2 && B.dim() == 2, "A and B must be 2-D ([M,K] and [N,K])");
+  TORCH_CHECK(A.scalar_type() == at::kFloat8_e4m3fn, "A must be float8_e4m3fn, got ",
+              A.scalar_type());
+  TORCH_CHECK(B.scalar_type() == at::kFloat8_e4m3fn, "B must be float8_e4m3fn, got ",
+              B.scalar_type());
+  TORCH_CHECK(As.scalar_type() == at::kFloat, "As must be float32, got ", As.scalar_type());
+  TORCH_CHECK(Bs.scalar_type() == at::kFloat, "Bs must be float32, got ", Bs.scalar_type());
+  const int64_t M = A.size(0), K = A.size(1), N = B.size(0);
+  TORCH_CHECK(B.size(1) == K, "A is [M,K]=[", M, ",", K, "] but B is [N,K]=[", N, ",",
+              B.size(1), "]");
+  TORCH_CHECK(block_n > 0 && block_k > 0, "block_size entries must be positive");
+  const int64_t kb = (K + block_k - 1) / block_k, nb = (N + block_n - 1) / block_n;
+  TORCH_CHECK(As.dim() == 2 && As.size(0) >= M && As.size(1) >= kb,
+              "As must be [M, ceil(K/block_k)] = [", M, ",", kb, "], got ", As.sizes());
+  TORCH_CHECK(Bs.dim() == 2 && Bs.size(0) >= nb && Bs.size(1) >= kb,
+              "Bs must be [ceil(N/block_n), ceil(K/block_k)] = [", nb, ",", kb, "], got ",
+              Bs.sizes());
+  TORCH_CHECK(K <= 1 || (A.stride(1) == 1 && B.stride(1) == 1),
+              "A and B must have unit stride along K");
+  TORCH_CHECK(B.device() == A.device() && As.device() == A.device() && Bs.device() == A.device(),
+              "all tensors must be on one device");
+  const int code = out_code(out_dtype);
+  at::hip::HIPGuardMasqueradingAsCUDA guard(A.device());
+  Tensor out = at::empty({M, N}, A.options().dtype(out_dtype));
+  if (M == 0 || N == 0) return out;
+  const size_t ws_bytes = fp8b_gemm_workspace_size(M, N, K, block_n, block_k);
+  Tensor ws;
+  if (ws_bytes) ws = at::empty({(int64_t)ws_bytes}, A.options().dtype(at::kByte));
+  const int64_t lda = std::max<int64_t>(M > 1 ? A.stride(0) : K, K);
+  const int64_t ldb = std::max<int64_t>(N > 1 ? B.stride(0) : K, K);
+  const int st = fp8b_w8a8_block_matmul(
+      A.data_ptr(), lda, B.data_ptr(), ldb, As.data_ptr<float>(), As.stride(0), As.stride(1),
+      Bs.data_ptr<float>(), Bs.stride(0), Bs.stride(1), out.data_ptr(), N, code, M, N, K,
+      block_n, block_k, ws_bytes ? ws.data_ptr() : nullptr, ws_bytes, current_stream(A));
+  check_status(st, "w8a8_block_fp8_matmul");
+  return out;
+}
+
+Tensor w8a8_block_fp8_matmul(const Tensor& A, const Tensor& B, const Tensor& As,
+                             const Tensor& Bs, int64_t block_n, int64_t block_k) {
+  return matmul_impl(A, B, As, Bs, block_n, block_k, at::kFloat);
+}
+
+Tensor w8a8_block_fp8_matmul_dtype(const Tensor& A, const Tensor& B, const Tensor& As,
+                                   const Tensor& Bs, int64_t block_n, int64_t block_k,
+                                   at::ScalarType output_dtype) {
+  return matmul_impl(A, B, As, Bs, block_n, block_k, output_dtype);
+}
+
+void check_group(int64_t g) {
+  TORCH_CHECK(g == 32 || g == 64 || g == 128 || g == 256,
+              "group size must be 32, 64, 128 or 256, got ", g);
+}
+
+std::tuple<Tensor, Tensor> act_quant(const Tensor& x, int64_t block_size) {
+  check_gpu(x, "x");
+  TORCH_CHECK(x.scalar_type() == at::kBFloat16, "x must be bfloat16, got ", x.scalar_type());
+  TORCH_CHECK(x.dim() >= 1, "x must have at least one dimension");
+  check_group(block_size);
+  const int64_t K = x.size(-1);
+  const int64_t groups = (K + block_size - 1) / block_size;
+  auto lead = x.sizes().vec();
+  lead.pop_back();
+  Tensor x2 = x.reshape({-1, K});
+  if (x2.numel() > 0 && K > 1 && x2.stride(1) != 1) x2 = x2.contiguous();
+  const int64_t M = x2.size(0);
+  at::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+  Tensor q = at::empty({M, K}, x.options().dtype(at::kFloat8_e4m3fn));
+  Tensor s = at::empty({M, groups}, x.options().dtype(at::kFloat));
+  if (M > 0 && K > 0) {
+    const int64_t ldx = std::max<int64_t>(M > 1 ? x2.stride(0) : K, K);
+    const int st = fp8b_act_quant(x2.data_ptr(), ldx, q.data_ptr(), K, s.data_ptr<float>(),
+                                  groups, 1, M, K, block_size, current_stream(x));
+    check_status(st, "act_quant");
+  }
+  auto qshape = lead;
+  qshape.push_back(K);
+  auto sshape = lead;
+  sshape.push_back(groups);
+  return {q.view(qshape), s.view(sshape)};
+}
+
+void silu_and_mul(Tensor& out, const Tensor& x) {
+  check_gpu(x, "x");
+  check_gpu(out, "out");
+  TORCH_CHECK(x.scalar_type() == at::kBFloat16 && out.scalar_type() == at::kBFloat16,
+              "silu_and_mul supports bfloat16 x and out");
+  const int64_t d = out.size(-1);
+  TORCH_CHECK(x.size(-1) == 2 * d, "x last dim must be 2*d = ", 2 * d, ", got ", x.size(-1));
+  TORCH_CHECK(out.is_contiguous() && x.is_contiguous(), "x and out must be contiguous");
+  const int64_t M = d > 0 ? out.numel() / d : 0;
+  TORCH_CHECK(d == 0 || x.numel() / (2 * d) == M, "x and out must have the same leading shape");
+  if (M == 0 || d == 0) return;
+  at::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+  const int st = fp8b_silu_and_mul(x.data_ptr(), 2 * d, out.data_ptr(), d, M, d,
+                                   current_stream(x));
+  check_status(st, "silu_and_mul");
+}
+
+std::tuple<Tensor, Tensor> silu_and_mul_quant(const Tensor& x, int64_t block_size) {
+  check_gpu(x, "x");
+  TORCH_CHECK(x.scalar_type() == at::kBFloat16, "x must be bfloat16, got ", x.scalar_type());
+  check_group(block_size);
+  TORCH_CHECK(x.dim() >= 1 && x.size(-1) % 2 == 0, "x last dim must be even");
+  const int64_t d = x.size(-1) / 2;
+  const int64_t groups = (d + block_size - 1) / block_size;
+  auto lead = x.sizes().vec();
+  lead.pop_back();
+  Tensor x2 = x.reshape({-1, 2 * d}).contiguous();
+  const int64_t M = x2.size(0);
+  at::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+  Tensor q = at::empty({M, d}, x.options().dtype(at::kFloat8_e4m3fn));
+  Tensor s = at::empty({M, groups}, x.options().dtype(at::kFloat));
+  if (M > 0 && d > 0) {
+    const int st = fp8b_silu_and_mul_quant(x2.data_ptr(), 2 * d, q.data_ptr(), d,
+                                           s.data_ptr<float>(), groups, 1, M, d, block_size,
+                                           current_stream(x));
+    check_status(st, "silu_and_mul_quant");
+  }
+  auto qshape = lead;
+  qshape.push_back(d);
+  auto sshape = lead;
+  sshape.push_back(groups);
+  return {q.view(qshape), s.view(sshape)};
+}
+
+// CPU tensors reach these: raise instead of computing anything.
+[[noreturn]] void no_cpu(const char* op) {
+  TORCH_CHECK(false, op, ": tensors must be on a ROCm GPU; this package has no CPU "
+              "implementation");
+}
+Tensor matmul_cpu(const Tensor&, const Tensor&, const Tensor&, const Tensor&, int64_t, int64_t) {
+  no_cpu("w8a8_block_fp8_matmul");
+}
+Tensor matmul_dtype_cpu(const Tensor&, const Tensor&, const Tensor&, const Tensor&, int64_t,
+                        int64_t, at::ScalarType) {
+  no_cpu("w8a8_block_fp8_matmul_dtype");
+}
+std::tuple<Tensor, Tensor> act_quant_cpu(const Tensor&, int64_t) { no_cpu("act_quant"); }
+void silu_and_mul_cpu(Tensor&, const Tensor&) { no_cpu("silu_and_mul"); }
+std::tuple<Tensor, Tensor> silu_and_mul_quant_cpu(const Tensor&, int64_t) {
+  no_cpu("silu_and_mul_quant");
+}
+
+}  // namespace
+
+TORCH_LIBRARY(_finegrained_fp8_helion_rocm_mi355x, m) {
+  m.def("w8a8_block_fp8_matmul(Tensor A, Tensor B, Tensor As, Tensor Bs, int block_n, "
+        "int block_k) -> Tensor");
+  m.def("w8a8_block_fp8_matmul_dtype(Tensor A, Tensor B, Tensor As, Tensor Bs, int block_n, "
+        "int block_k, ScalarType output_dtype) -> Tensor");
+  m.def("act_quant(Tensor x, int block_size) -> (Tensor, Tensor)");
+  m.def("silu_and_mul(Tensor(a!) out, Tensor x) -> ()");
+  m.def("silu_and_mul_quant(Tensor x, int block_size) -> (Tensor, Tensor)");
+}
+
+TORCH_LIBRARY_IMPL(_finegrained_fp8_helion_rocm_mi355x, CUDA, m) {
+  m.impl("w8a8_block_fp8_matmul", &w8a8_block_fp8_matmul);
+  m.impl("w8a8_block_fp8_matmul_dtype", &w8a8_block_fp8_matmul_dtype);
+  m.impl("act_quant", &act_quant);
+  m.impl("silu_and_mul", &silu_and_mul);
+  m.impl("silu_and_mul_quant", &silu_and_mul_quant);
+}
+
+TORCH_LIBRARY_IMPL(_finegrained_fp8_helion_rocm_mi355x, CPU, m) {
+  m.impl("w8a8_block_fp8_matmul", &matmul_cpu);
+  m.impl("w8a8_block_fp8_matmul_dtype", &matmul_dtype_cpu);
+  m.impl("act_quant", &act_quant_cpu);
+  m.impl("silu_and_mul", &silu_and_mul_cpu);
+  m.impl("silu_and_mul_quant", &silu_and_mul_quant_cpu);
+}

@@ -58,8 +58,11 @@ def test_fake_impls_give_reference_shapes():
         assert q.shape == (4, 256) and s.shape == (4, 2)
 
 
-def test_argument_validation_messages():
-    # validation happens before any device work; use meta-device-free checks
-    from hf_kernels_helion_amd.finegrained_fp8_helion import op
-    with pytest.raises(RuntimeError, match="group size"):
-        op._check_group(100)
+def test_op_schemas_match_reference():
+    # finegrained-fp8-helion/torch-ext/finegrained_fp8_helion/op.py:8-11 and
+    # activation-helion/.../op.py:15-16
+    ops = _ops.ops
+    sch = str(ops.w8a8_block_fp8_matmul.default._schema)
+    assert "(Tensor A, Tensor B, Tensor As, Tensor Bs, int block_n, int block_k) -> Tensor" in sch
+    sch = str(ops.silu_and_mul.default._schema)
+    assert "Tensor(a!) out, Tensor x) -> ()" in sch
