@@ -67,30 +67,44 @@ __device__ __forceinline__ uint32_t unpack_bf16x8(const v4i raw, float v[8]) {
 }
 
 // Fast path: group = 128, K % 128 == 0, 16-byte aligned rows of x, 8-byte
-// aligned rows of q. 16 lanes per group, 16 groups per 256-thread block.
+// aligned rows of q. 16 lanes per group; each 16-lane row handles UNROLL
+// groups spaced one block-stride apart and issues all their loads before
+// converting any of them, so a wave keeps UNROLL KiB of reads in flight.
+constexpr int kQuantUnroll = 4;
+
 __global__ void __launch_bounds__(256)
 act_quant_g128_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                       uint8_t* __restrict__ q, int64_t ldq,
                       float* __restrict__ s, int64_t ssm, int64_t ssg,
                       uint32_t groups, uint32_t groups_per_row) {
-  const uint32_t gi = (blockIdx.x * 256u + threadIdx.x) >> 4;
   const uint32_t sub = threadIdx.x & 15u;
-  if (gi >= groups) return;  // uniform across the 16-lane group
-  const uint32_t m = gi / groups_per_row;
-  const uint32_t g = gi - m * groups_per_row;
-  const v4i raw = __builtin_nontemporal_load(
-      reinterpret_cast<const v4i*>(x + (int64_t)m * ldx + g * 128u + sub * 8u));
-  float v[8];
-  const uint32_t mag = unpack_bf16x8(raw, v);
-  uint32_t w0, w1;
-  float scale;
-  quant_row16_8(v, mag, w0, w1, scale);
-  v2i packed;
-  packed[0] = (int)w0;
-  packed[1] = (int)w1;
-  __builtin_nontemporal_store(
-      packed, reinterpret_cast<v2i*>(q + (int64_t)m * ldq + g * 128u + sub * 8u));
-  if (sub == 0) s[(int64_t)m * ssm + (int64_t)g * ssg] = scale;
+  const uint32_t g_first = (blockIdx.x * kQuantUnroll * 256u + threadIdx.x) >> 4;
+  v4i raw[kQuantUnroll];
+  uint32_t mm[kQuantUnroll], gg[kQuantUnroll];
+#pragma unroll
+  for (int u = 0; u < kQuantUnroll; ++u) {
+    const uint32_t gi = g_first + u * 16u;  // 16 groups per 256 threads
+    const uint32_t gc = gi < groups ? gi : groups - 1;  // uniform per 16-lane row
+    mm[u] = gc / groups_per_row;
+    gg[u] = gc - mm[u] * groups_per_row;
+    raw[u] = __builtin_nontemporal_load(
+        reinterpret_cast<const v4i*>(x + (int64_t)mm[u] * ldx + gg[u] * 128u + sub * 8u));
+  }
+#pragma unroll
+  for (int u = 0; u < kQuantUnroll; ++u) {
+    if (g_first + u * 16u >= groups) break;  // uniform across the 16-lane group
+    float v[8];
+    const uint32_t mag = unpack_bf16x8(raw[u], v);
+    uint32_t w0, w1;
+    float scale;
+    quant_row16_8(v, mag, w0, w1, scale);
+    v2i packed;
+    packed[0] = (int)w0;
+    packed[1] = (int)w1;
+    __builtin_nontemporal_store(
+        packed, reinterpret_cast<v2i*>(q + (int64_t)mm[u] * ldq + gg[u] * 128u + sub * 8u));
+    if (sub == 0) s[(int64_t)mm[u] * ssm + (int64_t)gg[u] * ssg] = scale;
+  }
 }
 
 // Scalar reference-shaped path for any group size, ragged K or unaligned
@@ -272,7 +286,8 @@ extern "C" int fp8b_act_quant(const void* x, int64_t ldx, void* q, int64_t ldq,
                     aligned(x, 16) && aligned(q, 8) && M * gpr < (int64_t(1) << 31);
   if (fast) {
     const uint32_t groups = (uint32_t)(M * gpr);
-    const uint32_t blocks = (groups + 15u) / 16u;
+    const uint32_t per_block = 16u * kQuantUnroll;
+    const uint32_t blocks = (groups + per_block - 1) / per_block;
     act_quant_g128_kernel<<<blocks, 256, 0, st>>>((const uint16_t*)x, ldx, (uint8_t*)q, ldq, s,
                                                   s_stride_m, s_stride_g, groups, (uint32_t)gpr);
   } else {

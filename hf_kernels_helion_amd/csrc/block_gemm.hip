@@ -30,6 +30,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <cstdlib>
 
 namespace fp8b {
 
@@ -305,6 +306,125 @@ gemm_bs128_kernel(GemmArgs a) {
   }
 }
 
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Skinny GEMM (M <= 16*FM <= 48, the decode shapes): bandwidth-bound on the
+// weight stream. A 512-thread workgroup owns 16 weight rows (output columns
+// n0..n0+15) over the whole K; its 8 waves split the K-blocks into
+// contiguous ranges. Each wave streams its K-blocks through a private ring
+// of SK LDS slots filled by global_load_lds only (weight rows, activation
+// rows and their scales), so the only waits in the loop are explicit vmcnt
+// waits on this ring. Rows are staged eight lanes per 128-byte row (whole
+// cache lines per request) with the chunk swizzle of the tiled kernel. Each
+// K-block is one 16x16x128 MFMA per 16 activation rows (weights as the A
+// operand: the weight scale is wave-uniform and the activation scale is one
+// register per lane). The 8 partial tiles are summed in wave order through
+// LDS: deterministic, no workspace, no second kernel.
+template <int FM>
+__global__ void __launch_bounds__(512) gemm_skinny_kernel(GemmArgs a) {
+  constexpr int NWAVE = 8;
+  constexpr int SK = FM <= 2 ? 3 : 2;          // K-blocks in flight per wave
+  constexpr int ROWS = 16 + 16 * FM;           // weight rows, then activation rows
+  constexpr int LOADS = ROWS / 8;              // 1 KiB DMA instructions per K-block
+  constexpr int SCALE_OFF = ROWS * 128;        // 64 fp32: sa rows 0..16FM-1, sb at 63
+  constexpr int SLOT = SCALE_OFF + 256;
+  constexpr int PER_KB = LOADS + 1;            // DMA instructions per K-block
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[NWAVE][SK][SLOT];
+  const int lane = threadIdx.x & 63;
+  // Wave index as a scalar, so K ranges and loop conditions are uniform.
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n0 = blockIdx.x * 16;
+  const int kb0 = (int)((int64_t)a.KB * wid / NWAVE);
+  const int kb1 = (int)((int64_t)a.KB * (wid + 1) / NWAVE);
+  const int row = lane & 15;
+
+  // DMA sources: load L brings staged rows 8L..8L+7 (0..15 weights, then
+  // activations), lane i the logical chunk (i&7) ^ (r&7) of row 8L + (i>>3).
+  const uint8_t* src[LOADS];
+#pragma unroll
+  for (int L = 0; L < LOADS; ++L) {
+    const int r = L * 8 + (lane >> 3);
+    const int chunk = (lane & 7) ^ (r & 7);
+    src[L] = r < 16 ? a.B + (int64_t)min(n0 + r, a.N - 1) * a.ldb + chunk * 16
+                    : a.A + (int64_t)min(r - 16, a.M - 1) * a.lda + chunk * 16;
+  }
+  // Scale DMA (4 bytes per lane): lanes 0..16FM-1 the activation rows' scale,
+  // the remaining lanes the weight block's scale.
+  const float* ssrc = lane < 16 * FM ? a.As + (int64_t)min(lane, a.M - 1) * a.as_sm
+                                     : a.Bs + (int64_t)(min(n0, a.N - 1) >> 7) * a.bs_sn;
+  const int64_t sstep = lane < 16 * FM ? a.as_sk : a.bs_sk;
+  const int c0 = 2 * (lane >> 4);
+  const int r7 = row & 7;
+
+  auto issue = [&](int kb, int slot) {
+    uint8_t* dst = &ring[wid][slot][0];
+#pragma unroll
+    for (int L = 0; L < LOADS; ++L) lds_dma16(src[L] + (int64_t)kb * 128, dst + L * 1024);
+    lds_dma4(ssrc + (int64_t)kb * sstep, dst + SCALE_OFF);
+  };
+
+  v4f acc[FM];
+#pragma unroll
+  for (int f = 0; f < FM; ++f) acc[f] = v4f{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int u = 0; u < SK; ++u)
+    if (kb0 + u < kb1) issue(kb0 + u, u);
+  for (int kb = kb0; kb < kb1; kb += SK) {
+#pragma unroll
+    for (int u = 0; u < SK; ++u) {
+      if (kb + u < kb1) {
+        // In steady state the DMAs of the next SK-1 K-blocks were issued
+        // after this slot's, so allowing that many outstanding retires it;
+        // near the end of the range fewer exist: wait for all.
+        if (kb + u + SK - 1 < kb1) wait_vmcnt<PER_KB * (SK - 1)>();
+        else wait_vmcnt<0>();
+        const uint8_t* sl = &ring[wid][u][0];
+        const v8i w = lds_frag(sl + row * 128, c0, r7);
+        const float sb = *reinterpret_cast<const float*>(sl + SCALE_OFF + 63 * 4);
+#pragma unroll
+        for (int f = 0; f < FM; ++f) {
+          const v8i x = lds_frag(sl + (16 + f * 16 + row) * 128, c0, r7);
+          const float sc = *reinterpret_cast<const float*>(sl + SCALE_OFF + (f * 16 + row) * 4) * sb;
+          const v4f t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              w, x, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[f][r] = fmaf(t[r], sc, acc[f][r]);
+        }
+        // The MFMAs above consumed the slot (its LDS reads are complete): refill it.
+        if (kb + u + SK < kb1) issue(kb + u + SK, u);
+      }
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  // Partial tiles reuse the ring: [wave][f][r][lane] floats.
+  float* part = reinterpret_cast<float*>(&ring[0][0][0]);
+#pragma unroll
+  for (int f = 0; f < FM; ++f)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) part[((wid * FM + f) * 4 + r) * 64 + lane] = acc[f][r];
+  __syncthreads();
+  if (wid != 0) return;
+  // Wave 0 sums the 8 partial tiles in wave order and stores: lane holds
+  // row m = 16f + (lane & 15) and columns n0 + 4*(lane>>4) + 0..3.
+#pragma unroll
+  for (int f = 0; f < FM; ++f) {
+    v4f sum = {0.f, 0.f, 0.f, 0.f};
+    for (int w = 0; w < NWAVE; ++w)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sum[r] += part[((w * FM + f) * 4 + r) * 64 + lane];
+    store4(a, f * 16 + row, n0 + 4 * (lane >> 4), sum, false, 0);
+  }
+}
+
 // Sum split-K partials in split order and convert: 4 outputs per thread.
 __global__ void __launch_bounds__(256)
 splitk_reduce_kernel(GemmArgs a, int splits) {
@@ -410,7 +530,14 @@ using namespace fp8b;
 namespace {
 
 // Tile configurations of the MFMA path.
-enum TileCfg { CFG_256x256 = 0, CFG_128x128 = 1, CFG_64x128 = 2, CFG_32x128 = 3, CFG_COUNT };
+enum TileCfg {
+  CFG_256x256 = 0,
+  CFG_128x128 = 1,
+  CFG_64x128 = 2,
+  CFG_32x128 = 3,
+  CFG_SKINNY = 4,
+  CFG_COUNT
+};
 
 struct Plan {
   int cfg;
@@ -436,11 +563,31 @@ int device_cu_count() {
   return cus;
 }
 
+// Largest M served by the skinny kernel (at most 48: three 16-row activation
+// fragments per K-block slot). FP8B_SKINNY_MAX_M overrides it for A/B
+// measurements (0 sends every shape to the tiled path).
+int skinny_max_m() {
+  static const int v = [] {
+    const char* e = getenv("FP8B_SKINNY_MAX_M");
+    if (!e) return 48;
+    const int x = atoi(e);
+    return x < 0 ? 0 : (x > 48 ? 48 : x);
+  }();
+  return v;
+}
+
 Plan make_plan(int64_t M, int64_t N, int64_t K) {
   const int KB = (int)(K / 128);
   const int cus = device_cu_count();
   Plan p;
   auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+  if (M <= skinny_max_m()) {
+    // Skinny path: 16 output columns per workgroup, K split inside it.
+    p.cfg = CFG_SKINNY; p.bm = (int)(((M + 15) / 16) * 16); p.bn = 16;
+    p.splits = 1;
+    p.kb_per_split = KB;
+    return p;
+  }
   if (M <= 32) {
     p.cfg = CFG_32x128; p.bm = 32; p.bn = 128;
   } else if (M <= 64) {
@@ -559,6 +706,14 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
   a.vec_store = (p.splits > 1) ? (ws_vec ? 1 : 0) : (c_vec ? 1 : 0);
 
   switch (p.cfg) {
+    case CFG_SKINNY: {
+      const dim3 grid((unsigned)((N + 15) / 16));
+      const int fm = (int)((M + 15) / 16);
+      if (fm <= 1) gemm_skinny_kernel<1><<<grid, 512, 0, st>>>(a);
+      else if (fm == 2) gemm_skinny_kernel<2><<<grid, 512, 0, st>>>(a);
+      else gemm_skinny_kernel<3><<<grid, 512, 0, st>>>(a);
+      break;
+    }
     case CFG_256x256: launch_cfg<256, 256, 64, 128>(a, p.splits, st); break;
     case CFG_128x128: launch_cfg<128, 128, 64, 64>(a, p.splits, st); break;
     case CFG_64x128: launch_cfg<64, 128, 32, 64>(a, p.splits, st); break;

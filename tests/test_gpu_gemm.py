@@ -46,7 +46,8 @@ def _check(out_gpu, A, B, As, Bs, block=(128, 128), rows=None):
 
 @pytest.mark.parametrize("M,N,K", [(512, 512, 2048), (128, 256, 1024), (57, 200, 384),
                                    (1, 128, 128), (300, 640, 512), (32, 4096, 1024),
-                                   (64, 512, 2048), (257, 384, 256)])
+                                   (64, 512, 2048), (257, 384, 256), (3, 1000, 640),
+                                   (48, 130, 256), (65, 384, 512)])
 @pytest.mark.parametrize("kind", ["model", "harness"])
 def test_gemm_bf16_vs_oracle(M, N, K, kind, dev):
     print(f"gemm bf16 {kind} M={M} N={N} K={K}", flush=True)
@@ -58,9 +59,10 @@ def test_gemm_bf16_vs_oracle(M, N, K, kind, dev):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.float64])
-def test_gemm_output_dtypes(dtype, dev):
-    print(f"gemm out dtype {dtype}", flush=True)
-    M, N, K = 96, 384, 1024
+@pytest.mark.parametrize("M", [96, 17])
+def test_gemm_output_dtypes(dtype, M, dev):
+    print(f"gemm out dtype {dtype} M={M}", flush=True)
+    N, K = 384, 1024
     A, B, As, Bs = _operands(M, N, K, seed=5)
     out = fp8.w8a8_block_fp8_matmul(A.to(dev), B.to(dev), As.to(dev), Bs.to(dev), [128, 128],
                                     dtype)
