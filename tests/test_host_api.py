@@ -66,3 +66,27 @@ def test_op_schemas_match_reference():
     assert "(Tensor A, Tensor B, Tensor As, Tensor Bs, int block_n, int block_k) -> Tensor" in sch
     sch = str(ops.silu_and_mul.default._schema)
     assert "Tensor(a!) out, Tensor x) -> ()" in sch
+
+
+def test_synthetic_weight_quantiser_matches_oracle():
+    """The torch weight-block quantiser used for test/bench inputs is the
+    oracle's, bit for bit."""
+    import numpy as np
+    import oracle
+    from hf_kernels_helion_amd.finegrained_fp8_helion import synthetic
+    g = torch.Generator().manual_seed(3)
+    W = torch.randn(300, 260, generator=g) * 0.02
+    Wq, Bs = synthetic.quantize_weight_blockwise(W, 128, 128)
+    oq, obs = oracle.quant_weight_block(W.numpy(), (128, 128))
+    np.testing.assert_array_equal(Wq.view(torch.uint8).numpy(), oq)
+    np.testing.assert_array_equal(Bs.numpy(), obs)
+
+
+def test_bench_rejects_multi_gpu():
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = Path(__file__).resolve().parent.parent
+    r = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2 and "one GPU only" in r.stderr
