@@ -314,6 +314,279 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// Ping-pong GEMM for 256x256 tiles: 8 waves in two groups of four (one wave
+// of each group per SIMD). Every K-block is worked in four quarters; in a
+// quarter a wave first runs an "M" phase (apply the scale FMAs to the previous
+// quarter's MFMA results and read the next quarter's fragments from LDS) and
+// then a "C" phase (8 zero-accumulator MFMAs). Group 1 runs one phase behind
+// group 0 and every phase ends at a workgroup barrier, so on each SIMD one
+// wave issues MFMAs while the other does its FMAs and LDS reads: the FMAs
+// never wait on an MFMA of their own wave and the LDS latency hides under the
+// other wave's MFMAs. Operand tiles and scales arrive by global_load_lds into
+// two LDS stages exactly as in gemm_bs128_kernel; the DMA of K-block kb+2 is
+// issued right after the barrier that ends the last read of stage kb.
+__global__ void __launch_bounds__(512) gemm_pp256_kernel(GemmArgs a) {
+  constexpr int BM = 256, BN = 256, WM = 64, WN = 128;
+  constexpr int NWN = BN / WN, NW = 8;
+  constexpr int FM = WM / 16, FN = WN / 16;   // 4 activation, 8 weight fragments
+  constexpr int ROWS = BM + BN;
+  constexpr int SA_OFF = ROWS * 128;
+  constexpr int SB_OFF = SA_OFF + 4 * 256;
+  constexpr int STAGE = SB_OFF + 256;
+  constexpr int LOADS = ROWS / 8;
+  constexpr int EPI_PITCH = WN * 2 + 16;
+  constexpr int EPI = NW * WM * EPI_PITCH;
+  constexpr int SMEM = (2 * STAGE > EPI) ? 2 * STAGE : EPI;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int group = wid >> 2;  // waves 0-3 and 4-7: one of each per SIMD
+  const int wm = wid / NWN, wn = wid % NWN;
+
+  const int tiles = a.tiles_m * a.tiles_n;
+  int bid = blockIdx.x;
+  if (tiles % 8 == 0) bid = (bid & 7) * (tiles >> 3) + (bid >> 3);
+  constexpr int GROUP_M = 8;
+  const int group_size = GROUP_M * a.tiles_n;
+  const int first_m = (bid / group_size) * GROUP_M;
+  const int gm = min(a.tiles_m - first_m, GROUP_M);
+  const int tm = first_m + (bid % group_size) % gm;
+  const int tn = (bid % group_size) / gm;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int kb_begin = blockIdx.z * a.kb_per_split;
+  const int kb_end = min(kb_begin + a.kb_per_split, a.KB);
+  const int nkb = kb_end - kb_begin;
+
+  // DMA sources as wave-uniform tile bases plus 32-bit lane offsets.
+  const uint8_t* a_tile = a.A + (int64_t)m0 * a.lda;
+  const uint8_t* b_tile = a.B + (int64_t)n0 * a.ldb;
+  int src_off[LOADS / NW];
+#pragma unroll
+  for (int i = 0; i < LOADS / NW; ++i) {
+    const int L = wid + i * NW;
+    const int r = L * 8 + (lane >> 3);
+    const int chunk = (lane & 7) ^ (r & 7);
+    src_off[i] = L * 8 < BM ? min(r, a.M - 1 - m0) * (int)a.lda + chunk * 16
+                            : min(r - BM, a.N - 1 - n0) * (int)a.ldb + chunk * 16;
+  }
+  const int sa_off = min(m0 + min(wid * 64 + lane, BM - 1), a.M - 1) * (int)a.as_sm;
+  const int sb_off = min((n0 >> 7) + min(lane, 1), (a.N - 1) >> 7) * (int)a.bs_sn;
+  auto issue = [&](int kb, int stage) {
+    uint8_t* base = smem + stage * STAGE;
+    const uint8_t* ak = a_tile + (int64_t)kb * 128;
+    const uint8_t* bk = b_tile + (int64_t)kb * 128;
+#pragma unroll
+    for (int i = 0; i < LOADS / NW; ++i) {
+      const int L = wid + i * NW;
+      lds_dma16((L * 8 < BM ? ak : bk) + src_off[i], base + L * 1024);
+    }
+    if (wid < 4) lds_dma4(a.As + (int64_t)kb * a.as_sk + sa_off, base + SA_OFF + wid * 256);
+    if (wid == NW - 1) lds_dma4(a.Bs + (int64_t)kb * a.bs_sk + sb_off, base + SB_OFF);
+  };
+
+  const int c0 = 2 * (lane >> 4);
+  const int r7 = lane & 7;
+  const int a_row = (wm * WM + (lane & 15)) * 128;
+  const int b_row = (BM + wn * WN + (lane & 15)) * 128;
+  const int sa_row = SA_OFF + (wm * WM + (lane & 15)) * 4;
+  const int sb_slot = SB_OFF + ((wn * WN) >> 7) * 4;
+
+  v4f acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+  // Zero-initialised so the first fold (of a C phase that never ran, or of
+  // group 1's warm-up C phase on zero operands) adds exactly 0.
+  v8i xf[FM], wf[2];
+  v4f t[2][FM];
+  float sc[FM];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    xf[i] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+    sc[i] = 0.f;
+    t[0][i] = t[1][i] = v4f{0.f, 0.f, 0.f, 0.f};
+  }
+  wf[0] = wf[1] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+
+  // M phase, part 1: LDS reads of quarter q's fragments (and at q == 0 the
+  // K-block's scales and activation fragments).
+  auto m_reads = [&](int kb, int q, float (&scn)[FM]) {
+    const uint8_t* sbase = smem + ((kb - kb_begin) & 1) * STAGE;
+    if (q == 0) {
+      const float sbv = *reinterpret_cast<const float*>(sbase + sb_slot);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        scn[i] = *reinterpret_cast<const float*>(sbase + sa_row + i * 64) * sbv;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) xf[i] = lds_frag(sbase + a_row + i * 16 * 128, c0, r7);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) wf[h] = lds_frag(sbase + b_row + (2 * q + h) * 16 * 128, c0, r7);
+  };
+  // M phase, part 2: fold the previous quarter's products (weight groups
+  // 2p, 2p+1) into acc with the scales of the K-block that produced them.
+  // Register values pass through empty volatile asm at phase boundaries so
+  // that IR-level code motion cannot carry MFMAs or FMAs (which touch no
+  // memory) across the barriers that separate the phases.
+  auto pin4 = [](v4f& v) { asm volatile("" : "+v"(v)); };
+  auto pin8 = [](v8i& v) { asm volatile("" : "+v"(v)); };
+  auto m_fold = [&](int p) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < FM; ++i) pin4(t[h][i]);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          acc[i][2 * p + h][r] = fmaf(t[h][i][r], sc[i], acc[i][2 * p + h][r]);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < FM; ++i) pin4(acc[i][2 * p + h]);
+  };
+  auto phase_m = [&](int kb, int q) {
+    float scn[FM];
+    m_reads(kb, q, scn);
+    m_fold((q + 3) & 3);
+    if (q == 0) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i) sc[i] = scn[i];
+    }
+    // The next C phase's operands must be in registers before the barrier
+    // (the last M phase of a K-block is also the last read of its stage).
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  };
+  auto phase_c = [&]() {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) pin8(wf[h]);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) pin8(xf[i]);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        t[h][i] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+            wf[h], xf[i], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < FM; ++i) pin4(t[h][i]);
+  };
+  auto bar = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto end_of_kblock = [&](int kb) {
+    bar();
+    if (kb + 2 < kb_end) issue(kb + 2, (kb - kb_begin) & 1);
+  };
+
+  if (nkb > 0) {
+    issue(kb_begin, 0);
+    if (nkb > 1) issue(kb_begin + 1, 1);
+    // Stage 0 only: up to 8 DMA instructions of stage 1 may stay in flight.
+    if (nkb > 1) wait_vmcnt<8>(); else wait_vmcnt<0>();
+    __syncthreads();
+  }
+  // Slot sequence (a barrier ends every slot). Slot 2q of K-block kb:
+  // group 0 M(q), group 1 C(q-1) [C(3) of kb-1 at q == 0]; slot 2q+1:
+  // group 0 C(q), group 1 M(q). The two groups run separate loops with the
+  // same number of barriers.
+  if (group == 0) {
+    for (int kb = kb_begin; kb < kb_end; ++kb) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        phase_m(kb, q);
+        bar();
+        phase_c();
+        if (q < 3) {
+          bar();
+        } else {
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+          end_of_kblock(kb);
+        }
+      }
+    }
+    if (nkb > 0) {
+      m_fold(3);
+      bar();
+    }
+  } else {
+    for (int kb = kb_begin; kb < kb_end; ++kb) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        phase_c();
+        bar();
+        phase_m(kb, q);
+        if (q < 3) {
+          bar();
+        } else {
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+          end_of_kblock(kb);
+        }
+      }
+    }
+    if (nkb > 0) {
+      phase_c();
+      bar();
+      m_fold(3);
+    }
+  }
+  __syncthreads();
+
+  const bool to_ws = gridDim.z > 1;
+  if (to_ws || a.out_dtype == FP8B_F32) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int m = m0 + wm * WM + i * 16 + (lane & 15);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        store4(a, m, n0 + wn * WN + j * 16 + 4 * (lane >> 4), acc[i][j], to_ws, blockIdx.z);
+    }
+    return;
+  }
+  const bool bf = a.out_dtype == FP8B_BF16;
+  uint8_t* wbase = smem + wid * WM * EPI_PITCH;
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const v4f v = acc[i][j];
+      v2i w;
+      w[0] = (int)(bf ? pack_bf16x2(v[0], v[1]) : pack_f16x2(v[0], v[1]));
+      w[1] = (int)(bf ? pack_bf16x2(v[2], v[3]) : pack_f16x2(v[2], v[3]));
+      *reinterpret_cast<v2i*>(wbase + (i * 16 + (lane & 15)) * EPI_PITCH +
+                              (j * 16 + 4 * (lane >> 4)) * 2) = w;
+    }
+  }
+  __syncthreads();
+  constexpr int CPR = WN / 8, RPP = 64 / CPR;
+  const int c = lane % CPR;
+  const int n = n0 + wn * WN + c * 8;
+  uint16_t* C = reinterpret_cast<uint16_t*>(a.C);
+#pragma unroll
+  for (int p = 0; p < WM / RPP; ++p) {
+    const int r = p * RPP + lane / CPR;
+    const int m = m0 + wm * WM + r;
+    const v4i v = *reinterpret_cast<const v4i*>(wbase + r * EPI_PITCH + c * 16);
+    if (m >= a.M || n >= a.N) continue;
+    uint16_t* dst = C + (int64_t)m * a.ldc + n;
+    if (n + 8 <= a.N && a.vec_store) {
+      *reinterpret_cast<v4i*>(dst) = v;
+    } else {
+      for (int e = 0; e < 8 && n + e < a.N; ++e)
+        dst[e] = (uint16_t)(((uint32_t)v[e >> 1]) >> ((e & 1) * 16));
+    }
+  }
+}
+
 // Skinny GEMM (M <= 16*FM <= 48, the decode shapes): bandwidth-bound on the
 // weight stream. A 512-thread workgroup owns 16 weight rows (output columns
 // n0..n0+15) over the whole K; its 8 waves split the K-blocks into
@@ -563,6 +836,16 @@ int device_cu_count() {
   return cus;
 }
 
+// 256x256 tiles run the ping-pong kernel only with FP8B_PINGPONG=1 (A/B runs;
+// it measures slower than the two-stage kernel on 4096x4096x8192).
+bool use_pingpong() {
+  static const bool v = [] {
+    const char* e = getenv("FP8B_PINGPONG");
+    return e && e[0] == '1';
+  }();
+  return v;
+}
+
 // Largest M served by the skinny kernel (at most 48: three 16-row activation
 // fragments per K-block slot). FP8B_SKINNY_MAX_M overrides it for A/B
 // measurements (0 sends every shape to the tiled path).
@@ -714,7 +997,15 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
       else gemm_skinny_kernel<3><<<grid, 512, 0, st>>>(a);
       break;
     }
-    case CFG_256x256: launch_cfg<256, 256, 64, 128>(a, p.splits, st); break;
+    case CFG_256x256: {
+      if (use_pingpong()) {
+        dim3 grid(a.tiles_m * a.tiles_n, 1, p.splits);
+        gemm_pp256_kernel<<<grid, 512, 0, st>>>(a);
+      } else {
+        launch_cfg<256, 256, 64, 128>(a, p.splits, st);
+      }
+      break;
+    }
     case CFG_128x128: launch_cfg<128, 128, 64, 64>(a, p.splits, st); break;
     case CFG_64x128: launch_cfg<64, 128, 32, 64>(a, p.splits, st); break;
     default: launch_cfg<32, 128, 32, 32>(a, p.splits, st); break;
