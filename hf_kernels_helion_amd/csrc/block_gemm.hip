@@ -104,6 +104,57 @@ __device__ __forceinline__ v8i lds_frag(const uint8_t* row, int c0, int r7) {
   return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
+// 16-bit epilogue of one wave's WM x WN tile (rows mw.., columns nw..): the
+// wave writes its packed sub-tiles to its own LDS area (pitch WN*2+16 bytes,
+// conflict-free), then stores whole 16-byte runs of each output row. Every
+// wave of the workgroup must call it (it contains a barrier).
+template <int WM, int WN>
+__device__ __forceinline__ void epilogue16(const GemmArgs& a, uint8_t* wbase,
+                                           const v4f (&acc)[WM / 16][WN / 16], int mw, int nw,
+                                           int lane) {
+  constexpr int FM = WM / 16, FN = WN / 16;
+  constexpr int EPI_PITCH = WN * 2 + 16;
+  const bool bf = a.out_dtype == FP8B_BF16;
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const v4f v = acc[i][j];
+      v2i w;
+      w[0] = (int)(bf ? pack_bf16x2(v[0], v[1]) : pack_f16x2(v[0], v[1]));
+      w[1] = (int)(bf ? pack_bf16x2(v[2], v[3]) : pack_f16x2(v[2], v[3]));
+      *reinterpret_cast<v2i*>(wbase + (i * 16 + (lane & 15)) * EPI_PITCH +
+                              (j * 16 + 4 * (lane >> 4)) * 2) = w;
+    }
+  }
+  __syncthreads();
+  constexpr int CPR = WN / 8;   // 16-byte chunks per wave row
+  constexpr int RPP = 64 / CPR; // rows per pass
+  const int c = lane % CPR;
+  const int n = nw + c * 8;
+  uint16_t* C = reinterpret_cast<uint16_t*>(a.C);
+#pragma unroll
+  for (int p = 0; p < WM / RPP; ++p) {
+    const int r = p * RPP + lane / CPR;
+    const int m = mw + r;
+    const v4i v = *reinterpret_cast<const v4i*>(wbase + r * EPI_PITCH + c * 16);
+    if (m >= a.M || n >= a.N) continue;
+    uint16_t* dst = C + (int64_t)m * a.ldc + n;
+    if (n + 8 <= a.N && a.vec_store) {
+      *reinterpret_cast<v4i*>(dst) = v;
+    } else {
+      for (int e = 0; e < 8 && n + e < a.N; ++e)
+        dst[e] = (uint16_t)(((uint32_t)v[e >> 1]) >> ((e & 1) * 16));
+    }
+  }
+}
+
+__device__ __forceinline__ v8i lds_frag2(const uint8_t* p, int s_lo, int s_hi) {
+  const v4i lo = *reinterpret_cast<const v4i*>(p + s_lo);
+  const v4i hi = *reinterpret_cast<const v4i*>(p + s_hi);
+  return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
 // BM x BN output tile per workgroup, WM x WN per wavefront.
 //
 // LDS stage layout (two stages):
@@ -267,43 +318,9 @@ gemm_bs128_kernel(GemmArgs a) {
     }
     return;
   }
-  // 16-bit outputs: stage the wave's WM x WN tile in LDS (the operand stages
-  // are dead after the loop's last barrier), then write whole 16-byte runs of
-  // each output row.
-  const bool bf = a.out_dtype == FP8B_BF16;
-  uint8_t* wbase = smem + wid * WM * EPI_PITCH;
-#pragma unroll
-  for (int i = 0; i < FM; ++i) {
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const v4f v = acc[i][j];
-      v2i w;
-      w[0] = (int)(bf ? pack_bf16x2(v[0], v[1]) : pack_f16x2(v[0], v[1]));
-      w[1] = (int)(bf ? pack_bf16x2(v[2], v[3]) : pack_f16x2(v[2], v[3]));
-      *reinterpret_cast<v2i*>(wbase + (i * 16 + (lane & 15)) * EPI_PITCH +
-                              (j * 16 + 4 * (lane >> 4)) * 2) = w;
-    }
-  }
-  __syncthreads();
-  constexpr int CPR = WN / 8;   // 16-byte chunks per wave row
-  constexpr int RPP = 64 / CPR; // rows per pass
-  const int c = lane % CPR;
-  const int n = n0 + wn * WN + c * 8;
-  uint16_t* C = reinterpret_cast<uint16_t*>(a.C);
-#pragma unroll
-  for (int p = 0; p < WM / RPP; ++p) {
-    const int r = p * RPP + lane / CPR;
-    const int m = m0 + wm * WM + r;
-    const v4i v = *reinterpret_cast<const v4i*>(wbase + r * EPI_PITCH + c * 16);
-    if (m >= a.M || n >= a.N) continue;
-    uint16_t* dst = C + (int64_t)m * a.ldc + n;
-    if (n + 8 <= a.N && a.vec_store) {
-      *reinterpret_cast<v4i*>(dst) = v;
-    } else {
-      for (int e = 0; e < 8 && n + e < a.N; ++e)
-        dst[e] = (uint16_t)(((uint32_t)v[e >> 1]) >> ((e & 1) * 16));
-    }
-  }
+  // 16-bit outputs: staged through LDS (the operand stages are dead after
+  // the loop's last barrier).
+  epilogue16<WM, WN>(a, smem + wid * WM * EPI_PITCH, acc, m0 + wm * WM, n0 + wn * WN, lane);
 }
 
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
@@ -314,37 +331,73 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Ping-pong GEMM for 256x256 tiles: 8 waves in two groups of four (one wave
-// of each group per SIMD). Every K-block is worked in four quarters; in a
-// quarter a wave first runs an "M" phase (apply the scale FMAs to the previous
-// quarter's MFMA results and read the next quarter's fragments from LDS) and
-// then a "C" phase (8 zero-accumulator MFMAs). Group 1 runs one phase behind
-// group 0 and every phase ends at a workgroup barrier, so on each SIMD one
-// wave issues MFMAs while the other does its FMAs and LDS reads: the FMAs
-// never wait on an MFMA of their own wave and the LDS latency hides under the
-// other wave's MFMAs. Operand tiles and scales arrive by global_load_lds into
-// two LDS stages exactly as in gemm_bs128_kernel; the DMA of K-block kb+2 is
-// issued right after the barrier that ends the last read of stage kb.
-__global__ void __launch_bounds__(512) gemm_pp256_kernel(GemmArgs a) {
-  constexpr int BM = 256, BN = 256, WM = 64, WN = 128;
-  constexpr int NWN = BN / WN, NW = 8;
-  constexpr int FM = WM / 16, FN = WN / 16;   // 4 activation, 8 weight fragments
-  constexpr int ROWS = BM + BN;
-  constexpr int SA_OFF = ROWS * 128;
-  constexpr int SB_OFF = SA_OFF + 4 * 256;
-  constexpr int STAGE = SB_OFF + 256;
-  constexpr int LOADS = ROWS / 8;
+// ---------------------------------------------------------------------------
+// Pipelined 256x256 kernel (the large-GEMM path).
+//
+// Same arithmetic as gemm_bs128_kernel (one zero-accumulator MFMA per 16x16
+// sub-tile and K-block, folded by one FMA with the product of the two
+// scales), scheduled so that LDS reads, DMA and the workgroup barrier overlap
+// the MFMA stream:
+//   * 8 waves, each owning a 128x64 (activation rows x weight rows) piece:
+//     eight 16-row activation fragments and four weight fragments per
+//     K-block. The 32 MFMAs of a K-block run in a fixed order (rows 0-1 and
+//     6-7 column-major in pairs, rows 2-5 row-major), so every fragment is
+//     read from LDS several MFMAs before its first use and its registers are
+//     refilled right after its last use.
+//   * One barrier per K-block, placed before MFMA 24: by then every wave has
+//     read all of the current stage and its DMA of the next stage has landed.
+//     After it the wave reads the next K-block's first fragments and issues
+//     the DMA of K-block kb+2 into the stage just released, one instruction
+//     per MFMA, while its last 8 MFMAs run.
+//   * Each MFMA result is folded two MFMAs later, so the FMAs never wait on
+//     the MFMA that produced them.
+//   * Activation and weight scales arrive in windows of 8 K-blocks (32 bytes
+//     per activation row: two 16-byte DMA lanes) instead of one 4-byte
+//     gather per row and K-block; a window is double-buffered and issued with
+//     the operand DMA two K-blocks ahead.
+//   * The DMA is issued from inline asm (global_load_lds_dwordx4 with an
+//     SGPR base and a 32-bit VGPR offset). The compiler does not see these
+//     loads, so it neither tracks them (the kernel waits on vmcnt itself,
+//     before each barrier) nor treats them as LGKM events of unknown order,
+//     which would force lgkmcnt(0) before every fragment read.
+// Preconditions (checked by the host): As and Bs contiguous along K with row
+// strides that keep 16-byte alignment, KB and the split size multiples of 4,
+// and 255 * max(lda, ldb) + K below 2^32 for the 32-bit DMA offsets.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void dma16_soff(uint32_t voff, const void* sbase, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ void dma16_ptr(const void* g, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(g), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ uint32_t lds_u32(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+template <int KIND> struct PipeKind { static constexpr int value = KIND; };
+
+__global__ void __launch_bounds__(512) gemm_pipe256_kernel(GemmArgs a) {
+  constexpr int BM = 256, BN = 256, WM = 128, WN = 64, NWN = BN / WN, NW = 8;
+  constexpr int FM = WM / 16, FN = WN / 16;       // 8 activation, 4 weight fragments
+  constexpr int STAGE = (BM + BN) * 128;          // operand rows of one K-block
+  constexpr int WIN_SA = BM * 32;                 // 8 K-blocks of As per row
+  constexpr int WIN = WIN_SA + 256;               // + Bs of the 2 column blocks
+  constexpr int SW_OFF = 2 * STAGE;
   constexpr int EPI_PITCH = WN * 2 + 16;
   constexpr int EPI = NW * WM * EPI_PITCH;
-  constexpr int SMEM = (2 * STAGE > EPI) ? 2 * STAGE : EPI;
+  constexpr int SMEM = (2 * STAGE + 2 * WIN > EPI) ? 2 * STAGE + 2 * WIN : EPI;
+  static_assert(FM == 8 && FN == 4, "the MFMA order below is written for 8x4 fragments");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int group = wid >> 2;  // waves 0-3 and 4-7: one of each per SIMD
   const int wm = wid / NWN, wn = wid % NWN;
 
+  // Workgroup -> tile: XCD-contiguous runs walked in groups of 8 tile rows
+  // (as in gemm_bs128_kernel).
   const int tiles = a.tiles_m * a.tiles_n;
   int bid = blockIdx.x;
   if (tiles % 8 == 0) bid = (bid & 7) * (tiles >> 3) + (bid >> 3);
@@ -355,190 +408,189 @@ __global__ void __launch_bounds__(512) gemm_pp256_kernel(GemmArgs a) {
   const int tm = first_m + (bid % group_size) % gm;
   const int tn = (bid % group_size) / gm;
   const int m0 = tm * BM, n0 = tn * BN;
-  const int kb_begin = blockIdx.z * a.kb_per_split;
+
+  const int split = blockIdx.z;
+  const int kb_begin = split * a.kb_per_split;
   const int kb_end = min(kb_begin + a.kb_per_split, a.KB);
   const int nkb = kb_end - kb_begin;
 
-  // DMA sources as wave-uniform tile bases plus 32-bit lane offsets.
-  const uint8_t* a_tile = a.A + (int64_t)m0 * a.lda;
-  const uint8_t* b_tile = a.B + (int64_t)n0 * a.ldb;
-  int src_off[LOADS / NW];
-#pragma unroll
-  for (int i = 0; i < LOADS / NW; ++i) {
+  const uint32_t lds0 = lds_u32(smem);
+  // Operand DMA: wave-load L = wid + 8i brings stage rows 8L..8L+7 (A rows
+  // for L < 32, B rows after), eight lanes per 128-byte row; lane l fetches
+  // chunk (l&7)^(l>>3) of row 8L + (l>>3), i.e. chunk c of row r lands in
+  // slot c^(r&7). Rows past the matrix edge are clamped to the last row.
+  const int r8 = lane >> 3;
+  const int c16 = ((lane & 7) ^ r8) * 16;
+  const uint8_t* a_base = a.A + (int64_t)m0 * a.lda;
+  const uint8_t* b_base = a.B + (int64_t)n0 * a.ldb;
+  const int a_lim = a.M - 1 - m0, b_lim = a.N - 1 - n0;
+  auto issue_op = [&](int kb, int stage, int i) {
     const int L = wid + i * NW;
-    const int r = L * 8 + (lane >> 3);
-    const int chunk = (lane & 7) ^ (r & 7);
-    src_off[i] = L * 8 < BM ? min(r, a.M - 1 - m0) * (int)a.lda + chunk * 16
-                            : min(r - BM, a.N - 1 - n0) * (int)a.ldb + chunk * 16;
-  }
-  const int sa_off = min(m0 + min(wid * 64 + lane, BM - 1), a.M - 1) * (int)a.as_sm;
-  const int sb_off = min((n0 >> 7) + min(lane, 1), (a.N - 1) >> 7) * (int)a.bs_sn;
-  auto issue = [&](int kb, int stage) {
-    uint8_t* base = smem + stage * STAGE;
-    const uint8_t* ak = a_tile + (int64_t)kb * 128;
-    const uint8_t* bk = b_tile + (int64_t)kb * 128;
-#pragma unroll
-    for (int i = 0; i < LOADS / NW; ++i) {
-      const int L = wid + i * NW;
-      lds_dma16((L * 8 < BM ? ak : bk) + src_off[i], base + L * 1024);
+    const uint32_t lds = lds0 + stage * STAGE + L * 1024;
+    if (i < 4) {
+      const uint32_t voff = (uint32_t)min(L * 8 + r8, a_lim) * (uint32_t)a.lda + c16;
+      dma16_soff(voff, a_base + (int64_t)kb * 128, lds);
+    } else {
+      const uint32_t voff = (uint32_t)min((L - 32) * 8 + r8, b_lim) * (uint32_t)a.ldb + c16;
+      dma16_soff(voff, b_base + (int64_t)kb * 128, lds);
     }
-    if (wid < 4) lds_dma4(a.As + (int64_t)kb * a.as_sk + sa_off, base + SA_OFF + wid * 256);
-    if (wid == NW - 1) lds_dma4(a.Bs + (int64_t)kb * a.bs_sk + sb_off, base + SB_OFF);
+  };
+  // Scale window of 8 K-blocks from kb0: wave w brings As rows 32w..32w+31
+  // (two lanes per row, 4 K-blocks each); wave 7 also brings the Bs rows of
+  // the tile's two 128-column blocks. A half-window past kb_end re-reads the
+  // first half (KB is a multiple of 4), so no lane reads past the row.
+  const float* saw_src =
+      a.As + (int64_t)min(m0 + wid * 32 + (lane >> 1), a.M - 1) * a.as_sm + 4 * (lane & 1);
+  const float* sbw_src =
+      a.Bs + (int64_t)min((n0 >> 7) + min(lane >> 1, 1), (a.N - 1) >> 7) * a.bs_sn + 4 * (lane & 1);
+  auto issue_win = [&](int kb0, int wbuf) {
+    const int kk = (kb0 + 4 * (lane & 1) < kb_end) ? kb0 : kb0 - 4 * (lane & 1);
+    const uint32_t lb = lds0 + SW_OFF + wbuf * WIN;
+    dma16_ptr(saw_src + kk, lb + wid * 1024);
+    if (wid == NW - 1 && lane < 4) dma16_ptr(sbw_src + kk, lb + WIN_SA);
   };
 
-  const int c0 = 2 * (lane >> 4);
-  const int r7 = lane & 7;
-  const int a_row = (wm * WM + (lane & 15)) * 128;
-  const int b_row = (BM + wn * WN + (lane & 15)) * 128;
-  const int sa_row = SA_OFF + (wm * WM + (lane & 15)) * 4;
-  const int sb_slot = SB_OFF + ((wn * WN) >> 7) * 4;
+  // Fragment reads: rows (lane & 15) of a 16-row group, logical chunks
+  // 2*(lane>>4) and 2*(lane>>4)+1 at their swizzled slots.
+  const int r7 = lane & 7, g2 = 2 * (lane >> 4);
+  const int slo = (g2 ^ r7) << 4, shi = ((g2 + 1) ^ r7) << 4;
+  const int a_off = (wm * WM + (lane & 15)) * 128;
+  const int b_off = (BM + wn * WN + (lane & 15)) * 128;
+  auto rdx = [&](int stage, int i) {
+    return lds_frag2(smem + stage * STAGE + a_off + i * 2048, slo, shi);
+  };
+  auto rdw = [&](int stage, int j) {
+    return lds_frag2(smem + stage * STAGE + b_off + j * 2048, slo, shi);
+  };
+  const int sa_off = SW_OFF + (wm * WM + (lane & 15)) * 32;
+  const int sb_off = SW_OFF + WIN_SA + ((wn * WN) >> 7) * 32;
+  auto rdsa = [&](int rel, int i) {
+    const int o = ((rel >> 3) & 1) * WIN + (rel & 7) * 4;
+    return *reinterpret_cast<const float*>(smem + sa_off + o + i * 512);
+  };
+  auto rdsb = [&](int rel) {
+    const int o = ((rel >> 3) & 1) * WIN + (rel & 7) * 4;
+    return *reinterpret_cast<const float*>(smem + sb_off + o);
+  };
 
   v4f acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-  // Zero-initialised so the first fold (of a C phase that never ran, or of
-  // group 1's warm-up C phase on zero operands) adds exactly 0.
-  v8i xf[FM], wf[2];
-  v4f t[2][FM];
-  float sc[FM];
-#pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    xf[i] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
-    sc[i] = 0.f;
-    t[0][i] = t[1][i] = v4f{0.f, 0.f, 0.f, 0.f};
-  }
-  wf[0] = wf[1] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
 
-  // M phase, part 1: LDS reads of quarter q's fragments (and at q == 0 the
-  // K-block's scales and activation fragments).
-  auto m_reads = [&](int kb, int q, float (&scn)[FM]) {
-    const uint8_t* sbase = smem + ((kb - kb_begin) & 1) * STAGE;
-    if (q == 0) {
-      const float sbv = *reinterpret_cast<const float*>(sbase + sb_slot);
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-        scn[i] = *reinterpret_cast<const float*>(sbase + sa_row + i * 64) * sbv;
-#pragma unroll
-      for (int i = 0; i < FM; ++i) xf[i] = lds_frag(sbase + a_row + i * 16 * 128, c0, r7);
-    }
-#pragma unroll
-    for (int h = 0; h < 2; ++h) wf[h] = lds_frag(sbase + b_row + (2 * q + h) * 16 * 128, c0, r7);
-  };
-  // M phase, part 2: fold the previous quarter's products (weight groups
-  // 2p, 2p+1) into acc with the scales of the K-block that produced them.
-  // Register values pass through empty volatile asm at phase boundaries so
-  // that IR-level code motion cannot carry MFMAs or FMAs (which touch no
-  // memory) across the barriers that separate the phases.
-  auto pin4 = [](v4f& v) { asm volatile("" : "+v"(v)); };
-  auto pin8 = [](v8i& v) { asm volatile("" : "+v"(v)); };
-  auto m_fold = [&](int p) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int i = 0; i < FM; ++i) pin4(t[h][i]);
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          acc[i][2 * p + h][r] = fmaf(t[h][i][r], sc[i], acc[i][2 * p + h][r]);
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int i = 0; i < FM; ++i) pin4(acc[i][2 * p + h]);
-  };
-  auto phase_m = [&](int kb, int q) {
-    float scn[FM];
-    m_reads(kb, q, scn);
-    m_fold((q + 3) & 3);
-    if (q == 0) {
-#pragma unroll
-      for (int i = 0; i < FM; ++i) sc[i] = scn[i];
-    }
-    // The next C phase's operands must be in registers before the barrier
-    // (the last M phase of a K-block is also the last read of its stage).
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  };
-  auto phase_c = [&]() {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) pin8(wf[h]);
-#pragma unroll
-    for (int i = 0; i < FM; ++i) pin8(xf[i]);
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-        t[h][i] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-            wf[h], xf[i], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int i = 0; i < FM; ++i) pin4(t[h][i]);
-  };
-  auto bar = [&]() {
-    __builtin_amdgcn_sched_barrier(0);
-    __syncthreads();
-    __builtin_amdgcn_sched_barrier(0);
-  };
-  auto end_of_kblock = [&](int kb) {
-    bar();
-    if (kb + 2 < kb_end) issue(kb + 2, (kb - kb_begin) & 1);
-  };
+  // MFMA order of a K-block; activation row i lives in fragment slot i & 3.
+  constexpr int ORD_I[32] = {0, 1, 0, 1, 0, 1, 0, 1, 2, 2, 2, 2, 3, 3, 3, 3,
+                             4, 4, 4, 4, 5, 5, 5, 5, 6, 7, 6, 7, 6, 7, 6, 7};
+  constexpr int ORD_J[32] = {0, 0, 1, 1, 2, 2, 3, 3, 0, 1, 2, 3, 0, 1, 2, 3,
+                             0, 1, 2, 3, 0, 1, 2, 3, 0, 0, 1, 1, 2, 2, 3, 3};
+  v8i w[FN], xs[4];
+  float sc[FM], sa_t[FM], sb_n = 0.f, sc6_old = 0.f, sc7_old = 0.f;
+  v4f r1 = v4f{0.f, 0.f, 0.f, 0.f}, r2 = r1;  // results of MFMAs p-1 and p-2
 
   if (nkb > 0) {
-    issue(kb_begin, 0);
-    if (nkb > 1) issue(kb_begin + 1, 1);
-    // Stage 0 only: up to 8 DMA instructions of stage 1 may stay in flight.
-    if (nkb > 1) wait_vmcnt<8>(); else wait_vmcnt<0>();
+#pragma unroll
+    for (int i = 0; i < 8; ++i) issue_op(kb_begin, 0, i);
+    issue_win(kb_begin, 0);
+    if (nkb > 1) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) issue_op(kb_begin + 1, 1, i);
+      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
     __syncthreads();
+    w[0] = rdw(0, 0); w[1] = rdw(0, 1); w[2] = rdw(0, 2);
+    xs[0] = rdx(0, 0); xs[1] = rdx(0, 1);
+    sb_n = rdsb(0);
+    sa_t[0] = rdsa(0, 0); sa_t[1] = rdsa(0, 1);
   }
-  // Slot sequence (a barrier ends every slot). Slot 2q of K-block kb:
-  // group 0 M(q), group 1 C(q-1) [C(3) of kb-1 at q == 0]; slot 2q+1:
-  // group 0 C(q), group 1 M(q). The two groups run separate loops with the
-  // same number of barriers.
-  if (group == 0) {
-    for (int kb = kb_begin; kb < kb_end; ++kb) {
+
+  // One K-block. KIND 0: steady state (reads the next K-block, DMA of
+  // kb+2); 1: next K-block exists but no kb+2; 2: last K-block.
+  // The empty asm statements pin each MFMA result and accumulator update in
+  // program order (LLVM would otherwise sink the pure MFMA/FMA chain past the
+  // barrier), and sched_barrier keeps the machine scheduler from regrouping
+  // the reads and the DMA.
+  auto body = [&](int kb, auto tag) {
+    constexpr int KIND = decltype(tag)::value;
+    const int rel = kb - kb_begin;
+    const int s = rel & 1;
+    const float sb = sb_n;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        phase_m(kb, q);
-        bar();
-        phase_c();
-        if (q < 3) {
-          bar();
-        } else {
-          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-          end_of_kblock(kb);
-        }
+    for (int p = 0; p < 32; ++p) {
+      const int i = ORD_I[p], j = ORD_J[p];
+      if (p == 24 && KIND < 2) {
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (KIND == 0 && ((rel + 2) & 7) == 0) issue_win(kb + 2, ((rel + 2) >> 3) & 1);
       }
-    }
-    if (nkb > 0) {
-      m_fold(3);
-      bar();
-    }
-  } else {
-    for (int kb = kb_begin; kb < kb_end; ++kb) {
+      v4f res = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+          w[j], xs[i & 3], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
+      asm volatile("" : "+v"(res));
+      if (p >= 2) {
+        const int qi = ORD_I[p - 2], qj = ORD_J[p - 2];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        phase_c();
-        bar();
-        phase_m(kb, q);
-        if (q < 3) {
-          bar();
-        } else {
-          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-          end_of_kblock(kb);
-        }
+        for (int e = 0; e < 4; ++e) acc[qi][qj][e] = fmaf(r2[e], sc[qi], acc[qi][qj][e]);
+        asm volatile("" : "+v"(acc[qi][qj]));
+      } else {
+        // the previous K-block's last two MFMAs: rows 6 and 7, column 3
+        const int qi = 6 + p;
+        const float so = p == 0 ? sc6_old : sc7_old;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[qi][3][e] = fmaf(r2[e], so, acc[qi][3][e]);
+        asm volatile("" : "+v"(acc[qi][3]));
       }
+      r2 = r1;
+      r1 = res;
+      // This K-block's remaining fragments and activation scales.
+      if (p == 0) w[3] = rdw(s, 3);
+      if (p == 1) { xs[2] = rdx(s, 2); sa_t[2] = rdsa(rel, 2); }
+      if (p == 3) { xs[3] = rdx(s, 3); sa_t[3] = rdsa(rel, 3); }
+      if (p == 7) { xs[0] = rdx(s, 4); sa_t[4] = rdsa(rel, 4); }
+      if (p == 8) { xs[1] = rdx(s, 5); sa_t[5] = rdsa(rel, 5); }
+      if (p == 12) { xs[2] = rdx(s, 6); sa_t[6] = rdsa(rel, 6); }
+      if (p == 16) { xs[3] = rdx(s, 7); sa_t[7] = rdsa(rel, 7); }
+      // Scale of row i, computed just before the FMA of its first MFMA.
+      if (p == 1) { sc[0] = sa_t[0] * sb; sc[1] = sa_t[1] * sb; }
+      if (p == 9) sc[2] = sa_t[2] * sb;
+      if (p == 13) sc[3] = sa_t[3] * sb;
+      if (p == 17) sc[4] = sa_t[4] * sb;
+      if (p == 21) sc[5] = sa_t[5] * sb;
+      if (p == 25) { sc[6] = sa_t[6] * sb; sc[7] = sa_t[7] * sb; }
+      // After the barrier: the next K-block's first fragments (stage s^1)
+      // and the DMA of K-block kb+2 into stage s.
+      if (KIND < 2 && p >= 24) {
+        if (KIND == 0) issue_op(kb + 2, s, p - 24);
+        if (p == 24) { xs[0] = rdx(s ^ 1, 0); sb_n = rdsb(rel + 1); sa_t[0] = rdsa(rel + 1, 0); }
+        if (p == 25) { xs[1] = rdx(s ^ 1, 1); sa_t[1] = rdsa(rel + 1, 1); }
+        if (p == 26) w[0] = rdw(s ^ 1, 0);
+        if (p == 28) w[1] = rdw(s ^ 1, 1);
+        if (p == 30) w[2] = rdw(s ^ 1, 2);
+      }
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (nkb > 0) {
-      phase_c();
-      bar();
-      m_fold(3);
-    }
+    sc6_old = sc[6];
+    sc7_old = sc[7];
+  };
+
+  int kb = kb_begin;
+  for (; kb + 2 < kb_end; ++kb) body(kb, PipeKind<0>{});
+  if (kb + 1 < kb_end) {
+    body(kb, PipeKind<1>{});
+    ++kb;
   }
+  if (kb < kb_end) {
+    body(kb, PipeKind<2>{});
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[6][3][e] = fmaf(r2[e], sc[6], acc[6][3][e]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[7][3][e] = fmaf(r1[e], sc[7], acc[7][3][e]);
+  }
+  // The last K-block has no barrier: wait for every wave before the epilogue
+  // reuses the operand stages.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
   const bool to_ws = gridDim.z > 1;
@@ -547,44 +599,14 @@ __global__ void __launch_bounds__(512) gemm_pp256_kernel(GemmArgs a) {
     for (int i = 0; i < FM; ++i) {
       const int m = m0 + wm * WM + i * 16 + (lane & 15);
 #pragma unroll
-      for (int j = 0; j < FN; ++j)
-        store4(a, m, n0 + wn * WN + j * 16 + 4 * (lane >> 4), acc[i][j], to_ws, blockIdx.z);
+      for (int j = 0; j < FN; ++j) {
+        const int n = n0 + wn * WN + j * 16 + 4 * (lane >> 4);
+        store4(a, m, n, acc[i][j], to_ws, split);
+      }
     }
     return;
   }
-  const bool bf = a.out_dtype == FP8B_BF16;
-  uint8_t* wbase = smem + wid * WM * EPI_PITCH;
-#pragma unroll
-  for (int i = 0; i < FM; ++i) {
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const v4f v = acc[i][j];
-      v2i w;
-      w[0] = (int)(bf ? pack_bf16x2(v[0], v[1]) : pack_f16x2(v[0], v[1]));
-      w[1] = (int)(bf ? pack_bf16x2(v[2], v[3]) : pack_f16x2(v[2], v[3]));
-      *reinterpret_cast<v2i*>(wbase + (i * 16 + (lane & 15)) * EPI_PITCH +
-                              (j * 16 + 4 * (lane >> 4)) * 2) = w;
-    }
-  }
-  __syncthreads();
-  constexpr int CPR = WN / 8, RPP = 64 / CPR;
-  const int c = lane % CPR;
-  const int n = n0 + wn * WN + c * 8;
-  uint16_t* C = reinterpret_cast<uint16_t*>(a.C);
-#pragma unroll
-  for (int p = 0; p < WM / RPP; ++p) {
-    const int r = p * RPP + lane / CPR;
-    const int m = m0 + wm * WM + r;
-    const v4i v = *reinterpret_cast<const v4i*>(wbase + r * EPI_PITCH + c * 16);
-    if (m >= a.M || n >= a.N) continue;
-    uint16_t* dst = C + (int64_t)m * a.ldc + n;
-    if (n + 8 <= a.N && a.vec_store) {
-      *reinterpret_cast<v4i*>(dst) = v;
-    } else {
-      for (int e = 0; e < 8 && n + e < a.N; ++e)
-        dst[e] = (uint16_t)(((uint32_t)v[e >> 1]) >> ((e & 1) * 16));
-    }
-  }
+  epilogue16<WM, WN>(a, smem + wid * WM * EPI_PITCH, acc, m0 + wm * WM, n0 + wn * WN, lane);
 }
 
 // Skinny GEMM (M <= 16*FM <= 48, the decode shapes): bandwidth-bound on the
@@ -836,16 +858,6 @@ int device_cu_count() {
   return cus;
 }
 
-// 256x256 tiles run the ping-pong kernel only with FP8B_PINGPONG=1 (A/B runs;
-// it measures slower than the two-stage kernel on 4096x4096x8192).
-bool use_pingpong() {
-  static const bool v = [] {
-    const char* e = getenv("FP8B_PINGPONG");
-    return e && e[0] == '1';
-  }();
-  return v;
-}
-
 // Largest M served by the skinny kernel (at most 48: three 16-row activation
 // fragments per K-block slot). FP8B_SKINNY_MAX_M overrides it for A/B
 // measurements (0 sends every shape to the tiled path).
@@ -899,6 +911,21 @@ bool mfma_path_ok(const void* A, int64_t lda, const void* B, int64_t ldb, int64_
   return block_n == 128 && block_k == 128 && K % 128 == 0 && K > 0 && lda % 16 == 0 &&
          ldb % 16 == 0 && ((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0 &&
          M < (int64_t(1) << 30) && N < (int64_t(1) << 30) && K < (int64_t(1) << 30);
+}
+
+// Preconditions of gemm_pipe256_kernel: scale windows (As, Bs contiguous in
+// K, 16-byte aligned rows, K-block counts and split sizes multiples of 4) and
+// 32-bit DMA offsets within a 256-row tile. FP8B_PIPE256=0 turns it off.
+bool pipe256_ok(const GemmArgs& a, const Plan& p) {
+  static const bool enabled = [] {
+    const char* e = getenv("FP8B_PIPE256");
+    return !(e && e[0] == '0');
+  }();
+  if (!enabled) return false;
+  const bool splits_ok = p.splits == 1 || a.kb_per_split % 4 == 0;
+  return a.as_sk == 1 && a.bs_sk == 1 && a.as_sm % 4 == 0 && a.bs_sn % 4 == 0 &&
+         ((uintptr_t)a.As & 15) == 0 && ((uintptr_t)a.Bs & 15) == 0 && a.KB % 4 == 0 &&
+         splits_ok && 255 * std::max(a.lda, a.ldb) + a.K < (int64_t(1) << 32);
 }
 
 template <int BM, int BN, int WM, int WN>
@@ -998,9 +1025,9 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
       break;
     }
     case CFG_256x256: {
-      if (use_pingpong()) {
+      if (pipe256_ok(a, p)) {
         dim3 grid(a.tiles_m * a.tiles_n, 1, p.splits);
-        gemm_pp256_kernel<<<grid, 512, 0, st>>>(a);
+        gemm_pipe256_kernel<<<grid, 512, 0, st>>>(a);
       } else {
         launch_cfg<256, 256, 64, 128>(a, p.splits, st);
       }

@@ -172,6 +172,59 @@ def test_gemm_large_sampled_rows(M, N, K, outliers, dev):
     torch.testing.assert_close(out.float(), full.to(torch.bfloat16).float(), rtol=RTOL, atol=ATOL)
 
 
+def _full_check(out, Ad, Bd, Asd, Bsd):
+    """Every row against torch's fp32 dequant-matmul on the GPU."""
+    M, K = Ad.shape
+    N = Bd.shape[0]
+    saf = Asd.repeat_interleave(128, 1)[:, :K]
+    sbf = Bsd.repeat_interleave(128, 0)[:N].repeat_interleave(128, 1)[:, :K]
+    full = (Ad.float() * saf) @ (Bd.float() * sbf).T
+    if out.dtype != torch.float32:
+        full = full.to(out.dtype)
+    torch.testing.assert_close(out.float(), full.float(), rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 512), (4096, 4096, 1024), (4000, 4200, 1536),
+                                   (4096, 4352, 2560), (3001, 5000, 2048),
+                                   (4096, 4096, 384), (4096, 4096, 1152)])
+def test_gemm_large_tile_kernels(M, N, K, dev):
+    """Grids of at least one 256x256 tile per CU: the pipelined kernel (K-block
+    counts that are multiples of 4; windows of 8 K-blocks, full and half) and
+    the two-stage kernel it falls back to (K-block counts 3 and 9), with
+    ragged M and N edges. Every row against torch's fp32 dequant-matmul, a
+    sample of rows against the oracle."""
+    print(f"gemm large-tile M={M} N={N} K={K}", flush=True)
+    A, B, As, Bs = _operands(M, N, K, seed=K + M)
+    Ad, Bd, Asd, Bsd = A.to(dev), B.to(dev), As.to(dev), Bs.to(dev)
+    out = fp8.w8a8_block_fp8_matmul(Ad, Bd, Asd, Bsd, [128, 128], torch.bfloat16)
+    _full_check(out, Ad, Bd, Asd, Bsd)
+    rows = torch.cat([torch.tensor([0, M - 1]),
+                      torch.randperm(M, generator=torch.Generator().manual_seed(2))[:4]])
+    ref = oracle.block_gemm(_u8(A[rows]), _u8(B), As[rows].numpy(), Bs.numpy())
+    torch.testing.assert_close(out[rows.to(dev)].float().cpu(),
+                               torch.from_numpy(ref).to(torch.bfloat16).float(),
+                               rtol=RTOL, atol=ATOL)
+
+
+def test_gemm_large_tile_exact_and_fp32(dev):
+    """Pipelined kernel with small-integer operands and unit scales (exact
+    result), fp32 output; and with column-major As (two-stage fallback)."""
+    print("gemm large-tile exact", flush=True)
+    g = torch.Generator().manual_seed(5)
+    M, N, K = 4096, 4096, 512
+    A = torch.randint(-4, 5, (M, K), generator=g).float().to(torch.float8_e4m3fn).to(dev)
+    B = torch.randint(-4, 5, (N, K), generator=g).float().to(torch.float8_e4m3fn).to(dev)
+    As = torch.ones(M, K // 128, device=dev)
+    Bs = torch.ones(N // 128, K // 128, device=dev)
+    out = fp8.w8a8_block_fp8_matmul(A, B, As, Bs, [128, 128], torch.float32)
+    exact = A.double() @ B.double().T
+    assert torch.equal(out.double(), exact)
+    A2, B2, As2, Bs2 = [t.to(dev) for t in _operands(M, N, 1024, seed=9)]
+    As2_t = As2.T.contiguous().T
+    out2 = fp8.w8a8_block_fp8_matmul(A2, B2, As2_t, Bs2, [128, 128], torch.float32)
+    _full_check(out2, A2, B2, As2, Bs2)
+
+
 def test_gemm_golden_fixture(dev):
     """Float64 golden output; the fp8 MFMA sums a 128-long K-block with less
     than fp32 precision (measured ~2^-15 relative to the block's dot), so the
