@@ -609,6 +609,216 @@ __global__ void __launch_bounds__(512) gemm_pipe256_kernel(GemmArgs a) {
   epilogue16<WM, WN>(a, smem + wid * WM * EPI_PITCH, acc, m0 + wm * WM, n0 + wn * WN, lane);
 }
 
+// ---------------------------------------------------------------------------
+// Pipelined 128x128 kernel (grids below one 256x256 tile per CU, and the
+// split-K path). Waves of WM x WN (two per SIMD for 64x32); with half the operand
+// reuse of a 256x256 tile this size is bound by the operand stream, so it
+// keeps three K-blocks of DMA in flight: four LDS stages of 32 KiB, the DMA
+// of K-block kb+4 issued right after the barrier that opens K-block kb. Each
+// K-block's fragments are read from LDS during the previous K-block's MFMAs
+// into the other of two register sets; scale windows and asm DMA as in
+// gemm_pipe256_kernel.
+// ---------------------------------------------------------------------------
+template <int WM, int WN>
+__global__ void __launch_bounds__((128 / WM) * (128 / WN) * 64) gemm_pipe128_kernel(GemmArgs a) {
+  constexpr int BM = 128, BN = 128, NWN = BN / WN, NW = (BM / WM) * NWN;
+  constexpr int FM = WM / 16, FN = WN / 16;
+  static_assert(FM * FN >= FM + FN + 1, "next-K-block reads must fit between the MFMAs");
+  static_assert(NW >= BM / 32, "one scale-window instruction per 32 activation rows");
+  constexpr int NSTAGE = 4;
+  constexpr int STAGE = (BM + BN) * 128;   // 32 KiB
+  constexpr int WIN_SA = BM * 32;
+  constexpr int WIN = WIN_SA + 256;
+  constexpr int SW_OFF = NSTAGE * STAGE;
+  constexpr int EPI_PITCH = WN * 2 + 16;
+  constexpr int EPI = NW * WM * EPI_PITCH;
+  constexpr int SMEM = (SW_OFF + 2 * WIN > EPI) ? SW_OFF + 2 * WIN : EPI;
+  constexpr int LPW = (BM + BN) / 8 / NW;  // wave-loads per wave per K-block (8)
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wid / NWN, wn = wid % NWN;
+
+  const int tiles = a.tiles_m * a.tiles_n;
+  int bid = blockIdx.x;
+  if (tiles % 8 == 0) bid = (bid & 7) * (tiles >> 3) + (bid >> 3);
+  constexpr int GROUP_M = 8;
+  const int group_size = GROUP_M * a.tiles_n;
+  const int first_m = (bid / group_size) * GROUP_M;
+  const int gm = min(a.tiles_m - first_m, GROUP_M);
+  const int tm = first_m + (bid % group_size) % gm;
+  const int tn = (bid % group_size) / gm;
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  const int split = blockIdx.z;
+  const int kb_begin = split * a.kb_per_split;
+  const int kb_end = min(kb_begin + a.kb_per_split, a.KB);
+  const int nkb = kb_end - kb_begin;
+
+  const uint32_t lds0 = lds_u32(smem);
+  const int r8 = lane >> 3;
+  const int c16 = ((lane & 7) ^ r8) * 16;
+  const uint8_t* a_base = a.A + (int64_t)m0 * a.lda;
+  const uint8_t* b_base = a.B + (int64_t)n0 * a.ldb;
+  const int a_lim = a.M - 1 - m0, b_lim = a.N - 1 - n0;
+  auto issue_op = [&](int kb, int stage, int i) {
+    const int L = wid + i * NW;
+    const uint32_t lds = lds0 + stage * STAGE + L * 1024;
+    if (L < BM / 8) {
+      const uint32_t voff = (uint32_t)min(L * 8 + r8, a_lim) * (uint32_t)a.lda + c16;
+      dma16_soff(voff, a_base + (int64_t)kb * 128, lds);
+    } else {
+      const uint32_t voff = (uint32_t)min((L - BM / 8) * 8 + r8, b_lim) * (uint32_t)a.ldb + c16;
+      dma16_soff(voff, b_base + (int64_t)kb * 128, lds);
+    }
+  };
+  const float* saw_src =
+      a.As + (int64_t)min(m0 + wid * 32 + (lane >> 1), a.M - 1) * a.as_sm + 4 * (lane & 1);
+  const float* sbw_src = a.Bs + (int64_t)(n0 >> 7) * a.bs_sn + 4 * (lane & 1);
+  auto issue_win = [&](int kb0, int wbuf) {
+    const int kk = (kb0 + 4 * (lane & 1) < kb_end) ? kb0 : kb0 - 4 * (lane & 1);
+    const uint32_t lb = lds0 + SW_OFF + wbuf * WIN;
+    if (wid < BM / 32) dma16_ptr(saw_src + kk, lb + wid * 1024);
+    if (wid == NW - 1 && lane < 2) dma16_ptr(sbw_src + kk, lb + WIN_SA);
+  };
+  // DMA of one K-block (and, at a window start, its scale window).
+  auto issue_kb = [&](int kb) {
+    const int rel = kb - kb_begin;
+    if ((rel & 7) == 0) issue_win(kb, (rel >> 3) & 1);
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) issue_op(kb, rel % NSTAGE, i);
+  };
+
+  const int r7 = lane & 7, g2 = 2 * (lane >> 4);
+  const int slo = (g2 ^ r7) << 4, shi = ((g2 + 1) ^ r7) << 4;
+  const int a_off = (wm * WM + (lane & 15)) * 128;
+  const int b_off = (BM + wn * WN + (lane & 15)) * 128;
+  const int sa_off = SW_OFF + (wm * WM + (lane & 15)) * 32;
+  const int sb_off = SW_OFF + WIN_SA;
+
+  v4f acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+  v8i xf[2][FM], wf[2][FN];
+  float sc[2][FM];
+  v4f r1 = v4f{0.f, 0.f, 0.f, 0.f}, r2 = r1;
+
+  // Fragments and scales of K-block kb into register set S (reads spread
+  // over the caller's MFMAs by the caller's sched barriers).
+  auto read_frag = [&](int kb, int S, int f) {
+    const uint8_t* st = smem + ((kb - kb_begin) % NSTAGE) * STAGE;
+    if (f < FM) xf[S][f] = lds_frag2(st + a_off + f * 2048, slo, shi);
+    else wf[S][f - FM] = lds_frag2(st + b_off + (f - FM) * 2048, slo, shi);
+  };
+  auto read_scales = [&](int kb, int S) {
+    const int rel = kb - kb_begin;
+    const int o = ((rel >> 3) & 1) * WIN + (rel & 7) * 4;
+    const float sb = *reinterpret_cast<const float*>(smem + sb_off + o);
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      sc[S][i] = *reinterpret_cast<const float*>(smem + sa_off + o + i * 512) * sb;
+  };
+
+  // Waits until this wave's DMA of a K-block has landed, given how many
+  // K-blocks' DMAs it issued after that one (window instructions in between
+  // only make the wait stricter).
+  auto wait_after = [&](int n_after) {
+    if (n_after >= 3) wait_vmcnt<3 * LPW>();
+    else if (n_after == 2) wait_vmcnt<2 * LPW>();
+    else if (n_after == 1) wait_vmcnt<LPW>();
+    else wait_vmcnt<0>();
+  };
+
+  if (nkb > 0) {
+    for (int k = 0; k < NSTAGE && k < nkb; ++k) issue_kb(kb_begin + k);
+    wait_after(min(NSTAGE, nkb) - 1);
+    __syncthreads();
+#pragma unroll
+    for (int f = 0; f < FM + FN; ++f) read_frag(kb_begin, 0, f);
+    read_scales(kb_begin, 0);
+  }
+
+  auto body = [&](int kb, auto set_tag) {
+    constexpr int S = decltype(set_tag)::value, T = S ^ 1;
+    const bool more = kb + 1 < kb_end;
+    if (more) {
+      // outstanding: the DMAs of kb+1 .. min(kb+3, kb_end-1)
+      wait_after(min(2, kb_end - kb - 2));
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (kb + NSTAGE < kb_end) issue_kb(kb + NSTAGE);
+    }
+#pragma unroll
+    for (int p = 0; p < FM * FN; ++p) {
+      const int i = p / FN, j = p % FN;
+      v4f res = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+          wf[S][j], xf[S][i], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
+      asm volatile("" : "+v"(res));
+      if (p >= 2) {
+        const int qi = (p - 2) / FN, qj = (p - 2) % FN;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[qi][qj][e] = fmaf(r2[e], sc[S][qi], acc[qi][qj][e]);
+        asm volatile("" : "+v"(acc[qi][qj]));
+      } else {
+        const int qj = FN - 2 + p;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[FM - 1][qj][e] = fmaf(r2[e], sc[T][FM - 1], acc[FM - 1][qj][e]);
+        asm volatile("" : "+v"(acc[FM - 1][qj]));
+      }
+      r2 = r1;
+      r1 = res;
+      if (more) {
+        if (p < FM + FN) read_frag(kb + 1, T, p);
+        if (p == FM + FN) read_scales(kb + 1, T);
+      }
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // sc[1] starts at zero so the first K-block's two "previous" folds add 0.
+#pragma unroll
+  for (int i = 0; i < FM; ++i) sc[1][i] = 0.f;
+  int kb = kb_begin;
+  for (; kb + 1 < kb_end; kb += 2) {
+    body(kb, PipeKind<0>{});
+    body(kb + 1, PipeKind<1>{});
+  }
+  int last_set = 1;
+  if (kb < kb_end) {
+    body(kb, PipeKind<0>{});
+    last_set = 0;
+  }
+  if (nkb > 0) {
+    const float s3 = last_set == 0 ? sc[0][FM - 1] : sc[1][FM - 1];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[FM - 1][FN - 2][e] = fmaf(r2[e], s3, acc[FM - 1][FN - 2][e]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[FM - 1][FN - 1][e] = fmaf(r1[e], s3, acc[FM - 1][FN - 1][e]);
+  }
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  const bool to_ws = gridDim.z > 1;
+  if (to_ws || a.out_dtype == FP8B_F32) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int m = m0 + wm * WM + i * 16 + (lane & 15);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int n = n0 + wn * WN + j * 16 + 4 * (lane >> 4);
+        store4(a, m, n, acc[i][j], to_ws, split);
+      }
+    }
+    return;
+  }
+  epilogue16<WM, WN>(a, smem + wid * WM * EPI_PITCH, acc, m0 + wm * WM, n0 + wn * WN, lane);
+}
+
 // Skinny GEMM (M <= 16*FM <= 48, the decode shapes): bandwidth-bound on the
 // weight stream. A 512-thread workgroup owns 16 weight rows (output columns
 // n0..n0+15) over the whole K; its 8 waves split the K-blocks into
@@ -901,6 +1111,9 @@ Plan make_plan(int64_t M, int64_t N, int64_t K) {
   if (t < cus)
     while (t * splits < 2 * cus && KB / (splits * 2) >= 4) splits *= 2;
   p.kb_per_split = (KB + splits - 1) / splits;
+  // Split sizes in whole scale half-windows (multiples of 4 K-blocks) keep
+  // the pipelined kernels usable.
+  if (splits > 1 && KB % 4 == 0) p.kb_per_split = (p.kb_per_split + 3) / 4 * 4;
   p.splits = (KB + p.kb_per_split - 1) / p.kb_per_split;
   if (p.splits < 1) p.splits = 1;
   return p;
@@ -913,12 +1126,12 @@ bool mfma_path_ok(const void* A, int64_t lda, const void* B, int64_t ldb, int64_
          M < (int64_t(1) << 30) && N < (int64_t(1) << 30) && K < (int64_t(1) << 30);
 }
 
-// Preconditions of gemm_pipe256_kernel: scale windows (As, Bs contiguous in
-// K, 16-byte aligned rows, K-block counts and split sizes multiples of 4) and
-// 32-bit DMA offsets within a 256-row tile. FP8B_PIPE256=0 turns it off.
-bool pipe256_ok(const GemmArgs& a, const Plan& p) {
+// Preconditions of the pipelined kernels: scale windows (As, Bs contiguous
+// in K, 16-byte aligned rows, K-block counts and split sizes multiples of 4)
+// and 32-bit DMA offsets within a 256-row tile. FP8B_PIPE=0 turns them off.
+bool pipe_ok(const GemmArgs& a, const Plan& p) {
   static const bool enabled = [] {
-    const char* e = getenv("FP8B_PIPE256");
+    const char* e = getenv("FP8B_PIPE");
     return !(e && e[0] == '0');
   }();
   if (!enabled) return false;
@@ -1025,7 +1238,7 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
       break;
     }
     case CFG_256x256: {
-      if (pipe256_ok(a, p)) {
+      if (pipe_ok(a, p)) {
         dim3 grid(a.tiles_m * a.tiles_n, 1, p.splits);
         gemm_pipe256_kernel<<<grid, 512, 0, st>>>(a);
       } else {
@@ -1033,7 +1246,15 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
       }
       break;
     }
-    case CFG_128x128: launch_cfg<128, 128, 64, 64>(a, p.splits, st); break;
+    case CFG_128x128: {
+      if (pipe_ok(a, p)) {
+        dim3 grid(a.tiles_m * a.tiles_n, 1, p.splits);
+        gemm_pipe128_kernel<64, 32><<<grid, 512, 0, st>>>(a);
+      } else {
+        launch_cfg<128, 128, 64, 64>(a, p.splits, st);
+      }
+      break;
+    }
     case CFG_64x128: launch_cfg<64, 128, 32, 64>(a, p.splits, st); break;
     default: launch_cfg<32, 128, 32, 32>(a, p.splits, st); break;
   }

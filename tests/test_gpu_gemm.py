@@ -206,6 +206,25 @@ def test_gemm_large_tile_kernels(M, N, K, dev):
                                rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("M,N,K", [(2048, 2048, 4096), (1000, 3000, 3072), (130, 4096, 14336),
+                                   (3001, 4096, 14336), (200, 640, 1536)])
+def test_gemm_mid_tile_kernels(M, N, K, dev):
+    """Grids below one 256x256 tile per CU: 128x128 tiles with and without
+    split-K (split sizes rounded to whole half-windows of 4 K-blocks),
+    ragged M and N. Every row against torch's fp32 dequant-matmul, a sample
+    of rows against the oracle."""
+    print(f"gemm mid-tile M={M} N={N} K={K}", flush=True)
+    A, B, As, Bs = _operands(M, N, K, seed=K + N)
+    Ad, Bd, Asd, Bsd = A.to(dev), B.to(dev), As.to(dev), Bs.to(dev)
+    out = fp8.w8a8_block_fp8_matmul(Ad, Bd, Asd, Bsd, [128, 128], torch.bfloat16)
+    _full_check(out, Ad, Bd, Asd, Bsd)
+    rows = torch.tensor([0, M // 2, M - 1])
+    ref = oracle.block_gemm(_u8(A[rows]), _u8(B), As[rows].numpy(), Bs.numpy())
+    torch.testing.assert_close(out[rows.to(dev)].float().cpu(),
+                               torch.from_numpy(ref).to(torch.bfloat16).float(),
+                               rtol=RTOL, atol=ATOL)
+
+
 def test_gemm_large_tile_exact_and_fp32(dev):
     """Pipelined kernel with small-integer operands and unit scales (exact
     result), fp32 output; and with column-major As (two-stage fallback)."""
