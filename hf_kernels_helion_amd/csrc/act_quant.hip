@@ -19,6 +19,19 @@
 
 namespace fp8b {
 
+// x / s rounded to nearest even, for a group scale s > 0 (normal, finite)
+// and |x| <= 448 s, given recip = RN(1/s) from one IEEE division per group.
+// Markstein's theorem: q0 = RN(x * recip) is within one ulp of x/s, so
+// r = x - q0*s is exact in one FMA and RN(q0 + r*recip) = RN(x/s). The sign
+// is copied from x so that -0 stays -0 (q0 + r*recip would give +0). Below
+// the fp32 normal range the quotient may differ from IEEE division in its
+// last bits, but every such value converts to a signed fp8 zero.
+__device__ __forceinline__ float div_by_scale(float x, float s, float recip) {
+  const float q0 = x * recip;
+  const float r = fmaf(-q0, s, x);
+  return __builtin_copysignf(fmaf(r, recip, q0), x);
+}
+
 // Quantise 8 values held by one lane of a 16-lane group of 128.
 // `mag` is the max over this lane's 8 bf16 magnitude patterns.
 __device__ __forceinline__ void quant_row16_8(const float v[8], uint32_t mag,
@@ -28,9 +41,10 @@ __device__ __forceinline__ void quant_row16_8(const float v[8], uint32_t mag,
   if (gmag < 0x7F80u) {
     const float amax = fmaxf(bf16_to_f32(gmag), kAmaxFloor);
     scale = amax / kFp8Max;
+    const float recip = 1.0f / scale;
     float y[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = v[i] / scale;
+    for (int i = 0; i < 8; ++i) y[i] = div_by_scale(v[i], scale, recip);
     int p0 = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
     p0 = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], p0, true);
     int p1 = __builtin_amdgcn_cvt_pk_fp8_f32(y[4], y[5], 0, false);
