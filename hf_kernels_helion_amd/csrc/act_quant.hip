@@ -84,8 +84,9 @@ __device__ __forceinline__ uint32_t unpack_bf16x8(const v4i raw, float v[8]) {
 // aligned rows of q. 16 lanes per group; each 16-lane row handles UNROLL
 // groups spaced one block-stride apart and issues all their loads before
 // converting any of them, so a wave keeps UNROLL KiB of reads in flight.
-constexpr int kQuantUnroll = 4;
-
+// Small inputs (decode: a few rows) use UNROLL = 1 so that the groups spread
+// over as many CUs as possible and the kernel is one load latency long.
+template <int kQuantUnroll>
 __global__ void __launch_bounds__(256)
 act_quant_g128_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                       uint8_t* __restrict__ q, int64_t ldq,
@@ -300,10 +301,17 @@ extern "C" int fp8b_act_quant(const void* x, int64_t ldx, void* q, int64_t ldq,
                     aligned(x, 16) && aligned(q, 8) && M * gpr < (int64_t(1) << 31);
   if (fast) {
     const uint32_t groups = (uint32_t)(M * gpr);
-    const uint32_t per_block = 16u * kQuantUnroll;
-    const uint32_t blocks = (groups + per_block - 1) / per_block;
-    act_quant_g128_kernel<<<blocks, 256, 0, st>>>((const uint16_t*)x, ldx, (uint8_t*)q, ldq, s,
-                                                  s_stride_m, s_stride_g, groups, (uint32_t)gpr);
+    if (groups < 16u * 1024u) {
+      const uint32_t blocks = (groups + 15u) / 16u;
+      act_quant_g128_kernel<1><<<blocks, 256, 0, st>>>((const uint16_t*)x, ldx, (uint8_t*)q, ldq,
+                                                       s, s_stride_m, s_stride_g, groups,
+                                                       (uint32_t)gpr);
+    } else {
+      const uint32_t blocks = (groups + 63u) / 64u;
+      act_quant_g128_kernel<4><<<blocks, 256, 0, st>>>((const uint16_t*)x, ldx, (uint8_t*)q, ldq,
+                                                       s, s_stride_m, s_stride_g, groups,
+                                                       (uint32_t)gpr);
+    }
   } else {
     const int64_t groups = M * gpr;
     act_quant_generic_kernel<<<(unsigned)((groups + 63) / 64), 64, 0, st>>>(

@@ -372,6 +372,10 @@ __device__ __forceinline__ void dma16_ptr(const void* g, uint32_t lds) {
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                :: "v"(g), "{m0}"(lds) : "memory");
 }
+__device__ __forceinline__ void dma4_ptr(const void* g, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off"
+               :: "v"(g), "{m0}"(lds) : "memory");
+}
 __device__ __forceinline__ uint32_t lds_u32(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
@@ -819,6 +823,137 @@ __global__ void __launch_bounds__((128 / WM) * (128 / WN) * 64) gemm_pipe128_ker
   epilogue16<WM, WN>(a, smem + wid * WM * EPI_PITCH, acc, m0 + wm * WM, n0 + wn * WN, lane);
 }
 
+// ---------------------------------------------------------------------------
+// Decode GEMM (M <= 16*FM <= 48): bound by the weight stream from HBM. A
+// 512-thread workgroup owns 128 weight rows (output columns n0..n0+127) and a
+// K-range of kb_per_split K-blocks; grid.z splits K so that the grid covers
+// the CUs (partials go to the workspace and splitk_reduce_kernel sums them
+// in split order). Every K-block stages 128 weight rows and the 16*FM
+// activation rows once for all 8 waves (a wave owns 16 weight rows), so the
+// activations cost 16*FM/128 of the weight bytes in L2->LDS traffic. NS LDS
+// stages keep NS-1 K-blocks of DMA in flight; the stage of K-block kb-1 is
+// refilled right after the barrier that opens K-block kb. Scales arrive per
+// window of 8 K-blocks by 4-byte DMA (any As/Bs strides): slot-major, 32
+// activation rows per slot, and the 8 weight-block scales of the window.
+// ---------------------------------------------------------------------------
+template <int FM>
+__global__ void __launch_bounds__(512) gemm_decode_kernel(GemmArgs a) {
+  constexpr int NW = 8, BN = 128, AR = 16 * FM;  // activation rows staged
+  constexpr int ROWS = BN + AR;
+  constexpr int STAGE = ROWS * 128;
+  constexpr int NS = 4;  // measured: deeper rings only lengthen the start-up burst
+  constexpr int WIN_SA = 8 * 32 * 4 * ((FM + 1) / 2);  // 8 slots x 32 rows (x2 for FM=3)
+  constexpr int WIN = WIN_SA + 256;
+  constexpr int SW_OFF = NS * STAGE;
+  constexpr int SMEM = SW_OFF + 2 * WIN;
+  static_assert(SMEM <= 160 * 1024, "LDS budget");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
+
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n0 = blockIdx.x * BN;
+  const int split = blockIdx.z;
+  const int kb_begin = split * a.kb_per_split;
+  const int kb_end = min(kb_begin + a.kb_per_split, a.KB);
+  const int nkb = kb_end - kb_begin;
+
+  const uint32_t lds0 = lds_u32(smem);
+  const int r8 = lane >> 3;
+  const int c16 = ((lane & 7) ^ r8) * 16;
+  const uint8_t* b_base = a.B + (int64_t)n0 * a.ldb;
+  const int b_lim = a.N - 1 - n0, a_lim = a.M - 1;
+  // Wave w stages weight rows 16w..16w+15 (wave-loads w and w+8 of the
+  // stage); waves 0..2FM-1 also stage activation rows 8w..8w+7.
+  auto issue_kb = [&](int kb) {
+    const int stage = (kb - kb_begin) % NS;
+    const uint32_t lds = lds0 + stage * STAGE;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int r = (wid * 2 + h) * 8 + r8;
+      const uint32_t voff = (uint32_t)min(r, b_lim) * (uint32_t)a.ldb + c16;
+      dma16_soff(voff, b_base + (int64_t)kb * 128, lds + (wid * 2 + h) * 1024);
+    }
+    if (wid < 2 * FM) {
+      const uint32_t voff = (uint32_t)min(wid * 8 + r8, a_lim) * (uint32_t)a.lda + c16;
+      dma16_soff(voff, a.A + (int64_t)kb * 128, lds + (16 + wid) * 1024);
+    }
+  };
+  // Window from kb0: instruction j (wave j) brings slots 2j, 2j+1 for 32
+  // activation rows (lane i: row i & 31, slot 2j + (i >> 5)); wave 4 (and 5
+  // for rows 32..47) likewise; the last wave brings the 8 weight-block
+  // scales. K-blocks past kb_end repeat kb_end - 1.
+  auto issue_win = [&](int kb0) {
+    const int wbuf = ((kb0 - kb_begin) >> 3) & 1;
+    const uint32_t lb = lds0 + SW_OFF + wbuf * WIN;
+    constexpr int SA_INS = 4 * ((FM + 1) / 2);
+    if (wid < SA_INS) {
+      const int j = wid & 3, rb = (wid >> 2) * 32;
+      const int kb = min(kb0 + 2 * j + (lane >> 5), kb_end - 1);
+      const int m = min(rb + (lane & 31), a_lim);
+      dma4_ptr(a.As + (int64_t)m * a.as_sm + (int64_t)kb * a.as_sk, lb + wid * 256);
+    }
+    if (wid == NW - 1 && lane < 8) {
+      const int kb = min(kb0 + lane, kb_end - 1);
+      dma4_ptr(a.Bs + (int64_t)(n0 >> 7) * a.bs_sn + (int64_t)kb * a.bs_sk, lb + WIN_SA);
+    }
+  };
+
+  // Fragment offsets: this wave's 16 weight rows and the activation rows.
+  const int r7 = lane & 7, g2 = 2 * (lane >> 4);
+  const int slo = (g2 ^ r7) << 4, shi = ((g2 + 1) ^ r7) << 4;
+  const int w_off = (wid * 16 + (lane & 15)) * 128;
+  const int x_off = (BN + (lane & 15)) * 128;
+
+  v4f acc[FM];
+#pragma unroll
+  for (int f = 0; f < FM; ++f) acc[f] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  auto issue_next = [&](int kb) {
+    if (((kb - kb_begin) & 7) == 0) issue_win(kb);
+    issue_kb(kb);
+  };
+  for (int k = 0; k < NS - 1 && k < nkb; ++k) issue_next(kb_begin + k);
+
+  for (int kb = kb_begin; kb < kb_end; ++kb) {
+    const int rel = kb - kb_begin;
+    // DMAs this wave issued after K-block kb's: those of kb+1..kb+NS-2 that
+    // exist, at least two instructions each.
+    switch (min(NS - 2, kb_end - 1 - kb)) {
+      case 5: wait_vmcnt<10>(); break;
+      case 4: wait_vmcnt<8>(); break;
+      case 3: wait_vmcnt<6>(); break;
+      case 2: wait_vmcnt<4>(); break;
+      case 1: wait_vmcnt<2>(); break;
+      default: wait_vmcnt<0>(); break;
+    }
+    __syncthreads();
+    if (kb + NS - 1 < kb_end) issue_next(kb + NS - 1);
+    const uint8_t* st = smem + (rel % NS) * STAGE;
+    const uint8_t* win = smem + SW_OFF + ((rel >> 3) & 1) * WIN;
+    const int slot = rel & 7;
+    const float sb = *reinterpret_cast<const float*>(win + WIN_SA + slot * 4);
+    const v8i w = lds_frag2(st + w_off, slo, shi);
+#pragma unroll
+    for (int f = 0; f < FM; ++f) {
+      const v8i x = lds_frag2(st + x_off + f * 2048, slo, shi);
+      const int m = f * 16 + (lane & 15);
+      const float sa = *reinterpret_cast<const float*>(
+          win + (m >> 5) * 1024 + slot * 128 + (m & 31) * 4);
+      const v4f t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+          w, x, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
+      const float sc = sa * sb;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[f][r] = fmaf(t[r], sc, acc[f][r]);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  const bool to_ws = gridDim.z > 1;
+#pragma unroll
+  for (int f = 0; f < FM; ++f)
+    store4(a, f * 16 + (lane & 15), n0 + wid * 16 + 4 * (lane >> 4), acc[f], to_ws, split);
+}
+
 // Skinny GEMM (M <= 16*FM <= 48, the decode shapes): bandwidth-bound on the
 // weight stream. A 512-thread workgroup owns 16 weight rows (output columns
 // n0..n0+15) over the whole K; its 8 waves split the K-blocks into
@@ -930,7 +1065,9 @@ __global__ void __launch_bounds__(512) gemm_skinny_kernel(GemmArgs a) {
   }
 }
 
-// Sum split-K partials in split order and convert: 4 outputs per thread.
+// Sum split-K partials in split order and convert: 4 outputs per thread. The
+// partial loads go out eight splits at a time before any is added, so the
+// kernel costs about one memory latency per eight splits.
 __global__ void __launch_bounds__(256)
 splitk_reduce_kernel(GemmArgs a, int splits) {
   const int64_t quads_per_row = (a.N + 3) / 4;
@@ -941,14 +1078,23 @@ splitk_reduce_kernel(GemmArgs a, int splits) {
   v4f s = {0.f, 0.f, 0.f, 0.f};
   const int64_t plane = (int64_t)a.M * a.N;
   const float* p = a.ws + (int64_t)m * a.N + n;
-  for (int z = 0; z < splits; ++z) {
-    v4f v;
-    if (n + 3 < a.N && a.vec_store) {
-      v = *reinterpret_cast<const v4f*>(p + z * plane);
-    } else {
-      for (int r = 0; r < 4; ++r) v[r] = (n + r < a.N) ? p[z * plane + r] : 0.f;
+  const bool vec = n + 3 < a.N && a.vec_store;
+  for (int z0 = 0; z0 < splits; z0 += 8) {
+    v4f v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int z = z0 + u;
+      if (z < splits) {
+        if (vec) {
+          v[u] = *reinterpret_cast<const v4f*>(p + z * plane);
+        } else {
+          for (int r = 0; r < 4; ++r) v[u][r] = (n + r < a.N) ? p[z * plane + r] : 0.f;
+        }
+      }
     }
-    s += v;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (z0 + u < splits) s += v[u];
   }
   store4(a, m, n, s, false, 0);
 }
@@ -1041,6 +1187,7 @@ enum TileCfg {
   CFG_64x128 = 2,
   CFG_32x128 = 3,
   CFG_SKINNY = 4,
+  CFG_DECODE = 5,
   CFG_COUNT
 };
 
@@ -1068,9 +1215,20 @@ int device_cu_count() {
   return cus;
 }
 
+// M <= 48 runs gemm_decode_kernel unless FP8B_DECODE=0 (then the skinny
+// kernel, for A/B measurements).
+bool use_decode_kernel() {
+  static const bool v = [] {
+    const char* e = getenv("FP8B_DECODE");
+    return !(e && e[0] == '0');
+  }();
+  return v;
+}
+
 // Largest M served by the skinny kernel (at most 48: three 16-row activation
-// fragments per K-block slot). FP8B_SKINNY_MAX_M overrides it for A/B
-// measurements (0 sends every shape to the tiled path).
+// fragments per K-block slot) when FP8B_DECODE=0. FP8B_SKINNY_MAX_M
+// overrides it for A/B measurements (with FP8B_DECODE=0, 0 sends every shape
+// to the tiled path).
 int skinny_max_m() {
   static const int v = [] {
     const char* e = getenv("FP8B_SKINNY_MAX_M");
@@ -1086,11 +1244,22 @@ Plan make_plan(int64_t M, int64_t N, int64_t K) {
   const int cus = device_cu_count();
   Plan p;
   auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-  if (M <= skinny_max_m()) {
+  if (M <= skinny_max_m() && !use_decode_kernel()) {
     // Skinny path: 16 output columns per workgroup, K split inside it.
     p.cfg = CFG_SKINNY; p.bm = (int)(((M + 15) / 16) * 16); p.bn = 16;
     p.splits = 1;
     p.kb_per_split = KB;
+    return p;
+  }
+  if (M <= 48) {
+    // Decode path: 128 output columns per workgroup; split K until the grid
+    // covers the CUs.
+    p.cfg = CFG_DECODE; p.bm = (int)(((M + 15) / 16) * 16); p.bn = 128;
+    const int64_t t = (N + 127) / 128;
+    int splits = t < cus ? (int)((cus + t - 1) / t) : 1;
+    splits = std::max(1, std::min(splits, KB));
+    p.kb_per_split = (KB + splits - 1) / splits;
+    p.splits = (KB + p.kb_per_split - 1) / p.kb_per_split;
     return p;
   }
   if (M <= 32) {
@@ -1235,6 +1404,14 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
       if (fm <= 1) gemm_skinny_kernel<1><<<grid, 512, 0, st>>>(a);
       else if (fm == 2) gemm_skinny_kernel<2><<<grid, 512, 0, st>>>(a);
       else gemm_skinny_kernel<3><<<grid, 512, 0, st>>>(a);
+      break;
+    }
+    case CFG_DECODE: {
+      const dim3 grid((unsigned)((N + 127) / 128), 1, (unsigned)p.splits);
+      const int fm = (int)((M + 15) / 16);
+      if (fm <= 1) gemm_decode_kernel<1><<<grid, 512, 0, st>>>(a);
+      else if (fm == 2) gemm_decode_kernel<2><<<grid, 512, 0, st>>>(a);
+      else gemm_decode_kernel<3><<<grid, 512, 0, st>>>(a);
       break;
     }
     case CFG_256x256: {
