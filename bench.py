@@ -327,14 +327,21 @@ def run_only(what, steps, warmup, torch, fp8, synthetic, dev):
               "small": (512, 512, 2048), "decode": (32, 4096, 14336)}
     if what in shapes:
         M, N, K = shapes[what]
-        W, Bs = _gpu_weights(N, K, 40, dev, torch, synthetic)
         x = _gpu_acts(M, K, 41, dev, torch)
         q, s = fp8.act_quant(x, 128)
         if what == "decode":
+            # five weight copies (294 MB) rotate past the 256 MB MALL, as in
+            # the bench leg
+            ws_ = [_gpu_weights(N, K, 20 + i, dev, torch, synthetic) for i in range(5)]
+            it = [0]
+
             def fn():
+                i = it[0] = (it[0] + 1) % 5
                 q2, s2 = fp8.act_quant(x, 128)
-                return fp8.w8a8_block_fp8_matmul(q2, W, s2, Bs, [128, 128], torch.bfloat16)
+                return fp8.w8a8_block_fp8_matmul(q2, ws_[i][0], s2, ws_[i][1], [128, 128],
+                                                 torch.bfloat16)
         else:
+            W, Bs = _gpu_weights(N, K, 40, dev, torch, synthetic)
             fn = lambda: fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [128, 128], torch.bfloat16)
     elif what == "copy":
         # calibration for the rocprofv3 FETCH_SIZE/WRITE_SIZE counters: a
@@ -343,8 +350,14 @@ def run_only(what, steps, warmup, torch, fp8, synthetic, dev):
         dst = torch.empty_like(src)
         fn = lambda: dst.copy_(src)
     elif what == "act_quant":
-        x = _gpu_acts(4096, 8192, 10, dev, torch)
-        fn = lambda: fp8.act_quant(x, 128)
+        # four input sets (384 MB with outputs) rotate past the MALL, as in
+        # the bench leg
+        xs = [_gpu_acts(4096, 8192, 10 + i, dev, torch) for i in range(4)]
+        it = [0]
+
+        def fn():
+            i = it[0] = (it[0] + 1) % 4
+            return fp8.act_quant(xs[i], 128)
     elif what == "mlp":
         M, H, I = 3001, 4096, 14336
         w13, s13 = _gpu_weights(2 * I, H, 50, dev, torch, synthetic)
