@@ -45,7 +45,8 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--only", default=None,
-                   help="profile helper: run only one workload (gemm|act_quant|decode|mlp|medium|small|copy)"
+                   help="profile helper: run only one workload "
+                        "(gemm|act_quant|decode|decode_fused|mlp|medium|small|copy)"
                         " for --steps steps and exit without JSON")
     return p.parse_args()
 
@@ -265,35 +266,48 @@ def secondary(torch, fp8, synthetic, dev):
 
     # The same five steps captured once in a HIP graph (how a decode loop is
     # served): replays cost GPU time only, without per-op host dispatch.
-    def dec_all():
+    # Two forms: act_quant then the GEMM (two ops), and the fused op that
+    # quantises inside the GEMM kernel (same result bits).
+    def dec_two_op():
         outs = []
         for i in range(5):
             q, s = fp8.act_quant(xd, 128)
             outs.append(fp8.w8a8_block_fp8_matmul(q, ws_[i][0], s, ws_[i][1], [128, 128],
                                                   torch.bfloat16))
         return outs
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        for _ in range(3):
-            dec_all()
-    torch.cuda.current_stream().wait_stream(side)
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        gouts = dec_all()
-    for _ in range(2):  # every replay equals the eager result
-        graph.replay()
-        eager = dec_all()
-        torch.cuda.synchronize()
-        assert all(torch.equal(x_, y_) for x_, y_ in zip(gouts, eager)), "graph replay differs"
-    ms = time_events(graph.replay, 20, 5, torch) / 5
+
+    def dec_fused():
+        return [fp8.act_quant_w8a8_block_fp8_matmul(xd, ws_[i][0], ws_[i][1], [128, 128],
+                                                    torch.bfloat16) for i in range(5)]
+
+    def graph_time(fn):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                fn()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            gouts = fn()
+        for _ in range(2):  # every replay equals the eager two-op result
+            graph.replay()
+            eager = dec_two_op()
+            torch.cuda.synchronize()
+            assert all(torch.equal(x_, y_) for x_, y_ in zip(gouts, eager)), "replay differs"
+        t = time_events(graph.replay, 20, 5, torch) / 5
+        del graph, gouts
+        return t
+    ms = graph_time(dec_two_op)
+    ms_op = graph_time(dec_fused)
     byt = 2.0 * M * K + N * K + 4.0 * (N // 128) * (K // 128) + 2.0 * M * N
     res["decode_32x4096x14336"] = {"us": round(ms * 1e3, 2), "GB/s": round(byt / ms / 1e6, 1),
                                    "pct_hbm_peak": round(100 * byt / ms / 1e6 / PEAK_HBM_GBS, 1),
+                                   "act_quant_matmul_op_us": round(ms_op * 1e3, 2),
                                    "eager_us": round(ms_eager * 1e3, 2),
-                                   "includes": "act_quant + gemm (+ split-K reduce), HIP-graph "
-                                               "replay of 5 steps over 5 weight copies"}
-    del graph, gouts
+                                   "includes": "bf16 activations in: act_quant + GEMM "
+                                               "(+ split-K reduce); HIP-graph replay of 5 steps "
+                                               "over 5 weight copies"}
     log(f"decode: {res['decode_32x4096x14336']}")
     del ws_
 
@@ -324,12 +338,13 @@ def secondary(torch, fp8, synthetic, dev):
 def run_only(what, steps, warmup, torch, fp8, synthetic, dev):
     """Run one workload for profiling (rocprofv3) without the other legs."""
     shapes = {"gemm": (4096, 4096, 8192), "medium": (2048, 2048, 4096),
-              "small": (512, 512, 2048), "decode": (32, 4096, 14336)}
+              "small": (512, 512, 2048), "decode": (32, 4096, 14336),
+              "decode_fused": (32, 4096, 14336)}
     if what in shapes:
         M, N, K = shapes[what]
         x = _gpu_acts(M, K, 41, dev, torch)
         q, s = fp8.act_quant(x, 128)
-        if what == "decode":
+        if what in ("decode", "decode_fused"):
             # five weight copies (294 MB) rotate past the 256 MB MALL, as in
             # the bench leg
             ws_ = [_gpu_weights(N, K, 20 + i, dev, torch, synthetic) for i in range(5)]
@@ -337,6 +352,9 @@ def run_only(what, steps, warmup, torch, fp8, synthetic, dev):
 
             def fn():
                 i = it[0] = (it[0] + 1) % 5
+                if what == "decode_fused":
+                    return fp8.act_quant_w8a8_block_fp8_matmul(x, ws_[i][0], ws_[i][1],
+                                                               [128, 128], torch.bfloat16)
                 q2, s2 = fp8.act_quant(x, 128)
                 return fp8.w8a8_block_fp8_matmul(q2, ws_[i][0], s2, ws_[i][1], [128, 128],
                                                  torch.bfloat16)

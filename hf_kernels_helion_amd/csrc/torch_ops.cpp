@@ -9,6 +9,8 @@
 //   silu_and_mul(Tensor(a!) out, x) -> ()
 //       (schema of activation-helion/.../torch-ext/activation_helion/op.py:15-18)
 //   silu_and_mul_quant(x, block_size) -> (q, s)
+//   act_quant_matmul(x, B, Bs, block_n, block_k, ScalarType output_dtype) -> Tensor
+//       (act_quant then w8a8_block_fp8_matmul, one GEMM kernel for M <= 48)
 // Each op validates its tensors (TORCH_CHECK -> RuntimeError), allocates its
 // outputs and any split-K workspace from torch's caching allocator, and calls
 // one C-ABI entry point on torch's current HIP stream. CPU tensors raise: the
@@ -102,6 +104,46 @@ Tensor w8a8_block_fp8_matmul_dtype(const Tensor& A, const Tensor& B, const Tenso
   return matmul_impl(A, B, As, Bs, block_n, block_k, output_dtype);
 }
 
+Tensor act_quant_matmul(const Tensor& x, const Tensor& B, const Tensor& Bs, int64_t block_n,
+                        int64_t block_k, at::ScalarType output_dtype) {
+  check_gpu(x, "x");
+  check_gpu(B, "B");
+  check_gpu(Bs, "Bs");
+  TORCH_CHECK(x.dim() == 2 && B.dim() == 2, "x and B must be 2-D ([M,K] and [N,K])");
+  TORCH_CHECK(x.scalar_type() == at::kBFloat16, "x must be bfloat16, got ", x.scalar_type());
+  TORCH_CHECK(B.scalar_type() == at::kFloat8_e4m3fn, "B must be float8_e4m3fn, got ",
+              B.scalar_type());
+  TORCH_CHECK(Bs.scalar_type() == at::kFloat, "Bs must be float32, got ", Bs.scalar_type());
+  TORCH_CHECK(block_n == 128 && block_k == 128, "act_quant_matmul supports block_size "
+              "[128, 128] (1x128 activation groups), got [", block_n, ",", block_k, "]");
+  const int64_t M = x.size(0), K = x.size(1), N = B.size(0);
+  TORCH_CHECK(B.size(1) == K, "x is [M,K]=[", M, ",", K, "] but B is [N,K]=[", N, ",",
+              B.size(1), "]");
+  TORCH_CHECK(K % 128 == 0, "K must be a multiple of 128, got ", K);
+  const int64_t kb = K / 128, nb = (N + 127) / 128;
+  TORCH_CHECK(Bs.dim() == 2 && Bs.size(0) >= nb && Bs.size(1) >= kb,
+              "Bs must be [ceil(N/128), K/128] = [", nb, ",", kb, "], got ", Bs.sizes());
+  TORCH_CHECK(K <= 1 || (x.stride(1) == 1 && B.stride(1) == 1),
+              "x and B must have unit stride along K");
+  TORCH_CHECK(B.device() == x.device() && Bs.device() == x.device(),
+              "all tensors must be on one device");
+  const int code = out_code(output_dtype);
+  at::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+  Tensor out = at::empty({M, N}, x.options().dtype(output_dtype));
+  if (M == 0 || N == 0) return out;
+  const size_t ws_bytes = fp8b_act_quant_matmul_workspace_size(M, N, K);
+  Tensor ws;
+  if (ws_bytes) ws = at::empty({(int64_t)ws_bytes}, x.options().dtype(at::kByte));
+  const int64_t ldx = std::max<int64_t>(M > 1 ? x.stride(0) : K, K);
+  const int64_t ldb = std::max<int64_t>(N > 1 ? B.stride(0) : K, K);
+  const int st = fp8b_act_quant_matmul(
+      x.data_ptr(), ldx, B.data_ptr(), ldb, Bs.data_ptr<float>(), Bs.stride(0), Bs.stride(1),
+      out.data_ptr(), N, code, M, N, K, ws_bytes ? ws.data_ptr() : nullptr, ws_bytes,
+      current_stream(x));
+  check_status(st, "act_quant_matmul");
+  return out;
+}
+
 void check_group(int64_t g) {
   TORCH_CHECK(g == 32 || g == 64 || g == 128 || g == 256,
               "group size must be 32, 64, 128 or 256, got ", g);
@@ -192,6 +234,10 @@ Tensor matmul_dtype_cpu(const Tensor&, const Tensor&, const Tensor&, const Tenso
   no_cpu("w8a8_block_fp8_matmul_dtype");
 }
 std::tuple<Tensor, Tensor> act_quant_cpu(const Tensor&, int64_t) { no_cpu("act_quant"); }
+Tensor act_quant_matmul_cpu(const Tensor&, const Tensor&, const Tensor&, int64_t, int64_t,
+                            at::ScalarType) {
+  no_cpu("act_quant_matmul");
+}
 void silu_and_mul_cpu(Tensor&, const Tensor&) { no_cpu("silu_and_mul"); }
 std::tuple<Tensor, Tensor> silu_and_mul_quant_cpu(const Tensor&, int64_t) {
   no_cpu("silu_and_mul_quant");
@@ -207,6 +253,8 @@ TORCH_LIBRARY(_finegrained_fp8_helion_rocm_mi355x, m) {
   m.def("act_quant(Tensor x, int block_size) -> (Tensor, Tensor)");
   m.def("silu_and_mul(Tensor(a!) out, Tensor x) -> ()");
   m.def("silu_and_mul_quant(Tensor x, int block_size) -> (Tensor, Tensor)");
+  m.def("act_quant_matmul(Tensor x, Tensor B, Tensor Bs, int block_n, int block_k, "
+        "ScalarType output_dtype) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(_finegrained_fp8_helion_rocm_mi355x, CUDA, m) {
@@ -215,6 +263,7 @@ TORCH_LIBRARY_IMPL(_finegrained_fp8_helion_rocm_mi355x, CUDA, m) {
   m.impl("act_quant", &act_quant);
   m.impl("silu_and_mul", &silu_and_mul);
   m.impl("silu_and_mul_quant", &silu_and_mul_quant);
+  m.impl("act_quant_matmul", &act_quant_matmul);
 }
 
 TORCH_LIBRARY_IMPL(_finegrained_fp8_helion_rocm_mi355x, CPU, m) {
@@ -223,4 +272,5 @@ TORCH_LIBRARY_IMPL(_finegrained_fp8_helion_rocm_mi355x, CPU, m) {
   m.impl("act_quant", &act_quant_cpu);
   m.impl("silu_and_mul", &silu_and_mul_cpu);
   m.impl("silu_and_mul_quant", &silu_and_mul_quant_cpu);
+  m.impl("act_quant_matmul", &act_quant_matmul_cpu);
 }

@@ -59,8 +59,20 @@ def silu_and_mul_quant(x: torch.Tensor, block_size: int = 128):
     return ops.silu_and_mul_quant(x, int(block_size))
 
 
+def act_quant_w8a8_block_fp8_matmul(x: torch.Tensor, B: torch.Tensor, Bs: torch.Tensor,
+                                    block_size=(128, 128), output_dtype=torch.float32):
+    """w8a8_block_fp8_matmul(*act_quant(x, 128), B, Bs, block_size, output_dtype),
+    bit for bit, with the quantisation done inside the GEMM kernel for M <= 48
+    (decode). x: [M,K] bfloat16, K % 128 == 0; block_size must be [128, 128]."""
+    block_n, block_k = int(block_size[0]), int(block_size[1])
+    if output_dtype in _DIRECT_OUT:
+        return ops.act_quant_matmul(x, B, Bs, block_n, block_k, output_dtype)
+    return ops.act_quant_matmul(x, B, Bs, block_n, block_k, torch.float32).to(output_dtype)
+
+
 __all__ = [
     "w8a8_block_fp8_matmul",
+    "act_quant_w8a8_block_fp8_matmul",
     "act_quant",
     "per_token_group_quant_fp8",
     "silu_and_mul",

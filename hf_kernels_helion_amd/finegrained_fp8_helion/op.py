@@ -61,3 +61,8 @@ def _(x, block_size):
     groups = -(-d // block_size)
     return (x.new_empty((*x.shape[:-1], d), dtype=torch.float8_e4m3fn),
             x.new_empty((*x.shape[:-1], groups), dtype=torch.float32))
+
+
+@torch.library.register_fake(add_op_namespace_prefix("act_quant_matmul"))
+def _(x, B, Bs, block_n, block_k, output_dtype):
+    return x.new_empty((x.shape[0], B.shape[0]), dtype=output_dtype)

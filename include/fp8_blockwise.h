@@ -113,6 +113,32 @@ size_t fp8b_gemm_workspace_size(int64_t M, int64_t N, int64_t K,
                                 int64_t block_n, int64_t block_k);
 
 /*
+ * Act-quant fused with the block GEMM: C = w8a8(act_quant(x)) against B/Bs
+ * with block_n = block_k = 128, i.e. exactly fp8b_act_quant (group 128) into
+ * (q, s) followed by fp8b_w8a8_block_matmul(q, B, s, Bs), with the same
+ * result bits. No single counterpart in the reference: it composes the
+ * quantiser above with the Helion kernel of
+ * finegrained-fp8-helion/torch-ext/finegrained_fp8_helion/fp8.py:19-39 (the
+ * act-quant-into-the-GEMM step for small M). It quantises into the workspace
+ * and runs the GEMM; with FP8B_FUSED_QUANT=1 in the environment, M <= 48 with
+ * 16-byte aligned x rows instead runs one GEMM kernel that quantises x itself
+ * (measured slower on MI355X; kept for A/B).
+ * x : bf16 [M,K] row stride ldx (K % 128 == 0); B, Bs, C as in
+ * fp8b_w8a8_block_matmul. workspace: fp8b_act_quant_matmul_workspace_size()
+ * bytes, 256-byte aligned.
+ */
+int fp8b_act_quant_matmul(const void* x, int64_t ldx,
+                          const void* B, int64_t ldb,
+                          const float* Bs, int64_t bs_sn, int64_t bs_sk,
+                          void* C, int64_t ldc, int out_dtype,
+                          int64_t M, int64_t N, int64_t K,
+                          void* workspace, size_t workspace_bytes,
+                          void* stream);
+
+/* Bytes of device workspace fp8b_act_quant_matmul needs for these sizes. */
+size_t fp8b_act_quant_matmul_workspace_size(int64_t M, int64_t N, int64_t K);
+
+/*
  * Gated SiLU: out[m,j] = bf16( bf16(silu(fp32 x[m,j])) * x[m,d+j] ), j < d,
  * for bf16 x [M,2d] (row stride ldx) and out [M,d] (row stride ldo).
  * Replaces _silu_and_mul of

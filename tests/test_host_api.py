@@ -22,7 +22,7 @@ def test_namespace_follows_kernel_builder_scheme():
     assert _ops._OPS_NAME == "_finegrained_fp8_helion_rocm_mi355x"
     assert _ops.add_op_namespace_prefix("x") == "_finegrained_fp8_helion_rocm_mi355x::x"
     for name in ("w8a8_block_fp8_matmul", "w8a8_block_fp8_matmul_dtype", "act_quant",
-                 "silu_and_mul", "silu_and_mul_quant"):
+                 "silu_and_mul", "silu_and_mul_quant", "act_quant_matmul"):
         assert hasattr(_ops.ops, name)
 
 
@@ -37,6 +37,8 @@ def test_cpu_tensors_raise_not_fallback():
         fp8.w8a8_block_fp8_matmul(A, B, As, Bs, [128, 128], torch.bfloat16)
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         fp8.act_quant(torch.zeros(4, 256, dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        fp8.act_quant_w8a8_block_fp8_matmul(torch.zeros(4, 256, dtype=torch.bfloat16), B, Bs)
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         fp8.silu_and_mul(torch.empty(2, 8, dtype=torch.bfloat16),
                          torch.zeros(2, 16, dtype=torch.bfloat16))
@@ -56,6 +58,9 @@ def test_fake_impls_give_reference_shapes():
         assert s.shape == (3, 5, 3) and s.dtype == torch.float32
         q, s = _ops.ops.silu_and_mul_quant(torch.zeros(4, 512, dtype=torch.bfloat16), 128)
         assert q.shape == (4, 256) and s.shape == (4, 2)
+        out = _ops.ops.act_quant_matmul(torch.zeros(7, 384, dtype=torch.bfloat16), B, Bs, 128,
+                                        128, torch.bfloat16)
+        assert out.shape == (7, 200) and out.dtype == torch.bfloat16
 
 
 def test_op_schemas_match_reference():
