@@ -12,7 +12,8 @@ Prints ONE JSON line on stdout; progress goes to stderr. The line carries:
   cpu_baseline  the reference's PyTorch CPU dequantise-then-matmul path
                 (finegrained-fp8-helion/bench.py:11-14, restated in
                 oracle/torch_ref.py) on a row sample of the same workload;
-  secondary     act-quant, decode-shaped, medium, small and MLP-chain rows.
+  secondary     act-quant, decode-shaped, medium, small, weight-quantiser and MLP-chain
+                rows.
 """
 from __future__ import annotations
 
@@ -46,7 +47,7 @@ def parse():
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--only", default=None,
                    help="profile helper: run only one workload "
-                        "(gemm|act_quant|decode|decode_fused|mlp|medium|small|copy)"
+                        "(gemm|act_quant|decode|decode_fused|weight_quant|mlp|medium|small|copy)"
                         " for --steps steps and exit without JSON")
     return p.parse_args()
 
@@ -322,6 +323,24 @@ def secondary(torch, fp8, synthetic, dev):
                      "pct_fp8_peak": round(100 * tf / PEAK_FP8_TFLOPS, 1)}
         log(f"{name}: {res[name]}")
 
+    # offline weight-block quantiser, fp32 [4096, 14336] -> e4m3fn + scales;
+    # two inputs (470 MB) rotate past the MALL
+    N, K = 4096, 14336
+    wsrc = [torch.randn(N, K, device=dev) * 0.02 for _ in range(2)]
+    it[0] = 0
+
+    def wq():
+        i = it[0] = (it[0] + 1) % 2
+        return fp8.quantize_weight(wsrc[i])
+    ms = time_events(wq, 20, 5, torch)
+    byt = 4.0 * N * K + N * K + 4.0 * (N // 128) * (K // 128)
+    res["weight_quant_4096x14336_f32"] = {"us": round(ms * 1e3, 2),
+                                          "GB/s": round(byt / ms / 1e6, 1),
+                                          "pct_hbm_peak": round(100 * byt / ms / 1e6 /
+                                                                PEAK_HBM_GBS, 1)}
+    log(f"weight_quant: {res['weight_quant_4096x14336_f32']}")
+    del wsrc
+
     # MLP chain M=3001, H=4096, I=14336
     M, H, I = 3001, 4096, 14336
     w13, s13 = _gpu_weights(2 * I, H, 50, dev, torch, synthetic)
@@ -367,6 +386,13 @@ def run_only(what, steps, warmup, torch, fp8, synthetic, dev):
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
         fn = lambda: dst.copy_(src)
+    elif what == "weight_quant":
+        wsrc = [torch.randn(4096, 14336, device=dev) * 0.02 for _ in range(2)]
+        it = [0]
+
+        def fn():
+            i = it[0] = (it[0] + 1) % 2
+            return fp8.quantize_weight(wsrc[i])
     elif what == "act_quant":
         # four input sets (384 MB with outputs) rotate past the MALL, as in
         # the bench leg

@@ -47,6 +47,10 @@ SIGNATURES = {
          _i64, _i64, _i64, _vp, _sz, _vp],
     ),
     "fp8b_act_quant_matmul_workspace_size": (_sz, [_i64, _i64, _i64]),
+    "fp8b_weight_quant": (
+        ctypes.c_int,
+        [_vp, _i64, ctypes.c_int, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp],
+    ),
     "fp8b_silu_and_mul": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _i64, _vp]),
     "fp8b_silu_and_mul_quant": (
         ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _vp]),

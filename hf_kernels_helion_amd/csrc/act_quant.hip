@@ -319,3 +319,116 @@ extern "C" int fp8b_silu_and_mul_quant(const void* x, int64_t ldx, void* q, int6
   }
   return check_launch("fp8b_silu_and_mul_quant: kernel launch failed");
 }
+
+namespace fp8b {
+
+// 128x128 weight-block quantiser: one 256-thread workgroup per block. Wave w
+// handles block rows 32w..32w+31; for each row its 64 lanes read two
+// consecutive elements (coalesced 512 B of fp32 or 256 B of bf16 per row),
+// so a lane holds 64 values in registers and the block is read once.
+//   Bs[nb,kb] = max(amax_block, 1e-10) / 448 (IEEE), Wq = e4m3fn(W / Bs)
+// with IEEE division and the gfx950 OCP convert (RNE); elements past N or K
+// do not take part. NaN in a block propagates to its scale (as torch.amax
+// does) and every element of that block becomes the e4m3fn NaN 0x7F.
+template <typename T>
+__device__ __forceinline__ float load_w(const T* p);
+template <>
+__device__ __forceinline__ float load_w<float>(const float* p) { return *p; }
+template <>
+__device__ __forceinline__ float load_w<uint16_t>(const uint16_t* p) { return bf16_to_f32(*p); }
+
+template <typename T>
+__global__ void __launch_bounds__(256)
+weight_quant_block128_kernel(const T* __restrict__ W, int64_t ldw, uint8_t* __restrict__ q,
+                             int64_t ldq, float* __restrict__ s, int64_t s_sn, int64_t s_sk,
+                             int64_t N, int64_t K) {
+  const int nb = blockIdx.y, kb = blockIdx.x;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int64_t n0 = (int64_t)nb * 128 + wid * 32, k = (int64_t)kb * 128 + 2 * lane;
+  float v[32][2];
+  float amax = 0.f;
+  bool nan = false;
+#pragma unroll
+  for (int r = 0; r < 32; ++r) {
+    const int64_t n = n0 + r;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const bool in = n < N && k + e < K;
+      const float x = in ? load_w<T>(W + n * ldw + k + e) : 0.f;
+      v[r][e] = x;
+      nan |= x != x;
+      amax = fmaxf(amax, fabsf(x));
+    }
+  }
+  // Block max over the wave (DPP rows of 16, then the four rows) and the
+  // four waves.
+  uint32_t m = __float_as_uint(amax) | (nan ? 0x7FC00000u : 0u);
+  m = row16_max_u32(m);
+  m = max(m, (uint32_t)__builtin_amdgcn_readlane((int)m, 0));
+  m = max(m, (uint32_t)__builtin_amdgcn_readlane((int)m, 16));
+  m = max(m, (uint32_t)__builtin_amdgcn_readlane((int)m, 32));
+  m = max(m, (uint32_t)__builtin_amdgcn_readlane((int)m, 48));
+  __shared__ uint32_t wmax[4];
+  if (lane == 0) wmax[wid] = m;
+  __syncthreads();
+  m = max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
+  const bool block_nan = m > 0x7F800000u;
+  const float scale = block_nan ? __uint_as_float(0x7FC00000u)
+                                : fmaxf(__uint_as_float(m), kAmaxFloor) / kFp8Max;
+#pragma unroll
+  for (int r = 0; r < 32; ++r) {
+    const int64_t n = n0 + r;
+    if (n >= N) break;
+    uint32_t b;
+    if (block_nan) {
+      b = (uint32_t)kFp8NaN | ((uint32_t)kFp8NaN << 8);
+    } else {
+      b = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v[r][0] / scale, v[r][1] / scale, 0, false) &
+          0xFFFFu;
+    }
+    if (k + 1 < K) {
+      *reinterpret_cast<uint16_t*>(q + n * ldq + k) = (uint16_t)b;
+    } else if (k < K) {
+      q[n * ldq + k] = (uint8_t)b;
+    }
+  }
+  if (threadIdx.x == 0) s[(int64_t)nb * s_sn + (int64_t)kb * s_sk] = scale;
+}
+
+}  // namespace fp8b
+
+extern "C" int fp8b_weight_quant(const void* W, int64_t ldw, int w_dtype, void* q, int64_t ldq,
+                                 float* s, int64_t s_sn, int64_t s_sk, int64_t N, int64_t K,
+                                 void* stream) {
+  if (N < 0 || K < 0 || ldw < K || ldq < K) {
+    set_error("fp8b_weight_quant: bad dims (need N,K >= 0, ldw >= K, ldq >= K)");
+    return FP8B_ERR_DIMS;
+  }
+  if (w_dtype != FP8B_F32 && w_dtype != FP8B_BF16) {
+    set_error("fp8b_weight_quant: W must be FP8B_F32 or FP8B_BF16");
+    return FP8B_ERR_DTYPE;
+  }
+  if (N == 0 || K == 0) return FP8B_OK;
+  if (!W || !q || !s) {
+    set_error("fp8b_weight_quant: null pointer");
+    return FP8B_ERR_NULL;
+  }
+  if ((ldq % 2 != 0 || !aligned(q, 2)) ) {
+    set_error("fp8b_weight_quant: q rows must be 2-byte aligned (even ldq)");
+    return FP8B_ERR_ALIGN;
+  }
+  const int64_t NB = (N + 127) / 128, KB = (K + 127) / 128;
+  if (NB > 65535) {
+    set_error("fp8b_weight_quant: N too large");
+    return FP8B_ERR_DIMS;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)KB, (unsigned)NB);
+  if (w_dtype == FP8B_F32)
+    weight_quant_block128_kernel<float><<<grid, 256, 0, st>>>((const float*)W, ldw, (uint8_t*)q,
+                                                              ldq, s, s_sn, s_sk, N, K);
+  else
+    weight_quant_block128_kernel<uint16_t><<<grid, 256, 0, st>>>(
+        (const uint16_t*)W, ldw, (uint8_t*)q, ldq, s, s_sn, s_sk, N, K);
+  return check_launch("fp8b_weight_quant: kernel launch failed");
+}

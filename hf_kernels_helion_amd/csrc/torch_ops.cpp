@@ -10,6 +10,7 @@
 //       (schema of activation-helion/.../torch-ext/activation_helion/op.py:15-18)
 //   silu_and_mul_quant(x, block_size) -> (q, s)
 //   act_quant_matmul(x, B, Bs, block_n, block_k, ScalarType output_dtype) -> Tensor
+//   weight_quant(W, block_n, block_k) -> (Wq, Bs)   (128x128 blocks)
 //       (act_quant then w8a8_block_fp8_matmul, one GEMM kernel for M <= 48)
 // Each op validates its tensors (TORCH_CHECK -> RuntimeError), allocates its
 // outputs and any split-K workspace from torch's caching allocator, and calls
@@ -144,6 +145,30 @@ Tensor act_quant_matmul(const Tensor& x, const Tensor& B, const Tensor& Bs, int6
   return out;
 }
 
+std::tuple<Tensor, Tensor> weight_quant(const Tensor& W, int64_t block_n, int64_t block_k) {
+  check_gpu(W, "W");
+  TORCH_CHECK(W.dim() == 2, "W must be 2-D [N,K]");
+  TORCH_CHECK(W.scalar_type() == at::kFloat || W.scalar_type() == at::kBFloat16,
+              "W must be float32 or bfloat16, got ", W.scalar_type());
+  TORCH_CHECK(block_n == 128 && block_k == 128, "weight_quant supports 128x128 blocks, got [",
+              block_n, ",", block_k, "]");
+  const int64_t N = W.size(0), K = W.size(1);
+  TORCH_CHECK(K <= 1 || W.stride(1) == 1, "W must have unit stride along K");
+  at::hip::HIPGuardMasqueradingAsCUDA guard(W.device());
+  const int64_t kp = (K + 1) / 2 * 2;  // even row stride for the 2-byte stores
+  Tensor qbuf = at::empty({N, kp}, W.options().dtype(at::kFloat8_e4m3fn));
+  Tensor q = qbuf.narrow(1, 0, K);
+  Tensor s = at::empty({(N + 127) / 128, (K + 127) / 128}, W.options().dtype(at::kFloat));
+  if (N == 0 || K == 0) return {q, s};
+  const int64_t ldw = std::max<int64_t>(N > 1 ? W.stride(0) : K, K);
+  const int st = fp8b_weight_quant(W.data_ptr(), ldw,
+                                   W.scalar_type() == at::kFloat ? FP8B_F32 : FP8B_BF16,
+                                   q.data_ptr(), kp, s.data_ptr<float>(), s.stride(0),
+                                   s.stride(1), N, K, current_stream(W));
+  check_status(st, "weight_quant");
+  return {kp == K ? qbuf : q.contiguous(), s};
+}
+
 void check_group(int64_t g) {
   TORCH_CHECK(g == 32 || g == 64 || g == 128 || g == 256,
               "group size must be 32, 64, 128 or 256, got ", g);
@@ -238,6 +263,9 @@ Tensor act_quant_matmul_cpu(const Tensor&, const Tensor&, const Tensor&, int64_t
                             at::ScalarType) {
   no_cpu("act_quant_matmul");
 }
+std::tuple<Tensor, Tensor> weight_quant_cpu(const Tensor&, int64_t, int64_t) {
+  no_cpu("weight_quant");
+}
 void silu_and_mul_cpu(Tensor&, const Tensor&) { no_cpu("silu_and_mul"); }
 std::tuple<Tensor, Tensor> silu_and_mul_quant_cpu(const Tensor&, int64_t) {
   no_cpu("silu_and_mul_quant");
@@ -255,6 +283,7 @@ TORCH_LIBRARY(_finegrained_fp8_helion_rocm_mi355x, m) {
   m.def("silu_and_mul_quant(Tensor x, int block_size) -> (Tensor, Tensor)");
   m.def("act_quant_matmul(Tensor x, Tensor B, Tensor Bs, int block_n, int block_k, "
         "ScalarType output_dtype) -> Tensor");
+  m.def("weight_quant(Tensor W, int block_n, int block_k) -> (Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(_finegrained_fp8_helion_rocm_mi355x, CUDA, m) {
@@ -264,6 +293,7 @@ TORCH_LIBRARY_IMPL(_finegrained_fp8_helion_rocm_mi355x, CUDA, m) {
   m.impl("silu_and_mul", &silu_and_mul);
   m.impl("silu_and_mul_quant", &silu_and_mul_quant);
   m.impl("act_quant_matmul", &act_quant_matmul);
+  m.impl("weight_quant", &weight_quant);
 }
 
 TORCH_LIBRARY_IMPL(_finegrained_fp8_helion_rocm_mi355x, CPU, m) {
@@ -273,4 +303,5 @@ TORCH_LIBRARY_IMPL(_finegrained_fp8_helion_rocm_mi355x, CPU, m) {
   m.impl("silu_and_mul", &silu_and_mul_cpu);
   m.impl("silu_and_mul_quant", &silu_and_mul_quant_cpu);
   m.impl("act_quant_matmul", &act_quant_matmul_cpu);
+  m.impl("weight_quant", &weight_quant_cpu);
 }

@@ -70,8 +70,18 @@ def act_quant_w8a8_block_fp8_matmul(x: torch.Tensor, B: torch.Tensor, Bs: torch.
     return ops.act_quant_matmul(x, B, Bs, block_n, block_k, torch.float32).to(output_dtype)
 
 
+def quantize_weight(W: torch.Tensor, block_size=(128, 128)):
+    """Offline 128x128 block quantisation of a float32/bfloat16 weight [N,K]:
+    returns (Wq e4m3fn [N,K], Bs fp32 [ceil(N/128), ceil(K/128)]) with
+    Bs = max(block amax, 1e-10) / 448 and Wq = e4m3fn(W / Bs) -- the (B, Bs)
+    operands of w8a8_block_fp8_matmul and the weight/weight_scale_inv pair of
+    FP8 checkpoints."""
+    return ops.weight_quant(W, int(block_size[0]), int(block_size[1]))
+
+
 __all__ = [
     "w8a8_block_fp8_matmul",
+    "quantize_weight",
     "act_quant_w8a8_block_fp8_matmul",
     "act_quant",
     "per_token_group_quant_fp8",

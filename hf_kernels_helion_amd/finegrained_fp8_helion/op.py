@@ -66,3 +66,10 @@ def _(x, block_size):
 @torch.library.register_fake(add_op_namespace_prefix("act_quant_matmul"))
 def _(x, B, Bs, block_n, block_k, output_dtype):
     return x.new_empty((x.shape[0], B.shape[0]), dtype=output_dtype)
+
+
+@torch.library.register_fake(add_op_namespace_prefix("weight_quant"))
+def _(W, block_n, block_k):
+    N, K = W.shape
+    return (W.new_empty((N, K), dtype=torch.float8_e4m3fn),
+            W.new_empty((-(-N // block_n), -(-K // block_k)), dtype=torch.float32))

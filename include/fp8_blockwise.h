@@ -139,6 +139,23 @@ int fp8b_act_quant_matmul(const void* x, int64_t ldx,
 size_t fp8b_act_quant_matmul_workspace_size(int64_t M, int64_t N, int64_t K);
 
 /*
+ * Offline 128x128 weight-block quantiser (the format of FP8 checkpoints:
+ * e4m3fn weights with one fp32 scale per 128x128 block, "weight_scale_inv"):
+ *   Bs[nb,kb] = max(amax over block (nb,kb), 1e-10) / 448   (IEEE)
+ *   Wq[n,k]   = float8_e4m3fn(W[n,k] / Bs[n/128,k/128])     (IEEE, RNE)
+ * Elements past N or K do not take part; a NaN makes its block's scale NaN
+ * and every element of the block 0x7F. No counterpart in the reference: it
+ * produces the (B, Bs) operands its callers build with torch
+ * (scripts/rebench_llm.py:128-131 uses random fp8 instead).
+ * W : w_dtype (FP8B_F32 or FP8B_BF16) [N,K] row stride ldw;
+ * q : e4m3fn [N,K] row stride ldq (even); Bs (nb,kb) at s[nb*s_sn + kb*s_sk].
+ */
+int fp8b_weight_quant(const void* W, int64_t ldw, int w_dtype,
+                      void* q, int64_t ldq,
+                      float* s, int64_t s_sn, int64_t s_sk,
+                      int64_t N, int64_t K, void* stream);
+
+/*
  * Gated SiLU: out[m,j] = bf16( bf16(silu(fp32 x[m,j])) * x[m,d+j] ), j < d,
  * for bf16 x [M,2d] (row stride ldx) and out [M,d] (row stride ldo).
  * Replaces _silu_and_mul of

@@ -1,0 +1,62 @@
+"""GPU parity of the 128x128 weight-block quantiser (quantize_weight) with
+the torch quantiser the tests build operands with (synthetic.
+quantize_weight_blockwise), which the oracle pins
+(test_host_api.test_synthetic_weight_quantiser_matches_oracle): bit for bit
+on Wq and Bs, fp32 and bf16 inputs, ragged edges."""
+import pytest
+import torch
+
+from hf_kernels_helion_amd import finegrained_fp8_helion as fp8
+from hf_kernels_helion_amd.finegrained_fp8_helion import checkpoint, synthetic
+
+pytestmark = pytest.mark.gpu
+
+
+def _u8(t):
+    return t.cpu().contiguous().view(torch.uint8)
+
+
+@pytest.mark.parametrize("N,K", [(256, 384), (130, 260), (1, 129), (127, 1), (1024, 4096),
+                                 (300, 4097)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_weight_quant_matches_torch_quantiser(N, K, dtype, dev):
+    print(f"weight quant N={N} K={K} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(N + K)
+    W = (torch.randn(N, K, generator=g) * 0.02).to(dtype)
+    W[0, 0] = 0.5  # one large element in the first block
+    if N > 128 and K > 128:
+        W[128:256, 128:256] = 0  # an all-zero block: scale 1e-10/448, zeros
+    q, s = fp8.quantize_weight(W.to(dev))
+    rq, rs = synthetic.quantize_weight_blockwise(W.float())
+    assert q.dtype == torch.float8_e4m3fn and q.shape == (N, K)
+    assert torch.equal(_u8(q), _u8(rq))
+    assert torch.equal(s.cpu(), rs)
+
+
+def test_weight_quant_feeds_the_gemm(dev):
+    """Quantise on the GPU, multiply, compare with the fp32 dequant product."""
+    N, K, M = 512, 1024, 64
+    g = torch.Generator().manual_seed(9)
+    W = (torch.randn(N, K, generator=g) * 0.02).to(dev)
+    Wq, Bs = fp8.quantize_weight(W)
+    x = synthetic.activations(M, K, seed=10).to(dev)
+    q, s = fp8.act_quant(x, 128)
+    out = fp8.w8a8_block_fp8_matmul(q, Wq, s, Bs, [128, 128], torch.float32)
+    ref = (q.float() * s.repeat_interleave(128, 1)) @ (Wq.float() * Bs.repeat_interleave(
+        128, 0).repeat_interleave(128, 1)).T
+    torch.testing.assert_close(out, ref, rtol=1e-2, atol=1e-3)
+
+
+def test_quantize_state_dict_on_gpu(dev):
+    g = torch.Generator().manual_seed(2)
+    sd = {"a.weight": torch.randn(256, 512, generator=g) * 0.02,
+          "a.bias": torch.randn(256, generator=g),
+          "b.weight": (torch.randn(384, 256, generator=g) * 0.02).to(torch.bfloat16)}
+    out = checkpoint.quantize_state_dict(sd, device=dev)
+    assert set(out) == {"a.weight", "a.weight_scale_inv", "a.bias", "b.weight",
+                        "b.weight_scale_inv"}
+    for name in ("a.weight", "b.weight"):
+        rq, rs = synthetic.quantize_weight_blockwise(sd[name].float())
+        assert torch.equal(_u8(out[name]), _u8(rq))
+        assert torch.equal(out[checkpoint._scale_name(name)], rs)
+    assert set(checkpoint.fp8_linear_weights(out)) == {"a.weight", "b.weight"}

@@ -22,7 +22,7 @@ def test_namespace_follows_kernel_builder_scheme():
     assert _ops._OPS_NAME == "_finegrained_fp8_helion_rocm_mi355x"
     assert _ops.add_op_namespace_prefix("x") == "_finegrained_fp8_helion_rocm_mi355x::x"
     for name in ("w8a8_block_fp8_matmul", "w8a8_block_fp8_matmul_dtype", "act_quant",
-                 "silu_and_mul", "silu_and_mul_quant", "act_quant_matmul"):
+                 "silu_and_mul", "silu_and_mul_quant", "act_quant_matmul", "weight_quant"):
         assert hasattr(_ops.ops, name)
 
 
@@ -61,6 +61,8 @@ def test_fake_impls_give_reference_shapes():
         out = _ops.ops.act_quant_matmul(torch.zeros(7, 384, dtype=torch.bfloat16), B, Bs, 128,
                                         128, torch.bfloat16)
         assert out.shape == (7, 200) and out.dtype == torch.bfloat16
+        q, s = _ops.ops.weight_quant(torch.zeros(300, 260), 128, 128)
+        assert q.shape == (300, 260) and s.shape == (3, 3) and s.dtype == torch.float32
 
 
 def test_op_schemas_match_reference():
