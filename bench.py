@@ -47,7 +47,8 @@ def parse():
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--only", default=None,
                    help="profile helper: run only one workload "
-                        "(gemm|act_quant|decode|decode_fused|weight_quant|mlp|medium|small|copy)"
+                        "(gemm|act_quant|decode|decode_fused|weight_quant|mlp|medium|small|deep_gemm|"
+                        "deep_decode|copy)"
                         " for --steps steps and exit without JSON")
     return p.parse_args()
 
@@ -225,10 +226,10 @@ def main():
     print(json.dumps(result), flush=True)
 
 
-def _gpu_weights(N, K, seed, dev, torch, synthetic):
+def _gpu_weights(N, K, seed, dev, torch, synthetic, block_n=128):
     g = torch.Generator(device=dev).manual_seed(seed)
     W = torch.randn(N, K, generator=g, device=dev) * 0.02
-    return synthetic.quantize_weight_blockwise(W)
+    return synthetic.quantize_weight_blockwise(W, block_n, 128)
 
 
 def _gpu_acts(M, K, seed, dev, torch):
@@ -323,6 +324,29 @@ def secondary(torch, fp8, synthetic, dev):
                      "pct_fp8_peak": round(100 * tf / PEAK_FP8_TFLOPS, 1)}
         log(f"{name}: {res[name]}")
 
+    # deep-gemm layout (one weight scale per row and K-block, block_n = 1):
+    # the headline shape and the decode shape (5 weight copies, as above)
+    from hf_kernels_helion_amd import deep_gemm_helion as dg
+    for name, (M, N, K, copies) in {"deep_gemm_4096x4096x8192": (4096, 4096, 8192, 1),
+                                    "deep_gemm_32x4096x14336": (32, 4096, 14336, 5)}.items():
+        wl = [_gpu_weights(N, K, 60 + i, dev, torch, synthetic, block_n=1)
+              for i in range(copies)]
+        q, s = fp8.act_quant(_gpu_acts(M, K, 61, dev, torch), 128)
+        it[0] = 0
+
+        def dgf():
+            i = it[0] = (it[0] + 1) % copies
+            return dg.gemm_fp8_fp8_bf16_nt(q, wl[i][0], s, wl[i][1], 128)
+        ms = time_events(dgf, 50, 20, torch)
+        tf = 2.0 * M * N * K / ms / 1e9
+        byt = M * K + N * K + 4.0 * (M + N) * (K // 128) + 2.0 * M * N
+        res[name] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
+                     "pct_fp8_peak": round(100 * tf / PEAK_FP8_TFLOPS, 1),
+                     "GB/s": round(byt / ms / 1e6, 1),
+                     "pct_hbm_peak": round(100 * byt / ms / 1e6 / PEAK_HBM_GBS, 1)}
+        log(f"{name}: {res[name]}")
+        del wl
+
     # offline weight-block quantiser, fp32 [4096, 14336] -> e4m3fn + scales;
     # two inputs (470 MB) rotate past the MALL
     N, K = 4096, 14336
@@ -380,6 +404,16 @@ def run_only(what, steps, warmup, torch, fp8, synthetic, dev):
         else:
             W, Bs = _gpu_weights(N, K, 40, dev, torch, synthetic)
             fn = lambda: fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [128, 128], torch.bfloat16)
+    elif what in ("deep_gemm", "deep_decode"):
+        from hf_kernels_helion_amd import deep_gemm_helion as dg
+        M, N, K, copies = (4096, 4096, 8192, 1) if what == "deep_gemm" else (32, 4096, 14336, 5)
+        wl = [_gpu_weights(N, K, 60 + i, dev, torch, synthetic, block_n=1) for i in range(copies)]
+        q, s = fp8.act_quant(_gpu_acts(M, K, 61, dev, torch), 128)
+        it = [0]
+
+        def fn():
+            i = it[0] = (it[0] + 1) % copies
+            return dg.gemm_fp8_fp8_bf16_nt(q, wl[i][0], s, wl[i][1], 128)
     elif what == "copy":
         # calibration for the rocprofv3 FETCH_SIZE/WRITE_SIZE counters: a
         # plain 256 MiB device-to-device copy

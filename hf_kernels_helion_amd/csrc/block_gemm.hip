@@ -631,7 +631,7 @@ __global__ void __launch_bounds__(512) gemm_pipe256_kernel(GemmArgs a) {
 // into the other of two register sets; scale windows and asm DMA as in
 // gemm_pipe256_kernel.
 // ---------------------------------------------------------------------------
-template <int WM, int WN>
+template <int WM, int WN, bool PR>
 __global__ void __launch_bounds__((128 / WM) * (128 / WN) * 64) gemm_pipe128_kernel(GemmArgs a) {
   constexpr int BM = 128, BN = 128, NWN = BN / WN, NW = (BM / WM) * NWN;
   constexpr int FM = WM / 16, FN = WN / 16;
@@ -640,7 +640,9 @@ __global__ void __launch_bounds__((128 / WM) * (128 / WN) * 64) gemm_pipe128_ker
   constexpr int NSTAGE = 4;
   constexpr int STAGE = (BM + BN) * 128;   // 32 KiB
   constexpr int WIN_SA = BM * 32;
-  constexpr int WIN = WIN_SA + 256;
+  // PR (per-row weight scales, block_n = 1): Bs rows of the tile in the
+  // window as the As rows are (32 bytes per row: 8 K-blocks).
+  constexpr int WIN = WIN_SA + (PR ? BN * 32 : 256);
   constexpr int SW_OFF = NSTAGE * STAGE;
   constexpr int EPI_PITCH = WN * 2 + 16;
   constexpr int EPI = NW * WM * EPI_PITCH;
@@ -693,7 +695,15 @@ __global__ void __launch_bounds__((128 / WM) * (128 / WN) * 64) gemm_pipe128_ker
     const int kk = (kb0 + 4 * (lane & 1) < kb_end) ? kb0 : kb0 - 4 * (lane & 1);
     const uint32_t lb = lds0 + SW_OFF + wbuf * WIN;
     if (wid < BM / 32) dma16_ptr(saw_src + kk, lb + wid * 1024);
-    if (wid == NW - 1 && lane < 2) dma16_ptr(sbw_src + kk, lb + WIN_SA);
+    if constexpr (PR) {
+      if (wid >= NW - BN / 32) {
+        const int rw = (wid - (NW - BN / 32)) * 32 + (lane >> 1);
+        dma16_ptr(a.Bs + (int64_t)min(n0 + rw, a.N - 1) * a.bs_sn + 4 * (lane & 1) + kk,
+                  lb + WIN_SA + (wid - (NW - BN / 32)) * 1024);
+      }
+    } else {
+      if (wid == NW - 1 && lane < 2) dma16_ptr(sbw_src + kk, lb + WIN_SA);
+    }
   };
   // DMA of one K-block (and, at a window start, its scale window).
   auto issue_kb = [&](int kb) {
@@ -717,7 +727,13 @@ __global__ void __launch_bounds__((128 / WM) * (128 / WN) * 64) gemm_pipe128_ker
     for (int j = 0; j < FN; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
   v8i xf[2][FM], wf[2][FN];
   float sc[2][FM];
+  v4f sbr[2][PR ? FN : 1];  // PR: the weight-row scales of the lane's 4 columns
   v4f r1 = v4f{0.f, 0.f, 0.f, 0.f}, r2 = r1;
+  // Scale of output (row i, column group j, element e) in register set S.
+  auto scale_of = [&](int S, int i, int j, int e) {
+    if constexpr (PR) return sc[S][i] * sbr[S][j][e];
+    else return sc[S][i];
+  };
 
   // Fragments and scales of K-block kb into register set S (reads spread
   // over the caller's MFMAs by the caller's sched barriers).
@@ -729,10 +745,22 @@ __global__ void __launch_bounds__((128 / WM) * (128 / WN) * 64) gemm_pipe128_ker
   auto read_scales = [&](int kb, int S) {
     const int rel = kb - kb_begin;
     const int o = ((rel >> 3) & 1) * WIN + (rel & 7) * 4;
-    const float sb = *reinterpret_cast<const float*>(smem + sb_off + o);
+    if constexpr (PR) {
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
-      sc[S][i] = *reinterpret_cast<const float*>(smem + sa_off + o + i * 512) * sb;
+      for (int i = 0; i < FM; ++i)
+        sc[S][i] = *reinterpret_cast<const float*>(smem + sa_off + o + i * 512);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          sbr[S][j][e] = *reinterpret_cast<const float*>(
+              smem + sb_off + o + (wn * WN + j * 16 + 4 * (lane >> 4) + e) * 32);
+    } else {
+      const float sb = *reinterpret_cast<const float*>(smem + sb_off + o);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        sc[S][i] = *reinterpret_cast<const float*>(smem + sa_off + o + i * 512) * sb;
+    }
   };
 
   // Waits until this wave's DMA of a K-block has landed, given how many
@@ -773,12 +801,14 @@ __global__ void __launch_bounds__((128 / WM) * (128 / WN) * 64) gemm_pipe128_ker
       if (p >= 2) {
         const int qi = (p - 2) / FN, qj = (p - 2) % FN;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[qi][qj][e] = fmaf(r2[e], sc[S][qi], acc[qi][qj][e]);
+        for (int e = 0; e < 4; ++e)
+          acc[qi][qj][e] = fmaf(r2[e], scale_of(S, qi, qj, e), acc[qi][qj][e]);
         asm volatile("" : "+v"(acc[qi][qj]));
       } else {
         const int qj = FN - 2 + p;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[FM - 1][qj][e] = fmaf(r2[e], sc[T][FM - 1], acc[FM - 1][qj][e]);
+        for (int e = 0; e < 4; ++e)
+          acc[FM - 1][qj][e] = fmaf(r2[e], scale_of(T, FM - 1, qj, e), acc[FM - 1][qj][e]);
         asm volatile("" : "+v"(acc[FM - 1][qj]));
       }
       r2 = r1;
@@ -795,6 +825,8 @@ __global__ void __launch_bounds__((128 / WM) * (128 / WN) * 64) gemm_pipe128_ker
   // sc[1] starts at zero so the first K-block's two "previous" folds add 0.
 #pragma unroll
   for (int i = 0; i < FM; ++i) sc[1][i] = 0.f;
+#pragma unroll
+  for (int j = 0; j < (PR ? FN : 1); ++j) sbr[1][j] = v4f{0.f, 0.f, 0.f, 0.f};
   int kb = kb_begin;
   for (; kb + 1 < kb_end; kb += 2) {
     body(kb, PipeKind<0>{});
@@ -806,11 +838,17 @@ __global__ void __launch_bounds__((128 / WM) * (128 / WN) * 64) gemm_pipe128_ker
     last_set = 0;
   }
   if (nkb > 0) {
-    const float s3 = last_set == 0 ? sc[0][FM - 1] : sc[1][FM - 1];
+    const int L = last_set;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) acc[FM - 1][FN - 2][e] = fmaf(r2[e], s3, acc[FM - 1][FN - 2][e]);
+    for (int e = 0; e < 4; ++e)
+      acc[FM - 1][FN - 2][e] = fmaf(r2[e], L == 0 ? scale_of(0, FM - 1, FN - 2, e)
+                                                  : scale_of(1, FM - 1, FN - 2, e),
+                                    acc[FM - 1][FN - 2][e]);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) acc[FM - 1][FN - 1][e] = fmaf(r1[e], s3, acc[FM - 1][FN - 1][e]);
+    for (int e = 0; e < 4; ++e)
+      acc[FM - 1][FN - 1][e] = fmaf(r1[e], L == 0 ? scale_of(0, FM - 1, FN - 1, e)
+                                                  : scale_of(1, FM - 1, FN - 1, e),
+                                    acc[FM - 1][FN - 1][e]);
   }
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
   __syncthreads();
@@ -874,7 +912,7 @@ __device__ __forceinline__ void wait_vmcnt_rt(int n) {
 //   rows, with the row scales beside them; rows past M are zero with scale
 //   0. This fuses act-quant into the GEMM for decode shapes.
 // ---------------------------------------------------------------------------
-template <int FM, bool QA> struct DecodeCfg {
+template <int FM, bool QA, bool PR = false> struct DecodeCfg {
   static constexpr int NW = 8, BN = 128, AR = 16 * FM;
   // measured (fp8 path): deeper rings only lengthen the start-up burst; the
   // bf16 path waits one K-block further ahead, so it keeps one more stage.
@@ -883,7 +921,8 @@ template <int FM, bool QA> struct DecodeCfg {
   static constexpr int STAGE = (BN + ACT_ROWS) * 128;
   static constexpr int ACT_LOADS = ACT_ROWS / 8;           // 1 KiB wave-loads per K-block
   static constexpr int WIN_SA = QA ? 0 : 8 * 32 * 4 * ((FM + 1) / 2);
-  static constexpr int WIN = WIN_SA + 256;
+  // PR (per-row weight scales): Bs of the 128 rows, slot-major (8 x 512 B).
+  static constexpr int WIN = WIN_SA + (PR ? 8 * BN * 4 : 256);
   static constexpr int SW_OFF = NS * STAGE;
   static constexpr int AQ_OFF = SW_OFF + 2 * WIN;          // QA: two fp8 slots
   static constexpr int AQ_KB = AR * 128;
@@ -891,9 +930,10 @@ template <int FM, bool QA> struct DecodeCfg {
   static constexpr int SMEM = SQ_OFF + (QA ? 2 * AR * 4 : 0);
 };
 
-template <int FM, bool QA>
+template <int FM, bool QA, bool PR = false>
 __global__ void __launch_bounds__(512) gemm_decode_kernel(GemmArgs a) {
-  using Cfg = DecodeCfg<FM, QA>;
+  using Cfg = DecodeCfg<FM, QA, PR>;
+  static_assert(!(QA && PR), "the fused-quantisation path uses 128x128 weight blocks");
   constexpr int NW = Cfg::NW, BN = Cfg::BN, AR = Cfg::AR, NS = Cfg::NS;
   constexpr int STAGE = Cfg::STAGE, WIN_SA = Cfg::WIN_SA, WIN = Cfg::WIN;
   constexpr int SW_OFF = Cfg::SW_OFF, ACT_LOADS = Cfg::ACT_LOADS;
@@ -953,9 +993,20 @@ __global__ void __launch_bounds__(512) gemm_decode_kernel(GemmArgs a) {
       const int m = min(rb + (lane & 31), a_lim);
       dma4_ptr(a.As + (int64_t)m * a.as_sm + (int64_t)kb * a.as_sk, lb + wid * 256);
     }
-    if (wid == NW - 1 && lane < 8) {
-      const int kb = min(kb0 + lane, kb_end - 1);
-      dma4_ptr(a.Bs + (int64_t)(n0 >> 7) * a.bs_sn + (int64_t)kb * a.bs_sk, lb + WIN_SA);
+    if constexpr (PR) {
+      // wave w: slot w for rows 0..63 and 64..127 (lane = row)
+      const int kb = min(kb0 + wid, kb_end - 1);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int n = min(n0 + h * 64 + lane, a.N - 1);
+        dma4_ptr(a.Bs + (int64_t)n * a.bs_sn + (int64_t)kb * a.bs_sk,
+                 lb + WIN_SA + wid * 512 + h * 256);
+      }
+    } else {
+      if (wid == NW - 1 && lane < 8) {
+        const int kb = min(kb0 + lane, kb_end - 1);
+        dma4_ptr(a.Bs + (int64_t)(n0 >> 7) * a.bs_sn + (int64_t)kb * a.bs_sk, lb + WIN_SA);
+      }
     }
   };
   auto issue_next = [&](int kb) {
@@ -1036,7 +1087,14 @@ __global__ void __launch_bounds__(512) gemm_decode_kernel(GemmArgs a) {
     const uint8_t* st = smem + (rel % NS) * STAGE;
     const uint8_t* win = smem + SW_OFF + ((rel >> 3) & 1) * WIN;
     const int slot = rel & 7;
-    const float sb = *reinterpret_cast<const float*>(win + WIN_SA + slot * 4);
+    v4f sbv;
+    if constexpr (PR) {
+      sbv = *reinterpret_cast<const v4f*>(win + WIN_SA + slot * 512 +
+                                          (wid * 16 + 4 * (lane >> 4)) * 4);
+    } else {
+      const float sb = *reinterpret_cast<const float*>(win + WIN_SA + slot * 4);
+      sbv = v4f{sb, sb, sb, sb};
+    }
     const v8i w = lds_frag2(st + w_off, slo, shi);
 #pragma unroll
     for (int f = 0; f < FM; ++f) {
@@ -1053,9 +1111,8 @@ __global__ void __launch_bounds__(512) gemm_decode_kernel(GemmArgs a) {
       }
       const v4f t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
           w, x, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
-      const float sc = sa * sb;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[f][r] = fmaf(t[r], sc, acc[f][r]);
+      for (int r = 0; r < 4; ++r) acc[f][r] = fmaf(t[r], sa * sbv[r], acc[f][r]);
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -1351,19 +1408,21 @@ int skinny_max_m() {
   return v;
 }
 
-Plan make_plan(int64_t M, int64_t N, int64_t K) {
+// per_row: weight scales per output row (block_n = 1, the deep-gemm layout);
+// only the decode kernel (M <= 48) and gemm_pipe128_kernel implement it.
+Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
   const int KB = (int)(K / 128);
   const int cus = device_cu_count();
   Plan p;
   auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-  if (M <= skinny_max_m() && !use_decode_kernel()) {
+  if (M <= skinny_max_m() && !use_decode_kernel() && !per_row) {
     // Skinny path: 16 output columns per workgroup, K split inside it.
     p.cfg = CFG_SKINNY; p.bm = (int)(((M + 15) / 16) * 16); p.bn = 16;
     p.splits = 1;
     p.kb_per_split = KB;
     return p;
   }
-  if (M <= 48) {
+  if (M <= 48 && (use_decode_kernel() || per_row)) {
     // Decode path: 128 output columns per workgroup; split K until the grid
     // covers the CUs.
     p.cfg = CFG_DECODE; p.bm = (int)(((M + 15) / 16) * 16); p.bn = 128;
@@ -1374,7 +1433,9 @@ Plan make_plan(int64_t M, int64_t N, int64_t K) {
     p.splits = (KB + p.kb_per_split - 1) / p.kb_per_split;
     return p;
   }
-  if (M <= 32) {
+  if (per_row) {
+    p.cfg = CFG_128x128; p.bm = 128; p.bn = 128;
+  } else if (M <= 32) {
     p.cfg = CFG_32x128; p.bm = 32; p.bn = 128;
   } else if (M <= 64) {
     p.cfg = CFG_64x128; p.bm = 64; p.bn = 128;
@@ -1432,8 +1493,11 @@ void launch_cfg(const GemmArgs& a, int splits, hipStream_t st) {
 
 extern "C" size_t fp8b_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int64_t block_n,
                                            int64_t block_k) {
-  if (M <= 0 || N <= 0 || K <= 0 || block_n != 128 || block_k != 128 || K % 128 != 0) return 0;
-  const Plan p = make_plan(M, N, K);
+  const bool per_row = block_n == 1;
+  if (M <= 0 || N <= 0 || K <= 0 || (block_n != 128 && !per_row) || block_k != 128 ||
+      K % 128 != 0)
+    return 0;
+  const Plan p = make_plan(M, N, K, per_row);
   if (p.splits <= 1) return 0;
   return (size_t)p.splits * (size_t)M * (size_t)N * sizeof(float);
 }
@@ -1464,7 +1528,7 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
   hipStream_t st = (hipStream_t)stream;
   const size_t esz = out_dtype == FP8B_F32 ? 4 : 2;
 
-  if (!mfma_path_ok(A, lda, B, ldb, M, N, K, block_n, block_k)) {
+  auto run_generic = [&]() -> int {
     GenericArgs g;
     g.A = (const uint8_t*)A; g.B = (const uint8_t*)B; g.As = As; g.Bs = Bs; g.C = C;
     g.lda = lda; g.ldb = ldb; g.as_sm = as_sm; g.as_sk = as_sk; g.bs_sn = bs_sn;
@@ -1481,9 +1545,14 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
       return FP8B_ERR_LAUNCH;
     }
     return FP8B_OK;
-  }
+  };
+  // block_n = 1 (per-row weight scales, the deep-gemm layout) with
+  // block_k = 128 has MFMA kernels too.
+  const bool per_row = block_n == 1 && block_k == 128;
+  if (!mfma_path_ok(A, lda, B, ldb, M, N, K, per_row ? 128 : block_n, block_k))
+    return run_generic();
 
-  const Plan p = make_plan(M, N, K);
+  const Plan p = make_plan(M, N, K, per_row);
   const size_t need = p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
     set_error("fp8b_w8a8_block_matmul: workspace smaller than fp8b_gemm_workspace_size()");
@@ -1510,7 +1579,20 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
   const bool ws_vec = (N % 4 == 0);
   a.vec_store = (p.splits > 1) ? (ws_vec ? 1 : 0) : (c_vec ? 1 : 0);
 
-  switch (p.cfg) {
+  if (per_row) {
+    if (p.cfg == CFG_DECODE) {
+      const dim3 grid((unsigned)((N + 127) / 128), 1, (unsigned)p.splits);
+      const int fm = (int)((M + 15) / 16);
+      if (fm <= 1) gemm_decode_kernel<1, false, true><<<grid, 512, 0, st>>>(a);
+      else if (fm == 2) gemm_decode_kernel<2, false, true><<<grid, 512, 0, st>>>(a);
+      else gemm_decode_kernel<3, false, true><<<grid, 512, 0, st>>>(a);
+    } else if (pipe_ok(a, p)) {
+      dim3 grid(a.tiles_m * a.tiles_n, 1, p.splits);
+      gemm_pipe128_kernel<64, 32, true><<<grid, 512, 0, st>>>(a);
+    } else {
+      return run_generic();
+    }
+  } else switch (p.cfg) {
     case CFG_SKINNY: {
       const dim3 grid((unsigned)((N + 15) / 16));
       const int fm = (int)((M + 15) / 16);
@@ -1539,7 +1621,7 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
     case CFG_128x128: {
       if (pipe_ok(a, p)) {
         dim3 grid(a.tiles_m * a.tiles_n, 1, p.splits);
-        gemm_pipe128_kernel<64, 32><<<grid, 512, 0, st>>>(a);
+        gemm_pipe128_kernel<64, 32, false><<<grid, 512, 0, st>>>(a);
       } else {
         launch_cfg<128, 128, 64, 64>(a, p.splits, st);
       }

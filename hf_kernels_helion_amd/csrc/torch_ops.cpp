@@ -11,6 +11,10 @@
 //   silu_and_mul_quant(x, block_size) -> (q, s)
 //   act_quant_matmul(x, B, Bs, block_n, block_k, ScalarType output_dtype) -> Tensor
 //   weight_quant(W, block_n, block_k) -> (Wq, Bs)   (128x128 blocks)
+// and, in _deep_gemm_helion_rocm_mi355x (deep-gemm-helion's op,
+// deep-gemm-helion/deep-gemm-helion/torch-ext/deep_gemm_helion/op.py:7-14):
+//   gemm_fp8_fp8_bf16_nt(A, B, As, Bs, block_k) -> bf16 Tensor
+//       (per-row weight scales Bs [N, K/block_k]: block_n = 1)
 //       (act_quant then w8a8_block_fp8_matmul, one GEMM kernel for M <= 48)
 // Each op validates its tensors (TORCH_CHECK -> RuntimeError), allocates its
 // outputs and any split-K workspace from torch's caching allocator, and calls
@@ -169,6 +173,11 @@ std::tuple<Tensor, Tensor> weight_quant(const Tensor& W, int64_t block_n, int64_
   return {kp == K ? qbuf : q.contiguous(), s};
 }
 
+Tensor gemm_fp8_fp8_bf16_nt(const Tensor& A, const Tensor& B, const Tensor& As,
+                            const Tensor& Bs, int64_t block_k) {
+  return matmul_impl(A, B, As, Bs, 1, block_k, at::kBFloat16);
+}
+
 void check_group(int64_t g) {
   TORCH_CHECK(g == 32 || g == 64 || g == 128 || g == 256,
               "group size must be 32, 64, 128 or 256, got ", g);
@@ -266,6 +275,9 @@ Tensor act_quant_matmul_cpu(const Tensor&, const Tensor&, const Tensor&, int64_t
 std::tuple<Tensor, Tensor> weight_quant_cpu(const Tensor&, int64_t, int64_t) {
   no_cpu("weight_quant");
 }
+Tensor gemm_nt_cpu(const Tensor&, const Tensor&, const Tensor&, const Tensor&, int64_t) {
+  no_cpu("gemm_fp8_fp8_bf16_nt");
+}
 void silu_and_mul_cpu(Tensor&, const Tensor&) { no_cpu("silu_and_mul"); }
 std::tuple<Tensor, Tensor> silu_and_mul_quant_cpu(const Tensor&, int64_t) {
   no_cpu("silu_and_mul_quant");
@@ -304,4 +316,16 @@ TORCH_LIBRARY_IMPL(_finegrained_fp8_helion_rocm_mi355x, CPU, m) {
   m.impl("silu_and_mul_quant", &silu_and_mul_quant_cpu);
   m.impl("act_quant_matmul", &act_quant_matmul_cpu);
   m.impl("weight_quant", &weight_quant_cpu);
+}
+
+TORCH_LIBRARY(_deep_gemm_helion_rocm_mi355x, m) {
+  m.def("gemm_fp8_fp8_bf16_nt(Tensor A, Tensor B, Tensor As, Tensor Bs, int block_k) -> Tensor");
+}
+
+TORCH_LIBRARY_IMPL(_deep_gemm_helion_rocm_mi355x, CUDA, m) {
+  m.impl("gemm_fp8_fp8_bf16_nt", &gemm_fp8_fp8_bf16_nt);
+}
+
+TORCH_LIBRARY_IMPL(_deep_gemm_helion_rocm_mi355x, CPU, m) {
+  m.impl("gemm_fp8_fp8_bf16_nt", &gemm_nt_cpu);
 }

@@ -97,3 +97,22 @@ def test_bench_rejects_multi_gpu():
     r = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2 and "one GPU only" in r.stderr
+
+
+def test_deep_gemm_surface_matches_reference():
+    # deep-gemm-helion/torch-ext/deep_gemm_helion/__init__.py:6-8 and op.py:8-16
+    from hf_kernels_helion_amd import deep_gemm_helion as dg
+    from hf_kernels_helion_amd.deep_gemm_helion import _ops as dg_ops
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    sig = inspect.signature(dg.gemm_fp8_fp8_bf16_nt)
+    assert list(sig.parameters) == ["A", "B", "As", "Bs", "block_size"]
+    assert sig.parameters["block_size"].default == 128
+    assert dg_ops._OPS_NAME == "_deep_gemm_helion_rocm_mi355x"
+    sch = str(dg_ops.ops.gemm_fp8_fp8_bf16_nt.default._schema)
+    assert "(Tensor A, Tensor B, Tensor As, Tensor Bs, int block_k) -> Tensor" in sch
+    with FakeTensorMode():
+        out = dg.gemm_fp8_fp8_bf16_nt(_fp8(5, 256), _fp8(7, 256), torch.ones(5, 2),
+                                      torch.ones(7, 2))
+        assert out.shape == (5, 7) and out.dtype == torch.bfloat16
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        dg.gemm_fp8_fp8_bf16_nt(_fp8(5, 256), _fp8(7, 256), torch.ones(5, 2), torch.ones(7, 2))
