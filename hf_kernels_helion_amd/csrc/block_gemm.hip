@@ -1425,6 +1425,19 @@ int skinny_max_m() {
   return v;
 }
 
+// Grids of fewer 256x256 tiles than CUs: one partial wave of 256x256 tiles
+// still beats the 128x128 kernel when the latter needs three or more waves
+// and K is long. Measured per K-block in steady state: a 256x256 tile takes
+// ~1.75 us on one CU, a 128x128 tile ~0.71 us (it reuses each operand byte
+// half as often); with 32 K-blocks the 256x256 grid lost (1536x7168x4096:
+// 102 us against 75), with 64 and 112 it won (2560x4096x8192: 137 against
+// 140; 3001x4096x14336: 216 against 241).
+bool prefer_256(int64_t t256, int64_t t128, int cus, int KB) {
+  if (t256 * 2 <= cus || KB < 64) return false;
+  const int64_t w256 = (t256 + cus - 1) / cus, w128 = (t128 + cus - 1) / cus;
+  return 71 * w128 > 175 * w256;
+}
+
 // per_row: weight scales per output row (block_n = 1, the deep-gemm layout);
 // only the decode kernel (M <= 48) and gemm_pipe128_kernel implement it.
 Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
@@ -1456,7 +1469,7 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
     p.cfg = CFG_32x128; p.bm = 32; p.bn = 128;
   } else if (M <= 64) {
     p.cfg = CFG_64x128; p.bm = 64; p.bn = 128;
-  } else if (tiles(256, 256) >= cus) {
+  } else if (tiles(256, 256) >= cus || prefer_256(tiles(256, 256), tiles(128, 128), cus, KB)) {
     p.cfg = CFG_256x256; p.bm = 256; p.bn = 256;
   } else {
     p.cfg = CFG_128x128; p.bm = 128; p.bn = 128;

@@ -186,12 +186,13 @@ def _full_check(out, Ad, Bd, Asd, Bsd):
 
 @pytest.mark.parametrize("M,N,K", [(4096, 4096, 512), (4096, 4096, 1024), (4000, 4200, 1536),
                                    (4096, 4352, 2560), (3001, 5000, 2048),
-                                   (4096, 4096, 384), (4096, 4096, 1152)])
+                                   (4096, 4096, 384), (4096, 4096, 1152), (3001, 4096, 8192)])
 def test_gemm_large_tile_kernels(M, N, K, dev):
     """Grids of at least one 256x256 tile per CU: the pipelined kernel (K-block
     counts that are multiples of 4; windows of 8 K-blocks, full and half) and
     the two-stage kernel it falls back to (K-block counts 3 and 9), with
-    ragged M and N edges. Every row against torch's fp32 dequant-matmul, a
+    ragged M and N edges; 3001x4096x8192 is a partial wave of 256x256 tiles
+    (192 tiles, chosen over three waves of 128x128 tiles for long K). Every row against torch's fp32 dequant-matmul, a
     sample of rows against the oracle."""
     print(f"gemm large-tile M={M} N={N} K={K}", flush=True)
     A, B, As, Bs = _operands(M, N, K, seed=K + M)
