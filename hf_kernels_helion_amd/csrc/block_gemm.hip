@@ -1461,6 +1461,15 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
     splits = std::max(1, std::min(splits, KB));
     p.kb_per_split = (KB + splits - 1) / splits;
     p.splits = (KB + p.kb_per_split - 1) / p.kb_per_split;
+    // Four or fewer K-blocks per split: the split-K partials and their sum
+    // cost more than the skinny kernel's activation re-reads (measured
+    // 32x4096x4096: 11.5 us split-K, 8.2 us skinny; at 14 K-blocks per
+    // split, 32x4096x14336: 16.1 against 21.5).
+    if (!per_row && p.kb_per_split <= 4) {
+      p.cfg = CFG_SKINNY; p.bn = 16;
+      p.splits = 1;
+      p.kb_per_split = KB;
+    }
     return p;
   }
   if (per_row) {
@@ -1736,7 +1745,8 @@ extern "C" int fp8b_act_quant_matmul(const void* x, int64_t ldx, const void* B, 
   }
   hipStream_t st = (hipStream_t)stream;
   const int64_t KB = K / 128;
-  if (!fused_decode_ok(x, ldx, B, ldb, M, K)) {
+  const Plan p = make_plan(M, N, K);
+  if (!fused_decode_ok(x, ldx, B, ldb, M, K) || p.cfg != CFG_DECODE) {
     // Quantise into the workspace, then the block GEMM on (q, s).
     const size_t gemm = fp8b_gemm_workspace_size(M, N, K, 128, 128);
     uint8_t* q = (uint8_t*)workspace + align256(gemm);
@@ -1745,11 +1755,6 @@ extern "C" int fp8b_act_quant_matmul(const void* x, int64_t ldx, const void* B, 
     if (rc != FP8B_OK) return rc;
     return fp8b_w8a8_block_matmul(q, K, B, ldb, s, KB, 1, Bs, bs_sn, bs_sk, C, ldc, out_dtype,
                                   M, N, K, 128, 128, workspace, gemm, stream);
-  }
-  const Plan p = make_plan(M, N, K);
-  if (p.cfg != CFG_DECODE) {
-    set_error("fp8b_act_quant_matmul: internal plan does not fit the fused kernel");
-    return FP8B_ERR_LAUNCH;
   }
   GemmArgs a;
   a.X = (const uint16_t*)x; a.ldx = ldx;
