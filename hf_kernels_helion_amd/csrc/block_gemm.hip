@@ -1426,14 +1426,13 @@ int skinny_max_m() {
 }
 
 // Grids of fewer 256x256 tiles than CUs: one partial wave of 256x256 tiles
-// still beats the 128x128 kernel when the latter needs three or more waves
-// and K is long. Measured per K-block in steady state: a 256x256 tile takes
-// ~1.75 us on one CU, a 128x128 tile ~0.71 us (it reuses each operand byte
-// half as often); with 32 K-blocks the 256x256 grid lost (1536x7168x4096:
-// 102 us against 75), with 64 and 112 it won (2560x4096x8192: 137 against
-// 140; 3001x4096x14336: 216 against 241).
-bool prefer_256(int64_t t256, int64_t t128, int cus, int KB) {
-  if (t256 * 2 <= cus || KB < 64) return false;
+// (not split along K) still beats the 128x128 kernel when the latter needs
+// three or more waves. Measured per K-block: a 256x256 tile takes ~1.4-1.75
+// us on one CU, a 128x128 tile ~0.71 us (it reuses each operand byte half as
+// often); 3001x4096x14336: 157 us against 241, 2560x4096x8192: 87 against
+// 140, 1536x7168x4096: 48 against 75, 2560x4096x2048: 28.5 against 42.5.
+bool prefer_256(int64_t t256, int64_t t128, int cus) {
+  if (t256 * 2 <= cus) return false;
   const int64_t w256 = (t256 + cus - 1) / cus, w128 = (t128 + cus - 1) / cus;
   return 71 * w128 > 175 * w256;
 }
@@ -1478,7 +1477,7 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
     p.cfg = CFG_32x128; p.bm = 32; p.bn = 128;
   } else if (M <= 64) {
     p.cfg = CFG_64x128; p.bm = 64; p.bn = 128;
-  } else if (tiles(256, 256) >= cus || prefer_256(tiles(256, 256), tiles(128, 128), cus, KB)) {
+  } else if (tiles(256, 256) >= cus || prefer_256(tiles(256, 256), tiles(128, 128), cus)) {
     p.cfg = CFG_256x256; p.bm = 256; p.bn = 256;
   } else {
     p.cfg = CFG_128x128; p.bm = 128; p.bn = 128;
@@ -1489,7 +1488,9 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
   // already cover the CUs are not split: the fp32 partials would cost more
   // HBM traffic than the extra occupancy recovers.
   int splits = 1;
-  if (t < cus)
+  // (a partial wave of 256x256 tiles chosen by prefer_256 is not split: the
+  // fp32 partials of a long-K grid cost more than the idle CUs)
+  if (t < cus && p.cfg != CFG_256x256)
     while (t * splits < 2 * cus && KB / (splits * 2) >= 4) splits *= 2;
   p.kb_per_split = (KB + splits - 1) / splits;
   // Split sizes in whole scale half-windows (multiples of 4 K-blocks) keep
