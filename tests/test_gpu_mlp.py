@@ -17,15 +17,19 @@ def _bits(t):
 
 @pytest.mark.parametrize("M,d", [(1, 8), (7, 1000), (64, 14336), (3001, 256)])
 def test_silu_and_mul_vs_oracle(M, d, dev):
-    """silu goes through expf on both sides; results agree to 1 bf16 ulp."""
+    """The oracle evaluates silu with expf and an IEEE division, the kernel
+    with the hardware exp2 and reciprocal (a few fp32 ulps apart). Where the
+    fp32 silu straddles a bf16 rounding boundary the rounded silu moves by one
+    bf16 ulp and the rounded product by at most two: every element within
+    2^-6 relative, and at least 99.9% bit-identical."""
     print(f"silu_and_mul M={M} d={d}", flush=True)
     x = synthetic.activations(M, 2 * d, seed=d) * 3
     out = torch.empty(M, d, dtype=torch.bfloat16, device=dev)
     fp8.silu_and_mul(out, x.to(dev))
     ref = torch.from_numpy(oracle.silu_and_mul(_bits(x)).view(np.int16)).view(torch.bfloat16)
-    torch.testing.assert_close(out.cpu().float(), ref.float(), rtol=2 ** -7, atol=1e-6)
+    torch.testing.assert_close(out.cpu().float(), ref.float(), rtol=2 ** -6, atol=1e-6)
     exact = (out.cpu() == ref).float().mean().item()
-    assert exact > 0.99, exact
+    assert exact > 0.999, exact  # measured 0.9995-1.0 with the refined formula
 
 
 def test_silu_and_mul_3d(dev):
@@ -33,7 +37,7 @@ def test_silu_and_mul_3d(dev):
     out = torch.empty(2, 12, 256, dtype=torch.bfloat16, device=dev)
     fp8.silu_and_mul(out, x.to(dev))
     ref = torch_ref.silu_and_mul(x)
-    torch.testing.assert_close(out.cpu().float(), ref.float(), rtol=2 ** -7, atol=1e-6)
+    torch.testing.assert_close(out.cpu().float(), ref.float(), rtol=2 ** -6, atol=1e-6)
 
 
 @pytest.mark.parametrize("M,d,group", [(3001, 14336, 128), (5, 384, 128), (9, 200, 64),
