@@ -257,3 +257,41 @@ def test_gemm_golden_fixture(dev):
     out = fp8.w8a8_block_fp8_matmul(A.to(dev), B.to(dev), As.to(dev), Bs.to(dev),
                                     z["block"].tolist(), torch.float32)
     np.testing.assert_allclose(out.cpu().numpy(), z["C"], rtol=1e-3, atol=1e-4)
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 1024), (512, 512, 2048), (32, 4096, 14336),
+                                   (3001, 4096, 4096)])
+def test_gemm_power_of_two_row_scaling(M, N, K, dev):
+    """Scaling the activation scales of one row by 2^k scales that fp32
+    output row by exactly 2^k and leaves every other row bit-identical, on
+    each kernel family (256x256 pipelined, 128x128 pipelined, split-K decode,
+    partial-wave 256x256)."""
+    print(f"gemm 2^k row scaling M={M} N={N} K={K}", flush=True)
+    A, B, As, Bs = [t.to(dev) for t in _operands(M, N, K, seed=7 + M, kind="harness")]
+    out = fp8.w8a8_block_fp8_matmul(A, B, As, Bs, [128, 128], torch.float32)
+    rows = torch.tensor([0, M // 3, M - 1], device=dev)
+    As2 = As.clone()
+    As2[rows] *= 8.0
+    out2 = fp8.w8a8_block_fp8_matmul(A, B, As2, Bs, [128, 128], torch.float32)
+    assert torch.equal(out2[rows], out[rows] * 8.0)
+    keep = torch.ones(M, dtype=torch.bool, device=dev)
+    keep[rows] = False
+    assert torch.equal(out2[keep], out[keep])
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 1024), (300, 640, 2048), (32, 4096, 14336)])
+def test_gemm_k_block_permutation(M, N, K, dev):
+    """Permuting the K-blocks of A and B together with their scale columns
+    changes only the order of the fp32 sums: the result stays within the
+    tolerance of the unpermuted one."""
+    print(f"gemm K-block permutation M={M} N={N} K={K}", flush=True)
+    A, B, As, Bs = [t.to(dev) for t in _operands(M, N, K, seed=11 + M)]
+    KB = K // 128
+    perm = torch.randperm(KB, generator=torch.Generator().manual_seed(KB)).to(dev)
+    cols = (perm[:, None] * 128 + torch.arange(128, device=dev)[None, :]).reshape(-1)
+    Ap = A.view(torch.uint8)[:, cols].contiguous().view(torch.float8_e4m3fn)
+    Bp = B.view(torch.uint8)[:, cols].contiguous().view(torch.float8_e4m3fn)
+    out = fp8.w8a8_block_fp8_matmul(A, B, As, Bs, [128, 128], torch.bfloat16)
+    outp = fp8.w8a8_block_fp8_matmul(Ap, Bp, As[:, perm].contiguous(), Bs[:, perm].contiguous(),
+                                     [128, 128], torch.bfloat16)
+    torch.testing.assert_close(outp.float(), out.float(), rtol=RTOL, atol=ATOL)
