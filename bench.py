@@ -106,6 +106,14 @@ def cpu_baseline(A, B, As, Bs, torch):
         torch_ref.dequant_matmul(a, B, a_s, Bs)
         times.append(time.perf_counter() - t0)
     t = sum(times) / len(times)
+    cpu_model = "unknown CPU"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
     return {
         "value": 2.0 * R * N * K / t / 1e12,
         "unit": "TFLOP/s",
@@ -114,7 +122,7 @@ def cpu_baseline(A, B, As, Bs, torch):
         "sample": (f"{R} of {M} rows of the {M}x{N}x{K} workload: dequantise A rows and all of B "
                    f"with their block scales, fp32 matmul, bf16 cast (bench.py:11-14 restated); "
                    f"mean of {len(times)} iterations, {t * 1e3:.1f} ms each, "
-                   f"os.cpu_count()={os.cpu_count()}"),
+                   f"os.cpu_count()={os.cpu_count()}, {cpu_model}"),
     }
 
 
