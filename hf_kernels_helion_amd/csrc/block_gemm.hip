@@ -929,11 +929,14 @@ __device__ __forceinline__ void wait_vmcnt_rt(int n) {
 //   rows, with the row scales beside them; rows past M are zero with scale
 //   0. This fuses act-quant into the GEMM for decode shapes.
 // ---------------------------------------------------------------------------
-template <int FM, bool QA, bool PR = false> struct DecodeCfg {
+template <int FM, bool QA, bool PR = false, int NSX = 0> struct DecodeCfg {
   static constexpr int NW = 8, BN = 128, AR = 16 * FM;
   // measured (fp8 path): deeper rings only lengthen the start-up burst; the
   // bf16 path waits one K-block further ahead, so it keeps one more stage.
-  static constexpr int NS = QA ? 5 : 4;
+  // NSX = 3 (grids above one workgroup per CU): the smaller ring lets two
+  // workgroups share a CU, so the whole grid is resident (32x28672x4096,
+  // 448 workgroups: 29.7 us against 33.7 with four stages).
+  static constexpr int NS = NSX ? NSX : (QA ? 5 : 4);
   static constexpr int ACT_ROWS = QA ? 2 * AR : AR;        // 128-byte rows of activations
   static constexpr int STAGE = (BN + ACT_ROWS) * 128;
   static constexpr int ACT_LOADS = ACT_ROWS / 8;           // 1 KiB wave-loads per K-block
@@ -947,9 +950,9 @@ template <int FM, bool QA, bool PR = false> struct DecodeCfg {
   static constexpr int SMEM = SQ_OFF + (QA ? 2 * AR * 4 : 0);
 };
 
-template <int FM, bool QA, bool PR = false>
+template <int FM, bool QA, bool PR = false, int NSX = 0>
 __global__ void __launch_bounds__(512) gemm_decode_kernel(GemmArgs a) {
-  using Cfg = DecodeCfg<FM, QA, PR>;
+  using Cfg = DecodeCfg<FM, QA, PR, NSX>;
   static_assert(!(QA && PR), "the fused-quantisation path uses 128x128 weight blocks");
   constexpr int NW = Cfg::NW, BN = Cfg::BN, AR = Cfg::AR, NS = Cfg::NS;
   constexpr int STAGE = Cfg::STAGE, WIN_SA = Cfg::WIN_SA, WIN = Cfg::WIN;
@@ -1644,9 +1647,15 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
     case CFG_DECODE: {
       const dim3 grid((unsigned)((N + 127) / 128), 1, (unsigned)p.splits);
       const int fm = (int)((M + 15) / 16);
-      if (fm <= 1) gemm_decode_kernel<1, false><<<grid, 512, 0, st>>>(a);
-      else if (fm == 2) gemm_decode_kernel<2, false><<<grid, 512, 0, st>>>(a);
-      else gemm_decode_kernel<3, false><<<grid, 512, 0, st>>>(a);
+      if ((int64_t)grid.x * grid.z > device_cu_count()) {
+        if (fm <= 1) gemm_decode_kernel<1, false, false, 3><<<grid, 512, 0, st>>>(a);
+        else if (fm == 2) gemm_decode_kernel<2, false, false, 3><<<grid, 512, 0, st>>>(a);
+        else gemm_decode_kernel<3, false, false, 3><<<grid, 512, 0, st>>>(a);
+      } else {
+        if (fm <= 1) gemm_decode_kernel<1, false><<<grid, 512, 0, st>>>(a);
+        else if (fm == 2) gemm_decode_kernel<2, false><<<grid, 512, 0, st>>>(a);
+        else gemm_decode_kernel<3, false><<<grid, 512, 0, st>>>(a);
+      }
       break;
     }
     case CFG_256x256: {
