@@ -1463,11 +1463,13 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
     splits = std::max(1, std::min(splits, KB));
     p.kb_per_split = (KB + splits - 1) / splits;
     p.splits = (KB + p.kb_per_split - 1) / p.kb_per_split;
-    // Four or fewer K-blocks per split: the split-K partials and their sum
-    // cost more than the skinny kernel's activation re-reads (measured
-    // 32x4096x4096: 11.5 us split-K, 8.2 us skinny; at 14 K-blocks per
-    // split, 32x4096x14336: 16.1 against 21.5).
-    if (!per_row && p.kb_per_split <= 4) {
+    // Four or fewer K-blocks per split, or eight rows or fewer on an 8-way
+    // split: the split-K partials and their sum cost more than the skinny
+    // kernel's activation re-reads (measured 32x4096x4096: 11.5 us split-K,
+    // 8.2 us skinny; 1..8x4096x14336: 14.7-15.0 against 13.2-13.6; but
+    // 32x4096x14336: 16.1 against 21.5, 16x4096x14336 even, and 8x14336x4096
+    // with 3 splits 16.7 against 20.6).
+    if (!per_row && (p.kb_per_split <= 4 || (M <= 8 && p.splits >= 8))) {
       p.cfg = CFG_SKINNY; p.bn = 16;
       p.splits = 1;
       p.kb_per_split = KB;

@@ -47,7 +47,7 @@ def _check(out_gpu, A, B, As, Bs, block=(128, 128), rows=None):
 @pytest.mark.parametrize("M,N,K", [(512, 512, 2048), (128, 256, 1024), (57, 200, 384),
                                    (1, 128, 128), (300, 640, 512), (32, 4096, 1024),
                                    (64, 512, 2048), (257, 384, 256), (3, 1000, 640),
-                                   (48, 130, 256), (65, 384, 512)])
+                                   (48, 130, 256), (65, 384, 512), (8, 4096, 14336)])
 @pytest.mark.parametrize("kind", ["model", "harness"])
 def test_gemm_bf16_vs_oracle(M, N, K, kind, dev):
     print(f"gemm bf16 {kind} M={M} N={N} K={K}", flush=True)
