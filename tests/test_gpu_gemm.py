@@ -295,3 +295,25 @@ def test_gemm_k_block_permutation(M, N, K, dev):
     outp = fp8.w8a8_block_fp8_matmul(Ap, Bp, As[:, perm].contiguous(), Bs[:, perm].contiguous(),
                                      [128, 128], torch.bfloat16)
     torch.testing.assert_close(outp.float(), out.float(), rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1, 128), (5, 15, 384), (70, 1, 1024), (33, 17, 14336)])
+def test_gemm_tiny_n(M, N, K, dev):
+    """Weight row counts below one 16-row fragment (rows past N clamped on
+    load, masked on store) on the skinny, decode and tiled paths."""
+    print(f"gemm tiny N M={M} N={N} K={K}", flush=True)
+    A, B, As, Bs = _operands(M, N, K, seed=M * 7 + N)
+    out = fp8.w8a8_block_fp8_matmul(A.to(dev), B.to(dev), As.to(dev), Bs.to(dev), [128, 128],
+                                    torch.bfloat16)
+    assert out.shape == (M, N)
+    _check(out, A, B, As, Bs)
+
+
+def test_gemm_zero_k_gives_zeros(dev):
+    """K = 0: the reference kernel's accumulator starts at zero and no
+    K-block is added (fp8.py:29-38), so the output is all zeros."""
+    A = torch.empty(4, 0, dtype=torch.float8_e4m3fn, device=dev)
+    B = torch.empty(8, 0, dtype=torch.float8_e4m3fn, device=dev)
+    out = fp8.w8a8_block_fp8_matmul(A, B, torch.empty(4, 0, device=dev),
+                                    torch.empty(1, 0, device=dev), [128, 128], torch.float32)
+    assert out.shape == (4, 8) and torch.equal(out, torch.zeros_like(out))
