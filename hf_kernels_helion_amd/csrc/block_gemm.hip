@@ -712,10 +712,20 @@ __global__ void __launch_bounds__((128 / WM) * (128 / WN) * 64) gemm_pipe128_ker
     const uint32_t lb = lds0 + SW_OFF + wbuf * WIN;
     if (wid < BM / 32) dma16_ptr(saw_src + kk, lb + wid * 1024);
     if constexpr (PR) {
-      if (wid >= NW - BN / 32) {
-        const int rw = (wid - (NW - BN / 32)) * 32 + (lane >> 1);
-        dma16_ptr(a.Bs + (int64_t)min(n0 + rw, a.N - 1) * a.bs_sn + 4 * (lane & 1) + kk,
-                  lb + WIN_SA + (wid - (NW - BN / 32)) * 1024);
+      // slot-major (slot s: the 128 rows' scales of K-block kb0 + s as
+      // consecutive floats), so a lane reads its four rows in one 16-byte
+      // load: waves NW-4..NW-1 issue 4 instructions each, one 4-byte lane
+      // per row, for (slot, 64-row half) = (i/2, i%2), i = 4q + j
+      if (wid >= NW - 4) {
+        const int q = wid - (NW - 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int i = q * 4 + j, sl = i >> 1, h = i & 1;
+          const int kbs = min(kb0 + sl, kb_end - 1);
+          dma4_ptr(a.Bs + (int64_t)min(n0 + h * 64 + lane, a.N - 1) * a.bs_sn +
+                       (int64_t)kbs * a.bs_sk,
+                   lb + WIN_SA + sl * 512 + h * 256);
+        }
       }
     } else {
       if (wid == NW - 1 && lane < 2) dma16_ptr(sbw_src + kk, lb + WIN_SA);
@@ -766,12 +776,11 @@ __global__ void __launch_bounds__((128 / WM) * (128 / WN) * 64) gemm_pipe128_ker
 #pragma unroll
       for (int i = 0; i < FM; ++i)
         sc[S][i] = *reinterpret_cast<const float*>(smem + sa_off + o + i * 512);
+      const int ob = ((rel >> 3) & 1) * WIN + (rel & 7) * 512;
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          sbr[S][j][e] = *reinterpret_cast<const float*>(
-              smem + sb_off + o + (wn * WN + j * 16 + 4 * (lane >> 4) + e) * 32);
+        sbr[S][j] = *reinterpret_cast<const v4f*>(
+            smem + sb_off + ob + (wn * WN + j * 16 + 4 * (lane >> 4)) * 4);
     } else {
       const float sb = *reinterpret_cast<const float*>(smem + sb_off + o);
 #pragma unroll
