@@ -385,12 +385,18 @@ __device__ __forceinline__ uint32_t lds_u32(const void* p) {
 
 template <int KIND> struct PipeKind { static constexpr int value = KIND; };
 
+// PR (per-row weight scales, block_n = 1): the window also holds the 256
+// weight rows' scales slot-major (slot s: K-block kb0 + s, consecutive floats;
+// 4-byte DMA lanes, one per row); each fold multiplies the row scale by the
+// lane's four column scales, read once per K-block per weight fragment as one
+// 16-byte load, each into the register its previous value just left.
+template <bool PR>
 __global__ void __launch_bounds__(512) gemm_pipe256_kernel(GemmArgs a) {
   constexpr int BM = 256, BN = 256, WM = 128, WN = 64, NWN = BN / WN, NW = 8;
   constexpr int FM = WM / 16, FN = WN / 16;       // 8 activation, 4 weight fragments
   constexpr int STAGE = (BM + BN) * 128;          // operand rows of one K-block
   constexpr int WIN_SA = BM * 32;                 // 8 K-blocks of As per row
-  constexpr int WIN = WIN_SA + 256;               // + Bs of the 2 column blocks
+  constexpr int WIN = WIN_SA + (PR ? 8 * BN * 4 : 256);  // + Bs of the tile
   constexpr int SW_OFF = 2 * STAGE;
   constexpr int EPI_PITCH = WN * 2 + 16;
   constexpr int EPI = NW * WM * EPI_PITCH;
@@ -461,7 +467,21 @@ __global__ void __launch_bounds__(512) gemm_pipe256_kernel(GemmArgs a) {
     const int kk = (kb0 + 4 * (lane & 1) < kb_end) ? kb0 : kb0 - 4 * (lane & 1);
     const uint32_t lb = lds0 + SW_OFF + wbuf * WIN;
     dma16_ptr(saw_src + kk, lb + wid * 1024);
-    if (wid == NW - 1 && lane < 4) dma16_ptr(sbw_src + kk, lb + WIN_SA);
+    if constexpr (PR) {
+      // wave w: slot w, rows 64h + lane for h = 0..3
+      // (the row is pinned so that the addresses are formed here, once per
+      // window, instead of being held in registers across the loop)
+      const int kbs = min(kb0 + wid, kb_end - 1);
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        int row = n0 + h * 64 + lane;
+        asm volatile("" : "+v"(row));
+        dma4_ptr(a.Bs + (int64_t)min(row, a.N - 1) * a.bs_sn + kbs,
+                 lb + WIN_SA + wid * 1024 + h * 256);
+      }
+    } else {
+      if (wid == NW - 1 && lane < 4) dma16_ptr(sbw_src + kk, lb + WIN_SA);
+    }
   };
 
   // Fragment reads: rows (lane & 15) of a 16-row group, logical chunks
@@ -487,8 +507,15 @@ __global__ void __launch_bounds__(512) gemm_pipe256_kernel(GemmArgs a) {
     return *reinterpret_cast<const float*>(smem + sa_off + o + i * 512);
   };
   auto rdsb = [&](int rel) {
+    if constexpr (PR) return 1.0f;
     const int o = ((rel >> 3) & 1) * WIN + (rel & 7) * 4;
     return *reinterpret_cast<const float*>(smem + sb_off + o);
+  };
+  // PR: the lane's four column scales of weight fragment j at K-block rel
+  auto rdsbj = [&](int rel, int j) {
+    const int o = ((rel >> 3) & 1) * WIN + (rel & 7) * 1024;
+    return *reinterpret_cast<const v4f*>(smem + SW_OFF + WIN_SA + o +
+                                         (wn * WN + j * 16 + 4 * (lane >> 4)) * 4);
   };
 
   v4f acc[FM][FN];
@@ -504,6 +531,9 @@ __global__ void __launch_bounds__(512) gemm_pipe256_kernel(GemmArgs a) {
                              0, 1, 2, 3, 0, 1, 2, 3, 0, 0, 1, 1, 2, 2, 3, 3};
   v8i w[FN], xs[4];
   float sc[FM], sa_t[FM], sb_n = 0.f, sc6_old = 0.f, sc7_old = 0.f;
+  v4f sbj[PR ? FN : 1];
+#pragma unroll
+  for (int j = 0; j < (PR ? FN : 1); ++j) sbj[j] = v4f{0.f, 0.f, 0.f, 0.f};
   v4f r1 = v4f{0.f, 0.f, 0.f, 0.f}, r2 = r1;  // results of MFMAs p-1 and p-2
 
   if (nkb > 0) {
@@ -522,6 +552,7 @@ __global__ void __launch_bounds__(512) gemm_pipe256_kernel(GemmArgs a) {
     xs[0] = rdx(0, 0); xs[1] = rdx(0, 1);
     sb_n = rdsb(0);
     sa_t[0] = rdsa(0, 0); sa_t[1] = rdsa(0, 1);
+    if constexpr (PR) { sbj[0] = rdsbj(0, 0); sbj[1] = rdsbj(0, 1); }
   }
 
   // One K-block. KIND 0: steady state (reads the next K-block, DMA of
@@ -557,6 +588,12 @@ __global__ void __launch_bounds__(512) gemm_pipe256_kernel(GemmArgs a) {
       if (p == 8) { xs[1] = rdx(s, 5); sa_t[5] = rdsa(rel, 5); }
       if (p == 12) { xs[2] = rdx(s, 6); sa_t[6] = rdsa(rel, 6); }
       if (p == 16) { xs[3] = rdx(s, 7); sa_t[7] = rdsa(rel, 7); }
+      // PR: column scales of fragments 2 and 3, each read once the previous
+      // K-block's last fold with it has been issued
+      if constexpr (PR) {
+        if (p == 0) sbj[2] = rdsbj(rel, 2);
+        if (p == 2) sbj[3] = rdsbj(rel, 3);
+      }
       // Scale of row i, computed just before the FMA of its first MFMA.
       if (p == 1) { sc[0] = sa_t[0] * sb; sc[1] = sa_t[1] * sb; }
       if (p == 9) sc[2] = sa_t[2] * sb;
@@ -573,20 +610,28 @@ __global__ void __launch_bounds__(512) gemm_pipe256_kernel(GemmArgs a) {
         if (p == 26) w[0] = rdw(s ^ 1, 0);
         if (p == 28) w[1] = rdw(s ^ 1, 1);
         if (p == 30) w[2] = rdw(s ^ 1, 2);
+        if constexpr (PR) {
+          if (p == 28) sbj[0] = rdsbj(rel + 1, 0);
+          if (p == 30) sbj[1] = rdsbj(rel + 1, 1);
+        }
       }
       asm volatile("" ::: "memory");
       __builtin_amdgcn_sched_barrier(0);
       if (p >= 2) {
         const int qi = ORD_I[p - 2], qj = ORD_J[p - 2];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[qi][qj][e] = fmaf(r2[e], sc[qi], acc[qi][qj][e]);
+        for (int e = 0; e < 4; ++e)
+          acc[qi][qj][e] = fmaf(r2[e], PR ? sc[qi] * sbj[qj % (PR ? FN : 1)][e] : sc[qi],
+                                acc[qi][qj][e]);
         asm volatile("" : "+v"(acc[qi][qj]));
       } else {
         // the previous K-block's last two MFMAs: rows 6 and 7, column 3
+        // (PR: fragment 3's column scales are reloaded only at p == 2)
         const int qi = 6 + p;
         const float so = p == 0 ? sc6_old : sc7_old;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[qi][3][e] = fmaf(r2[e], so, acc[qi][3][e]);
+        for (int e = 0; e < 4; ++e)
+          acc[qi][3][e] = fmaf(r2[e], PR ? so * sbj[PR ? 3 : 0][e] : so, acc[qi][3][e]);
         asm volatile("" : "+v"(acc[qi][3]));
       }
       r2 = r1;
@@ -607,9 +652,11 @@ __global__ void __launch_bounds__(512) gemm_pipe256_kernel(GemmArgs a) {
   if (kb < kb_end) {
     body(kb, PipeKind<2>{});
 #pragma unroll
-    for (int e = 0; e < 4; ++e) acc[6][3][e] = fmaf(r2[e], sc[6], acc[6][3][e]);
+    for (int e = 0; e < 4; ++e)
+      acc[6][3][e] = fmaf(r2[e], PR ? sc[6] * sbj[PR ? 3 : 0][e] : sc[6], acc[6][3][e]);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) acc[7][3][e] = fmaf(r1[e], sc[7], acc[7][3][e]);
+    for (int e = 0; e < 4; ++e)
+      acc[7][3][e] = fmaf(r1[e], PR ? sc[7] * sbj[PR ? 3 : 0][e] : sc[7], acc[7][3][e]);
   }
   // The last K-block has no barrier: wait for every wave before the epilogue
   // reuses the operand stages.
@@ -1450,7 +1497,8 @@ bool prefer_256(int64_t t256, int64_t t128, int cus) {
 }
 
 // per_row: weight scales per output row (block_n = 1, the deep-gemm layout);
-// only the decode kernel (M <= 48) and gemm_pipe128_kernel implement it.
+// only the decode kernel (M <= 48), gemm_pipe128_kernel and
+// gemm_pipe256_kernel implement it.
 Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
   const int KB = (int)(K / 128);
   const int cus = device_cu_count();
@@ -1485,7 +1533,7 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
     }
     return p;
   }
-  if (per_row) {
+  if (per_row && M <= 64) {
     p.cfg = CFG_128x128; p.bm = 128; p.bn = 128;
   } else if (M <= 32) {
     p.cfg = CFG_32x128; p.bm = 32; p.bn = 128;
@@ -1642,7 +1690,8 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
       else gemm_decode_kernel<3, false, true><<<grid, 512, 0, st>>>(a);
     } else if (pipe_ok(a, p)) {
       dim3 grid(a.tiles_m * a.tiles_n, 1, p.splits);
-      gemm_pipe128_kernel<64, 32, true><<<grid, 512, 0, st>>>(a);
+      if (p.cfg == CFG_256x256) gemm_pipe256_kernel<true><<<grid, 512, 0, st>>>(a);
+      else gemm_pipe128_kernel<64, 32, true><<<grid, 512, 0, st>>>(a);
     } else {
       return run_generic();
     }
@@ -1672,7 +1721,7 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
     case CFG_256x256: {
       if (pipe_ok(a, p)) {
         dim3 grid(a.tiles_m * a.tiles_n, 1, p.splits);
-        gemm_pipe256_kernel<<<grid, 512, 0, st>>>(a);
+        gemm_pipe256_kernel<false><<<grid, 512, 0, st>>>(a);
       } else {
         launch_cfg<256, 256, 64, 128>(a, p.splits, st);
       }

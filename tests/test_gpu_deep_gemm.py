@@ -3,7 +3,7 @@ gemm_fp8_fp8_bf16_nt, deep-gemm-helion/.../deep_gemm_helion/fp8.py:13-29:
 (A*As) @ (B*Bs)^T with Bs [N, K/128]) against the oracle's blockwise formula
 with block_n = 1, within the north-star tolerance (1e-2 relative, 1e-3
 absolute of the bf16 result). Covers the decode kernel (M <= 48), the 128x128
-pipelined kernel with and without split-K, the generic fallback (column-major
+and 256x256 pipelined kernels, split-K, the generic fallback (column-major
 As) and ragged edges."""
 import pytest
 import torch
@@ -61,6 +61,23 @@ def test_per_row_full_check_and_fp32(dev):
                                atol=ATOL)
     f32 = fp8.w8a8_block_fp8_matmul(q, Wd, s, Bsd, [1, 128], torch.float32)
     assert torch.equal(f32.to(torch.bfloat16), out)
+
+
+@pytest.mark.parametrize("M,N,K", [(2999, 4000, 1536), (4096, 4096, 8192)])
+def test_per_row_256_tiles(M, N, K, dev):
+    """Grids that get 256x256 tiles: a partial wave with ragged edges and a
+    K-block count (12) that leaves the second 8-block scale window half
+    empty, and the full 4096-square wave. Every element against torch's fp32
+    dequant-matmul."""
+    print(f"deep-gemm per-row 256x256 tiles M={M} N={N} K={K}", flush=True)
+    x, Wq, Bs = _operands(M, N, K, seed=7)
+    q, s = fp8.act_quant(x.to(dev), 128)
+    Wd, Bsd = Wq.to(dev), Bs.to(dev)
+    out = dg.gemm_fp8_fp8_bf16_nt(q, Wd, s, Bsd)
+    full = (q.float() * s.repeat_interleave(128, 1)) @ (Wd.float() * Bsd.repeat_interleave(
+        128, 1)).T
+    torch.testing.assert_close(out.float(), full.to(torch.bfloat16).float(), rtol=RTOL,
+                               atol=ATOL)
 
 
 def test_per_row_generic_fallback(dev):
