@@ -18,49 +18,62 @@
 #include "common.h"
 #include "quant.h"
 
+#include <algorithm>
+
 namespace fp8b {
 
 // Fast path: group = 128, K % 128 == 0, 16-byte aligned rows of x, 8-byte
-// aligned rows of q. 16 lanes per group; each 16-lane row handles UNROLL
-// groups spaced one block-stride apart and issues all their loads before
-// converting any of them, so a wave keeps UNROLL KiB of reads in flight.
-// Small inputs (decode: a few rows) use UNROLL = 1 so that the groups spread
-// over as many CUs as possible and the kernel is one load latency long.
-template <int kQuantUnroll>
+// aligned rows of q. 16 lanes per group (one 16-byte load each). Block
+// (bx, by) quantises groups bx*16U .. bx*16U + 16U - 1 of rows by,
+// by + gridDim.y, ...: 16-lane row r of the block takes groups
+// bx*16U + r + 16u, u < U, and issues all U loads before converting any.
+// The row is uniform over the block, so its base addresses are scalar and
+// each lane adds a 32-bit offset (no per-lane index division).
+template <int U>
 __global__ void __launch_bounds__(256)
 act_quant_g128_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                       uint8_t* __restrict__ q, int64_t ldq,
                       float* __restrict__ s, int64_t ssm, int64_t ssg,
-                      uint32_t groups, uint32_t groups_per_row) {
+                      uint32_t rows, uint32_t groups_per_row) {
   const uint32_t sub = threadIdx.x & 15u;
-  const uint32_t g_first =
-      (uint32_t)(((uint64_t)blockIdx.x * kQuantUnroll * 256u + threadIdx.x) >> 4);
-  v4i raw[kQuantUnroll];
-  uint32_t mm[kQuantUnroll], gg[kQuantUnroll];
+  const uint32_t g0 = blockIdx.x * 16u * U + (threadIdx.x >> 4);
+  for (uint32_t m = blockIdx.y; m < rows; m += gridDim.y) {
+    const uint16_t* xr = x + (int64_t)m * ldx;
+    v4i raw[U];
 #pragma unroll
-  for (int u = 0; u < kQuantUnroll; ++u) {
-    const uint32_t gi = g_first + u * 16u;  // 16 groups per 256 threads
-    const uint32_t gc = gi < groups ? gi : groups - 1;  // uniform per 16-lane row
-    mm[u] = gc / groups_per_row;
-    gg[u] = gc - mm[u] * groups_per_row;
-    raw[u] = __builtin_nontemporal_load(
-        reinterpret_cast<const v4i*>(x + (int64_t)mm[u] * ldx + gg[u] * 128u + sub * 8u));
-  }
+    for (int u = 0; u < U; ++u) {
+      const uint32_t g = min(g0 + 16u * u, groups_per_row - 1);  // uniform per 16-lane row
+      raw[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(xr + g * 128u + sub * 8u));
+    }
+    uint8_t* qr = q + (int64_t)m * ldq;
+    float* sr = s + (int64_t)m * ssm;
 #pragma unroll
-  for (int u = 0; u < kQuantUnroll; ++u) {
-    if (g_first + u * 16u >= groups) break;  // uniform across the 16-lane group
-    float v[8];
-    const uint32_t mag = unpack_bf16x8(raw[u], v);
-    uint32_t w0, w1;
-    float scale;
-    quant_row16_8(v, mag, w0, w1, scale);
-    v2i packed;
-    packed[0] = (int)w0;
-    packed[1] = (int)w1;
-    __builtin_nontemporal_store(
-        packed, reinterpret_cast<v2i*>(q + (int64_t)mm[u] * ldq + gg[u] * 128u + sub * 8u));
-    if (sub == 0) s[(int64_t)mm[u] * ssm + (int64_t)gg[u] * ssg] = scale;
+    for (int u = 0; u < U; ++u) {
+      const uint32_t g = g0 + 16u * u;
+      if (g >= groups_per_row) break;  // uniform across the 16-lane group
+      float v[8];
+      const uint32_t mag = unpack_bf16x8(raw[u], v);
+      uint32_t w0, w1;
+      float scale;
+      quant_row16_8(v, mag, w0, w1, scale);
+      v2i packed;
+      packed[0] = (int)w0;
+      packed[1] = (int)w1;
+      __builtin_nontemporal_store(packed, reinterpret_cast<v2i*>(qr + g * 128u + sub * 8u));
+      if (sub == 0) sr[(int64_t)g * ssg] = scale;
+    }
   }
+}
+
+// Groups per block column of the fast kernels: 16*U with U in {4, 2, 1},
+// the largest that divides the groups of a row (no idle lanes at the row's
+// end), and 1 when there are few groups in all (decode: spread them over
+// as many CUs as possible).
+inline int g128_unroll(int64_t rows, int64_t gpr) {
+  if (rows * gpr < 16 * 1024) return 1;
+  if (gpr % 64 == 0) return 4;
+  if (gpr % 32 == 0) return 2;
+  return 1;
 }
 
 // Scalar reference-shaped path for any group size, ragged K or unaligned
@@ -168,52 +181,53 @@ silu_and_mul_generic_kernel(const uint16_t* __restrict__ x, int64_t ldx,
 
 // Fused silu_and_mul + group-128 quantisation: identical arithmetic to
 // silu_and_mul_vec_kernel followed by act_quant_g128_kernel, without the
-// bf16 round trip through memory. Requires d % 128 == 0. Each 16-lane row
-// handles U groups (16 groups apart) and issues all their loads first, as
-// act_quant_g128_kernel does.
+// bf16 round trip through memory. Requires d % 128 == 0. Blocks and 16-lane
+// rows map to (row, group) as in act_quant_g128_kernel; each lane loads its
+// 8 gate and 8 up values of U groups before converting any.
 template <int U>
 __global__ void __launch_bounds__(256)
 silu_mul_quant_g128_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                            uint8_t* __restrict__ q, int64_t ldq,
                            float* __restrict__ s, int64_t ssm, int64_t ssg,
-                           uint32_t groups, uint32_t groups_per_row, int64_t d) {
+                           uint32_t rows, uint32_t groups_per_row, int64_t d) {
   const uint32_t sub = threadIdx.x & 15u;
-  const uint32_t g_first = (uint32_t)(((uint64_t)blockIdx.x * U * 256u + threadIdx.x) >> 4);
-  v4i gr[U], ur[U];
-  uint32_t mm[U], gg[U];
+  const uint32_t g0 = blockIdx.x * 16u * U + (threadIdx.x >> 4);
+  for (uint32_t m = blockIdx.y; m < rows; m += gridDim.y) {
+    const uint16_t* xr = x + (int64_t)m * ldx;
+    const uint16_t* ur_ = xr + d;
+    v4i gr[U], ur[U];
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const uint32_t gi = g_first + u * 16u;
-    const uint32_t gc = gi < groups ? gi : groups - 1;  // uniform per 16-lane row
-    mm[u] = gc / groups_per_row;
-    gg[u] = gc - mm[u] * groups_per_row;
-    const uint16_t* xr = x + (int64_t)mm[u] * ldx + gg[u] * 128u + sub * 8u;
-    gr[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(xr));
-    ur[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(xr + d));
-  }
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    if (g_first + u * 16u >= groups) break;  // uniform across the 16-lane group
-    float v[8];
-    uint32_t mag = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t gw = (uint32_t)gr[u][i], uw = (uint32_t)ur[u][i];
-      const uint32_t lo = silu_mul_bits(gw & 0xFFFFu, uw & 0xFFFFu);
-      const uint32_t hi = silu_mul_bits(gw >> 16, uw >> 16);
-      v[2 * i] = bf16_to_f32(lo);
-      v[2 * i + 1] = bf16_to_f32(hi);
-      mag = max(mag, max(lo & 0x7FFFu, hi & 0x7FFFu));
+    for (int u = 0; u < U; ++u) {
+      const uint32_t g = min(g0 + 16u * u, groups_per_row - 1);  // uniform per 16-lane row
+      gr[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(xr + g * 128u + sub * 8u));
+      ur[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(ur_ + g * 128u + sub * 8u));
     }
-    uint32_t w0, w1;
-    float scale;
-    quant_row16_8(v, mag, w0, w1, scale);
-    v2i packed;
-    packed[0] = (int)w0;
-    packed[1] = (int)w1;
-    __builtin_nontemporal_store(
-        packed, reinterpret_cast<v2i*>(q + (int64_t)mm[u] * ldq + gg[u] * 128u + sub * 8u));
-    if (sub == 0) s[(int64_t)mm[u] * ssm + (int64_t)gg[u] * ssg] = scale;
+    uint8_t* qr = q + (int64_t)m * ldq;
+    float* sr = s + (int64_t)m * ssm;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t g = g0 + 16u * u;
+      if (g >= groups_per_row) break;  // uniform across the 16-lane group
+      float v[8];
+      v4i h;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t gw = (uint32_t)gr[u][i], uw = (uint32_t)ur[u][i];
+        const uint32_t lo = silu_mul_bits(gw & 0xFFFFu, uw & 0xFFFFu);
+        const uint32_t hi = silu_mul_bits(gw >> 16, uw >> 16);
+        v[2 * i] = bf16_to_f32(lo);
+        v[2 * i + 1] = bf16_to_f32(hi);
+        h[i] = (int)(lo | (hi << 16));
+      }
+      uint32_t w0, w1;
+      float scale;
+      quant_row16_8(v, max_mag_bf16x8(h), w0, w1, scale);
+      v2i packed;
+      packed[0] = (int)w0;
+      packed[1] = (int)w1;
+      __builtin_nontemporal_store(packed, reinterpret_cast<v2i*>(qr + g * 128u + sub * 8u));
+      if (sub == 0) sr[(int64_t)g * ssg] = scale;
+    }
   }
 }
 
@@ -277,18 +291,15 @@ extern "C" int fp8b_act_quant(const void* x, int64_t ldx, void* q, int64_t ldq,
   const bool fast = group == 128 && K % 128 == 0 && ldx % 8 == 0 && ldq % 8 == 0 &&
                     aligned(x, 16) && aligned(q, 8) && M * gpr < (int64_t(1) << 31);
   if (fast) {
-    const uint32_t groups = (uint32_t)(M * gpr);
-    if (groups < 16u * 1024u) {
-      const uint32_t blocks = (groups + 15u) / 16u;
-      act_quant_g128_kernel<1><<<blocks, 256, 0, st>>>((const uint16_t*)x, ldx, (uint8_t*)q, ldq,
-                                                       s, s_stride_m, s_stride_g, groups,
-                                                       (uint32_t)gpr);
-    } else {
-      const uint32_t blocks = (groups + 63u) / 64u;
-      act_quant_g128_kernel<4><<<blocks, 256, 0, st>>>((const uint16_t*)x, ldx, (uint8_t*)q, ldq,
-                                                       s, s_stride_m, s_stride_g, groups,
-                                                       (uint32_t)gpr);
-    }
+    const int U = g128_unroll(M, gpr);
+    const dim3 grid((unsigned)((gpr + 16 * U - 1) / (16 * U)), (unsigned)std::min<int64_t>(M, 65535));
+    auto launch = [&](auto kernel) {
+      kernel<<<grid, 256, 0, st>>>((const uint16_t*)x, ldx, (uint8_t*)q, ldq, s, s_stride_m,
+                                   s_stride_g, (uint32_t)M, (uint32_t)gpr);
+    };
+    if (U == 4) launch(act_quant_g128_kernel<4>);
+    else if (U == 2) launch(act_quant_g128_kernel<2>);
+    else launch(act_quant_g128_kernel<1>);
   } else {
     const int64_t groups = M * gpr;
     act_quant_generic_kernel<<<(unsigned)((groups + 63) / 64), 64, 0, st>>>(
@@ -345,15 +356,15 @@ extern "C" int fp8b_silu_and_mul_quant(const void* x, int64_t ldx, void* q, int6
   const bool fast = group == 128 && d % 128 == 0 && ldx % 8 == 0 && ldq % 8 == 0 &&
                     aligned(x, 16) && aligned(q, 8) && M * gpr < (int64_t(1) << 31);
   if (fast) {
-    const uint32_t groups = (uint32_t)(M * gpr);
-    if (groups >= 16384u)
-      silu_mul_quant_g128_kernel<4><<<(groups + 63u) / 64u, 256, 0, st>>>(
-          (const uint16_t*)x, ldx, (uint8_t*)q, ldq, s, s_stride_m, s_stride_g, groups,
-          (uint32_t)gpr, d);
-    else
-      silu_mul_quant_g128_kernel<1><<<(groups + 15u) / 16u, 256, 0, st>>>(
-          (const uint16_t*)x, ldx, (uint8_t*)q, ldq, s, s_stride_m, s_stride_g, groups,
-          (uint32_t)gpr, d);
+    const int U = g128_unroll(M, gpr);
+    const dim3 grid((unsigned)((gpr + 16 * U - 1) / (16 * U)), (unsigned)std::min<int64_t>(M, 65535));
+    auto launch = [&](auto kernel) {
+      kernel<<<grid, 256, 0, st>>>((const uint16_t*)x, ldx, (uint8_t*)q, ldq, s, s_stride_m,
+                                   s_stride_g, (uint32_t)M, (uint32_t)gpr, d);
+    };
+    if (U == 4) launch(silu_mul_quant_g128_kernel<4>);
+    else if (U == 2) launch(silu_mul_quant_g128_kernel<2>);
+    else launch(silu_mul_quant_g128_kernel<1>);
   } else {
     const int64_t groups = M * gpr;
     silu_mul_quant_generic_kernel<<<(unsigned)((groups + 63) / 64), 64, 0, st>>>(

@@ -3,7 +3,8 @@
 // Numerics (the contract written in include/fp8_blockwise.h):
 //   amax  = max |x| over the group, taken as the max of the 15-bit magnitude
 //           patterns of the bf16 inputs, so NaN (pattern > 0x7F80) wins;
-//   scale = max(amax, 1e-10) / 448 as one IEEE fp32 division;
+//   scale = max(amax, 1e-10) / 448, rounded as one IEEE fp32 division is
+//           (computed without one: scale_from_amax);
 //   q     = e4m3fn(x / scale) rounded to nearest even.
 //   NaN group -> scale NaN, q = 0x7F; +inf group -> scale +inf, q = signed
 //   zero for finite x and 0x7F for +-inf.
@@ -26,6 +27,29 @@ __device__ __forceinline__ float div_by_scale(float x, float s, float recip) {
   return __builtin_copysignf(fmaf(r, recip, q0), x);
 }
 
+// scale = amax / 448 rounded to nearest even without a division: with
+// c = RN(1/448), q0 = RN(amax*c) is within an ulp of the quotient, the
+// residual amax - q0*448 is exact in one FMA, and RN(q0 + r*c) is the
+// correctly rounded quotient (Markstein). Bit-identical to the IEEE division
+// for every amax the kernels form (every finite bf16 magnitude, floored at
+// 1e-10): checked exhaustively in tests/scale_recip_check.c.
+__device__ __forceinline__ float scale_from_amax(float amax) {
+  constexpr float c = 0x1.24924ap-9f;  // RN(1/448)
+  const float q0 = amax * c;
+  const float r = fmaf(-q0, kFp8Max, amax);
+  return fmaf(r, c, q0);
+}
+
+// RN(1/s) for a group scale: v_rcp_f32 is within one ulp of 1/s, and one
+// Newton step y + y*(1 - s*y) (the residual exact in an FMA) then rounds to
+// the correctly rounded reciprocal for every s whose mantissa is not all
+// ones; no scale_from_amax() result has one. Both facts are checked
+// exhaustively in tests/scale_recip_check.c.
+__device__ __forceinline__ float recip_of_scale(float s) {
+  const float y = __builtin_amdgcn_rcpf(s);
+  return fmaf(fmaf(-s, y, 1.0f), y, y);
+}
+
 // Quantise 8 values held by one lane of a 16-lane group of 128.
 // `mag` is the max over this lane's 8 bf16 magnitude patterns.
 __device__ __forceinline__ void quant_row16_8(const float v[8], uint32_t mag,
@@ -34,8 +58,8 @@ __device__ __forceinline__ void quant_row16_8(const float v[8], uint32_t mag,
   const uint32_t gmag = row16_max_u32(mag);
   if (gmag < 0x7F80u) {
     const float amax = fmaxf(bf16_to_f32(gmag), kAmaxFloor);
-    scale = amax / kFp8Max;
-    const float recip = 1.0f / scale;
+    scale = scale_from_amax(amax);
+    const float recip = recip_of_scale(scale);
     float y[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) y[i] = div_by_scale(v[i], scale, recip);
@@ -60,18 +84,27 @@ __device__ __forceinline__ void quant_row16_8(const float v[8], uint32_t mag,
   }
 }
 
+// Max over the 8 bf16 magnitude patterns of one 16-byte load: sign bits
+// cleared, then packed 16-bit maxima (v_pk_max_u16).
+__device__ __forceinline__ uint32_t max_mag_bf16x8(const v4i raw) {
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  u16x2 h[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) h[i] = __builtin_bit_cast(u16x2, (uint32_t)raw[i] & 0x7FFF7FFFu);
+  const u16x2 m = __builtin_elementwise_max(__builtin_elementwise_max(h[0], h[1]),
+                                            __builtin_elementwise_max(h[2], h[3]));
+  return max((uint32_t)m[0], (uint32_t)m[1]);
+}
+
 // Unpack 8 bf16 (one 16-byte load) into fp32 values and the max magnitude.
 __device__ __forceinline__ uint32_t unpack_bf16x8(const v4i raw, float v[8]) {
-  uint32_t mag = 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t w = (uint32_t)raw[i];
-    const uint32_t lo = w & 0xFFFFu, hi = w >> 16;
-    v[2 * i] = bf16_to_f32(lo);
-    v[2 * i + 1] = bf16_to_f32(hi);
-    mag = max(mag, max(lo & 0x7FFFu, hi & 0x7FFFu));
+    v[2 * i] = __uint_as_float(w << 16);
+    v[2 * i + 1] = __uint_as_float(w & 0xFFFF0000u);
   }
-  return mag;
+  return max_mag_bf16x8(raw);
 }
 
 }  // namespace fp8b

@@ -25,3 +25,21 @@ def test_fast_division_matches_ieee_for_fp8(tmp_path):
     fields = dict(kv.split("=") for kv in r.stdout.split())
     assert int(fields["pairs"]) > 10**9
     assert fields["large"] == "0" and fields["sign"] == "0"
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="needs gcc")
+def test_division_free_scale_and_reciprocal(tmp_path):
+    """The kernels form scale = amax/448 with one multiply and two FMAs and
+    its reciprocal from v_rcp_f32 with one Newton step; both must give the
+    IEEE results bit for bit on their whole domain (scale_recip_check.c)."""
+    src = Path(__file__).parent / "scale_recip_check.c"
+    exe = tmp_path / "scale_recip_check"
+    subprocess.run(["gcc", "-O2", "-ffp-contract=off", str(src), "-o", str(exe), "-lm"],
+                   check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout
+    fields = dict(kv.split("=") for kv in r.stdout.split())
+    assert int(fields["scales"]) == 0x7F80 and fields["scale_bad"] == "0"
+    assert fields["allones_scales"] == "0"
+    assert int(fields["recip_bad_mantissas"]) <= 1  # only the all-ones mantissa

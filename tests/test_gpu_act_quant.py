@@ -83,6 +83,24 @@ def test_act_quant_scales_sweep_exact(dev):
     _assert_exact(x, 128, dev)
 
 
+def test_act_quant_every_amax_exact(dev):
+    """One group per finite bf16 magnitude as its amax (0 included): the
+    scale and its reciprocal, formed without a division, take every value
+    the kernels can produce; the group's other 127 values are random bf16
+    no larger in magnitude, with random signs."""
+    print("act_quant every amax", flush=True)
+    g = torch.Generator().manual_seed(11)
+    amax = torch.arange(0, 0x7F80, dtype=torch.int32)                     # 32640 patterns
+    frac = torch.rand(amax.numel(), 127, generator=g)
+    others = (frac * (amax[:, None].float() + 1)).floor().clamp(max=amax[:, None].float())
+    pats = torch.cat([amax[:, None], others.to(torch.int32)], 1)
+    signs = torch.randint(0, 2, pats.shape, generator=g, dtype=torch.int32) << 15
+    perm = torch.argsort(torch.rand(pats.shape, generator=g), 1)            # amax anywhere
+    pats = torch.gather(pats | signs, 1, perm)
+    x = pats.to(torch.int16).view(torch.bfloat16).reshape(-1, 64 * 128)     # 510 x 8192
+    _assert_exact(x, 128, dev)
+
+
 def test_act_quant_nonfinite_and_zero_groups(dev):
     print("act_quant nonfinite", flush=True)
     x = torch.randn(4, 512).to(torch.bfloat16)
