@@ -51,7 +51,27 @@ struct GemmArgs {
   int tiles_m, tiles_n;
   int out_dtype;     // fp8b_dtype; ignored when writing split-K partials
   int vec_store;     // 1 if 4 consecutive outputs can be stored as one vector
+  // gemm_pipe128_kernel only: when rem_base >= 0, workgroup w computes
+  // quarter w % 4 of 256x256 tile rem_base + w / 4 of a rem_tiles_m x
+  // rem_tiles_n grid (the tiles a gemm_pipe256_kernel launch of rem_base
+  // workgroups left), instead of 128x128 tile w.
+  int rem_base, rem_tiles_m, rem_tiles_n;
 };
+
+// Workgroup -> output tile of a tiles_m x tiles_n grid: XCD-contiguous runs
+// (workgroup b runs on XCD b % 8, so b goes to tile (b % 8) * tiles/8 + b/8
+// when 8 divides the tile count), walked in groups of 8 tile rows.
+__device__ __forceinline__ void tile_of_bid(int bid, int tiles_m, int tiles_n, int& tm,
+                                            int& tn) {
+  const int tiles = tiles_m * tiles_n;
+  if (tiles % 8 == 0) bid = (bid & 7) * (tiles >> 3) + (bid >> 3);
+  constexpr int GROUP_M = 8;
+  const int group_size = GROUP_M * tiles_n;
+  const int first_m = (bid / group_size) * GROUP_M;
+  const int gm = min(tiles_m - first_m, GROUP_M);
+  tm = first_m + (bid % group_size) % gm;
+  tn = (bid % group_size) / gm;
+}
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -409,17 +429,8 @@ __global__ void __launch_bounds__(512) gemm_pipe256_kernel(GemmArgs a) {
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wid / NWN, wn = wid % NWN;
 
-  // Workgroup -> tile: XCD-contiguous runs walked in groups of 8 tile rows
-  // (as in gemm_bs128_kernel).
-  const int tiles = a.tiles_m * a.tiles_n;
-  int bid = blockIdx.x;
-  if (tiles % 8 == 0) bid = (bid & 7) * (tiles >> 3) + (bid >> 3);
-  constexpr int GROUP_M = 8;
-  const int group_size = GROUP_M * a.tiles_n;
-  const int first_m = (bid / group_size) * GROUP_M;
-  const int gm = min(a.tiles_m - first_m, GROUP_M);
-  const int tm = first_m + (bid % group_size) % gm;
-  const int tn = (bid % group_size) / gm;
+  int tm, tn;
+  tile_of_bid((int)blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
 
   const int split = blockIdx.z;
@@ -713,16 +724,17 @@ __global__ void __launch_bounds__((128 / WM) * (128 / WN) * 64) gemm_pipe128_ker
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wid / NWN, wn = wid % NWN;
 
-  const int tiles = a.tiles_m * a.tiles_n;
-  int bid = blockIdx.x;
-  if (tiles % 8 == 0) bid = (bid & 7) * (tiles >> 3) + (bid >> 3);
-  constexpr int GROUP_M = 8;
-  const int group_size = GROUP_M * a.tiles_n;
-  const int first_m = (bid / group_size) * GROUP_M;
-  const int gm = min(a.tiles_m - first_m, GROUP_M);
-  const int tm = first_m + (bid % group_size) % gm;
-  const int tn = (bid % group_size) / gm;
+  int tm, tn;
+  if (a.rem_base >= 0) {
+    // a quarter of one of the 256x256 tiles a gemm_pipe256_kernel launch left
+    tile_of_bid(a.rem_base + (int)blockIdx.x / 4, a.rem_tiles_m, a.rem_tiles_n, tm, tn);
+    tm = 2 * tm + (((int)blockIdx.x >> 1) & 1);
+    tn = 2 * tn + ((int)blockIdx.x & 1);
+  } else {
+    tile_of_bid((int)blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
+  }
   const int m0 = tm * BM, n0 = tn * BN;
+  if (m0 >= a.M || n0 >= a.N) return;  // a quarter past the matrix edge (whole workgroup)
 
   const int split = blockIdx.z;
   const int kb_begin = split * a.kb_per_split;
@@ -1585,6 +1597,35 @@ bool pipe_ok(const GemmArgs& a, const Plan& p) {
          splits_ok && 255 * std::max(a.lda, a.ldb) + a.K < (int64_t(1) << 32);
 }
 
+// One unsplit grid of 256x256 tiles on gemm_pipe256_kernel. When the tiles
+// leave a last partial wave of at most a quarter of the CUs, that wave's
+// tiles run as 128x128 quarters on gemm_pipe128_kernel (one wave), with the
+// same arithmetic per output: MLP gate/up 3001x28672x4096 has 1344 tiles,
+// five full waves and 64 left; the 64 tiles take 35 us as quarters against
+// ~40 us as a sixth wave. FP8B_TAIL128=0 keeps the whole grid on
+// gemm_pipe256_kernel (A/B measurements; read on every call so that tests
+// can compare both).
+template <bool PR>
+void launch_pipe256(const GemmArgs& a, hipStream_t st) {
+  const char* e = getenv("FP8B_TAIL128");
+  const bool tail_on = !(e && e[0] == '0');
+  const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
+  const int64_t cus = device_cu_count();
+  const int64_t full = tiles / cus * cus, rest = tiles - full;
+  if (!tail_on || full == 0 || rest == 0 || 4 * rest > cus || a.kb_per_split < a.KB) {
+    gemm_pipe256_kernel<PR><<<(unsigned)tiles, 512, 0, st>>>(a);
+    return;
+  }
+  gemm_pipe256_kernel<PR><<<(unsigned)full, 512, 0, st>>>(a);
+  GemmArgs r = a;
+  r.rem_base = (int)full;
+  r.rem_tiles_m = a.tiles_m;
+  r.rem_tiles_n = a.tiles_n;
+  r.tiles_m = (a.M + 127) / 128;
+  r.tiles_n = (a.N + 127) / 128;
+  gemm_pipe128_kernel<64, 32, PR><<<(unsigned)(4 * rest), 512, 0, st>>>(r);
+}
+
 template <int BM, int BN, int WM, int WN>
 void launch_cfg(const GemmArgs& a, int splits, hipStream_t st) {
   dim3 grid(a.tiles_m * a.tiles_n, 1, splits);
@@ -1674,6 +1715,7 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
   a.tiles_m = (int)((M + p.bm - 1) / p.bm);
   a.tiles_n = (int)((N + p.bn - 1) / p.bn);
   a.out_dtype = out_dtype;
+  a.rem_base = -1; a.rem_tiles_m = 0; a.rem_tiles_n = 0;
   // Vector stores: 4 fp32 (16 B) for fp32 C and split-K partials, 8 x 16-bit
   // (16 B) for bf16/fp16 C.
   const bool c_vec = esz == 4 ? (ldc % 4 == 0 && ((uintptr_t)C & 15) == 0)
@@ -1690,7 +1732,7 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
       else gemm_decode_kernel<3, false, true><<<grid, 512, 0, st>>>(a);
     } else if (pipe_ok(a, p)) {
       dim3 grid(a.tiles_m * a.tiles_n, 1, p.splits);
-      if (p.cfg == CFG_256x256) gemm_pipe256_kernel<true><<<grid, 512, 0, st>>>(a);
+      if (p.cfg == CFG_256x256) launch_pipe256<true>(a, st);
       else gemm_pipe128_kernel<64, 32, true><<<grid, 512, 0, st>>>(a);
     } else {
       return run_generic();
@@ -1720,8 +1762,7 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
     }
     case CFG_256x256: {
       if (pipe_ok(a, p)) {
-        dim3 grid(a.tiles_m * a.tiles_n, 1, p.splits);
-        gemm_pipe256_kernel<false><<<grid, 512, 0, st>>>(a);
+        launch_pipe256<false>(a, st);
       } else {
         launch_cfg<256, 256, 64, 128>(a, p.splits, st);
       }
@@ -1836,6 +1877,7 @@ extern "C" int fp8b_act_quant_matmul(const void* x, int64_t ldx, const void* B, 
   a.tiles_m = 1;
   a.tiles_n = (int)((N + 127) / 128);
   a.out_dtype = out_dtype;
+  a.rem_base = -1; a.rem_tiles_m = 0; a.rem_tiles_n = 0;
   const size_t esz = out_dtype == FP8B_F32 ? 4 : 2;
   const bool c_vec = esz == 4 ? (ldc % 4 == 0 && ((uintptr_t)C & 15) == 0)
                               : (ldc % 8 == 0 && ((uintptr_t)C & 15) == 0);

@@ -317,3 +317,39 @@ def test_gemm_zero_k_gives_zeros(dev):
     out = fp8.w8a8_block_fp8_matmul(A, B, torch.empty(4, 0, device=dev),
                                     torch.empty(1, 0, device=dev), [128, 128], torch.float32)
     assert out.shape == (4, 8) and torch.equal(out, torch.zeros_like(out))
+
+
+@pytest.mark.parametrize("M,N,K,block_n", [(3001, 28672, 4096, 128), (4224, 4096, 1024, 128),
+                                           (4096, 4224, 1024, 128), (4100, 4096, 2048, 128),
+                                           (4224, 4096, 1024, 1)])
+def test_gemm_partial_last_wave_on_128_tiles(M, N, K, block_n, dev):
+    """Grids of 256x256 tiles that leave a last partial wave of at most a
+    quarter of the CUs run it as 128x128 quarters on the 128x128 kernel; the
+    per-output arithmetic is the same, so the result must equal the one-kernel
+    grid (FP8B_TAIL128=0) bit for bit. Covers the MLP gate/up shape (1344
+    tiles), quarters past the M or N edge (4224 = 16.5 tiles), a ragged last
+    row of tiles, and per-row weight scales."""
+    import os
+    print(f"gemm 128x128 tail M={M} N={N} K={K} block_n={block_n}", flush=True)
+    x = synthetic.activations(M, K, seed=M + N)
+    q, s = fp8.act_quant(x.to(dev), 128)
+    W, Bs = synthetic.weights(N, K, seed=N, block_n=block_n)
+    W, Bs = W.to(dev), Bs.to(dev)
+    f = lambda: fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [block_n, 128], torch.bfloat16)
+    out = f()
+    old = os.environ.get("FP8B_TAIL128")
+    os.environ["FP8B_TAIL128"] = "0"
+    try:
+        ref = f()
+    finally:
+        if old is None:
+            del os.environ["FP8B_TAIL128"]
+        else:
+            os.environ["FP8B_TAIL128"] = old
+    torch.testing.assert_close(out, ref, rtol=0, atol=0)
+    rows = torch.tensor([0, M // 2, M - 1])
+    orc = oracle.block_gemm(_u8(q.cpu()[rows]), _u8(W.cpu()), s.cpu()[rows].numpy(),
+                            Bs.cpu().numpy(), (block_n, 128))
+    torch.testing.assert_close(out[rows.to(dev)].float().cpu(),
+                               torch.from_numpy(orc).to(torch.bfloat16).float(),
+                               rtol=RTOL, atol=ATOL)
