@@ -9,10 +9,15 @@
 // Numerics (the contract written in include/fp8_blockwise.h):
 //   amax  = max |x| over the group, taken as the max of the 15-bit magnitude
 //           patterns of the bf16 inputs, so NaN (pattern > 0x7F80) wins;
-//   scale = max(amax, 1e-10) / 448 as one IEEE fp32 division;
-//   q     = e4m3fn(x / scale): IEEE fp32 division, then the gfx950 OCP fp8
-//           convert (round to nearest even). |x/scale| <= 448 * (1 + 2^-23)
-//           for finite groups, which the convert rounds into range.
+//   scale = max(amax, 1e-10) / 448 rounded as one IEEE fp32 division;
+//   q     = e4m3fn(x / scale) with the quotient rounded as IEEE fp32
+//           division, then the gfx950 OCP fp8 convert (round to nearest
+//           even). |x/scale| <= 448 * (1 + 2^-23) for finite groups, which
+//           the convert rounds into range.
+// The kernels form the scale, its reciprocal and the quotients without
+// division instructions (quant.h); the results are the IEEE ones, checked
+// over their whole input domain in tests/scale_recip_check.c and
+// tests/fastdiv_check.c.
 //   NaN group -> scale NaN, q = 0x7F; +inf group -> scale +inf, q = signed
 //   zero for finite x and 0x7F for +-inf.
 #include "common.h"
