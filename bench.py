@@ -40,9 +40,11 @@ def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
-    # The GPU clock ramps over the first ~10 ms of sustained MFMA work; 200
-    # warmup steps (~25 ms for the headline GEMM) reach the steady state.
-    p.add_argument("--warmup", type=int, default=200)
+    # The GPU clock and power state settle over the first ~100 ms of
+    # sustained MFMA work: after 200 warmup steps (~22 ms) the headline step
+    # still measured 112-113 us, after 1000 or 3000 steps 109.5-110.3 us
+    # (the kernel alone: 110 us either way).
+    p.add_argument("--warmup", type=int, default=1000)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--only", default=None,
