@@ -37,6 +37,14 @@ def test_act_quant_g128_exact(M, K, dev):
     _assert_exact(x, 128, dev)
 
 
+@pytest.mark.parametrize("M,K", [(70000, 256), (66000, 1024)])
+def test_act_quant_more_rows_than_grid_y(M, K, dev):
+    """Rows past the 65535 grid rows: each block walks rows m, m + 65535, ..."""
+    print(f"act_quant rows M={M} K={K}", flush=True)
+    x = synthetic.activations(M, K, seed=M + K)
+    _assert_exact(x, 128, dev)
+
+
 def test_act_quant_outliers_exact(dev):
     print("act_quant outliers", flush=True)
     x = synthetic.activations(256, 4096, seed=99, outlier_frac=0.01)

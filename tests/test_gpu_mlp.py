@@ -41,7 +41,7 @@ def test_silu_and_mul_3d(dev):
 
 
 @pytest.mark.parametrize("M,d,group", [(3001, 14336, 128), (5, 384, 128), (9, 200, 64),
-                                       (4, 256, 256)])
+                                       (4, 256, 256), (70000, 256, 128)])
 def test_silu_and_mul_quant_equals_two_ops(M, d, group, dev):
     """Fused kernel == silu_and_mul then act_quant, bit for bit."""
     print(f"silu_and_mul_quant M={M} d={d} group={group}", flush=True)
