@@ -49,7 +49,7 @@ def parse():
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--only", default=None,
                    help="profile helper: run only one workload "
-                        "(gemm|act_quant|decode|decode_fused|weight_quant|mlp|medium|small|deep_gemm|"
+                        "(gemm|act_quant|decode|decode_fused|weight_quant|mlp|mlp_il|medium|small|deep_gemm|"
                         "deep_decode|copy)"
                         " for --steps steps and exit without JSON")
     return p.parse_args()
@@ -425,6 +425,20 @@ def secondary(torch, fp8, synthetic, dev):
     res["mlp_chain_3001"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(fl / ms / 1e9, 1),
                              "pct_fp8_peak": round(100 * fl / ms / 1e9 / PEAK_FP8_TFLOPS, 1)}
     log(f"mlp: {res['mlp_chain_3001']}")
+    # the same chain with the gate/up weight interleaved once (outside the
+    # timing): the gate/up GEMM's epilogue applies SiLU·up and the act-quant
+    wi, si = fp8.interleave_gate_up(w13, s13)
+    y0 = fp8.fp8_mlp(x, w13, s13, w2, s2)
+    y1 = fp8.fp8_mlp(x, wi, si, w2, s2, gate_up_interleaved=True)
+    assert torch.equal(y0, y1), "interleaved MLP chain differs from the default chain"
+    del w13, s13, y0, y1
+    ms = time_events(lambda: fp8.fp8_mlp(x, wi, si, w2, s2, gate_up_interleaved=True),
+                     10, 3, torch)
+    res["mlp_chain_3001_interleaved"] = {
+        "us": round(ms * 1e3, 2), "TFLOP/s": round(fl / ms / 1e9, 1),
+        "pct_fp8_peak": round(100 * fl / ms / 1e9 / PEAK_FP8_TFLOPS, 1),
+        "equals_default_chain": True}
+    log(f"mlp interleaved: {res['mlp_chain_3001_interleaved']}")
     return res
 
 
@@ -492,6 +506,14 @@ def run_only(what, steps, warmup, torch, fp8, synthetic, dev):
         w2, s2 = _gpu_weights(H, I, 51, dev, torch, synthetic)
         x = _gpu_acts(M, H, 52, dev, torch)
         fn = lambda: fp8.fp8_mlp(x, w13, s13, w2, s2)
+    elif what == "mlp_il":
+        M, H, I = 3001, 4096, 14336
+        w13, s13 = _gpu_weights(2 * I, H, 50, dev, torch, synthetic)
+        wi, si = fp8.interleave_gate_up(w13, s13)
+        del w13, s13
+        w2, s2 = _gpu_weights(H, I, 51, dev, torch, synthetic)
+        x = _gpu_acts(M, H, 52, dev, torch)
+        fn = lambda: fp8.fp8_mlp(x, wi, si, w2, s2, gate_up_interleaved=True)
     else:
         raise SystemExit(f"unknown --only {what}")
     ms = time_events(fn, steps, warmup, torch)

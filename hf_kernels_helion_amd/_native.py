@@ -54,6 +54,11 @@ SIGNATURES = {
     "fp8b_silu_and_mul": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _i64, _vp]),
     "fp8b_silu_and_mul_quant": (
         ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _vp]),
+    "fp8b_gate_up_silu_quant": (
+        ctypes.c_int,
+        [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _i64,
+         _i64, _i64, _i64, _vp],
+    ),
 }
 
 _lock = threading.Lock()

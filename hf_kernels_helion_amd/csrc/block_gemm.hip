@@ -56,6 +56,11 @@ struct GemmArgs {
   // rem_tiles_n grid (the tiles a gemm_pipe256_kernel launch of rem_base
   // workgroups left), instead of 128x128 tile w.
   int rem_base, rem_tiles_m, rem_tiles_n;
+  // gemm_pipe256_kernel<false, true> only (the gate/up GEMM that writes
+  // silu(gate) * up quantised): C is the e4m3fn output [M, N/2] (row stride
+  // ldc) and the group scale of (m, g) goes to Sq[m * sq_sm + g * sq_sg].
+  float* Sq;
+  int64_t sq_sm, sq_sg;
 };
 
 // Workgroup -> output tile of a tiles_m x tiles_n grid: XCD-contiguous runs
@@ -132,12 +137,10 @@ __device__ __forceinline__ v8i lds_frag(const uint8_t* row, int c0, int r7) {
 // conflict-free), then stores whole 16-byte runs of each output row. Every
 // wave of the workgroup must call it (it contains a barrier).
 template <int WM, int WN>
-__device__ __forceinline__ void epilogue16(const GemmArgs& a, uint8_t* wbase,
-                                           const v4f (&acc)[WM / 16][WN / 16], int mw, int nw,
-                                           int lane) {
+__device__ __forceinline__ void stage16(uint8_t* wbase, const v4f (&acc)[WM / 16][WN / 16],
+                                        int lane, bool bf) {
   constexpr int FM = WM / 16, FN = WN / 16;
   constexpr int EPI_PITCH = WN * 2 + 16;
-  const bool bf = a.out_dtype == FP8B_BF16;
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -150,6 +153,14 @@ __device__ __forceinline__ void epilogue16(const GemmArgs& a, uint8_t* wbase,
                               (j * 16 + 4 * (lane >> 4)) * 2) = w;
     }
   }
+}
+
+template <int WM, int WN>
+__device__ __forceinline__ void epilogue16(const GemmArgs& a, uint8_t* wbase,
+                                           const v4f (&acc)[WM / 16][WN / 16], int mw, int nw,
+                                           int lane) {
+  constexpr int EPI_PITCH = WN * 2 + 16;
+  stage16<WM, WN>(wbase, acc, lane, a.out_dtype == FP8B_BF16);
   __syncthreads();
   constexpr int CPR = WN / 8;   // 16-byte chunks per wave row
   constexpr int RPP = 64 / CPR; // rows per pass
@@ -410,7 +421,15 @@ template <int KIND> struct PipeKind { static constexpr int value = KIND; };
 // 4-byte DMA lanes, one per row); each fold multiplies the row scale by the
 // lane's four column scales, read once per K-block per weight fragment as one
 // 16-byte load, each into the register its previous value just left.
-template <bool PR>
+//
+// SWIGLU (gate/up GEMM of a gated MLP, weights interleaved in 128-row blocks
+// so that columns 0..127 of every 256-column tile are gate columns and
+// 128..255 the matching up columns): the epilogue stages the bf16 tile in LDS
+// as epilogue16 does, then each 16-lane DPP row takes one tile row, forms
+// silu(gate) * up in bf16 (silu_mul_bits) and quantises the 128 results as
+// one group: e4m3fn codes to C [M, N/2], the scale to Sq. Bit-identical to
+// storing the bf16 tile, then silu_and_mul_quant.
+template <bool PR, bool SWIGLU = false>
 __global__ void __launch_bounds__(512) gemm_pipe256_kernel(GemmArgs a) {
   constexpr int BM = 256, BN = 256, WM = 128, WN = 64, NWN = BN / WN, NW = 8;
   constexpr int FM = WM / 16, FN = WN / 16;       // 8 activation, 4 weight fragments
@@ -674,6 +693,57 @@ __global__ void __launch_bounds__(512) gemm_pipe256_kernel(GemmArgs a) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
+  if constexpr (SWIGLU) {
+    stage16<WM, WN>(smem + wid * WM * EPI_PITCH, acc, lane, true);
+    __syncthreads();
+    // Thread t: tile row 32p + t/16 in pass p, output columns 8(t%16)..+7 of
+    // the group; its gate values sit in wave (row/128, (t%16)/8)'s staging
+    // area, the up values two waves further.
+    const int sub = tid & 15;
+    const int cb = (sub & 7) * 16;
+    const int half = sub >> 3;
+    uint8_t* qout = reinterpret_cast<uint8_t*>(a.C) + tn * 128 + sub * 8;
+    // All LDS reads first (the accumulators are dead, so registers are
+    // plentiful), then the eight rows' arithmetic back to back.
+    constexpr int NP = BM / 32;
+    v4i gv[NP], uv[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int r = p * 32 + (tid >> 4);
+      const uint8_t* row = smem + (r & (WM - 1)) * EPI_PITCH + cb;
+      const int wg = (r / WM) * NWN + half;
+      gv[p] = *reinterpret_cast<const v4i*>(row + wg * WM * EPI_PITCH);
+      uv[p] = *reinterpret_cast<const v4i*>(row + (wg + 2) * WM * EPI_PITCH);
+    }
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int r = p * 32 + (tid >> 4);
+      const v4i g = gv[p], u = uv[p];
+      float v[8];
+      v4i h;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t gw = (uint32_t)g[i], uw = (uint32_t)u[i];
+        const uint32_t lo = silu_mul_bits(gw & 0xFFFFu, uw & 0xFFFFu);
+        const uint32_t hi = silu_mul_bits(gw >> 16, uw >> 16);
+        v[2 * i] = bf16_to_f32(lo);
+        v[2 * i + 1] = bf16_to_f32(hi);
+        h[i] = (int)(lo | (hi << 16));
+      }
+      uint32_t w0, w1;
+      float scale;
+      quant_row16_8(v, max_mag_bf16x8(h), w0, w1, scale);
+      const int m = m0 + r;
+      if (m < a.M) {
+        v2i packed;
+        packed[0] = (int)w0;
+        packed[1] = (int)w1;
+        *reinterpret_cast<v2i*>(qout + (int64_t)m * a.ldc) = packed;
+        if (sub == 0) a.Sq[(int64_t)m * a.sq_sm + (int64_t)tn * a.sq_sg] = scale;
+      }
+    }
+    return;
+  }
   const bool to_ws = gridDim.z > 1;
   if (to_ws || a.out_dtype == FP8B_F32) {
 #pragma unroll
@@ -1716,6 +1786,7 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
   a.tiles_n = (int)((N + p.bn - 1) / p.bn);
   a.out_dtype = out_dtype;
   a.rem_base = -1; a.rem_tiles_m = 0; a.rem_tiles_n = 0;
+  a.Sq = nullptr; a.sq_sm = 0; a.sq_sg = 0;
   // Vector stores: 4 fp32 (16 B) for fp32 C and split-K partials, 8 x 16-bit
   // (16 B) for bf16/fp16 C.
   const bool c_vec = esz == 4 ? (ldc % 4 == 0 && ((uintptr_t)C & 15) == 0)
@@ -1878,6 +1949,7 @@ extern "C" int fp8b_act_quant_matmul(const void* x, int64_t ldx, const void* B, 
   a.tiles_n = (int)((N + 127) / 128);
   a.out_dtype = out_dtype;
   a.rem_base = -1; a.rem_tiles_m = 0; a.rem_tiles_n = 0;
+  a.Sq = nullptr; a.sq_sm = 0; a.sq_sg = 0;
   const size_t esz = out_dtype == FP8B_F32 ? 4 : 2;
   const bool c_vec = esz == 4 ? (ldc % 4 == 0 && ((uintptr_t)C & 15) == 0)
                               : (ldc % 8 == 0 && ((uintptr_t)C & 15) == 0);
@@ -1901,6 +1973,65 @@ extern "C" int fp8b_act_quant_matmul(const void* x, int64_t ldx, const void* B, 
       set_error("fp8b_act_quant_matmul: split-K reduce launch failed");
       return FP8B_ERR_LAUNCH;
     }
+  }
+  return FP8B_OK;
+}
+
+extern "C" int fp8b_gate_up_silu_quant(const void* A, int64_t lda, const void* B, int64_t ldb,
+                                       const float* As, int64_t as_sm, int64_t as_sk,
+                                       const float* Bs, int64_t bs_sn, int64_t bs_sk, void* q,
+                                       int64_t ldq, float* s, int64_t s_stride_m,
+                                       int64_t s_stride_g, int64_t M, int64_t I, int64_t K,
+                                       void* stream) {
+  if (M < 0 || I < 0 || K < 0 || lda < K || ldb < K || ldq < I) {
+    set_error("fp8b_gate_up_silu_quant: bad dims (need M,I,K >= 0, lda,ldb >= K, ldq >= I)");
+    return FP8B_ERR_DIMS;
+  }
+  if (I % 128 != 0 || K % 512 != 0 || K == 0) {
+    set_error("fp8b_gate_up_silu_quant: I must be a multiple of 128 and K a positive "
+              "multiple of 512");
+    return FP8B_ERR_DIMS;
+  }
+  if (M == 0 || I == 0) return FP8B_OK;
+  if (!A || !B || !As || !Bs || !q || !s) {
+    set_error("fp8b_gate_up_silu_quant: null pointer");
+    return FP8B_ERR_NULL;
+  }
+  const int64_t N = 2 * I;
+  if (!mfma_path_ok(A, lda, B, ldb, M, N, K, 128, 128) || as_sk != 1 || bs_sk != 1 ||
+      as_sm % 4 != 0 || bs_sn % 4 != 0 || ((uintptr_t)As & 15) != 0 ||
+      ((uintptr_t)Bs & 15) != 0 || ldq % 8 != 0 || ((uintptr_t)q & 7) != 0) {
+    set_error("fp8b_gate_up_silu_quant: need 16-byte aligned A, B (lda, ldb multiples of 16), "
+              "K-contiguous 16-byte aligned As, Bs (row strides multiples of 4) and an "
+              "8-byte aligned q with ldq a multiple of 8");
+    return FP8B_ERR_ALIGN;
+  }
+  if (255 * std::max(lda, ldb) + K >= (int64_t(1) << 32)) {
+    set_error("fp8b_gate_up_silu_quant: leading dimensions too large for 32-bit tile offsets");
+    return FP8B_ERR_DIMS;
+  }
+  GemmArgs a;
+  a.X = nullptr; a.ldx = 0;
+  a.A = (const uint8_t*)A; a.B = (const uint8_t*)B; a.As = As; a.Bs = Bs; a.C = q;
+  a.ws = nullptr;
+  a.lda = lda; a.ldb = ldb; a.as_sm = as_sm; a.as_sk = 1; a.bs_sn = bs_sn; a.bs_sk = 1;
+  a.ldc = ldq; a.M = (int)M; a.N = (int)N; a.K = (int)K; a.KB = (int)(K / 128);
+  a.kb_per_split = a.KB;
+  a.tiles_m = (int)((M + 255) / 256);
+  a.tiles_n = (int)(N / 256);
+  a.out_dtype = FP8B_BF16;
+  a.vec_store = 0;
+  a.rem_base = -1; a.rem_tiles_m = 0; a.rem_tiles_n = 0;
+  a.Sq = s; a.sq_sm = s_stride_m; a.sq_sg = s_stride_g;
+  const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
+  if (tiles >= (int64_t(1) << 31)) {
+    set_error("fp8b_gate_up_silu_quant: too many tiles");
+    return FP8B_ERR_DIMS;
+  }
+  gemm_pipe256_kernel<false, true><<<(unsigned)tiles, 512, 0, (hipStream_t)stream>>>(a);
+  if (hipGetLastError() != hipSuccess) {
+    set_error("fp8b_gate_up_silu_quant: kernel launch failed");
+    return FP8B_ERR_LAUNCH;
   }
   return FP8B_OK;
 }

@@ -9,6 +9,7 @@
 //   silu_and_mul(Tensor(a!) out, x) -> ()
 //       (schema of activation-helion/.../torch-ext/activation_helion/op.py:15-18)
 //   silu_and_mul_quant(x, block_size) -> (q, s)
+//   gate_up_silu_quant(A, B, As, Bs) -> (q, s)   (gate/up weights interleaved)
 //   act_quant_matmul(x, B, Bs, block_n, block_k, ScalarType output_dtype) -> Tensor
 //   weight_quant(W, block_n, block_k) -> (Wq, Bs)   (128x128 blocks)
 // and, in _deep_gemm_helion_rocm_mi355x (deep-gemm-helion's op,
@@ -255,6 +256,45 @@ std::tuple<Tensor, Tensor> silu_and_mul_quant(const Tensor& x, int64_t block_siz
   return {q.view(qshape), s.view(sshape)};
 }
 
+// Gate/up GEMM with SiLU(gate)*up and group-128 quantisation in its
+// epilogue; B/Bs hold gate and up interleaved in 128-row blocks
+// (interleave_gate_up in finegrained_fp8_helion/mlp.py).
+std::tuple<Tensor, Tensor> gate_up_silu_quant(const Tensor& A, const Tensor& B,
+                                              const Tensor& As, const Tensor& Bs) {
+  check_gpu(A, "A");
+  check_gpu(B, "B");
+  check_gpu(As, "As");
+  check_gpu(Bs, "Bs");
+  TORCH_CHECK(A.dim() == 2 && B.dim() == 2, "A and B must be 2-D ([M,K] and [2I,K])");
+  TORCH_CHECK(A.scalar_type() == at::kFloat8_e4m3fn && B.scalar_type() == at::kFloat8_e4m3fn,
+              "A and B must be float8_e4m3fn");
+  TORCH_CHECK(As.scalar_type() == at::kFloat && Bs.scalar_type() == at::kFloat,
+              "As and Bs must be float32");
+  const int64_t M = A.size(0), K = A.size(1), N = B.size(0);
+  TORCH_CHECK(B.size(1) == K, "A is [M,K]=[", M, ",", K, "] but B is [2I,K]=[", N, ",",
+              B.size(1), "]");
+  TORCH_CHECK(N % 256 == 0, "B must have 2I rows with I a multiple of 128, got ", N);
+  TORCH_CHECK(As.dim() == 2 && As.size(0) >= M && As.size(1) >= K / 128,
+              "As must be [M, K/128], got ", As.sizes());
+  TORCH_CHECK(Bs.dim() == 2 && Bs.size(0) >= N / 128 && Bs.size(1) >= K / 128,
+              "Bs must be [2I/128, K/128], got ", Bs.sizes());
+  TORCH_CHECK(A.stride(1) == 1 && B.stride(1) == 1 && As.stride(1) == 1 && Bs.stride(1) == 1,
+              "A, B, As and Bs must be contiguous in K");
+  const int64_t I = N / 2;
+  at::hip::HIPGuardMasqueradingAsCUDA guard(A.device());
+  Tensor q = at::empty({M, I}, A.options());
+  Tensor s = at::empty({M, I / 128}, As.options());
+  if (M > 0) {
+    const int64_t lda = std::max<int64_t>(M > 1 ? A.stride(0) : K, K);
+    const int st = fp8b_gate_up_silu_quant(
+        A.data_ptr(), lda, B.data_ptr(), B.stride(0), As.data_ptr<float>(),
+        As.stride(0), 1, Bs.data_ptr<float>(), Bs.stride(0), 1, q.data_ptr(), I,
+        s.data_ptr<float>(), I / 128, 1, M, I, K, current_stream(A));
+    check_status(st, "gate_up_silu_quant");
+  }
+  return {q, s};
+}
+
 // CPU tensors reach these: raise instead of computing anything.
 [[noreturn]] void no_cpu(const char* op) {
   TORCH_CHECK(false, op, ": tensors must be on a ROCm GPU; this package has no CPU "
@@ -282,6 +322,10 @@ void silu_and_mul_cpu(Tensor&, const Tensor&) { no_cpu("silu_and_mul"); }
 std::tuple<Tensor, Tensor> silu_and_mul_quant_cpu(const Tensor&, int64_t) {
   no_cpu("silu_and_mul_quant");
 }
+std::tuple<Tensor, Tensor> gate_up_silu_quant_cpu(const Tensor&, const Tensor&, const Tensor&,
+                                                  const Tensor&) {
+  no_cpu("gate_up_silu_quant");
+}
 
 }  // namespace
 
@@ -293,6 +337,7 @@ TORCH_LIBRARY(_finegrained_fp8_helion_rocm_mi355x, m) {
   m.def("act_quant(Tensor x, int block_size) -> (Tensor, Tensor)");
   m.def("silu_and_mul(Tensor(a!) out, Tensor x) -> ()");
   m.def("silu_and_mul_quant(Tensor x, int block_size) -> (Tensor, Tensor)");
+  m.def("gate_up_silu_quant(Tensor A, Tensor B, Tensor As, Tensor Bs) -> (Tensor, Tensor)");
   m.def("act_quant_matmul(Tensor x, Tensor B, Tensor Bs, int block_n, int block_k, "
         "ScalarType output_dtype) -> Tensor");
   m.def("weight_quant(Tensor W, int block_n, int block_k) -> (Tensor, Tensor)");
@@ -304,6 +349,7 @@ TORCH_LIBRARY_IMPL(_finegrained_fp8_helion_rocm_mi355x, CUDA, m) {
   m.impl("act_quant", &act_quant);
   m.impl("silu_and_mul", &silu_and_mul);
   m.impl("silu_and_mul_quant", &silu_and_mul_quant);
+  m.impl("gate_up_silu_quant", &gate_up_silu_quant);
   m.impl("act_quant_matmul", &act_quant_matmul);
   m.impl("weight_quant", &weight_quant);
 }
@@ -314,6 +360,7 @@ TORCH_LIBRARY_IMPL(_finegrained_fp8_helion_rocm_mi355x, CPU, m) {
   m.impl("act_quant", &act_quant_cpu);
   m.impl("silu_and_mul", &silu_and_mul_cpu);
   m.impl("silu_and_mul_quant", &silu_and_mul_quant_cpu);
+  m.impl("gate_up_silu_quant", &gate_up_silu_quant_cpu);
   m.impl("act_quant_matmul", &act_quant_matmul_cpu);
   m.impl("weight_quant", &weight_quant_cpu);
 }

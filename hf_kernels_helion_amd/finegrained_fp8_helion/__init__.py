@@ -11,7 +11,7 @@ import torch
 
 from ._ops import ops
 from . import op as _op  # registers the custom ops
-from .mlp import fp8_mlp
+from .mlp import fp8_mlp, gate_up_silu_quant, interleave_gate_up
 
 _DIRECT_OUT = (torch.float32, torch.bfloat16, torch.float16)
 
@@ -88,4 +88,6 @@ __all__ = [
     "silu_and_mul",
     "silu_and_mul_quant",
     "fp8_mlp",
+    "interleave_gate_up",
+    "gate_up_silu_quant",
 ]

@@ -8,6 +8,12 @@
 
 The gate/up GEMM's output columns are [gate | up], the layout silu_and_mul
 consumes (activation-helion/.../act.py:20-28).
+
+With the gate/up weight interleaved once in 128-row blocks
+(``interleave_gate_up``), every 256-column tile of the gate/up GEMM holds a
+gate block and its matching up block, and the GEMM's epilogue forms
+silu(gate) * up and quantises it itself (``gate_up_silu_quant``): the bf16
+h [M, 2I] is never written. Same bits as the three-step chain.
 """
 from __future__ import annotations
 
@@ -16,16 +22,47 @@ import torch
 from ._ops import ops
 
 
+def interleave_gate_up(w_gate_up: torch.Tensor, s_gate_up: torch.Tensor):
+    """Reorder a [gate; up] weight [2I, H] and its block scales [2I/128, H/128]
+    into 128-row blocks [gate 0, up 0, gate 1, up 1, ...] (a one-time weight
+    preparation for ``gate_up_silu_quant``). I must be a multiple of 128."""
+    n2, h = w_gate_up.shape
+    if n2 % 256 != 0:
+        raise ValueError(f"gate/up weight must have 2I rows with I % 128 == 0, got {n2}")
+    nb = n2 // 256
+    w = w_gate_up.reshape(2, nb, 128, h).transpose(0, 1).reshape(n2, h).contiguous()
+    s = s_gate_up.reshape(2, nb, s_gate_up.shape[-1]).transpose(0, 1)
+    return w, s.reshape(2 * nb, s_gate_up.shape[-1]).contiguous()
+
+
+def gate_up_silu_quant(xq: torch.Tensor, xs: torch.Tensor, w_il: torch.Tensor,
+                       s_il: torch.Tensor):
+    """act_quant(silu_and_mul(w8a8 GEMM(xq, w, xs, s) in bf16), 128), bit for
+    bit, in one kernel; (w_il, s_il) from ``interleave_gate_up``. Needs
+    block_size (128, 128) and H % 512 == 0. Returns (q [M, I] e4m3fn,
+    s [M, I/128] fp32)."""
+    return ops.gate_up_silu_quant(xq, w_il, xs, s_il)
+
+
 def fp8_mlp(x: torch.Tensor, w_gate_up: torch.Tensor, s_gate_up: torch.Tensor,
             w_down: torch.Tensor, s_down: torch.Tensor, block_size=(128, 128),
-            fuse_quant: bool = True) -> torch.Tensor:
+            fuse_quant: bool = True, gate_up_interleaved: bool = False) -> torch.Tensor:
     """y = down(silu(gate(x)) * up(x)) with e4m3fn weights and 128x128 block
     scales. ``fuse_quant=False`` runs silu_and_mul and act_quant as two ops
-    (bit-identical result, one more bf16 round trip through HBM)."""
+    (bit-identical result, one more bf16 round trip through HBM).
+    ``gate_up_interleaved=True``: (w_gate_up, s_gate_up) come from
+    ``interleave_gate_up`` and the gate/up GEMM, SiLU·up and its quantisation
+    run as one kernel (same result)."""
     bn, bk = int(block_size[0]), int(block_size[1])
     lead = x.shape[:-1]
     x2 = x.reshape(-1, x.shape[-1])
     xq, xs = ops.act_quant(x2, bk)
+    if gate_up_interleaved:
+        if (bn, bk) != (128, 128):
+            raise ValueError("gate_up_interleaved needs block_size (128, 128)")
+        hq, hs = ops.gate_up_silu_quant(xq, w_gate_up, xs, s_gate_up)
+        y = ops.w8a8_block_fp8_matmul_dtype(hq, w_down, hs, s_down, bn, bk, torch.bfloat16)
+        return y.reshape(*lead, y.shape[-1])
     h = ops.w8a8_block_fp8_matmul_dtype(xq, w_gate_up, xs, s_gate_up, bn, bk, torch.bfloat16)
     if fuse_quant:
         hq, hs = ops.silu_and_mul_quant(h, bk)

@@ -63,6 +63,13 @@ def _(x, block_size):
             x.new_empty((*x.shape[:-1], groups), dtype=torch.float32))
 
 
+@torch.library.register_fake(add_op_namespace_prefix("gate_up_silu_quant"))
+def _(A, B, As, Bs):
+    i = B.shape[0] // 2
+    return (A.new_empty((A.shape[0], i), dtype=torch.float8_e4m3fn),
+            As.new_empty((A.shape[0], i // 128), dtype=torch.float32))
+
+
 @torch.library.register_fake(add_op_namespace_prefix("act_quant_matmul"))
 def _(x, B, Bs, block_n, block_k, output_dtype):
     return x.new_empty((x.shape[0], B.shape[0]), dtype=output_dtype)

@@ -178,6 +178,32 @@ int fp8b_silu_and_mul_quant(const void* x, int64_t ldx,
                             int64_t M, int64_t d, int64_t group,
                             void* stream);
 
+/*
+ * Gate/up GEMM of a gated FP8 MLP with SiLU(gate)*up and the group-128
+ * quantisation of its result in the GEMM epilogue:
+ *   h = bf16(w8a8 GEMM of A [M,K] with B [2I,K])   (as fp8b_w8a8_block_matmul)
+ *   q, s = act-quant(silu_and_mul(h)) with group 128
+ * bit for bit, without writing h. B and Bs must hold the gate and up
+ * weights interleaved in 128-row blocks: rows 256t..256t+127 of B are gate
+ * rows 128t..128t+127 and rows 256t+128..256t+255 the matching up rows;
+ * Bs block row 2t is gate block row t and 2t+1 up block row t.
+ * A, As: as fp8b_w8a8_block_matmul (block_n = block_k = 128, As and Bs
+ * contiguous in K, 16-byte aligned); q: e4m3fn [M,I] row stride ldq (a
+ * multiple of 8); scale of (m, g) at s[m*s_stride_m + g*s_stride_g].
+ * Needs I % 128 == 0 and K % 512 == 0.
+ * No single counterpart in the reference: it composes the gate/up call of
+ * w8a8_block_fp8_matmul (finegrained-fp8-helion/.../fp8.py:28-38) with
+ * act.py:20-28 and the quantiser above, as fp8b_silu_and_mul_quant does.
+ */
+int fp8b_gate_up_silu_quant(const void* A, int64_t lda,
+                            const void* B, int64_t ldb,
+                            const float* As, int64_t as_sm, int64_t as_sk,
+                            const float* Bs, int64_t bs_sn, int64_t bs_sk,
+                            void* q, int64_t ldq,
+                            float* s, int64_t s_stride_m, int64_t s_stride_g,
+                            int64_t M, int64_t I, int64_t K,
+                            void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -76,6 +76,25 @@ def test_act_quant_rejects_bad_args_without_gpu():
     assert lib.fp8b_silu_and_mul_quant(None, 256, None, 128, None, 1, 1, 2, 128, 48, None) == 4
 
 
+def test_gate_up_silu_quant_rejects_bad_args_without_gpu():
+    lib = _native.load()
+    f = lib.fp8b_gate_up_silu_quant
+    # (A, lda, B, ldb, As, as_sm, as_sk, Bs, bs_sn, bs_sk, q, ldq, s, s_sm, s_sg, M, I, K, stream)
+    assert f(None, 512, None, 512, None, 4, 1, None, 4, 1, None, 128, None, 1, 1,
+             -1, 128, 512, None) == 2
+    assert f(None, 512, None, 512, None, 4, 1, None, 4, 1, None, 64, None, 1, 1,
+             4, 128, 512, None) == 2                                     # ldq < I
+    assert f(None, 512, None, 512, None, 4, 1, None, 4, 1, None, 192, None, 1, 1,
+             4, 192, 512, None) == 2                                     # I % 128
+    assert f(None, 384, None, 384, None, 4, 1, None, 4, 1, None, 128, None, 1, 1,
+             4, 128, 384, None) == 2                                     # K % 512
+    assert b"multiple of 512" in lib.fp8b_last_error()
+    assert f(None, 512, None, 512, None, 4, 1, None, 4, 1, None, 128, None, 1, 1,
+             4, 128, 512, None) == 1                                     # null pointers
+    assert f(None, 512, None, 512, None, 4, 1, None, 4, 1, None, 128, None, 1, 1,
+             0, 128, 512, None) == 0                                     # empty
+
+
 def test_workspace_size_zero_for_unsupported_blocks():
     lib = _native.load()
     assert lib.fp8b_gemm_workspace_size(32, 4096, 14336, 64, 128) == 0

@@ -85,3 +85,77 @@ def test_fp8_mlp_chain_ragged(dev):
                            hs.cpu().numpy(), s2.numpy())
     torch.testing.assert_close(y.float().cpu(), torch.from_numpy(yo).to(torch.bfloat16).float(),
                                rtol=1e-2, atol=1e-3)
+
+
+def _gate_up_chain(xq, xs, w13, s13, M):
+    """h = bf16 GEMM, then silu_and_mul_quant: the two-kernel reference of
+    gate_up_silu_quant. Small M is padded to 256 rows (zero activations) so
+    that the GEMM runs on the unsplit MFMA kernels whose per-output
+    arithmetic (one MFMA and one scale FMA per K-block, in K order) the fused
+    kernel shares; rows are independent, so the first M rows are the ones of
+    the unpadded problem."""
+    if M < 256:
+        pad = 256 - M
+        xq = torch.cat([xq, torch.zeros(pad, xq.shape[1], dtype=xq.dtype, device=xq.device)])
+        xs = torch.cat([xs, torch.full((pad, xs.shape[1]), 1.0, device=xs.device)])
+    h = fp8.w8a8_block_fp8_matmul(xq, w13, xs, s13, [128, 128], torch.bfloat16)
+    q, s = fp8.silu_and_mul_quant(h, 128)
+    return q[:M], s[:M], h[:M]
+
+
+@pytest.mark.parametrize("M,I,H", [(1, 128, 512), (5, 256, 1024), (200, 384, 512),
+                                   (257, 512, 512), (3001, 1024, 512), (3001, 14336, 4096)])
+def test_gate_up_silu_quant_equals_chain(M, I, H, dev):
+    """GEMM + SiLU·up + act-quant in one kernel == bf16 GEMM then
+    silu_and_mul_quant, fp8 codes and scales bit for bit; the bf16 GEMM is
+    checked against the oracle on a sample of rows."""
+    print(f"gate_up_silu_quant M={M} I={I} H={H}", flush=True)
+    x = synthetic.activations(M, H, seed=M + I)
+    w13, s13 = synthetic.weights(2 * I, H, seed=I + H)
+    xq, xs = fp8.act_quant(x.to(dev), 128)
+    w13d, s13d = w13.to(dev), s13.to(dev)
+    q_ref, s_ref, h = _gate_up_chain(xq, xs, w13d, s13d, M)
+    wi, si = fp8.interleave_gate_up(w13d, s13d)
+    q, s = fp8.gate_up_silu_quant(xq, xs, wi, si)
+    assert q.shape == (M, I) and s.shape == (M, I // 128)
+    assert torch.equal(q.view(torch.uint8), q_ref.view(torch.uint8))
+    assert torch.equal(s.view(torch.int32), s_ref.view(torch.int32))
+    rows = torch.arange(0, M, max(1, M // 16))
+    ho = oracle.block_gemm(xq[rows.to(dev)].cpu().view(torch.uint8).numpy(),
+                           w13.view(torch.uint8).numpy(), xs[rows.to(dev)].cpu().numpy(),
+                           s13.numpy())
+    torch.testing.assert_close(h[rows.to(dev)].float().cpu(),
+                               torch.from_numpy(ho).to(torch.bfloat16).float(),
+                               rtol=1e-2, atol=1e-3)
+
+
+def test_gate_up_silu_quant_strided_outputs_and_repeat(dev):
+    """A second call on the same buffers gives the same bits (no state kept
+    between calls), and a row-strided A/As view is read correctly."""
+    print("gate_up_silu_quant strided", flush=True)
+    M, I, H = 300, 256, 512
+    x = synthetic.activations(M, 2 * H, seed=3)
+    xq_full, xs_full = fp8.act_quant(x.to(dev), 128)
+    xq, xs = xq_full[:, :H], xs_full[:, : H // 128]           # row strides 2H, 2H/128
+    w13, s13 = synthetic.weights(2 * I, H, seed=4)
+    wi, si = fp8.interleave_gate_up(w13.to(dev), s13.to(dev))
+    q1, s1 = fp8.gate_up_silu_quant(xq, xs, wi, si)
+    q2, s2 = fp8.gate_up_silu_quant(xq.contiguous(), xs.contiguous(), wi, si)
+    assert torch.equal(q1.view(torch.uint8), q2.view(torch.uint8))
+    assert torch.equal(s1, s2)
+    q_ref, s_ref, _ = _gate_up_chain(xq.contiguous(), xs.contiguous(), w13.to(dev),
+                                     s13.to(dev), M)
+    assert torch.equal(q1.view(torch.uint8), q_ref.view(torch.uint8))
+
+
+def test_fp8_mlp_interleaved_equals_default(dev):
+    print("fp8 mlp interleaved M=3001", flush=True)
+    M, H, I = 3001, 512, 1024
+    x = synthetic.activations(M, H, seed=41).to(dev)
+    w13, s13 = synthetic.weights(2 * I, H, seed=42)
+    w2, s2 = synthetic.weights(H, I, seed=43)
+    w13, s13, w2, s2 = w13.to(dev), s13.to(dev), w2.to(dev), s2.to(dev)
+    y = fp8.fp8_mlp(x, w13, s13, w2, s2)
+    wi, si = fp8.interleave_gate_up(w13, s13)
+    y2 = fp8.fp8_mlp(x, wi, si, w2, s2, gate_up_interleaved=True)
+    assert torch.equal(y, y2)

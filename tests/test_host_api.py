@@ -22,7 +22,8 @@ def test_namespace_follows_kernel_builder_scheme():
     assert _ops._OPS_NAME == "_finegrained_fp8_helion_rocm_mi355x"
     assert _ops.add_op_namespace_prefix("x") == "_finegrained_fp8_helion_rocm_mi355x::x"
     for name in ("w8a8_block_fp8_matmul", "w8a8_block_fp8_matmul_dtype", "act_quant",
-                 "silu_and_mul", "silu_and_mul_quant", "act_quant_matmul", "weight_quant"):
+                 "silu_and_mul", "silu_and_mul_quant", "act_quant_matmul", "weight_quant",
+                 "gate_up_silu_quant"):
         assert hasattr(_ops.ops, name)
 
 
@@ -58,6 +59,9 @@ def test_fake_impls_give_reference_shapes():
         assert s.shape == (3, 5, 3) and s.dtype == torch.float32
         q, s = _ops.ops.silu_and_mul_quant(torch.zeros(4, 512, dtype=torch.bfloat16), 128)
         assert q.shape == (4, 256) and s.shape == (4, 2)
+        q, s = _ops.ops.gate_up_silu_quant(_fp8(7, 512), _fp8(512, 512), torch.ones(7, 4),
+                                           torch.ones(4, 4))
+        assert q.shape == (7, 256) and q.dtype == torch.float8_e4m3fn and s.shape == (7, 2)
         out = _ops.ops.act_quant_matmul(torch.zeros(7, 384, dtype=torch.bfloat16), B, Bs, 128,
                                         128, torch.bfloat16)
         assert out.shape == (7, 200) and out.dtype == torch.bfloat16
@@ -116,3 +120,20 @@ def test_deep_gemm_surface_matches_reference():
         assert out.shape == (5, 7) and out.dtype == torch.bfloat16
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         dg.gemm_fp8_fp8_bf16_nt(_fp8(5, 256), _fp8(7, 256), torch.ones(5, 2), torch.ones(7, 2))
+
+
+def test_interleave_gate_up_layout():
+    """128-row blocks [gate t, up t]; scale block rows 2t = gate t, 2t+1 = up t."""
+    I, H = 384, 256
+    w = torch.arange(2 * I, dtype=torch.float32)[:, None].expand(2 * I, H).contiguous()
+    s = torch.arange(2 * I // 128, dtype=torch.float32)[:, None].expand(-1, 2).contiguous()
+    wi, si = fp8.interleave_gate_up(w, s)
+    for t in range(I // 128):
+        assert torch.equal(wi[256 * t: 256 * t + 128, 0], torch.arange(128 * t, 128 * t + 128.))
+        assert torch.equal(wi[256 * t + 128: 256 * t + 256, 0],
+                           torch.arange(I + 128 * t, I + 128 * t + 128.))
+        assert si[2 * t, 0] == t and si[2 * t + 1, 0] == I // 128 + t
+    with pytest.raises(ValueError):
+        fp8.interleave_gate_up(torch.zeros(200, 256), torch.zeros(2, 2))
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        fp8.gate_up_silu_quant(_fp8(4, 512), torch.ones(4, 4), _fp8(256, 512), torch.ones(2, 4))
