@@ -159,3 +159,33 @@ def test_fp8_mlp_interleaved_equals_default(dev):
     wi, si = fp8.interleave_gate_up(w13, s13)
     y2 = fp8.fp8_mlp(x, wi, si, w2, s2, gate_up_interleaved=True)
     assert torch.equal(y, y2)
+
+
+@pytest.mark.parametrize("interleaved", [False, True])
+def test_fp8_mlp_graph_replays(interleaved, dev):
+    """The MLP chain captured in a HIP graph (a serving loop's form): every
+    replay, with eager work in between, equals the eager result."""
+    print(f"fp8 mlp graph interleaved={interleaved}", flush=True)
+    M, H, I = 300, 512, 1024
+    x = synthetic.activations(M, H, seed=51).to(dev)
+    w13, s13 = synthetic.weights(2 * I, H, seed=52)
+    w2, s2 = synthetic.weights(H, I, seed=53)
+    w13, s13, w2, s2 = w13.to(dev), s13.to(dev), w2.to(dev), s2.to(dev)
+    if interleaved:
+        w13, s13 = fp8.interleave_gate_up(w13, s13)
+    f = lambda: fp8.fp8_mlp(x, w13, s13, w2, s2, gate_up_interleaved=interleaved)
+    eager = f()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        f()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = f()
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        f()  # eager work between replays
+        torch.cuda.synchronize()
