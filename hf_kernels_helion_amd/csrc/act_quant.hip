@@ -132,14 +132,8 @@ silu_and_mul_vec_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   const uint16_t* xr = x + (int64_t)m * ldx + c * 8u;
   const v4i g = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(xr));
   const v4i u = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(xr + d));
-  v4i o;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t gw = (uint32_t)g[i], uw = (uint32_t)u[i];
-    const uint32_t lo = silu_mul_bits(gw & 0xFFFFu, uw & 0xFFFFu);
-    const uint32_t hi = silu_mul_bits(gw >> 16, uw >> 16);
-    o[i] = (int)(lo | (hi << 16));
-  }
+  float v[8];
+  const v4i o = silu_mul_bf16x8(g, u, v);
   __builtin_nontemporal_store(o, reinterpret_cast<v4i*>(out + (int64_t)m * ldo + c * 8u));
 }
 
@@ -182,16 +176,7 @@ silu_mul_quant_g128_kernel(const uint16_t* __restrict__ x, int64_t ldx,
       const uint32_t g = g0 + 16u * u;
       if (g >= groups_per_row) break;  // uniform across the 16-lane group
       float v[8];
-      v4i h;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t gw = (uint32_t)gr[u][i], uw = (uint32_t)ur[u][i];
-        const uint32_t lo = silu_mul_bits(gw & 0xFFFFu, uw & 0xFFFFu);
-        const uint32_t hi = silu_mul_bits(gw >> 16, uw >> 16);
-        v[2 * i] = bf16_to_f32(lo);
-        v[2 * i + 1] = bf16_to_f32(hi);
-        h[i] = (int)(lo | (hi << 16));
-      }
+      const v4i h = silu_mul_bf16x8(gr[u], ur[u], v);
       uint32_t w0, w1;
       float scale;
       quant_row16_8(v, max_mag_bf16x8(h), w0, w1, scale);

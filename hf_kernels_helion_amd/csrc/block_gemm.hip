@@ -718,18 +718,8 @@ __global__ void __launch_bounds__(512) gemm_pipe256_kernel(GemmArgs a) {
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
       const int r = p * 32 + (tid >> 4);
-      const v4i g = gv[p], u = uv[p];
       float v[8];
-      v4i h;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t gw = (uint32_t)g[i], uw = (uint32_t)u[i];
-        const uint32_t lo = silu_mul_bits(gw & 0xFFFFu, uw & 0xFFFFu);
-        const uint32_t hi = silu_mul_bits(gw >> 16, uw >> 16);
-        v[2 * i] = bf16_to_f32(lo);
-        v[2 * i + 1] = bf16_to_f32(hi);
-        h[i] = (int)(lo | (hi << 16));
-      }
+      const v4i h = silu_mul_bf16x8(gv[p], uv[p], v);
       uint32_t w0, w1;
       float scale;
       quant_row16_8(v, max_mag_bf16x8(h), w0, w1, scale);

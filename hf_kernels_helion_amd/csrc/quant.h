@@ -141,4 +141,57 @@ __device__ __forceinline__ uint32_t silu_mul_bits(uint32_t gate_bits, uint32_t u
   return f32_to_bf16_bits(silu_b * bf16_to_f32(up_bits));
 }
 
+// silu_mul_bits for |gate| < 64 (bf16 magnitude pattern below 0x4280): then
+// |t| < 93, so t, e^-a and 1 + e^-a are finite and both guarded corrections
+// of silu_mul_bits apply; this is the same arithmetic without the guards.
+constexpr uint32_t kSiluFastMag = 0x4280u;  // bf16 pattern of 64.0
+__device__ __forceinline__ uint32_t silu_mul_bits_small(uint32_t gate_bits, uint32_t up_bits) {
+  constexpr float kLog2eHi = 1.4426950216293335f;
+  constexpr float kLog2eLo = 1.925962989091e-08f;
+  constexpr float kLn2 = 0.6931471805599453f;
+  const float a = bf16_to_f32(gate_bits);
+  const float t = -a * kLog2eHi;
+  const float r = fmaf(-a, kLog2eHi, -t) - a * kLog2eLo;
+  const float e0 = __builtin_amdgcn_exp2f(t);
+  const float y = 1.0f + fmaf(e0, r * kLn2, e0);
+  const float inv0 = __builtin_amdgcn_rcpf(y);
+  const float silu = a * fmaf(inv0, fmaf(-y, inv0, 1.0f), inv0);
+  const float silu_b = bf16_to_f32(f32_to_bf16_bits(silu));
+  return f32_to_bf16_bits(silu_b * bf16_to_f32(up_bits));
+}
+
+// True when every active lane of the wave has pred set (wave-uniform).
+__device__ __forceinline__ bool wave_all(bool pred) {
+  return __builtin_amdgcn_ballot_w64(!pred) == 0;
+}
+
+// SiLU(gate)*up of 8 packed bf16 pairs (one 16-byte load of each): packed
+// bf16 results, their fp32 values in v. Takes the guard-free form when every
+// gate of the wave is below 64 in magnitude (the same bits either way).
+__device__ __forceinline__ v4i silu_mul_bf16x8(const v4i g, const v4i u, float v[8]) {
+  v4i h;
+  if (wave_all(max_mag_bf16x8(g) < kSiluFastMag)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t gw = (uint32_t)g[i], uw = (uint32_t)u[i];
+      const uint32_t lo = silu_mul_bits_small(gw & 0xFFFFu, uw & 0xFFFFu);
+      const uint32_t hi = silu_mul_bits_small(gw >> 16, uw >> 16);
+      v[2 * i] = bf16_to_f32(lo);
+      v[2 * i + 1] = bf16_to_f32(hi);
+      h[i] = (int)(lo | (hi << 16));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t gw = (uint32_t)g[i], uw = (uint32_t)u[i];
+      const uint32_t lo = silu_mul_bits(gw & 0xFFFFu, uw & 0xFFFFu);
+      const uint32_t hi = silu_mul_bits(gw >> 16, uw >> 16);
+      v[2 * i] = bf16_to_f32(lo);
+      v[2 * i + 1] = bf16_to_f32(hi);
+      h[i] = (int)(lo | (hi << 16));
+    }
+  }
+  return h;
+}
+
 }  // namespace fp8b
