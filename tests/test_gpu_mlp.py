@@ -189,3 +189,52 @@ def test_fp8_mlp_graph_replays(interleaved, dev):
         assert torch.equal(out, eager)
         f()  # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_silu_fast_path_same_bits(dev):
+    """Every bf16 gate with |a| < 64 (both signs), each against a random bf16
+    up value: a wave whose gates are all below 64 takes the guard-free SiLU,
+    a wave holding one larger gate the guarded one; the two give the same
+    bits. One 512-wide row is one wave of silu_and_mul_vec_kernel (64
+    chunks of 8); the last column holds the gate that selects the path."""
+    print("silu fast path exhaustive", flush=True)
+    mags = torch.arange(0, 0x4280, dtype=torch.int32)
+    pats = torch.cat([mags, mags | 0x8000])                 # 34048 gates
+    per = 511
+    rows = -(-pats.numel() // per)
+    g = torch.zeros(rows * per, dtype=torch.int32)
+    g[: pats.numel()] = pats
+    gates = torch.zeros(rows, 512, dtype=torch.int32)
+    gates[:, :per] = g.view(rows, per)
+    gen = torch.Generator().manual_seed(17)
+    up = (torch.randn(rows, 512, generator=gen) * 4).to(torch.bfloat16)
+    fast_x = torch.cat([gates.to(torch.int16).view(torch.bfloat16), up], 1)
+    slow_x = fast_x.clone()
+    slow_x[:, per] = 100.0                                   # forces the guarded path
+    outs = []
+    for x in (fast_x, slow_x):
+        out = torch.empty(rows, 512, dtype=torch.bfloat16, device=dev)
+        fp8.silu_and_mul(out, x.to(dev))
+        outs.append(out[:, :per].cpu())
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+
+
+def test_gate_up_silu_quant_nonfinite_rows(dev):
+    """Rows whose activation scale makes h overflow to +-inf (and a NaN
+    scale): the epilogue's non-finite groups equal the chain's, bit for bit."""
+    print("gate_up_silu_quant non-finite", flush=True)
+    M, I, H = 300, 256, 512
+    x = synthetic.activations(M, H, seed=61)
+    w13, s13 = synthetic.weights(2 * I, H, seed=62)
+    xq, xs = fp8.act_quant(x.to(dev), 128)
+    xs = xs.clone()
+    xs[3] = 3e38            # h = +-inf where the dot is non-zero
+    xs[10, 1] = 1e30        # one K-block huge: finite or inf by sign
+    xs[20] = float("nan")   # NaN rows
+    w13d, s13d = w13.to(dev), s13.to(dev)
+    q_ref, s_ref, h = _gate_up_chain(xq, xs, w13d, s13d, M)
+    assert not torch.isfinite(h[3].float()).all() and torch.isnan(h[20].float()).all()
+    wi, si = fp8.interleave_gate_up(w13d, s13d)
+    q, s = fp8.gate_up_silu_quant(xq, xs, wi, si)
+    assert torch.equal(q.view(torch.uint8), q_ref.view(torch.uint8))
+    assert torch.equal(s.view(torch.int32), s_ref.view(torch.int32))
