@@ -348,11 +348,24 @@ __device__ __forceinline__ float load_w<float>(const float* p) { return *p; }
 template <>
 __device__ __forceinline__ float load_w<uint16_t>(const uint16_t* p) { return bf16_to_f32(*p); }
 
+// Max of a 256-thread block's values (the block max of 128x128 weights):
+// DPP rows of 16, then the four rows, then the four waves through LDS.
+__device__ __forceinline__ uint32_t block128_max_u32(uint32_t m, int lane, int wid) {
+  m = row16_max_u32(m);
+  m = max(m, (uint32_t)__builtin_amdgcn_readlane((int)m, 0));
+  m = max(m, (uint32_t)__builtin_amdgcn_readlane((int)m, 16));
+  m = max(m, (uint32_t)__builtin_amdgcn_readlane((int)m, 32));
+  m = max(m, (uint32_t)__builtin_amdgcn_readlane((int)m, 48));
+  __shared__ uint32_t wmax[4];
+  if (lane == 0) wmax[wid] = m;
+  __syncthreads();
+  return max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
+}
+
 template <typename T>
-__global__ void __launch_bounds__(256)
-weight_quant_block128_kernel(const T* __restrict__ W, int64_t ldw, uint8_t* __restrict__ q,
-                             int64_t ldq, float* __restrict__ s, int64_t s_sn, int64_t s_sk,
-                             int64_t N, int64_t K) {
+__device__ __forceinline__ void weight_quant_block128_body(
+    const T* __restrict__ W, int64_t ldw, uint8_t* __restrict__ q, int64_t ldq,
+    float* __restrict__ s, int64_t s_sn, int64_t s_sk, int64_t N, int64_t K) {
   const int nb = blockIdx.y, kb = blockIdx.x;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int64_t n0 = (int64_t)nb * 128 + wid * 32, k = (int64_t)kb * 128 + 2 * lane;
@@ -371,18 +384,8 @@ weight_quant_block128_kernel(const T* __restrict__ W, int64_t ldw, uint8_t* __re
       amax = fmaxf(amax, fabsf(x));
     }
   }
-  // Block max over the wave (DPP rows of 16, then the four rows) and the
-  // four waves.
-  uint32_t m = __float_as_uint(amax) | (nan ? 0x7FC00000u : 0u);
-  m = row16_max_u32(m);
-  m = max(m, (uint32_t)__builtin_amdgcn_readlane((int)m, 0));
-  m = max(m, (uint32_t)__builtin_amdgcn_readlane((int)m, 16));
-  m = max(m, (uint32_t)__builtin_amdgcn_readlane((int)m, 32));
-  m = max(m, (uint32_t)__builtin_amdgcn_readlane((int)m, 48));
-  __shared__ uint32_t wmax[4];
-  if (lane == 0) wmax[wid] = m;
-  __syncthreads();
-  m = max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
+  const uint32_t m =
+      block128_max_u32(__float_as_uint(amax) | (nan ? 0x7FC00000u : 0u), lane, wid);
   const bool block_nan = m > 0x7F800000u;
   const float scale = block_nan ? __uint_as_float(0x7FC00000u)
                                 : fmaxf(__uint_as_float(m), kAmaxFloor) / kFp8Max;
@@ -402,6 +405,65 @@ weight_quant_block128_kernel(const T* __restrict__ W, int64_t ldw, uint8_t* __re
     } else if (k < K) {
       q[n * ldq + k] = (uint8_t)b;
     }
+  }
+  if (threadIdx.x == 0) s[(int64_t)nb * s_sn + (int64_t)kb * s_sk] = scale;
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256)
+weight_quant_block128_kernel(const T* __restrict__ W, int64_t ldw, uint8_t* __restrict__ q,
+                             int64_t ldq, float* __restrict__ s, int64_t s_sn, int64_t s_sk,
+                             int64_t N, int64_t K) {
+  weight_quant_block128_body<T>(W, ldw, q, ldq, s, s_sn, s_sk, N, K);
+}
+
+// fp32 weights with 16-byte rows (ldw % 4 == 0, W 16-byte aligned) and
+// 4-byte aligned q rows: the same block quantiser with 16-byte loads. A lane
+// holds 4 consecutive columns of 16 rows (wave w: rows 32w + 2i + lane/32,
+// i < 16), so each load instruction covers two 512-byte rows and each store
+// writes 4 codes; the blocks on the matrix edge take the per-element kernel's
+// path. Same max, same scale, same per-element IEEE division: same bits.
+__global__ void __launch_bounds__(256)
+weight_quant_f32x4_kernel(const float* __restrict__ W, int64_t ldw, uint8_t* __restrict__ q,
+                          int64_t ldq, float* __restrict__ s, int64_t s_sn, int64_t s_sk,
+                          int64_t N, int64_t K) {
+  const int nb = blockIdx.y, kb = blockIdx.x;
+  if ((int64_t)nb * 128 + 128 > N || (int64_t)kb * 128 + 128 > K) {
+    weight_quant_block128_body<float>(W, ldw, q, ldq, s, s_sn, s_sk, N, K);
+    return;
+  }
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int64_t n0 = (int64_t)nb * 128 + wid * 32 + (lane >> 5);
+  const int64_t k = (int64_t)kb * 128 + (lane & 31) * 4;
+  v4f v[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    v[i] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(W + (n0 + 2 * i) * ldw + k));
+  float amax = 0.f;
+  bool nan = false;
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      nan |= v[i][e] != v[i][e];
+      amax = fmaxf(amax, fabsf(v[i][e]));
+    }
+  const uint32_t m =
+      block128_max_u32(__float_as_uint(amax) | (nan ? 0x7FC00000u : 0u), lane, wid);
+  const bool block_nan = m > 0x7F800000u;
+  const float scale = block_nan ? __uint_as_float(0x7FC00000u)
+                                : fmaxf(__uint_as_float(m), kAmaxFloor) / kFp8Max;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    uint32_t b;
+    if (block_nan) {
+      b = 0x7F7F7F7Fu;
+    } else {
+      int p = __builtin_amdgcn_cvt_pk_fp8_f32(v[i][0] / scale, v[i][1] / scale, 0, false);
+      p = __builtin_amdgcn_cvt_pk_fp8_f32(v[i][2] / scale, v[i][3] / scale, p, true);
+      b = (uint32_t)p;
+    }
+    *reinterpret_cast<uint32_t*>(q + (n0 + 2 * i) * ldq + k) = b;
   }
   if (threadIdx.x == 0) s[(int64_t)nb * s_sn + (int64_t)kb * s_sk] = scale;
 }
@@ -435,7 +497,10 @@ extern "C" int fp8b_weight_quant(const void* W, int64_t ldw, int w_dtype, void* 
   }
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid((unsigned)KB, (unsigned)NB);
-  if (w_dtype == FP8B_F32)
+  if (w_dtype == FP8B_F32 && ldw % 4 == 0 && aligned(W, 16) && ldq % 4 == 0 && aligned(q, 4))
+    weight_quant_f32x4_kernel<<<grid, 256, 0, st>>>((const float*)W, ldw, (uint8_t*)q, ldq, s,
+                                                    s_sn, s_sk, N, K);
+  else if (w_dtype == FP8B_F32)
     weight_quant_block128_kernel<float><<<grid, 256, 0, st>>>((const float*)W, ldw, (uint8_t*)q,
                                                               ldq, s, s_sn, s_sk, N, K);
   else

@@ -60,3 +60,29 @@ def test_quantize_state_dict_on_gpu(dev):
         assert torch.equal(_u8(out[name]), _u8(rq))
         assert torch.equal(out[checkpoint._scale_name(name)], rs)
     assert set(checkpoint.fp8_linear_weights(out)) == {"a.weight", "b.weight"}
+
+
+def test_weight_quant_vector_path_equals_scalar_path(dev):
+    """fp32 W with 16-byte rows takes the 16-byte-load kernel (edge blocks
+    inside it take the per-element path); a row-strided view of the same
+    values (row stride not a multiple of 4) takes the per-element kernel.
+    Same codes and scales, bit for bit, with NaN, +-inf, subnormal and zero
+    blocks."""
+    print("weight quant vector vs scalar path", flush=True)
+    N, K = 384, 640 + 72   # ragged last block column (K % 128 = 72)
+    g = torch.Generator().manual_seed(77)
+    buf = (torch.randn(N, K + 2, generator=g) * 0.02)
+    buf[5, 300] = float("nan")
+    buf[200, 10] = float("inf")
+    buf[300, 600] = -float("inf")
+    buf[130:140, 0:128] = 1e-40
+    buf[256:384, 256:384] = 0.0
+    buf = buf.to(dev)
+    Wc = buf[:, :K].contiguous()
+    Ws = buf[:, :K]
+    assert Ws.stride(0) % 4 != 0
+    q1, s1 = fp8.quantize_weight(Wc)
+    q2, s2 = fp8.quantize_weight(Ws)
+    assert torch.equal(_u8(q1), _u8(q2))
+    assert torch.equal(s1.cpu().view(torch.int32), s2.cpu().view(torch.int32))
+    assert torch.isnan(s1[0, 2]) and torch.isinf(s1[1, 0]) and s1[2, 2] > 0
