@@ -417,34 +417,50 @@ weight_quant_block128_kernel(const T* __restrict__ W, int64_t ldw, uint8_t* __re
   weight_quant_block128_body<T>(W, ldw, q, ldq, s, s_sn, s_sk, N, K);
 }
 
-// fp32 weights with 16-byte rows (ldw % 4 == 0, W 16-byte aligned) and
-// 4-byte aligned q rows: the same block quantiser with 16-byte loads. A lane
-// holds 4 consecutive columns of 16 rows (wave w: rows 32w + 2i + lane/32,
-// i < 16), so each load instruction covers two 512-byte rows and each store
-// writes 4 codes; the blocks on the matrix edge take the per-element kernel's
-// path. Same max, same scale, same per-element IEEE division: same bits.
+// Weights whose rows are 16-byte multiples (fp32: ldw % 4 == 0, bf16:
+// ldw % 8 == 0; W 16-byte aligned) and q rows aligned to one lane's codes:
+// the same block quantiser with 16-byte loads. A lane holds VPL = 16 /
+// sizeof(T) consecutive columns of NL rows (a load instruction covers
+// RPL = 64 * VPL / 128 rows of the block: 2 for fp32, 4 for bf16); each
+// store writes VPL codes. Blocks on the matrix edge take the per-element
+// kernel's path. Same max, same scale, same per-element IEEE division: same
+// bits.
+template <typename T>
 __global__ void __launch_bounds__(256)
-weight_quant_f32x4_kernel(const float* __restrict__ W, int64_t ldw, uint8_t* __restrict__ q,
-                          int64_t ldq, float* __restrict__ s, int64_t s_sn, int64_t s_sk,
-                          int64_t N, int64_t K) {
+weight_quant_vec_kernel(const T* __restrict__ W, int64_t ldw, uint8_t* __restrict__ q,
+                        int64_t ldq, float* __restrict__ s, int64_t s_sn, int64_t s_sk,
+                        int64_t N, int64_t K) {
+  constexpr int VPL = 16 / sizeof(T), LPR = 128 / VPL, RPL = 64 / LPR, NL = 32 / RPL;
   const int nb = blockIdx.y, kb = blockIdx.x;
   if ((int64_t)nb * 128 + 128 > N || (int64_t)kb * 128 + 128 > K) {
-    weight_quant_block128_body<float>(W, ldw, q, ldq, s, s_sn, s_sk, N, K);
+    weight_quant_block128_body<T>(W, ldw, q, ldq, s, s_sn, s_sk, N, K);
     return;
   }
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int64_t n0 = (int64_t)nb * 128 + wid * 32 + (lane >> 5);
-  const int64_t k = (int64_t)kb * 128 + (lane & 31) * 4;
-  v4f v[16];
+  const int64_t n0 = (int64_t)nb * 128 + wid * 32 + lane / LPR;
+  const int64_t k = (int64_t)kb * 128 + (lane % LPR) * VPL;
+  float v[NL][VPL];
 #pragma unroll
-  for (int i = 0; i < 16; ++i)
-    v[i] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(W + (n0 + 2 * i) * ldw + k));
+  for (int i = 0; i < NL; ++i) {
+    const v4i raw = __builtin_nontemporal_load(
+        reinterpret_cast<const v4i*>(W + (n0 + RPL * i) * ldw + k));
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t u = (uint32_t)raw[w];
+      if constexpr (VPL == 4) {
+        v[i][w] = __uint_as_float(u);
+      } else {
+        v[i][2 * w] = __uint_as_float(u << 16);
+        v[i][2 * w + 1] = __uint_as_float(u & 0xFFFF0000u);
+      }
+    }
+  }
   float amax = 0.f;
   bool nan = false;
 #pragma unroll
-  for (int i = 0; i < 16; ++i)
+  for (int i = 0; i < NL; ++i)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+    for (int e = 0; e < VPL; ++e) {
       nan |= v[i][e] != v[i][e];
       amax = fmaxf(amax, fabsf(v[i][e]));
     }
@@ -454,16 +470,29 @@ weight_quant_f32x4_kernel(const float* __restrict__ W, int64_t ldw, uint8_t* __r
   const float scale = block_nan ? __uint_as_float(0x7FC00000u)
                                 : fmaxf(__uint_as_float(m), kAmaxFloor) / kFp8Max;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    uint32_t b;
-    if (block_nan) {
-      b = 0x7F7F7F7Fu;
-    } else {
-      int p = __builtin_amdgcn_cvt_pk_fp8_f32(v[i][0] / scale, v[i][1] / scale, 0, false);
-      p = __builtin_amdgcn_cvt_pk_fp8_f32(v[i][2] / scale, v[i][3] / scale, p, true);
-      b = (uint32_t)p;
+  for (int i = 0; i < NL; ++i) {
+    uint32_t b[VPL / 4];
+#pragma unroll
+    for (int c = 0; c < VPL / 4; ++c) {
+      if (block_nan) {
+        b[c] = 0x7F7F7F7Fu;
+      } else {
+        int p = __builtin_amdgcn_cvt_pk_fp8_f32(v[i][4 * c] / scale, v[i][4 * c + 1] / scale,
+                                                0, false);
+        p = __builtin_amdgcn_cvt_pk_fp8_f32(v[i][4 * c + 2] / scale, v[i][4 * c + 3] / scale,
+                                            p, true);
+        b[c] = (uint32_t)p;
+      }
     }
-    *reinterpret_cast<uint32_t*>(q + (n0 + 2 * i) * ldq + k) = b;
+    uint8_t* dst = q + (n0 + RPL * i) * ldq + k;
+    if constexpr (VPL == 4) {
+      *reinterpret_cast<uint32_t*>(dst) = b[0];
+    } else {
+      v2i w2;
+      w2[0] = (int)b[0];
+      w2[1] = (int)b[1];
+      *reinterpret_cast<v2i*>(dst) = w2;
+    }
   }
   if (threadIdx.x == 0) s[(int64_t)nb * s_sn + (int64_t)kb * s_sk] = scale;
 }
@@ -498,8 +527,12 @@ extern "C" int fp8b_weight_quant(const void* W, int64_t ldw, int w_dtype, void* 
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid((unsigned)KB, (unsigned)NB);
   if (w_dtype == FP8B_F32 && ldw % 4 == 0 && aligned(W, 16) && ldq % 4 == 0 && aligned(q, 4))
-    weight_quant_f32x4_kernel<<<grid, 256, 0, st>>>((const float*)W, ldw, (uint8_t*)q, ldq, s,
-                                                    s_sn, s_sk, N, K);
+    weight_quant_vec_kernel<float><<<grid, 256, 0, st>>>((const float*)W, ldw, (uint8_t*)q, ldq,
+                                                         s, s_sn, s_sk, N, K);
+  else if (w_dtype == FP8B_BF16 && ldw % 8 == 0 && aligned(W, 16) && ldq % 8 == 0 &&
+           aligned(q, 8))
+    weight_quant_vec_kernel<uint16_t><<<grid, 256, 0, st>>>(
+        (const uint16_t*)W, ldw, (uint8_t*)q, ldq, s, s_sn, s_sk, N, K);
   else if (w_dtype == FP8B_F32)
     weight_quant_block128_kernel<float><<<grid, 256, 0, st>>>((const float*)W, ldw, (uint8_t*)q,
                                                               ldq, s, s_sn, s_sk, N, K);

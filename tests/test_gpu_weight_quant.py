@@ -62,13 +62,14 @@ def test_quantize_state_dict_on_gpu(dev):
     assert set(checkpoint.fp8_linear_weights(out)) == {"a.weight", "b.weight"}
 
 
-def test_weight_quant_vector_path_equals_scalar_path(dev):
-    """fp32 W with 16-byte rows takes the 16-byte-load kernel (edge blocks
-    inside it take the per-element path); a row-strided view of the same
-    values (row stride not a multiple of 4) takes the per-element kernel.
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_weight_quant_vector_path_equals_scalar_path(dtype, dev):
+    """W with 16-byte rows takes the 16-byte-load kernel (edge blocks inside
+    it take the per-element path); a row-strided view of the same values
+    (row stride not a multiple of 16 bytes) takes the per-element kernel.
     Same codes and scales, bit for bit, with NaN, +-inf, subnormal and zero
     blocks."""
-    print("weight quant vector vs scalar path", flush=True)
+    print(f"weight quant vector vs scalar path {dtype}", flush=True)
     N, K = 384, 640 + 72   # ragged last block column (K % 128 = 72)
     g = torch.Generator().manual_seed(77)
     buf = (torch.randn(N, K + 2, generator=g) * 0.02)
@@ -77,10 +78,10 @@ def test_weight_quant_vector_path_equals_scalar_path(dev):
     buf[300, 600] = -float("inf")
     buf[130:140, 0:128] = 1e-40
     buf[256:384, 256:384] = 0.0
-    buf = buf.to(dev)
+    buf = buf.to(dtype).to(dev)
     Wc = buf[:, :K].contiguous()
     Ws = buf[:, :K]
-    assert Ws.stride(0) % 4 != 0
+    assert (Ws.stride(0) * Ws.element_size()) % 16 != 0
     q1, s1 = fp8.quantize_weight(Wc)
     q2, s2 = fp8.quantize_weight(Ws)
     assert torch.equal(_u8(q1), _u8(q2))
