@@ -413,6 +413,21 @@ def secondary(torch, fp8, synthetic, dev):
                                           "pct_hbm_peak": round(100 * byt / ms / 1e6 /
                                                                 PEAK_HBM_GBS, 1)}
     log(f"weight_quant: {res['weight_quant_4096x14336_f32']}")
+    # the same from bf16 weights (the usual checkpoint dtype); four inputs
+    # (470 MB) rotate past the MALL
+    wsrc = [(torch.randn(N, K, device=dev) * 0.02).to(torch.bfloat16) for _ in range(4)]
+    it[0] = 0
+
+    def wqb():
+        i = it[0] = (it[0] + 1) % 4
+        return fp8.quantize_weight(wsrc[i])
+    ms = time_events(wqb, 20, 5, torch)
+    byt = 2.0 * N * K + N * K + 4.0 * (N // 128) * (K // 128)
+    res["weight_quant_4096x14336_bf16"] = {"us": round(ms * 1e3, 2),
+                                           "GB/s": round(byt / ms / 1e6, 1),
+                                           "pct_hbm_peak": round(100 * byt / ms / 1e6 /
+                                                                 PEAK_HBM_GBS, 1)}
+    log(f"weight_quant bf16: {res['weight_quant_4096x14336_bf16']}")
     del wsrc
 
     # MLP chain M=3001, H=4096, I=14336
