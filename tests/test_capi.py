@@ -93,6 +93,20 @@ def test_gate_up_silu_quant_rejects_bad_args_without_gpu():
              4, 128, 512, None) == 1                                     # null pointers
     assert f(None, 512, None, 512, None, 4, 1, None, 4, 1, None, 128, None, 1, 1,
              0, 128, 512, None) == 0                                     # empty
+    # rejected before any launch (fake, non-null, 256-byte aligned pointers:
+    # nothing is dereferenced or launched on these paths)
+    P = 1 << 20
+    assert f(P, 512, P, 512, P, 4, 2, P, 4, 1, P, 128, P, 1, 1,
+             4, 128, 512, None) == 3                                     # As not K-contiguous
+    assert b"K-contiguous" in lib.fp8b_last_error()
+    assert f(P, 512, P, 512, P, 4, 1, P, 6, 1, P, 128, P, 1, 1,
+             4, 128, 512, None) == 3                                     # Bs row stride % 4
+    assert f(P + 8, 512, P, 512, P, 4, 1, P, 4, 1, P, 128, P, 1, 1,
+             4, 128, 512, None) == 3                                     # A not 16-byte aligned
+    assert f(P, 512, P, 512, P, 4, 1, P, 4, 1, P + 4, 128, P, 1, 1,
+             4, 128, 512, None) == 3                                     # q not 8-byte aligned
+    assert f(P, 512, P, 512, P, 4, 1, P, 4, 1, P, 132, P, 1, 1,
+             4, 128, 512, None) == 3                                     # ldq % 8
 
 
 def test_workspace_size_zero_for_unsupported_blocks():
