@@ -142,8 +142,9 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
-              "(every GPU box in this build has a single MI355X; see DESIGN.md for how the "
-              "path would shard)", file=sys.stderr)
+              "(every GPU box in this build has a single MI355X; across GPUs act-quant "
+              "would shard by rows and the GEMM by output columns, or by K with one "
+              "all-reduce of the output; that path is not built)", file=sys.stderr)
         sys.exit(2)
 
     import torch
