@@ -246,8 +246,10 @@ extern "C" int fp8b_act_quant(const void* x, int64_t ldx, void* q, int64_t ldq,
   }
   const int64_t gpr = (K + group - 1) / group;
   hipStream_t st = (hipStream_t)stream;
+  // (the fast kernel forms in-row offsets g * 128 in 32 bits)
   const bool fast = group == 128 && K % 128 == 0 && ldx % 8 == 0 && ldq % 8 == 0 &&
-                    aligned(x, 16) && aligned(q, 8) && M * gpr < (int64_t(1) << 31);
+                    aligned(x, 16) && aligned(q, 8) && M * gpr < (int64_t(1) << 31) &&
+                    K < (int64_t(1) << 32);
   if (fast) {
     const int U = g128_unroll(M, gpr);
     const dim3 grid((unsigned)((gpr + 16 * U - 1) / (16 * U)), (unsigned)std::min<int64_t>(M, 65535));
@@ -312,7 +314,8 @@ extern "C" int fp8b_silu_and_mul_quant(const void* x, int64_t ldx, void* q, int6
   const int64_t gpr = (d + group - 1) / group;
   hipStream_t st = (hipStream_t)stream;
   const bool fast = group == 128 && d % 128 == 0 && ldx % 8 == 0 && ldq % 8 == 0 &&
-                    aligned(x, 16) && aligned(q, 8) && M * gpr < (int64_t(1) << 31);
+                    aligned(x, 16) && aligned(q, 8) && M * gpr < (int64_t(1) << 31) &&
+                    d < (int64_t(1) << 31);
   if (fast) {
     const int U = g128_unroll(M, gpr);
     const dim3 grid((unsigned)((gpr + 16 * U - 1) / (16 * U)), (unsigned)std::min<int64_t>(M, 65535));
@@ -340,9 +343,17 @@ namespace fp8b {
 //   Bs[nb,kb] = max(amax_block, 1e-10) / 448 (IEEE), Wq = e4m3fn(W / Bs)
 // with IEEE division and the gfx950 OCP convert (RNE); elements past N or K
 // do not take part. NaN in a block propagates to its scale (as torch.amax
-// does) and every element of that block becomes the e4m3fn NaN 0x7F.
+// does) and every element of that block becomes the e4m3fn NaN 0x7F; a
+// block whose amax is +inf gets scale +inf, 0x7F for its +-inf elements and
+// a signed zero (x / inf) for the finite ones, the act-quant policy.
 template <typename T>
 __device__ __forceinline__ float load_w(const T* p);
+
+// Code of x in a block of scale +inf.
+__device__ __forceinline__ uint32_t inf_block_code(float x) {
+  const uint32_t u = __float_as_uint(x);
+  return (u & 0x7FFFFFFFu) == 0x7F800000u ? (uint32_t)kFp8NaN : (u >> 24) & 0x80u;
+}
 template <>
 __device__ __forceinline__ float load_w<float>(const float* p) { return *p; }
 template <>
@@ -387,6 +398,7 @@ __device__ __forceinline__ void weight_quant_block128_body(
   const uint32_t m =
       block128_max_u32(__float_as_uint(amax) | (nan ? 0x7FC00000u : 0u), lane, wid);
   const bool block_nan = m > 0x7F800000u;
+  const bool block_inf = m == 0x7F800000u;
   const float scale = block_nan ? __uint_as_float(0x7FC00000u)
                                 : fmaxf(__uint_as_float(m), kAmaxFloor) / kFp8Max;
 #pragma unroll
@@ -396,6 +408,8 @@ __device__ __forceinline__ void weight_quant_block128_body(
     uint32_t b;
     if (block_nan) {
       b = (uint32_t)kFp8NaN | ((uint32_t)kFp8NaN << 8);
+    } else if (block_inf) {
+      b = inf_block_code(v[r][0]) | (inf_block_code(v[r][1]) << 8);
     } else {
       b = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v[r][0] / scale, v[r][1] / scale, 0, false) &
           0xFFFFu;
@@ -467,6 +481,7 @@ weight_quant_vec_kernel(const T* __restrict__ W, int64_t ldw, uint8_t* __restric
   const uint32_t m =
       block128_max_u32(__float_as_uint(amax) | (nan ? 0x7FC00000u : 0u), lane, wid);
   const bool block_nan = m > 0x7F800000u;
+  const bool block_inf = m == 0x7F800000u;
   const float scale = block_nan ? __uint_as_float(0x7FC00000u)
                                 : fmaxf(__uint_as_float(m), kAmaxFloor) / kFp8Max;
 #pragma unroll
@@ -476,6 +491,9 @@ weight_quant_vec_kernel(const T* __restrict__ W, int64_t ldw, uint8_t* __restric
     for (int c = 0; c < VPL / 4; ++c) {
       if (block_nan) {
         b[c] = 0x7F7F7F7Fu;
+      } else if (block_inf) {
+        b[c] = inf_block_code(v[i][4 * c]) | (inf_block_code(v[i][4 * c + 1]) << 8) |
+               (inf_block_code(v[i][4 * c + 2]) << 16) | (inf_block_code(v[i][4 * c + 3]) << 24);
       } else {
         int p = __builtin_amdgcn_cvt_pk_fp8_f32(v[i][4 * c] / scale, v[i][4 * c + 1] / scale,
                                                 0, false);

@@ -36,8 +36,6 @@
 namespace fp8b {
 
 struct GemmArgs {
-  const uint16_t* X;  // bf16 activations (fused act-quant decode path only)
-  int64_t ldx;
   const uint8_t* A;
   const uint8_t* B;
   const float* As;
@@ -79,6 +77,18 @@ __device__ __forceinline__ void tile_of_bid(int bid, int tiles_m, int tiles_n, i
 }
 
 typedef __attribute__((address_space(3))) void lds_void;
+
+// One 16x16x128 fp8 (e4m3) MFMA with a zero accumulator: 16 rows of a (the
+// MFMA A operand, lane = row & 15, K bytes 32*(lane>>4)..+31) times 16 rows of
+// b, summed over 128 K. With both scale operands 0 the compiler selects the
+// unscaled v_mfma_f32_16x16x128_f8f6f4 (one 8-byte instruction) instead of
+// the E8M0-scaled form with scale 127 = 1.0 (a v_mfma_ld_scale_b32 prefix
+// plus the MFMA): the same product bit for bit, one instruction less per
+// MFMA (measured 2.4% faster on the large GEMM at steady clock).
+__device__ __forceinline__ v4f mfma16x16x128(const v8i& a, const v8i& b) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0,
+                                                          0, 0, 0);
+}
 
 __device__ __forceinline__ void lds_dma16(const void* gsrc, uint8_t* ldst) {
   __builtin_amdgcn_global_load_lds(gsrc, (lds_void*)ldst, 16, 0, 0);
@@ -317,15 +327,13 @@ gemm_bs128_kernel(GemmArgs a) {
       for (int j = 0; j < FN / 2; ++j)
         wf[j] = lds_frag(sbase + b_row + (h * FN / 2 + j) * 16 * 128, c0, r7);
       // Software pipeline: the FMAs of one sub-tile run under the next MFMA.
-      v4f prev = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-          wf[0], xf[0], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
+      v4f prev = mfma16x16x128(wf[0], xf[0]);
 #pragma unroll
       for (int t = 1; t <= FM * (FN / 2); ++t) {
         v4f cur = prev;
         if (t < FM * (FN / 2)) {
           const int i = t / (FN / 2), j = t % (FN / 2);
-          cur = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-              wf[j], xf[i], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
+          cur = mfma16x16x128(wf[j], xf[i]);
         }
         const int pi = (t - 1) / (FN / 2), pj = h * (FN / 2) + (t - 1) % (FN / 2);
 #pragma unroll
@@ -604,8 +612,7 @@ __global__ void __launch_bounds__(512) gemm_pipe256_kernel(GemmArgs a) {
         __syncthreads();
         if (KIND == 0 && ((rel + 2) & 7) == 0) issue_win(kb + 2, ((rel + 2) >> 3) & 1);
       }
-      v4f res = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-          w[j], xs[i & 3], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
+      v4f res = mfma16x16x128(w[j], xs[i & 3]);
       asm volatile("" : "+v"(res));
       // Within the step: MFMA, then the LDS reads and DMA, then the folds of
       // MFMA p-2 (measured 2-3% faster than folding before the reads).
@@ -940,8 +947,7 @@ __global__ void __launch_bounds__((128 / WM) * (128 / WN) * 64) gemm_pipe128_ker
 #pragma unroll
     for (int p = 0; p < FM * FN; ++p) {
       const int i = p / FN, j = p % FN;
-      v4f res = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-          wf[S][j], xf[S][i], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
+      v4f res = mfma16x16x128(wf[S][j], xf[S][i]);
       asm volatile("" : "+v"(res));
       if (p >= 2) {
         const int qi = (p - 2) / FN, qj = (p - 2) % FN;
@@ -1043,46 +1049,34 @@ __device__ __forceinline__ void wait_vmcnt_rt(int n) {
 // the CUs (partials go to the workspace and splitk_reduce_kernel sums them
 // in split order). Each K-block stages 128 weight rows (a wave owns 16) and
 // the 16*FM activation rows once for all 8 waves, so activations cost
-// 16*FM/128 (fp8) or 32*FM/128 (bf16) of the weight bytes in L2->LDS
-// traffic. NS LDS stages keep the DMA of the next K-blocks in flight; the
-// stage of K-block kb-1 is refilled right after the barrier that opens
-// K-block kb. Weight-block scales arrive per window of 8 K-blocks by 4-byte
-// DMA (any Bs strides).
-// QA = false: fp8 A and As from act-quant; As arrives in the scale windows
-//   (slot-major, 32 rows per slot).
-// QA = true: bf16 x. The stage carries the K-block's bf16 activation rows;
-//   right after the barrier that opens K-block kb the workgroup quantises
-//   K-block kb+1's rows (the act-quant arithmetic of quant.h, one 16-lane
-//   row per 128-group) into one of two fp8 slots laid out like the staged
-//   rows, with the row scales beside them; rows past M are zero with scale
-//   0. This fuses act-quant into the GEMM for decode shapes.
+// 16*FM/128 of the weight bytes in L2->LDS traffic. NS LDS stages keep the
+// DMA of the next K-blocks in flight; the stage of K-block kb-1 is refilled
+// right after the barrier that opens K-block kb. Activation and weight-block
+// scales arrive per window of 8 K-blocks by 4-byte DMA (any strides; the
+// activation scales slot-major, 32 rows per slot).
+// Preconditions (checked by the host, decode_offsets_ok): the 32-bit DMA
+// offsets row * ldb + 127 (row <= 127) and row * lda + 127 (row <= 47) fit.
 // ---------------------------------------------------------------------------
-template <int FM, bool QA, bool PR = false, int NSX = 0> struct DecodeCfg {
+template <int FM, bool PR = false, int NSX = 0> struct DecodeCfg {
   static constexpr int NW = 8, BN = 128, AR = 16 * FM;
-  // measured (fp8 path): deeper rings only lengthen the start-up burst; the
-  // bf16 path waits one K-block further ahead, so it keeps one more stage.
-  // NSX = 3 (grids above one workgroup per CU): the smaller ring lets two
-  // workgroups share a CU, so the whole grid is resident (32x28672x4096,
-  // 448 workgroups: 29.7 us against 33.7 with four stages).
-  static constexpr int NS = NSX ? NSX : (QA ? 5 : 4);
-  static constexpr int ACT_ROWS = QA ? 2 * AR : AR;        // 128-byte rows of activations
-  static constexpr int STAGE = (BN + ACT_ROWS) * 128;
-  static constexpr int ACT_LOADS = ACT_ROWS / 8;           // 1 KiB wave-loads per K-block
-  static constexpr int WIN_SA = QA ? 0 : 8 * 32 * 4 * ((FM + 1) / 2);
+  // measured: deeper rings only lengthen the start-up burst. NSX = 3 (grids
+  // above one workgroup per CU): the smaller ring lets two workgroups share
+  // a CU, so the whole grid is resident (32x28672x4096, 448 workgroups:
+  // 29.7 us against 33.7 with four stages).
+  static constexpr int NS = NSX ? NSX : 4;
+  static constexpr int STAGE = (BN + AR) * 128;
+  static constexpr int ACT_LOADS = AR / 8;                 // 1 KiB wave-loads per K-block
+  static constexpr int WIN_SA = 8 * 32 * 4 * ((FM + 1) / 2);
   // PR (per-row weight scales): Bs of the 128 rows, slot-major (8 x 512 B).
   static constexpr int WIN = WIN_SA + (PR ? 8 * BN * 4 : 256);
   static constexpr int SW_OFF = NS * STAGE;
-  static constexpr int AQ_OFF = SW_OFF + 2 * WIN;          // QA: two fp8 slots
-  static constexpr int AQ_KB = AR * 128;
-  static constexpr int SQ_OFF = AQ_OFF + (QA ? 2 * AQ_KB : 0);  // QA: their scales
-  static constexpr int SMEM = SQ_OFF + (QA ? 2 * AR * 4 : 0);
+  static constexpr int SMEM = SW_OFF + 2 * WIN;
 };
 
-template <int FM, bool QA, bool PR = false, int NSX = 0>
+template <int FM, bool PR = false, int NSX = 0>
 __global__ void __launch_bounds__(512) gemm_decode_kernel(GemmArgs a) {
-  using Cfg = DecodeCfg<FM, QA, PR, NSX>;
-  static_assert(!(QA && PR), "the fused-quantisation path uses 128x128 weight blocks");
-  constexpr int NW = Cfg::NW, BN = Cfg::BN, AR = Cfg::AR, NS = Cfg::NS;
+  using Cfg = DecodeCfg<FM, PR, NSX>;
+  constexpr int NW = Cfg::NW, BN = Cfg::BN, NS = Cfg::NS;
   constexpr int STAGE = Cfg::STAGE, WIN_SA = Cfg::WIN_SA, WIN = Cfg::WIN;
   constexpr int SW_OFF = Cfg::SW_OFF, ACT_LOADS = Cfg::ACT_LOADS;
   static_assert(Cfg::SMEM <= 160 * 1024, "LDS budget");
@@ -1104,9 +1098,8 @@ __global__ void __launch_bounds__(512) gemm_decode_kernel(GemmArgs a) {
   // Activation wave-loads of this wave per K-block (waves w, w+8, ...).
   const int act_loads = (ACT_LOADS - wid + NW - 1) / NW;
   // Wave w stages weight rows 16w..16w+15 (wave-loads 2w and 2w+1 of the
-  // stage) and activation wave-loads w, w+8, ...: fp8 rows 8L..8L+7 (eight
-  // lanes per row, chunk-swizzled), or bf16 rows 4L..4L+3 (sixteen lanes per
-  // 256-byte row, in order).
+  // stage) and activation wave-loads w, w+8, ...: rows 8L..8L+7, eight lanes
+  // per 128-byte row, chunk-swizzled.
   auto issue_kb = [&](int kb) {
     const int stage = (kb - kb_begin) % NS;
     const uint32_t lds = lds0 + stage * STAGE;
@@ -1117,24 +1110,18 @@ __global__ void __launch_bounds__(512) gemm_decode_kernel(GemmArgs a) {
       dma16_soff(voff, b_base + (int64_t)kb * 128, lds + (wid * 2 + h) * 1024);
     }
     for (int L = wid; L < ACT_LOADS; L += NW) {
-      if constexpr (QA) {
-        const int row = min(L * 4 + (lane >> 4), a_lim);
-        const uint32_t voff = (uint32_t)row * (uint32_t)(a.ldx * 2) + (lane & 15) * 16;
-        dma16_soff(voff, a.X + (int64_t)kb * 128, lds + (16 + L) * 1024);
-      } else {
-        const uint32_t voff = (uint32_t)min(L * 8 + r8, a_lim) * (uint32_t)a.lda + c16;
-        dma16_soff(voff, a.A + (int64_t)kb * 128, lds + (16 + L) * 1024);
-      }
+      const uint32_t voff = (uint32_t)min(L * 8 + r8, a_lim) * (uint32_t)a.lda + c16;
+      dma16_soff(voff, a.A + (int64_t)kb * 128, lds + (16 + L) * 1024);
     }
   };
-  // Window from kb0: without QA, instruction j (wave j) brings slots 2j, 2j+1
-  // for 32 activation rows (lane i: row i & 31, slot 2j + (i >> 5)); waves
-  // 4..7 do rows 32..63 when FM = 3. The last wave brings the 8 weight-block
-  // scales. K-blocks past kb_end repeat kb_end - 1.
+  // Window from kb0: instruction j (wave j) brings slots 2j, 2j+1 for 32
+  // activation rows (lane i: row i & 31, slot 2j + (i >> 5)); waves 4..7 do
+  // rows 32..63 when FM = 3. The last wave brings the 8 weight-block scales.
+  // K-blocks past kb_end repeat kb_end - 1.
   auto issue_win = [&](int kb0) {
     const int wbuf = ((kb0 - kb_begin) >> 3) & 1;
     const uint32_t lb = lds0 + SW_OFF + wbuf * WIN;
-    constexpr int SA_INS = QA ? 0 : 4 * ((FM + 1) / 2);
+    constexpr int SA_INS = 4 * ((FM + 1) / 2);
     if (wid < SA_INS) {
       const int j = wid & 3, rb = (wid >> 2) * 32;
       const int kb = min(kb0 + 2 * j + (lane >> 5), kb_end - 1);
@@ -1167,37 +1154,6 @@ __global__ void __launch_bounds__(512) gemm_decode_kernel(GemmArgs a) {
   const int per_kb = 2 + act_loads;
   auto wait_after = [&](int n_after) { wait_vmcnt_rt(min(n_after * per_kb, 15)); };
 
-  // QA: quantise the bf16 rows of K-block kb (its stage has landed) into fp8
-  // slot kb & 1. Group (row) g is handled by the 16-lane row g of the pass.
-  auto quantise = [&](int kb) {
-    const int rel = kb - kb_begin;
-    const uint8_t* st = smem + (rel % NS) * STAGE + BN * 128;
-    uint8_t* aq = smem + Cfg::AQ_OFF + (rel & 1) * Cfg::AQ_KB;
-    float* sq = reinterpret_cast<float*>(smem + Cfg::SQ_OFF) + (rel & 1) * AR;
-    const int sub = lane & 15;
-#pragma unroll
-    for (int g0 = 0; g0 < AR; g0 += 32) {
-      if (g0 + wid * 4 >= AR) break;  // the wave's four rows are all past AR
-      const int g = g0 + (int)(threadIdx.x >> 4);
-      const int gr = min(g, AR - 1);
-      const v4i raw = *reinterpret_cast<const v4i*>(st + gr * 256 + sub * 16);
-      float v[8];
-      const uint32_t mag = unpack_bf16x8(raw, v);
-      uint32_t w0, w1;
-      float scale;
-      quant_row16_8(v, mag, w0, w1, scale);
-      if (g < AR) {
-        const bool live = g < a.M;
-        v2i packed;
-        packed[0] = live ? (int)w0 : 0;
-        packed[1] = live ? (int)w1 : 0;
-        *reinterpret_cast<v2i*>(aq + g * 128 + (((sub >> 1) ^ (g & 7)) << 4) + (sub & 1) * 8) =
-            packed;
-        if (sub == 0) sq[g] = live ? scale : 0.f;
-      }
-    }
-  };
-
   // Fragment offsets: this wave's 16 weight rows and the activation rows.
   const int r7 = lane & 7, g2 = 2 * (lane >> 4);
   const int slo = (g2 ^ r7) << 4, shi = ((g2 + 1) ^ r7) << 4;
@@ -1209,29 +1165,13 @@ __global__ void __launch_bounds__(512) gemm_decode_kernel(GemmArgs a) {
   for (int f = 0; f < FM; ++f) acc[f] = v4f{0.f, 0.f, 0.f, 0.f};
 
   for (int k = 0; k < NS - 1 && k < nkb; ++k) issue_next(kb_begin + k);
-  if constexpr (QA) {
-    if (nkb > 0) {
-      wait_after(min(NS - 2, nkb - 1));
-      __syncthreads();
-      quantise(kb_begin);
-    }
-  }
 
   for (int kb = kb_begin; kb < kb_end; ++kb) {
     const int rel = kb - kb_begin;
-    if constexpr (QA) {
-      // the stage of kb+1 (quantised below) must have landed: DMAs issued
-      // after it are those of kb+2 .. min(kb+NS-2, kb_end-1)
-      if (kb + 1 < kb_end) wait_after(min(NS - 3, kb_end - kb - 2));
-    } else {
-      // DMAs issued after K-block kb's: those of kb+1..kb+NS-2 that exist
-      wait_after(min(NS - 2, kb_end - 1 - kb));
-    }
+    // DMAs issued after K-block kb's: those of kb+1..kb+NS-2 that exist
+    wait_after(min(NS - 2, kb_end - 1 - kb));
     __syncthreads();
     if (kb + NS - 1 < kb_end) issue_next(kb + NS - 1);
-    if constexpr (QA) {
-      if (kb + 1 < kb_end) quantise(kb + 1);
-    }
     const uint8_t* st = smem + (rel % NS) * STAGE;
     const uint8_t* win = smem + SW_OFF + ((rel >> 3) & 1) * WIN;
     const int slot = rel & 7;
@@ -1247,18 +1187,10 @@ __global__ void __launch_bounds__(512) gemm_decode_kernel(GemmArgs a) {
 #pragma unroll
     for (int f = 0; f < FM; ++f) {
       const int m = f * 16 + (lane & 15);
-      v8i x;
-      float sa;
-      if constexpr (QA) {
-        x = lds_frag2(smem + Cfg::AQ_OFF + (rel & 1) * Cfg::AQ_KB + (f * 16 + (lane & 15)) * 128,
-                      slo, shi);
-        sa = reinterpret_cast<const float*>(smem + Cfg::SQ_OFF)[(rel & 1) * AR + m];
-      } else {
-        x = lds_frag2(st + x_off + f * 2048, slo, shi);
-        sa = *reinterpret_cast<const float*>(win + (m >> 5) * 1024 + slot * 128 + (m & 31) * 4);
-      }
-      const v4f t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-          w, x, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
+      const v8i x = lds_frag2(st + x_off + f * 2048, slo, shi);
+      const float sa =
+          *reinterpret_cast<const float*>(win + (m >> 5) * 1024 + slot * 128 + (m & 31) * 4);
+      const v4f t = mfma16x16x128(w, x);
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[f][r] = fmaf(t[r], sa * sbv[r], acc[f][r]);
     }
@@ -1349,8 +1281,7 @@ __global__ void __launch_bounds__(512) gemm_skinny_kernel(GemmArgs a) {
         for (int f = 0; f < FM; ++f) {
           const v8i x = lds_frag(sl + (16 + f * 16 + row) * 128, c0, r7);
           const float sc = *reinterpret_cast<const float*>(sl + SCALE_OFF + (f * 16 + row) * 4) * sb;
-          const v4f t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-              w, x, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
+          const v4f t = mfma16x16x128(w, x);
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc[f][r] = fmaf(t[r], sc, acc[f][r]);
         }
@@ -1502,9 +1433,8 @@ enum TileCfg {
   CFG_256x256 = 0,
   CFG_128x128 = 1,
   CFG_64x128 = 2,
-  CFG_32x128 = 3,
-  CFG_SKINNY = 4,
-  CFG_DECODE = 5,
+  CFG_SKINNY = 3,
+  CFG_DECODE = 4,
   CFG_COUNT
 };
 
@@ -1532,27 +1462,25 @@ int device_cu_count() {
   return cus;
 }
 
-// M <= 48 runs gemm_decode_kernel unless FP8B_DECODE=0 (then the skinny
-// kernel, for A/B measurements).
+// Environment switches for A/B measurements, read once per process:
+//   FP8B_DECODE=0   M <= 48 always takes the skinny kernel (no split-K
+//                   decode kernel; per-row scales then take the 128x128 path);
+//   FP8B_PIPE=0     no pipelined kernels (gemm_bs128_kernel instead);
+//   FP8B_TAIL128=0  no 128x128 quarters for a small last wave of 256x256 tiles.
+bool env_flag_on(const char* name) {
+  const char* e = getenv(name);
+  return !(e && e[0] == '0');
+}
 bool use_decode_kernel() {
-  static const bool v = [] {
-    const char* e = getenv("FP8B_DECODE");
-    return !(e && e[0] == '0');
-  }();
+  static const bool v = env_flag_on("FP8B_DECODE");
   return v;
 }
-
-// Largest M served by the skinny kernel (at most 48: three 16-row activation
-// fragments per K-block slot) when FP8B_DECODE=0. FP8B_SKINNY_MAX_M
-// overrides it for A/B measurements (with FP8B_DECODE=0, 0 sends every shape
-// to the tiled path).
-int skinny_max_m() {
-  static const int v = [] {
-    const char* e = getenv("FP8B_SKINNY_MAX_M");
-    if (!e) return 48;
-    const int x = atoi(e);
-    return x < 0 ? 0 : (x > 48 ? 48 : x);
-  }();
+bool use_pipelined_kernels() {
+  static const bool v = env_flag_on("FP8B_PIPE");
+  return v;
+}
+bool use_tail128() {
+  static const bool v = env_flag_on("FP8B_TAIL128");
   return v;
 }
 
@@ -1576,14 +1504,14 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
   const int cus = device_cu_count();
   Plan p;
   auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-  if (M <= skinny_max_m() && !use_decode_kernel() && !per_row) {
+  if (M <= 48 && !use_decode_kernel() && !per_row) {
     // Skinny path: 16 output columns per workgroup, K split inside it.
     p.cfg = CFG_SKINNY; p.bm = (int)(((M + 15) / 16) * 16); p.bn = 16;
     p.splits = 1;
     p.kb_per_split = KB;
     return p;
   }
-  if (M <= 48 && (use_decode_kernel() || per_row)) {
+  if (M <= 48 && use_decode_kernel()) {
     // Decode path: 128 output columns per workgroup; split K until the grid
     // covers the CUs.
     p.cfg = CFG_DECODE; p.bm = (int)(((M + 15) / 16) * 16); p.bn = 128;
@@ -1607,8 +1535,6 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
   }
   if (per_row && M <= 64) {
     p.cfg = CFG_128x128; p.bm = 128; p.bn = 128;
-  } else if (M <= 32) {
-    p.cfg = CFG_32x128; p.bm = 32; p.bn = 128;
   } else if (M <= 64) {
     p.cfg = CFG_64x128; p.bm = 64; p.bn = 128;
   } else if (tiles(256, 256) >= cus || prefer_256(tiles(256, 256), tiles(128, 128), cus)) {
@@ -1635,6 +1561,12 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
   return p;
 }
 
+// 32-bit DMA offsets of gemm_decode_kernel: weight rows up to 127 of a tile
+// (row * ldb + 127) and activation rows up to 47 (row * lda + 127).
+bool decode_offsets_ok(int64_t lda, int64_t ldb) {
+  return 127 * ldb + 128 <= (int64_t(1) << 32) && 47 * lda + 128 <= (int64_t(1) << 32);
+}
+
 bool mfma_path_ok(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N,
                   int64_t K, int64_t block_n, int64_t block_k) {
   return block_n == 128 && block_k == 128 && K % 128 == 0 && K > 0 && lda % 16 == 0 &&
@@ -1646,11 +1578,7 @@ bool mfma_path_ok(const void* A, int64_t lda, const void* B, int64_t ldb, int64_
 // in K, 16-byte aligned rows, K-block counts and split sizes multiples of 4)
 // and 32-bit DMA offsets within a 256-row tile. FP8B_PIPE=0 turns them off.
 bool pipe_ok(const GemmArgs& a, const Plan& p) {
-  static const bool enabled = [] {
-    const char* e = getenv("FP8B_PIPE");
-    return !(e && e[0] == '0');
-  }();
-  if (!enabled) return false;
+  if (!use_pipelined_kernels()) return false;
   const bool splits_ok = p.splits == 1 || a.kb_per_split % 4 == 0;
   return a.as_sk == 1 && a.bs_sk == 1 && a.as_sm % 4 == 0 && a.bs_sn % 4 == 0 &&
          ((uintptr_t)a.As & 15) == 0 && ((uintptr_t)a.Bs & 15) == 0 && a.KB % 4 == 0 &&
@@ -1663,12 +1591,10 @@ bool pipe_ok(const GemmArgs& a, const Plan& p) {
 // same arithmetic per output: MLP gate/up 3001x28672x4096 has 1344 tiles,
 // five full waves and 64 left; the 64 tiles take 35 us as quarters against
 // ~40 us as a sixth wave. FP8B_TAIL128=0 keeps the whole grid on
-// gemm_pipe256_kernel (A/B measurements; read on every call so that tests
-// can compare both).
+// gemm_pipe256_kernel.
 template <bool PR>
 void launch_pipe256(const GemmArgs& a, hipStream_t st) {
-  const char* e = getenv("FP8B_TAIL128");
-  const bool tail_on = !(e && e[0] == '0');
+  const bool tail_on = use_tail128();
   const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
   const int64_t cus = device_cu_count();
   const int64_t full = tiles / cus * cus, rest = tiles - full;
@@ -1755,8 +1681,8 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
   if (!mfma_path_ok(A, lda, B, ldb, M, N, K, per_row ? 128 : block_n, block_k))
     return run_generic();
 
-  const Plan p = make_plan(M, N, K, per_row);
-  const size_t need = p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
+  const Plan p0 = make_plan(M, N, K, per_row);
+  const size_t need = p0.splits > 1 ? (size_t)p0.splits * M * N * sizeof(float) : 0;
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
     set_error("fp8b_w8a8_block_matmul: workspace smaller than fp8b_gemm_workspace_size()");
     return FP8B_ERR_WORKSPACE;
@@ -1765,32 +1691,44 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
     set_error("fp8b_w8a8_block_matmul: workspace must be 16-byte aligned");
     return FP8B_ERR_ALIGN;
   }
-  GemmArgs a;
-  a.X = nullptr; a.ldx = 0;
-  a.A = (const uint8_t*)A; a.B = (const uint8_t*)B; a.As = As; a.Bs = Bs; a.C = C;
-  a.ws = (float*)workspace;
-  a.lda = lda; a.ldb = ldb; a.as_sm = as_sm; a.as_sk = as_sk; a.bs_sn = bs_sn; a.bs_sk = bs_sk;
-  a.ldc = ldc; a.M = (int)M; a.N = (int)N; a.K = (int)K; a.KB = (int)(K / 128);
-  a.kb_per_split = p.kb_per_split;
-  a.tiles_m = (int)((M + p.bm - 1) / p.bm);
-  a.tiles_n = (int)((N + p.bn - 1) / p.bn);
-  a.out_dtype = out_dtype;
-  a.rem_base = -1; a.rem_tiles_m = 0; a.rem_tiles_n = 0;
-  a.Sq = nullptr; a.sq_sm = 0; a.sq_sg = 0;
   // Vector stores: 4 fp32 (16 B) for fp32 C and split-K partials, 8 x 16-bit
   // (16 B) for bf16/fp16 C.
   const bool c_vec = esz == 4 ? (ldc % 4 == 0 && ((uintptr_t)C & 15) == 0)
                               : (ldc % 8 == 0 && ((uintptr_t)C & 15) == 0);
   const bool ws_vec = (N % 4 == 0);
-  a.vec_store = (p.splits > 1) ? (ws_vec ? 1 : 0) : (c_vec ? 1 : 0);
+  auto make_args = [&](const Plan& p) {
+    GemmArgs a;
+    a.A = (const uint8_t*)A; a.B = (const uint8_t*)B; a.As = As; a.Bs = Bs; a.C = C;
+    a.ws = (float*)workspace;
+    a.lda = lda; a.ldb = ldb; a.as_sm = as_sm; a.as_sk = as_sk; a.bs_sn = bs_sn;
+    a.bs_sk = bs_sk; a.ldc = ldc; a.M = (int)M; a.N = (int)N; a.K = (int)K;
+    a.KB = (int)(K / 128);
+    a.kb_per_split = p.kb_per_split;
+    a.tiles_m = (int)((M + p.bm - 1) / p.bm);
+    a.tiles_n = (int)((N + p.bn - 1) / p.bn);
+    a.out_dtype = out_dtype;
+    a.rem_base = -1; a.rem_tiles_m = 0; a.rem_tiles_n = 0;
+    a.Sq = nullptr; a.sq_sm = 0; a.sq_sg = 0;
+    a.vec_store = (p.splits > 1) ? (ws_vec ? 1 : 0) : (c_vec ? 1 : 0);
+    return a;
+  };
 
+  // Leading dimensions too large for the decode kernel's 32-bit DMA offsets:
+  // the skinny kernel (64-bit addresses, no workspace) or, for per-row
+  // scales, the generic kernel.
+  Plan p = p0;
+  if (p.cfg == CFG_DECODE && !decode_offsets_ok(lda, ldb)) {
+    if (per_row) return run_generic();
+    p.cfg = CFG_SKINNY; p.bn = 16; p.splits = 1; p.kb_per_split = (int)(K / 128);
+  }
+  GemmArgs a = make_args(p);
   if (per_row) {
     if (p.cfg == CFG_DECODE) {
       const dim3 grid((unsigned)((N + 127) / 128), 1, (unsigned)p.splits);
       const int fm = (int)((M + 15) / 16);
-      if (fm <= 1) gemm_decode_kernel<1, false, true><<<grid, 512, 0, st>>>(a);
-      else if (fm == 2) gemm_decode_kernel<2, false, true><<<grid, 512, 0, st>>>(a);
-      else gemm_decode_kernel<3, false, true><<<grid, 512, 0, st>>>(a);
+      if (fm <= 1) gemm_decode_kernel<1, true><<<grid, 512, 0, st>>>(a);
+      else if (fm == 2) gemm_decode_kernel<2, true><<<grid, 512, 0, st>>>(a);
+      else gemm_decode_kernel<3, true><<<grid, 512, 0, st>>>(a);
     } else if (pipe_ok(a, p)) {
       dim3 grid(a.tiles_m * a.tiles_n, 1, p.splits);
       if (p.cfg == CFG_256x256) launch_pipe256<true>(a, st);
@@ -1811,9 +1749,9 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
       const dim3 grid((unsigned)((N + 127) / 128), 1, (unsigned)p.splits);
       const int fm = (int)((M + 15) / 16);
       if ((int64_t)grid.x * grid.z > device_cu_count()) {
-        if (fm <= 1) gemm_decode_kernel<1, false, false, 3><<<grid, 512, 0, st>>>(a);
-        else if (fm == 2) gemm_decode_kernel<2, false, false, 3><<<grid, 512, 0, st>>>(a);
-        else gemm_decode_kernel<3, false, false, 3><<<grid, 512, 0, st>>>(a);
+        if (fm <= 1) gemm_decode_kernel<1, false, 3><<<grid, 512, 0, st>>>(a);
+        else if (fm == 2) gemm_decode_kernel<2, false, 3><<<grid, 512, 0, st>>>(a);
+        else gemm_decode_kernel<3, false, 3><<<grid, 512, 0, st>>>(a);
       } else {
         if (fm <= 1) gemm_decode_kernel<1, false><<<grid, 512, 0, st>>>(a);
         else if (fm == 2) gemm_decode_kernel<2, false><<<grid, 512, 0, st>>>(a);
@@ -1838,8 +1776,7 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
       }
       break;
     }
-    case CFG_64x128: launch_cfg<64, 128, 32, 64>(a, p.splits, st); break;
-    default: launch_cfg<32, 128, 32, 32>(a, p.splits, st); break;
+    default: launch_cfg<64, 128, 32, 64>(a, p.splits, st); break;
   }
   if (hipGetLastError() != hipSuccess) {
     set_error("fp8b_w8a8_block_matmul: MFMA kernel launch failed");
@@ -1860,30 +1797,20 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
 
 namespace {
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
-// The decode kernel that quantises bf16 x itself (QA) measured slower than
-// act_quant_g128_kernel<1> followed by the fp8 decode kernel (22 µs against
-// 3.5 + 14.4 µs at 32x4096x14336): it runs only with FP8B_FUSED_QUANT=1, read
-// on every call so tests can exercise both paths. Both give the same bits.
-bool use_fused_quant() {
-  const char* e = getenv("FP8B_FUSED_QUANT");
-  return e && e[0] == '1';
-}
-
-// The QA decode kernel needs M <= 48, 16-byte aligned bf16 rows and
-// MFMA-path weights; other shapes (and the default) quantise into the
-// workspace and run the block GEMM.
-bool fused_decode_ok(const void* x, int64_t ldx, const void* B, int64_t ldb, int64_t M,
-                     int64_t K) {
-  return use_fused_quant() && M <= 48 && use_decode_kernel() && K % 128 == 0 && ldx % 8 == 0 &&
-         ((uintptr_t)x & 15) == 0 && ldb % 16 == 0 && ((uintptr_t)B & 15) == 0 &&
-         127 * ldb + K < (int64_t(1) << 32) && 47 * 2 * ldx + 2 * K < (int64_t(1) << 32);
-}
 }  // namespace
 
+// Act-quant then the block GEMM, as two launches on the caller's stream: the
+// quantiser writes (q, s) into the workspace and the GEMM reads them (plus
+// its own split-K partials, at the start of the workspace). Three one-launch
+// forms were built, checked bit-identical and measured slower at
+// 32x4096x14336 (a decode kernel quantising its bf16 K-blocks in LDS, 22 us
+// against 3.5 + 14.4 us; per-split prologue quantisation; quantisation shared
+// across workgroups through device-coherent memory): the act-quant's work
+// either repeats per column tile or needs a cross-XCD hand-off that costs what
+// the saved launch does.
 extern "C" size_t fp8b_act_quant_matmul_workspace_size(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 128 != 0) return 0;
-  // GEMM workspace, then room for q [M,K] and s [M,K/128] for the shapes
-  // that quantise before the GEMM (the fused path leaves it unused).
+  // GEMM workspace, then q [M,K] and s [M,K/128].
   const size_t gemm = fp8b_gemm_workspace_size(M, N, K, 128, 128);
   return align256(gemm) + align256((size_t)M * K) + (size_t)M * (K / 128) * sizeof(float);
 }
@@ -1915,56 +1842,17 @@ extern "C" int fp8b_act_quant_matmul(const void* x, int64_t ldx, const void* B, 
     set_error("fp8b_act_quant_matmul: workspace must be 256-byte aligned");
     return FP8B_ERR_ALIGN;
   }
-  hipStream_t st = (hipStream_t)stream;
+  if (K == 0) return fp8b_w8a8_block_matmul(nullptr, 0, B, ldb, nullptr, 1, 1, Bs, bs_sn, bs_sk,
+                                           C, ldc, out_dtype, M, N, 0, 128, 128, nullptr, 0,
+                                           stream);
   const int64_t KB = K / 128;
-  const Plan p = make_plan(M, N, K);
-  if (!fused_decode_ok(x, ldx, B, ldb, M, K) || p.cfg != CFG_DECODE) {
-    // Quantise into the workspace, then the block GEMM on (q, s).
-    const size_t gemm = fp8b_gemm_workspace_size(M, N, K, 128, 128);
-    uint8_t* q = (uint8_t*)workspace + align256(gemm);
-    float* s = (float*)(q + align256((size_t)M * K));
-    int rc = fp8b_act_quant(x, ldx, q, K, s, KB, 1, M, K, 128, stream);
-    if (rc != FP8B_OK) return rc;
-    return fp8b_w8a8_block_matmul(q, K, B, ldb, s, KB, 1, Bs, bs_sn, bs_sk, C, ldc, out_dtype,
-                                  M, N, K, 128, 128, workspace, gemm, stream);
-  }
-  GemmArgs a;
-  a.X = (const uint16_t*)x; a.ldx = ldx;
-  a.A = nullptr; a.B = (const uint8_t*)B; a.As = nullptr; a.Bs = Bs; a.C = C;
-  a.ws = (float*)workspace;
-  a.lda = 0; a.ldb = ldb; a.as_sm = 0; a.as_sk = 0; a.bs_sn = bs_sn; a.bs_sk = bs_sk;
-  a.ldc = ldc; a.M = (int)M; a.N = (int)N; a.K = (int)K; a.KB = (int)KB;
-  a.kb_per_split = p.kb_per_split;
-  a.tiles_m = 1;
-  a.tiles_n = (int)((N + 127) / 128);
-  a.out_dtype = out_dtype;
-  a.rem_base = -1; a.rem_tiles_m = 0; a.rem_tiles_n = 0;
-  a.Sq = nullptr; a.sq_sm = 0; a.sq_sg = 0;
-  const size_t esz = out_dtype == FP8B_F32 ? 4 : 2;
-  const bool c_vec = esz == 4 ? (ldc % 4 == 0 && ((uintptr_t)C & 15) == 0)
-                              : (ldc % 8 == 0 && ((uintptr_t)C & 15) == 0);
-  const bool ws_vec = (N % 4 == 0);
-  a.vec_store = (p.splits > 1) ? (ws_vec ? 1 : 0) : (c_vec ? 1 : 0);
-  const dim3 grid((unsigned)a.tiles_n, 1, (unsigned)p.splits);
-  const int fm = (int)((M + 15) / 16);
-  if (fm <= 1) gemm_decode_kernel<1, true><<<grid, 512, 0, st>>>(a);
-  else if (fm == 2) gemm_decode_kernel<2, true><<<grid, 512, 0, st>>>(a);
-  else gemm_decode_kernel<3, true><<<grid, 512, 0, st>>>(a);
-  if (hipGetLastError() != hipSuccess) {
-    set_error("fp8b_act_quant_matmul: kernel launch failed");
-    return FP8B_ERR_LAUNCH;
-  }
-  if (p.splits > 1) {
-    GemmArgs r = a;
-    r.vec_store = (ws_vec && c_vec) ? 1 : 0;
-    const int64_t quads = M * ((N + 3) / 4);
-    splitk_reduce_kernel<<<(unsigned)((quads + 255) / 256), 256, 0, st>>>(r, p.splits);
-    if (hipGetLastError() != hipSuccess) {
-      set_error("fp8b_act_quant_matmul: split-K reduce launch failed");
-      return FP8B_ERR_LAUNCH;
-    }
-  }
-  return FP8B_OK;
+  const size_t gemm = fp8b_gemm_workspace_size(M, N, K, 128, 128);
+  uint8_t* q = (uint8_t*)workspace + align256(gemm);
+  float* s = (float*)(q + align256((size_t)M * K));
+  int rc = fp8b_act_quant(x, ldx, q, K, s, KB, 1, M, K, 128, stream);
+  if (rc != FP8B_OK) return rc;
+  return fp8b_w8a8_block_matmul(q, K, B, ldb, s, KB, 1, Bs, bs_sn, bs_sk, C, ldc, out_dtype, M, N,
+                                K, 128, 128, gemm ? workspace : nullptr, gemm, stream);
 }
 
 extern "C" int fp8b_gate_up_silu_quant(const void* A, int64_t lda, const void* B, int64_t ldb,
@@ -2001,7 +1889,6 @@ extern "C" int fp8b_gate_up_silu_quant(const void* A, int64_t lda, const void* B
     return FP8B_ERR_DIMS;
   }
   GemmArgs a;
-  a.X = nullptr; a.ldx = 0;
   a.A = (const uint8_t*)A; a.B = (const uint8_t*)B; a.As = As; a.Bs = Bs; a.C = q;
   a.ws = nullptr;
   a.lda = lda; a.ldb = ldb; a.as_sm = as_sm; a.as_sk = 1; a.bs_sn = bs_sn; a.bs_sk = 1;

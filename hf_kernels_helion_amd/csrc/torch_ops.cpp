@@ -45,6 +45,23 @@ void check_gpu(const Tensor& t, const char* name) {
               "); this package has no CPU implementation");
 }
 
+// A 2-D operand the kernels can read in place: unit stride along the last
+// dimension and rows at least a row apart (no overlap). Anything else (an
+// expanded row with stride 0, an unfold view, a transposed tensor) is copied
+// to a contiguous tensor first, so the row stride passed down is always
+// >= the row length.
+Tensor rows_apart(const Tensor& t) {
+  const int64_t rows = t.size(0), len = t.size(1);
+  const bool unit_k = len <= 1 || t.stride(1) == 1;
+  const bool apart = rows <= 1 || t.stride(0) >= std::max<int64_t>(len, 1);
+  return (unit_k && apart) ? t : t.contiguous();
+}
+
+// Row stride to pass for a tensor returned by rows_apart.
+int64_t row_stride(const Tensor& t) {
+  return t.size(0) > 1 ? std::max<int64_t>(t.stride(0), t.size(1)) : t.size(1);
+}
+
 int out_code(at::ScalarType t) {
   switch (t) {
     case at::kFloat: return FP8B_F32;
@@ -55,13 +72,14 @@ int out_code(at::ScalarType t) {
   return -1;
 }
 
-Tensor matmul_impl(const Tensor& A, const Tensor& B, const Tensor& As, const Tensor& Bs,
+Tensor matmul_impl(const Tensor& A_in, const Tensor& B_in, const Tensor& As, const Tensor& Bs,
                    int64_t block_n, int64_t block_k, at::ScalarType out_dtype) {
-  check_gpu(A, "A");
-  check_gpu(B, "B");
+  check_gpu(A_in, "A");
+  check_gpu(B_in, "B");
   check_gpu(As, "As");
   check_gpu(Bs, "Bs");
-  TORCH_CHECK(A.dim() == 2 && B.dim() == 2, "A and B must be 2-D ([M,K] and [N,K])");
+  TORCH_CHECK(A_in.dim() == 2 && B_in.dim() == 2, "A and B must be 2-D ([M,K] and [N,K])");
+  const Tensor A = rows_apart(A_in), B = rows_apart(B_in);
   TORCH_CHECK(A.scalar_type() == at::kFloat8_e4m3fn, "A must be float8_e4m3fn, got ",
               A.scalar_type());
   TORCH_CHECK(B.scalar_type() == at::kFloat8_e4m3fn, "B must be float8_e4m3fn, got ",
@@ -78,8 +96,6 @@ Tensor matmul_impl(const Tensor& A, const Tensor& B, const Tensor& As, const Ten
   TORCH_CHECK(Bs.dim() == 2 && Bs.size(0) >= nb && Bs.size(1) >= kb,
               "Bs must be [ceil(N/block_n), ceil(K/block_k)] = [", nb, ",", kb, "], got ",
               Bs.sizes());
-  TORCH_CHECK(K <= 1 || (A.stride(1) == 1 && B.stride(1) == 1),
-              "A and B must have unit stride along K");
   TORCH_CHECK(B.device() == A.device() && As.device() == A.device() && Bs.device() == A.device(),
               "all tensors must be on one device");
   const int code = out_code(out_dtype);
@@ -89,8 +105,7 @@ Tensor matmul_impl(const Tensor& A, const Tensor& B, const Tensor& As, const Ten
   const size_t ws_bytes = fp8b_gemm_workspace_size(M, N, K, block_n, block_k);
   Tensor ws;
   if (ws_bytes) ws = at::empty({(int64_t)ws_bytes}, A.options().dtype(at::kByte));
-  const int64_t lda = std::max<int64_t>(M > 1 ? A.stride(0) : K, K);
-  const int64_t ldb = std::max<int64_t>(N > 1 ? B.stride(0) : K, K);
+  const int64_t lda = row_stride(A), ldb = row_stride(B);
   const int st = fp8b_w8a8_block_matmul(
       A.data_ptr(), lda, B.data_ptr(), ldb, As.data_ptr<float>(), As.stride(0), As.stride(1),
       Bs.data_ptr<float>(), Bs.stride(0), Bs.stride(1), out.data_ptr(), N, code, M, N, K,
@@ -110,12 +125,13 @@ Tensor w8a8_block_fp8_matmul_dtype(const Tensor& A, const Tensor& B, const Tenso
   return matmul_impl(A, B, As, Bs, block_n, block_k, output_dtype);
 }
 
-Tensor act_quant_matmul(const Tensor& x, const Tensor& B, const Tensor& Bs, int64_t block_n,
-                        int64_t block_k, at::ScalarType output_dtype) {
-  check_gpu(x, "x");
-  check_gpu(B, "B");
+Tensor act_quant_matmul(const Tensor& x_in, const Tensor& B_in, const Tensor& Bs,
+                        int64_t block_n, int64_t block_k, at::ScalarType output_dtype) {
+  check_gpu(x_in, "x");
+  check_gpu(B_in, "B");
   check_gpu(Bs, "Bs");
-  TORCH_CHECK(x.dim() == 2 && B.dim() == 2, "x and B must be 2-D ([M,K] and [N,K])");
+  TORCH_CHECK(x_in.dim() == 2 && B_in.dim() == 2, "x and B must be 2-D ([M,K] and [N,K])");
+  const Tensor x = rows_apart(x_in), B = rows_apart(B_in);
   TORCH_CHECK(x.scalar_type() == at::kBFloat16, "x must be bfloat16, got ", x.scalar_type());
   TORCH_CHECK(B.scalar_type() == at::kFloat8_e4m3fn, "B must be float8_e4m3fn, got ",
               B.scalar_type());
@@ -129,8 +145,6 @@ Tensor act_quant_matmul(const Tensor& x, const Tensor& B, const Tensor& Bs, int6
   const int64_t kb = K / 128, nb = (N + 127) / 128;
   TORCH_CHECK(Bs.dim() == 2 && Bs.size(0) >= nb && Bs.size(1) >= kb,
               "Bs must be [ceil(N/128), K/128] = [", nb, ",", kb, "], got ", Bs.sizes());
-  TORCH_CHECK(K <= 1 || (x.stride(1) == 1 && B.stride(1) == 1),
-              "x and B must have unit stride along K");
   TORCH_CHECK(B.device() == x.device() && Bs.device() == x.device(),
               "all tensors must be on one device");
   const int code = out_code(output_dtype);
@@ -140,8 +154,7 @@ Tensor act_quant_matmul(const Tensor& x, const Tensor& B, const Tensor& Bs, int6
   const size_t ws_bytes = fp8b_act_quant_matmul_workspace_size(M, N, K);
   Tensor ws;
   if (ws_bytes) ws = at::empty({(int64_t)ws_bytes}, x.options().dtype(at::kByte));
-  const int64_t ldx = std::max<int64_t>(M > 1 ? x.stride(0) : K, K);
-  const int64_t ldb = std::max<int64_t>(N > 1 ? B.stride(0) : K, K);
+  const int64_t ldx = row_stride(x), ldb = row_stride(B);
   const int st = fp8b_act_quant_matmul(
       x.data_ptr(), ldx, B.data_ptr(), ldb, Bs.data_ptr<float>(), Bs.stride(0), Bs.stride(1),
       out.data_ptr(), N, code, M, N, K, ws_bytes ? ws.data_ptr() : nullptr, ws_bytes,
@@ -150,22 +163,22 @@ Tensor act_quant_matmul(const Tensor& x, const Tensor& B, const Tensor& Bs, int6
   return out;
 }
 
-std::tuple<Tensor, Tensor> weight_quant(const Tensor& W, int64_t block_n, int64_t block_k) {
-  check_gpu(W, "W");
-  TORCH_CHECK(W.dim() == 2, "W must be 2-D [N,K]");
+std::tuple<Tensor, Tensor> weight_quant(const Tensor& W_in, int64_t block_n, int64_t block_k) {
+  check_gpu(W_in, "W");
+  TORCH_CHECK(W_in.dim() == 2, "W must be 2-D [N,K]");
+  const Tensor W = rows_apart(W_in);
   TORCH_CHECK(W.scalar_type() == at::kFloat || W.scalar_type() == at::kBFloat16,
               "W must be float32 or bfloat16, got ", W.scalar_type());
   TORCH_CHECK(block_n == 128 && block_k == 128, "weight_quant supports 128x128 blocks, got [",
               block_n, ",", block_k, "]");
   const int64_t N = W.size(0), K = W.size(1);
-  TORCH_CHECK(K <= 1 || W.stride(1) == 1, "W must have unit stride along K");
   at::hip::HIPGuardMasqueradingAsCUDA guard(W.device());
   const int64_t kp = (K + 1) / 2 * 2;  // even row stride for the 2-byte stores
   Tensor qbuf = at::empty({N, kp}, W.options().dtype(at::kFloat8_e4m3fn));
   Tensor q = qbuf.narrow(1, 0, K);
   Tensor s = at::empty({(N + 127) / 128, (K + 127) / 128}, W.options().dtype(at::kFloat));
   if (N == 0 || K == 0) return {q, s};
-  const int64_t ldw = std::max<int64_t>(N > 1 ? W.stride(0) : K, K);
+  const int64_t ldw = row_stride(W);
   const int st = fp8b_weight_quant(W.data_ptr(), ldw,
                                    W.scalar_type() == at::kFloat ? FP8B_F32 : FP8B_BF16,
                                    q.data_ptr(), kp, s.data_ptr<float>(), s.stride(0),
@@ -194,13 +207,13 @@ std::tuple<Tensor, Tensor> act_quant(const Tensor& x, int64_t block_size) {
   auto lead = x.sizes().vec();
   lead.pop_back();
   Tensor x2 = x.reshape({-1, K});
-  if (x2.numel() > 0 && K > 1 && x2.stride(1) != 1) x2 = x2.contiguous();
+  if (x2.numel() > 0) x2 = rows_apart(x2);
   const int64_t M = x2.size(0);
   at::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
   Tensor q = at::empty({M, K}, x.options().dtype(at::kFloat8_e4m3fn));
   Tensor s = at::empty({M, groups}, x.options().dtype(at::kFloat));
   if (M > 0 && K > 0) {
-    const int64_t ldx = std::max<int64_t>(M > 1 ? x2.stride(0) : K, K);
+    const int64_t ldx = row_stride(x2);
     const int st = fp8b_act_quant(x2.data_ptr(), ldx, q.data_ptr(), K, s.data_ptr<float>(),
                                   groups, 1, M, K, block_size, current_stream(x));
     check_status(st, "act_quant");
@@ -259,13 +272,14 @@ std::tuple<Tensor, Tensor> silu_and_mul_quant(const Tensor& x, int64_t block_siz
 // Gate/up GEMM with SiLU(gate)*up and group-128 quantisation in its
 // epilogue; B/Bs hold gate and up interleaved in 128-row blocks
 // (interleave_gate_up in finegrained_fp8_helion/mlp.py).
-std::tuple<Tensor, Tensor> gate_up_silu_quant(const Tensor& A, const Tensor& B,
+std::tuple<Tensor, Tensor> gate_up_silu_quant(const Tensor& A_in, const Tensor& B_in,
                                               const Tensor& As, const Tensor& Bs) {
-  check_gpu(A, "A");
-  check_gpu(B, "B");
+  check_gpu(A_in, "A");
+  check_gpu(B_in, "B");
   check_gpu(As, "As");
   check_gpu(Bs, "Bs");
-  TORCH_CHECK(A.dim() == 2 && B.dim() == 2, "A and B must be 2-D ([M,K] and [2I,K])");
+  TORCH_CHECK(A_in.dim() == 2 && B_in.dim() == 2, "A and B must be 2-D ([M,K] and [2I,K])");
+  const Tensor A = rows_apart(A_in), B = rows_apart(B_in);
   TORCH_CHECK(A.scalar_type() == at::kFloat8_e4m3fn && B.scalar_type() == at::kFloat8_e4m3fn,
               "A and B must be float8_e4m3fn");
   TORCH_CHECK(As.scalar_type() == at::kFloat && Bs.scalar_type() == at::kFloat,
@@ -285,9 +299,8 @@ std::tuple<Tensor, Tensor> gate_up_silu_quant(const Tensor& A, const Tensor& B,
   Tensor q = at::empty({M, I}, A.options());
   Tensor s = at::empty({M, I / 128}, As.options());
   if (M > 0) {
-    const int64_t lda = std::max<int64_t>(M > 1 ? A.stride(0) : K, K);
     const int st = fp8b_gate_up_silu_quant(
-        A.data_ptr(), lda, B.data_ptr(), B.stride(0), As.data_ptr<float>(),
+        A.data_ptr(), row_stride(A), B.data_ptr(), row_stride(B), As.data_ptr<float>(),
         As.stride(0), 1, Bs.data_ptr<float>(), Bs.stride(0), 1, q.data_ptr(), I,
         s.data_ptr<float>(), I / 128, 1, M, I, K, current_stream(A));
     check_status(st, "gate_up_silu_quant");

@@ -144,7 +144,9 @@ size_t fp8b_act_quant_matmul_workspace_size(int64_t M, int64_t N, int64_t K);
  *   Bs[nb,kb] = max(amax over block (nb,kb), 1e-10) / 448   (IEEE)
  *   Wq[n,k]   = float8_e4m3fn(W[n,k] / Bs[n/128,k/128])     (IEEE, RNE)
  * Elements past N or K do not take part; a NaN makes its block's scale NaN
- * and every element of the block 0x7F. No counterpart in the reference: it
+ * and every element of the block 0x7F; otherwise a +-inf makes the block's
+ * scale +inf, its +-inf elements 0x7F and its finite elements a signed zero
+ * (the act-quant policy above). No counterpart in the reference: it
  * produces the (B, Bs) operands its callers build with torch
  * (scripts/rebench_llm.py:128-131 uses random fp8 instead).
  * W : w_dtype (FP8B_F32 or FP8B_BF16) [N,K] row stride ldw;

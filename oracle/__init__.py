@@ -19,7 +19,8 @@ Parity status of each function (how it is pinned; see tests/test_oracle.py):
   silu_and_mul     : pinned against torch.nn.functional.silu in fp32 with the
       reference's rounding points, to 1 bf16 ulp.
   quant_weight_block : pinned by the same closed forms as act_quant applied per
-      128x128 block.
+      128x128 block, torch's float8_e4m3fn cast of W / Bs on finite blocks, and
+      the non-finite policy cases (NaN block, +-inf block, subnormal block).
 """
 from .oracle import (  # noqa: F401
     load,

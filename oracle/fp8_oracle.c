@@ -23,8 +23,12 @@
  *   oracle_dequant_matmul : finegrained-fp8-helion/bench.py:11-14
  *       generalised to 2-D Bs: (A*As) @ (B*Bs)^T with the scales expanded.
  *   oracle_silu_and_mul : activation-helion/.../act.py:20-28.
- *   oracle_quant_weight_block : 128x128 weight-block quantiser used to build
- *       test inputs (Bs = max(amax,1e-10)/448 per block, Wq = e4m3fn(W/Bs)).
+ *   oracle_quant_weight_block : 128x128 weight-block quantiser, the format of
+ *       FP8 checkpoints' "weight" + "weight_scale_inv" (Bs = max(amax,1e-10)/448
+ *       per block, Wq = e4m3fn(W/Bs)); no reference counterpart (the reference
+ *       harness draws random fp8 weights, scripts/rebench_llm.py:130-131);
+ *       non-finite blocks as act-quant: NaN -> Bs NaN, codes 0x7F; +inf ->
+ *       Bs +inf, codes 0x7F for +-inf and signed zero for finite values.
  */
 #include <math.h>
 #include <stdint.h>
@@ -196,7 +200,11 @@ void oracle_silu_and_mul(const uint16_t* x, int64_t M, int64_t d, uint16_t* out)
   }
 }
 
-/* W fp32 [N,K] -> Wq [N,K] bytes, Bs [ceil(N/bn), ceil(K/bk)] */
+/* W fp32 [N,K] -> Wq [N,K] bytes, Bs [ceil(N/bn), ceil(K/bk)].
+ * Non-finite blocks follow the act-quant policy above: a NaN anywhere in the
+ * block gives Bs = NaN and every code 0x7F; otherwise an infinite amax gives
+ * Bs = +inf, codes 0x7F for +-inf elements and a signed zero for finite
+ * ones (x / inf). */
 void oracle_quant_weight_block(const float* W, int64_t N, int64_t K, int64_t bn, int64_t bk,
                                uint8_t* Wq, float* Bs) {
   const int64_t NB = (N + bn - 1) / bn, KB = (K + bk - 1) / bk;
@@ -205,9 +213,28 @@ void oracle_quant_weight_block(const float* W, int64_t N, int64_t K, int64_t bn,
       const int64_t n0 = nb * bn, n1 = (n0 + bn < N) ? n0 + bn : N;
       const int64_t k0 = kb * bk, k1 = (k0 + bk < K) ? k0 + bk : K;
       float amax = 0.0f;
+      int has_nan = 0;
       for (int64_t n = n0; n < n1; ++n)
-        for (int64_t k = k0; k < k1; ++k)
-          if (fabsf(W[n * K + k]) > amax) amax = fabsf(W[n * K + k]);
+        for (int64_t k = k0; k < k1; ++k) {
+          const float v = W[n * K + k];
+          if (isnan(v)) has_nan = 1;
+          else if (fabsf(v) > amax) amax = fabsf(v);
+        }
+      if (has_nan) {
+        Bs[nb * KB + kb] = NAN;
+        for (int64_t n = n0; n < n1; ++n)
+          for (int64_t k = k0; k < k1; ++k) Wq[n * K + k] = 0x7F;
+        continue;
+      }
+      if (isinf(amax)) {
+        Bs[nb * KB + kb] = INFINITY;
+        for (int64_t n = n0; n < n1; ++n)
+          for (int64_t k = k0; k < k1; ++k) {
+            const float v = W[n * K + k];
+            Wq[n * K + k] = isinf(v) ? 0x7F : (signbit(v) ? 0x80 : 0x00);
+          }
+        continue;
+      }
       const float am = amax < 1e-10f ? 1e-10f : amax;
       const float sc = am / 448.0f;
       Bs[nb * KB + kb] = sc;

@@ -49,12 +49,3 @@ def silu_and_mul(x: torch.Tensor) -> torch.Tensor:
     a = x[..., :d].float()
     return (torch.nn.functional.silu(a).to(x.dtype) * x[..., d:]).to(x.dtype)
 
-
-def mlp_chain(x, w13, s13, w2, s2, block_size=(128, 128)):
-    """CPU FP8 MLP: act_quant -> gate/up GEMM -> silu*mul -> act_quant -> down GEMM."""
-    bk = int(block_size[1])
-    xq, xs = act_quant(x, bk)
-    h = dequant_matmul(xq, w13, xs, s13, block_size)
-    a = silu_and_mul(h)
-    aq, as_ = act_quant(a, bk)
-    return dequant_matmul(aq, w2, as_, s2, block_size)

@@ -45,6 +45,27 @@ def test_act_quant_more_rows_than_grid_y(M, K, dev):
     _assert_exact(x, 128, dev)
 
 
+def _g128_unroll(M, K):
+    """Groups per block column / 16 that fp8b_act_quant picks for group 128
+    (g128_unroll in act_quant.hip)."""
+    gpr = K // 128
+    if M * gpr < 16 * 1024:
+        return 1
+    return 4 if gpr % 64 == 0 else (2 if gpr % 32 == 0 else 1)
+
+
+@pytest.mark.parametrize("M,K,unroll", [(2048, 4096, 2), (3001, 4096, 2), (512, 4096, 2),
+                                        (256, 8192, 4), (300, 14336, 1)])
+def test_act_quant_every_unroll_on_config_inputs(M, K, unroll, dev):
+    """The BASELINE config inputs (~N(0,1) with 1% outliers x20 per row) on
+    each unrolled kernel variant: [2048,4096] (C2) and [3001,4096] (C5) run
+    act_quant_g128_kernel<2>, [256,8192] <4>, [300,14336] <1>."""
+    assert _g128_unroll(M, K) == unroll
+    print(f"act_quant U={unroll} M={M} K={K}", flush=True)
+    x = synthetic.activations(M, K, seed=M + 3 * K, outlier_frac=0.01)
+    _assert_exact(x, 128, dev)
+
+
 def test_act_quant_outliers_exact(dev):
     print("act_quant outliers", flush=True)
     x = synthetic.activations(256, 4096, seed=99, outlier_frac=0.01)

@@ -1,29 +1,20 @@
-"""GPU parity of the fused act-quant + GEMM op against the two-op composition
-act_quant -> w8a8_block_fp8_matmul, bit for bit, on both of its paths: the
-decode kernel that quantises bf16 x itself (M <= 48, FP8B_FUSED_QUANT=1)
-quantises with the same arithmetic and sums in the same order; the default
-path quantises into the workspace and runs the GEMM. The composition itself
-is checked against the oracle in test_gpu_act_quant.py and test_gpu_gemm.py."""
-import os
-
+"""GPU parity of the act-quant + GEMM op (act_quant_w8a8_block_fp8_matmul):
+bit for bit against the two public ops it composes (act_quant, then
+w8a8_block_fp8_matmul), and against the CPU oracle chain
+oracle.block_gemm(oracle.act_quant(x)) within the north-star tolerance
+(1e-2 relative, 1e-3 absolute of the oracle's result rounded to the output
+dtype)."""
+import numpy as np
 import pytest
 import torch
 
+import oracle
 from hf_kernels_helion_amd import finegrained_fp8_helion as fp8
 from hf_kernels_helion_amd.finegrained_fp8_helion import synthetic
 
 pytestmark = pytest.mark.gpu
 
-
-@pytest.fixture(params=["fused", "two_kernel"], autouse=True)
-def quant_path(request):
-    old = os.environ.get("FP8B_FUSED_QUANT")
-    os.environ["FP8B_FUSED_QUANT"] = "1" if request.param == "fused" else "0"
-    yield request.param
-    if old is None:
-        del os.environ["FP8B_FUSED_QUANT"]
-    else:
-        os.environ["FP8B_FUSED_QUANT"] = old
+RTOL, ATOL = 1e-2, 1e-3
 
 
 def _weights(N, K, seed, dev):
@@ -40,17 +31,33 @@ def _same(a, b):
     torch.testing.assert_close(a, b, rtol=0, atol=0, equal_nan=True)
 
 
+def _bits(x):
+    return x.cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _oracle_chain(x, W, Bs, rows):
+    """oracle.act_quant then oracle.block_gemm on the given rows of x."""
+    q, s = oracle.act_quant(_bits(x[rows]), 128)
+    return oracle.block_gemm(q, W.cpu().view(torch.uint8).numpy(), s, Bs.cpu().numpy())
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 256, 128), (16, 4096, 14336), (17, 1000, 1024),
                                    (32, 4096, 14336), (33, 512, 2048), (48, 640, 3072),
                                    (32, 28672, 4096), (64, 512, 1024), (100, 384, 512)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_fused_equals_two_ops(M, N, K, dtype, dev):
-    print(f"fused act-quant matmul M={M} N={N} K={K} {dtype}", flush=True)
+def test_fused_equals_two_ops_and_oracle(M, N, K, dtype, dev):
+    print(f"act-quant matmul M={M} N={N} K={K} {dtype}", flush=True)
     x = synthetic.activations(M, K, seed=M + K, outlier_frac=0.01).to(dev)
     W, Bs = _weights(N, K, N, dev)
     out = fp8.act_quant_w8a8_block_fp8_matmul(x, W, Bs, [128, 128], dtype)
     assert out.dtype == dtype and out.shape == (M, N)
     _same(out, _two_op(x, W, Bs, dtype))
+    rows = torch.unique(torch.tensor([0, M // 3, M // 2, M - 1]))
+    cols = slice(0, min(N, 1024))
+    ref = _oracle_chain(x, W[cols], Bs, rows)
+    ref_t = torch.from_numpy(ref).to(dtype).float()
+    torch.testing.assert_close(out[rows.to(dev), cols].float().cpu(), ref_t, rtol=RTOL,
+                               atol=ATOL)
 
 
 def test_fused_nonfinite_and_zero_groups(dev):
@@ -61,20 +68,31 @@ def test_fused_nonfinite_and_zero_groups(dev):
     x[11, 600] = -float("inf")
     x[13, :] = 0
     W, Bs = _weights(N, K, 4, dev)
-    _same(fp8.act_quant_w8a8_block_fp8_matmul(x, W, Bs, [128, 128], torch.float32),
-          _two_op(x, W, Bs, torch.float32))
+    out = fp8.act_quant_w8a8_block_fp8_matmul(x, W, Bs, [128, 128], torch.float32)
+    _same(out, _two_op(x, W, Bs, torch.float32))
+    # the all-zero row is exactly zero; rows with a NaN or inf group are NaN
+    assert torch.equal(out[13], torch.zeros_like(out[13]))
+    assert torch.isnan(out[2]).all() and torch.isnan(out[7]).all() and torch.isnan(out[11]).all()
+    finite = [r for r in range(M) if r not in (2, 7, 11)]
+    rows = torch.tensor(finite)
+    ref = _oracle_chain(x, W, Bs, rows)
+    torch.testing.assert_close(out[rows.to(dev)].cpu(), torch.from_numpy(ref), rtol=RTOL,
+                               atol=ATOL)
 
 
 def test_fused_strided_and_unaligned_rows(dev):
     M, N, K = 20, 384, 1024
     big = synthetic.activations(M, K + 64, seed=5).to(dev)
     W, Bs = _weights(N, K, 6, dev)
-    xs = big[:, :K]                        # row stride K + 64, aligned: fused kernel
+    xs = big[:, :K]                        # row stride K + 64
     _same(fp8.act_quant_w8a8_block_fp8_matmul(xs, W, Bs, [128, 128], torch.bfloat16),
           _two_op(xs, W, Bs, torch.bfloat16))
-    xu = big[:, 1:K + 1]                   # 2-byte offset rows: quantise-then-GEMM path
+    xu = big[:, 1:K + 1]                   # 2-byte offset rows: the generic quantiser
     _same(fp8.act_quant_w8a8_block_fp8_matmul(xu, W, Bs, [128, 128], torch.bfloat16),
           _two_op(xu.contiguous(), W, Bs, torch.bfloat16))
+    xe = big[:1, :K].expand(M, K)          # row stride 0: copied to rows before the launch
+    _same(fp8.act_quant_w8a8_block_fp8_matmul(xe, W, Bs, [128, 128], torch.bfloat16),
+          _two_op(xe.contiguous(), W, Bs, torch.bfloat16))
 
 
 def test_fused_graph_replays(dev):

@@ -324,35 +324,90 @@ def test_gemm_zero_k_gives_zeros(dev):
                                            (4224, 4096, 1024, 1)])
 def test_gemm_partial_last_wave_on_128_tiles(M, N, K, block_n, dev):
     """Grids of 256x256 tiles that leave a last partial wave of at most a
-    quarter of the CUs run it as 128x128 quarters on the 128x128 kernel; the
-    per-output arithmetic is the same, so the result must equal the one-kernel
-    grid (FP8B_TAIL128=0) bit for bit. Covers the MLP gate/up shape (1344
-    tiles), quarters past the M or N edge (4224 = 16.5 tiles), a ragged last
-    row of tiles, and per-row weight scales."""
-    import os
+    quarter of the CUs run it as 128x128 quarters on the 128x128 kernel. The
+    per-output arithmetic of every unsplit MFMA plan is the same (one MFMA per
+    K-block, folded as acc + dot * (As * Bs) in K order), so the result must
+    equal, bit for bit, the same rows computed by separate calls on row
+    slices of 1024 (the last one ending at row M) whose grids have no tail
+    and no split-K. Covers the MLP gate/up shape (1344 tiles), quarters past
+    the M or N edge (4224 = 16.5 tiles), a ragged last row of tiles, and
+    per-row weight scales."""
+    from hf_kernels_helion_amd import _native
     print(f"gemm 128x128 tail M={M} N={N} K={K} block_n={block_n}", flush=True)
     x = synthetic.activations(M, K, seed=M + N)
     q, s = fp8.act_quant(x.to(dev), 128)
     W, Bs = synthetic.weights(N, K, seed=N, block_n=block_n)
     W, Bs = W.to(dev), Bs.to(dev)
-    f = lambda: fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [block_n, 128], torch.bfloat16)
-    out = f()
-    old = os.environ.get("FP8B_TAIL128")
-    os.environ["FP8B_TAIL128"] = "0"
-    try:
-        ref = f()
-    finally:
-        if old is None:
-            del os.environ["FP8B_TAIL128"]
-        else:
-            os.environ["FP8B_TAIL128"] = old
-    torch.testing.assert_close(out, ref, rtol=0, atol=0)
+    out = fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [block_n, 128], torch.bfloat16)
+    lib = _native.load()
+    slices = [(r0, r0 + 1024) for r0 in range(0, M - 1024, 1024)] + [(M - 1024, M)]
+    for r0, r1 in slices:
+        assert lib.fp8b_gemm_workspace_size(r1 - r0, N, K, block_n, 128) == 0
+        part = fp8.w8a8_block_fp8_matmul(q[r0:r1], W, s[r0:r1], Bs, [block_n, 128],
+                                         torch.bfloat16)
+        torch.testing.assert_close(out[r0:r1], part, rtol=0, atol=0)
     rows = torch.tensor([0, M // 2, M - 1])
     orc = oracle.block_gemm(_u8(q.cpu()[rows]), _u8(W.cpu()), s.cpu()[rows].numpy(),
                             Bs.cpu().numpy(), (block_n, 128))
     torch.testing.assert_close(out[rows.to(dev)].float().cpu(),
                                torch.from_numpy(orc).to(torch.bfloat16).float(),
                                rtol=RTOL, atol=ATOL)
+
+
+def _one_hot_rows(N, K, dev):
+    """B [N,K] e4m3fn with row n = 1.0 at k < 8(n+1) and 0 elsewhere, so that
+    with A = 1.0 and unit scales C[m,n] = 8(n+1) exactly."""
+    k = torch.arange(K, device=dev)
+    n = torch.arange(N, device=dev)
+    return (k[None, :] < 8 * (n[:, None] + 1)).to(torch.float8_e4m3fn)
+
+
+@pytest.mark.parametrize("block_n", [128, 1])
+def test_gemm_decode_leading_dim_past_32bit_offsets(block_n, dev):
+    """Decode-sized M (16 rows) against weight rows 34e6 bytes apart: the
+    decode kernel's 32-bit DMA offsets (row * ldb, rows up to 127) would wrap
+    past 2^32, so the plan falls back to kernels with 64-bit addressing
+    (skinny for 128x128 blocks, generic for per-row scales). Closed-form
+    result: A = 1.0, unit scales and one-hot-prefix weight rows give
+    C[m,n] = 8(n+1). block_n = 128 needs K = 139264 (1088 K-blocks) for the
+    decode plan's split size to exceed four K-blocks at N = 128."""
+    M, N = 16, 128
+    K = 139264 if block_n == 128 else 1024
+    ldb = 34_000_000
+    assert 127 * ldb + K > 2 ** 32 and ldb % 16 == 0
+    print(f"gemm decode ldb={ldb} K={K} block_n={block_n}", flush=True)
+    buf = torch.zeros((N - 1) * ldb + K, dtype=torch.uint8, device=dev)
+    B = buf.view(torch.float8_e4m3fn).as_strided((N, K), (ldb, 1))
+    B.copy_(_one_hot_rows(N, K, dev))
+    A = torch.ones(M, K, device=dev).to(torch.float8_e4m3fn)
+    KB = K // 128
+    As = torch.ones(M, KB, device=dev)
+    Bs = torch.ones(N if block_n == 1 else 1, KB, device=dev)
+    out = fp8.w8a8_block_fp8_matmul(A, B, As, Bs, [block_n, 128], torch.float32)
+    expect = (8.0 * (torch.arange(N, device=dev) + 1)).expand(M, N)
+    assert torch.equal(out, expect), (out[0, :8], expect[0, :8])
+    del buf
+
+
+def test_gemm_expanded_and_transposed_operands(dev):
+    """Operands whose rows overlap (an expanded row, stride 0) or whose K
+    stride is not 1 are copied to rows before the launch: the result equals
+    the contiguous operands' bit for bit."""
+    M, N, K = 96, 384, 1024
+    A, B, As, Bs = [t.to(dev) for t in _operands(M, N, K, seed=12)]
+    Ae = A[:1].expand(M, K)
+    ref = fp8.w8a8_block_fp8_matmul(Ae.contiguous(), B, As, Bs, [128, 128], torch.bfloat16)
+    out = fp8.w8a8_block_fp8_matmul(Ae, B, As, Bs, [128, 128], torch.bfloat16)
+    torch.testing.assert_close(out, ref, rtol=0, atol=0)
+    Bt = B.t().contiguous().t()                     # [N,K] with strides (1, N)
+    assert Bt.stride(1) != 1
+    ref = fp8.w8a8_block_fp8_matmul(A, B, As, Bs, [128, 128], torch.bfloat16)
+    torch.testing.assert_close(fp8.w8a8_block_fp8_matmul(A, Bt, As, Bs, [128, 128],
+                                                         torch.bfloat16), ref, rtol=0, atol=0)
+    x1 = synthetic.activations(1, 2 * K, seed=3).to(dev)[:, ::2]   # one row, K stride 2
+    q1, s1 = fp8.act_quant(x1, 128)
+    q2, s2 = fp8.act_quant(x1.contiguous(), 128)
+    assert torch.equal(q1.view(torch.uint8), q2.view(torch.uint8)) and torch.equal(s1, s2)
 
 
 def _random_shapes(n, seed):

@@ -41,9 +41,14 @@ def test_silu_and_mul_3d(dev):
 
 
 @pytest.mark.parametrize("M,d,group", [(3001, 14336, 128), (5, 384, 128), (9, 200, 64),
-                                       (4, 256, 256), (70000, 256, 128)])
+                                       (4, 256, 256), (70000, 256, 128), (512, 4096, 128),
+                                       (256, 8192, 128), (1000, 8192, 128)])
 def test_silu_and_mul_quant_equals_two_ops(M, d, group, dev):
-    """Fused kernel == silu_and_mul then act_quant, bit for bit."""
+    """Fused kernel == silu_and_mul then act_quant, bit for bit, and its codes
+    and scales are oracle.act_quant of the GPU's bf16 silu_and_mul output.
+    d = 14336 runs silu_mul_quant_g128_kernel<1>, d = 4096 with 512 rows <2>,
+    d = 8192 with 256 or more rows <4> (16*U groups per block column, U the
+    largest of 4, 2, 1 dividing the row's groups, 1 below 16384 groups)."""
     print(f"silu_and_mul_quant M={M} d={d} group={group}", flush=True)
     x = (synthetic.activations(M, 2 * d, seed=M + d) * 2).to(dev)
     q, s = fp8.silu_and_mul_quant(x, group)
@@ -55,6 +60,7 @@ def test_silu_and_mul_quant_equals_two_ops(M, d, group, dev):
     # and act_quant of the GPU bf16 intermediate is the oracle's, bit for bit
     qo, so = oracle.act_quant(_bits(h), group)
     np.testing.assert_array_equal(q.cpu().view(torch.uint8).numpy(), qo)
+    np.testing.assert_array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32))
 
 
 def test_fp8_mlp_chain_ragged(dev):
@@ -238,3 +244,52 @@ def test_gate_up_silu_quant_nonfinite_rows(dev):
     q, s = fp8.gate_up_silu_quant(xq, xs, wi, si)
     assert torch.equal(q.view(torch.uint8), q_ref.view(torch.uint8))
     assert torch.equal(s.view(torch.int32), s_ref.view(torch.int32))
+
+
+@pytest.mark.parametrize("interleaved", [False, True])
+def test_fp8_mlp_full_width_vs_oracle_stages(interleaved, dev):
+    """BASELINE config 5 at full width: M=3001 (57-row tail), H=4096,
+    I=14336. Sampled rows of every stage against the pinned oracle functions,
+    each stage fed the GPU's own previous output (a one-ulp bf16 difference
+    in h can flip an fp8 code downstream, so the chain is compared per
+    stage): x -> (xq, xs) bit-exact; h = bf16 gate/up GEMM within 1e-2/1e-3;
+    silu_and_mul(h) within 2^-6 of the oracle's; (hq, hs) bit-exact to
+    oracle.act_quant of the GPU's silu output; y within 1e-2/1e-3 of
+    oracle.block_gemm(hq, w2, hs, s2). The interleaved chain (SiLU·up and
+    act-quant in the gate/up GEMM epilogue) equals the default chain bit for
+    bit."""
+    print(f"fp8 mlp full width interleaved={interleaved}", flush=True)
+    M, H, I = 3001, 4096, 14336
+    x = synthetic.activations(M, H, seed=71)
+    w13, s13 = synthetic.weights(2 * I, H, seed=72)
+    w2, s2 = synthetic.weights(H, I, seed=73)
+    xd, w13d, s13d, w2d, s2d = x.to(dev), w13.to(dev), s13.to(dev), w2.to(dev), s2.to(dev)
+    y = fp8.fp8_mlp(xd, w13d, s13d, w2d, s2d)
+    if interleaved:
+        wi, si = fp8.interleave_gate_up(w13d, s13d)
+        y_il = fp8.fp8_mlp(xd, wi, si, w2d, s2d, gate_up_interleaved=True)
+        assert torch.equal(y_il, y)
+        return
+    rows = torch.tensor([0, 1, 777, 1500, 2047, 2944, 2999, 3000])
+    rd = rows.to(dev)
+    xq, xs = fp8.act_quant(xd, 128)
+    qo, so = oracle.act_quant(_bits(x[rows]), 128)
+    np.testing.assert_array_equal(xq[rd].cpu().view(torch.uint8).numpy(), qo)
+    np.testing.assert_array_equal(xs[rd].cpu().numpy(), so)
+    h = fp8.w8a8_block_fp8_matmul(xq, w13d, xs, s13d, [128, 128], torch.bfloat16)
+    ho = oracle.block_gemm(qo, w13.view(torch.uint8).numpy(), so, s13.numpy())
+    torch.testing.assert_close(h[rd].float().cpu(), torch.from_numpy(ho).to(torch.bfloat16).float(),
+                               rtol=1e-2, atol=1e-3)
+    a = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
+    fp8.silu_and_mul(a, h)
+    ao = torch.from_numpy(oracle.silu_and_mul(_bits(h[rd])).view(np.int16)).view(torch.bfloat16)
+    torch.testing.assert_close(a[rd].cpu().float(), ao.float(), rtol=2 ** -6, atol=1e-6)
+    hq, hs = fp8.silu_and_mul_quant(h, 128)
+    aqo, aso = oracle.act_quant(_bits(a[rd]), 128)
+    np.testing.assert_array_equal(hq[rd].cpu().view(torch.uint8).numpy(), aqo)
+    np.testing.assert_array_equal(hs[rd].cpu().numpy(), aso)
+    yo = oracle.block_gemm(aqo, w2.view(torch.uint8).numpy(), aso, s2.numpy())
+    torch.testing.assert_close(y[rd].float().cpu(), torch.from_numpy(yo).to(torch.bfloat16).float(),
+                               rtol=1e-2, atol=1e-3)
+    y3 = fp8.w8a8_block_fp8_matmul(hq, w2d, hs, s2d, [128, 128], torch.bfloat16)
+    assert torch.equal(y3, y)

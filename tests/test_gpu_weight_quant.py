@@ -87,3 +87,46 @@ def test_weight_quant_vector_path_equals_scalar_path(dtype, dev):
     assert torch.equal(_u8(q1), _u8(q2))
     assert torch.equal(s1.cpu().view(torch.int32), s2.cpu().view(torch.int32))
     assert torch.isnan(s1[0, 2]) and torch.isinf(s1[1, 0]) and s1[2, 2] > 0
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("strided", [False, True])
+def test_weight_quant_nonfinite_blocks_match_oracle(dtype, strided, dev):
+    """Codes and scales bit for bit against oracle.quant_weight_block, with a
+    NaN block (NaN and +inf together), a +-inf block, a subnormal block, an
+    all-zero block and a ragged edge; contiguous rows take the 16-byte-load
+    kernel, a row stride of K + 2 the per-element kernel."""
+    import numpy as np
+    import oracle
+    print(f"weight quant nonfinite vs oracle {dtype} strided={strided}", flush=True)
+    N, K = 300, 640 + 72
+    g = torch.Generator().manual_seed(78)
+    buf = torch.randn(N, K + 2, generator=g) * 0.02
+    buf[5, 30] = float("nan")
+    buf[6, 31] = float("inf")
+    buf[140, 200] = float("inf")
+    buf[141, 201] = -float("inf")
+    buf[142, 202] = -0.0
+    buf[256:300, 384:512] = 1e-40
+    buf[0:128, 512:640] = 0.0
+    buf = buf.to(dtype)
+    W = buf[:, :K] if strided else buf[:, :K].contiguous()
+    q, s = fp8.quantize_weight(W.to(dev) if not strided else buf.to(dev)[:, :K])
+    qo, so = oracle.quant_weight_block(W.float().contiguous().numpy(), (128, 128))
+    np.testing.assert_array_equal(_u8(q).numpy(), qo)
+    np.testing.assert_array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32))
+    assert np.isnan(so[0, 0]) and so[1, 1] == np.inf and so[2, 3] > 0
+
+
+@pytest.mark.parametrize("N,K", [(256, 384), (130, 260), (1024, 4096), (300, 4097)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_weight_quant_matches_oracle(N, K, dtype, dev):
+    import numpy as np
+    import oracle
+    print(f"weight quant vs oracle N={N} K={K} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(N * K)
+    W = (torch.randn(N, K, generator=g) * 0.05).to(dtype)
+    q, s = fp8.quantize_weight(W.to(dev))
+    qo, so = oracle.quant_weight_block(W.float().numpy(), (128, 128))
+    np.testing.assert_array_equal(_u8(q).numpy(), qo)
+    np.testing.assert_array_equal(s.cpu().numpy(), so)

@@ -288,3 +288,45 @@ def test_quant_weight_block_closed_forms():
     np.testing.assert_array_equal(
         Wq, _torch_e4m3((W.reshape(300, 260) /
                          np.repeat(np.repeat(Bs, 128, 0)[:300], 128, 1)[:, :260]).astype(np.float32)))
+
+
+def test_quant_weight_block_nonfinite_policy():
+    """NaN block -> scale NaN and every code 0x7F; +-inf block (no NaN) ->
+    scale +inf, 0x7F for the infinities and a signed zero for every finite
+    element; the other blocks are untouched by their neighbours."""
+    g = torch.Generator().manual_seed(17)
+    W = (torch.randn(256, 384, generator=g) * 0.02).numpy()
+    W[3, 5] = np.nan                      # block (0, 0)
+    W[4, 6] = np.inf                      # NaN wins in the same block
+    W[130, 140] = -np.inf                 # block (1, 1)
+    W[131, 141] = -0.0
+    W[200, 300] = np.inf                  # block (1, 2)
+    Wq, Bs = oracle.quant_weight_block(W, (128, 128))
+    assert np.isnan(Bs[0, 0]) and np.all(Wq[:128, :128] == 0x7F)
+    assert Bs[1, 1] == np.inf and Bs[1, 2] == np.inf
+    blk = W[128:256, 128:256]
+    expect = np.where(np.isinf(blk), 0x7F, np.where(np.signbit(blk), 0x80, 0x00)).astype(np.uint8)
+    np.testing.assert_array_equal(Wq[128:256, 128:256], expect)
+    assert Wq[130, 140] == 0x7F and Wq[131, 141] == 0x80
+    assert Wq[200, 300] == 0x7F
+    # finite blocks: max(amax, 1e-10) / 448 and torch's cast of W / Bs
+    for nb, kb in ((0, 1), (0, 2), (1, 0)):
+        b = W[nb * 128:(nb + 1) * 128, kb * 128:(kb + 1) * 128]
+        s = np.maximum(np.abs(b).max(), np.float32(1e-10)) / np.float32(448)
+        assert Bs[nb, kb] == s
+        np.testing.assert_array_equal(Wq[nb * 128:(nb + 1) * 128, kb * 128:(kb + 1) * 128],
+                                      _torch_e4m3((b / s).astype(np.float32)))
+
+
+def test_quant_weight_block_subnormal_and_zero_blocks():
+    """amax below 1e-10 (fp32 subnormals, zeros): the floor sets the scale to
+    1e-10/448 and the codes are torch's cast of W / scale (all signed zeros
+    here, since |W| / scale < 2^-10)."""
+    W = np.zeros((128, 256), np.float32)
+    W[:, :128] = np.float32(1e-40) * np.where(np.arange(128) % 2, 1, -1)[:, None]
+    W[5, 200] = -0.0
+    Wq, Bs = oracle.quant_weight_block(W, (128, 128))
+    floor = np.float32(1e-10) / np.float32(448)
+    assert Bs[0, 0] == floor and Bs[0, 1] == floor
+    np.testing.assert_array_equal(Wq, _torch_e4m3(W / floor))
+    assert Wq[0, 0] == 0x80 and Wq[1, 0] == 0x00 and Wq[5, 200] == 0x80
