@@ -119,10 +119,8 @@ size_t fp8b_gemm_workspace_size(int64_t M, int64_t N, int64_t K,
  * result bits. No single counterpart in the reference: it composes the
  * quantiser above with the Helion kernel of
  * finegrained-fp8-helion/torch-ext/finegrained_fp8_helion/fp8.py:19-39 (the
- * act-quant-into-the-GEMM step for small M). It quantises into the workspace
- * and runs the GEMM; with FP8B_FUSED_QUANT=1 in the environment, M <= 48 with
- * 16-byte aligned x rows instead runs one GEMM kernel that quantises x itself
- * (measured slower on MI355X; kept for A/B).
+ * act-quant-into-the-GEMM step for small M). Two launches on `stream`: the
+ * quantiser writes (q, s) into the workspace, then the GEMM reads them.
  * x : bf16 [M,K] row stride ldx (K % 128 == 0); B, Bs, C as in
  * fp8b_w8a8_block_matmul. workspace: fp8b_act_quant_matmul_workspace_size()
  * bytes, 256-byte aligned.
