@@ -41,6 +41,11 @@ SIGNATURES = {
          _i64, _i64, _i64, _i64, _i64, _vp, _sz, _vp],
     ),
     "fp8b_gemm_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64]),
+    "fp8b_w8a8_block_matmul_noalloc": (
+        ctypes.c_int,
+        [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, ctypes.c_int,
+         _i64, _i64, _i64, _i64, _i64, _vp],
+    ),
     "fp8b_act_quant_matmul": (
         ctypes.c_int,
         [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _vp, _i64, ctypes.c_int,

@@ -32,6 +32,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cstdlib>
+#include <mutex>
 
 namespace fp8b {
 
@@ -1793,6 +1794,71 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
     }
   }
   return FP8B_OK;
+}
+
+// ---------------------------------------------------------------------------
+// fp8b_w8a8_block_matmul_noalloc: the split-K partials go to `scratch`, a
+// library-owned device array (one copy per GPU, held until the process
+// ends), so the call needs no workspace and allocates nothing. The array's
+// name is a host-side stand-in in host code: its device address on the
+// current GPU comes from hipGetSymbolAddress, taken once per device and kept
+// in g_scratch_dev, and only that address is passed to kernels.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) uint8_t scratch[FP8B_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (nullptr on failure,
+// with the error text set).
+void* scratch_on_current_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("fp8b_w8a8_block_matmul_noalloc: no current HIP device (or device index >= 64)");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) {
+      (void)hipGetLastError();
+      set_error("fp8b_w8a8_block_matmul_noalloc: hipGetSymbolAddress of the scratch array failed");
+      return nullptr;
+    }
+    g_scratch_dev[dev] = ptr;
+  }
+  return g_scratch_dev[dev];
+}
+}  // namespace
+
+extern "C" int fp8b_w8a8_block_matmul_noalloc(const void* A, int64_t lda, const void* B,
+                                              int64_t ldb, const float* As, int64_t as_sm,
+                                              int64_t as_sk, const float* Bs, int64_t bs_sn,
+                                              int64_t bs_sk, void* C, int64_t ldc, int out_dtype,
+                                              int64_t M, int64_t N, int64_t K, int64_t block_n,
+                                              int64_t block_k, void* stream) {
+  // Argument errors first, with the same codes and texts as the allocating
+  // entry point (it returns before touching the workspace for all of them).
+  if (M < 0 || N < 0 || K < 0 || lda < K || ldb < K || ldc < N || block_n <= 0 ||
+      block_k <= 0 || (out_dtype != FP8B_F32 && out_dtype != FP8B_BF16 &&
+                       out_dtype != FP8B_F16) || M == 0 || N == 0)
+    return fp8b_w8a8_block_matmul(A, lda, B, ldb, As, as_sm, as_sk, Bs, bs_sn, bs_sk, C, ldc,
+                                  out_dtype, M, N, K, block_n, block_k, nullptr, 0, stream);
+  const size_t need = fp8b_gemm_workspace_size(M, N, K, block_n, block_k);
+  if (need > (size_t)FP8B_NOALLOC_SCRATCH_BYTES) {
+    set_error("fp8b_w8a8_block_matmul_noalloc: this shape's split-K partials need more than "
+              "FP8B_NOALLOC_SCRATCH_BYTES (32 MiB); use fp8b_w8a8_block_matmul with a workspace");
+    return FP8B_ERR_WORKSPACE;
+  }
+  void* ws = nullptr;
+  if (need > 0) {
+    ws = scratch_on_current_device();
+    if (ws == nullptr) return FP8B_ERR_LAUNCH;
+  }
+  return fp8b_w8a8_block_matmul(A, lda, B, ldb, As, as_sm, as_sk, Bs, bs_sn, bs_sk, C, ldc,
+                                out_dtype, M, N, K, block_n, block_k, ws, need, stream);
 }
 
 namespace {

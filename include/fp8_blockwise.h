@@ -113,6 +113,29 @@ size_t fp8b_gemm_workspace_size(int64_t M, int64_t N, int64_t K,
                                 int64_t block_n, int64_t block_k);
 
 /*
+ * fp8b_w8a8_block_matmul without a workspace: it allocates nothing, for
+ * callers that cannot call hipMalloc (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid allocation). No counterpart in the
+ * reference. Same arguments, semantics and result bits as
+ * fp8b_w8a8_block_matmul, minus (workspace, workspace_bytes): the split-K
+ * partials go to a library-owned device array of FP8B_NOALLOC_SCRATCH_BYTES,
+ * one per GPU, held until the process ends. Shapes whose partials need more
+ * (fp8b_gemm_workspace_size() above the limit) return FP8B_ERR_WORKSPACE.
+ * Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * (other streams, other threads) race and must be serialised by the caller.
+ * The stream must belong to the current device.
+ */
+#define FP8B_NOALLOC_SCRATCH_BYTES (32u << 20)
+int fp8b_w8a8_block_matmul_noalloc(const void* A, int64_t lda,
+                                   const void* B, int64_t ldb,
+                                   const float* As, int64_t as_sm, int64_t as_sk,
+                                   const float* Bs, int64_t bs_sn, int64_t bs_sk,
+                                   void* C, int64_t ldc, int out_dtype,
+                                   int64_t M, int64_t N, int64_t K,
+                                   int64_t block_n, int64_t block_k,
+                                   void* stream);
+
+/*
  * Act-quant fused with the block GEMM: C = w8a8(act_quant(x)) against B/Bs
  * with block_n = block_k = 128, i.e. exactly fp8b_act_quant (group 128) into
  * (q, s) followed by fp8b_w8a8_block_matmul(q, B, s, Bs), with the same

@@ -1,0 +1,96 @@
+"""fp8b_w8a8_block_matmul_noalloc (the entry point that allocates nothing)
+against fp8b_w8a8_block_matmul with a caller workspace, through the C ABI:
+bit for bit (same kernels, same summation order), on calls in a row that
+reuse the library's scratch array with a smaller problem second, on the
+split-K 128x128 and decode plans and a plan without split-K; plans whose
+partials exceed the scratch size are refused with FP8B_ERR_WORKSPACE."""
+import pytest
+import torch
+
+from hf_kernels_helion_amd import _native
+from hf_kernels_helion_amd.finegrained_fp8_helion import synthetic
+
+pytestmark = pytest.mark.gpu
+
+SCRATCH_BYTES = 32 << 20  # FP8B_NOALLOC_SCRATCH_BYTES
+
+
+def _operands(M, N, K, seed, dev):
+    x = synthetic.activations(M, K, seed=seed)
+    from hf_kernels_helion_amd import finegrained_fp8_helion as fp8
+    q, s = fp8.act_quant(x.to(dev), 128)
+    W, Bs = synthetic.weights(N, K, seed=seed + 1)
+    return q, W.to(dev), s, Bs.to(dev)
+
+
+def _args(A, B, As, Bs, C, code):
+    M, K = A.shape
+    N = B.shape[0]
+    return (A.data_ptr(), A.stride(0), B.data_ptr(), B.stride(0), As.data_ptr(), As.stride(0),
+            As.stride(1), Bs.data_ptr(), Bs.stride(0), Bs.stride(1), C.data_ptr(), C.stride(0),
+            code, M, N, K, 128, 128)
+
+
+def _both(A, B, As, Bs, dtype):
+    lib = _native.load()
+    code = {torch.float32: _native.F32, torch.bfloat16: _native.BF16}[dtype]
+    M, K = A.shape
+    N = B.shape[0]
+    stream = torch.cuda.current_stream().cuda_stream
+    ws_n = lib.fp8b_gemm_workspace_size(M, N, K, 128, 128)
+    ws = torch.empty(max(ws_n, 1), dtype=torch.uint8, device=A.device)
+    ref = torch.empty(M, N, dtype=dtype, device=A.device)
+    st = lib.fp8b_w8a8_block_matmul(*_args(A, B, As, Bs, ref, code),
+                                    ws.data_ptr() if ws_n else None, ws_n, stream)
+    _native.check(st, "fp8b_w8a8_block_matmul")
+    out = torch.full((M, N), float("nan"), dtype=dtype, device=A.device)
+    st = lib.fp8b_w8a8_block_matmul_noalloc(*_args(A, B, As, Bs, out, code), stream)
+    _native.check(st, "fp8b_w8a8_block_matmul_noalloc")
+    torch.cuda.synchronize()
+    return out, ref, ws_n
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_noalloc_equals_workspace_entry_point_twice(dtype, dev):
+    """Two calls in a row through the scratch array, the second smaller (so
+    the scratch still holds the first call's partials beyond the second's),
+    then a decode shape and an unsplit one."""
+    shapes = [(300, 1024, 8192), (100, 512, 2048), (32, 4096, 14336), (1024, 4096, 1024)]
+    used = []
+    for i, (M, N, K) in enumerate(shapes):
+        print(f"noalloc M={M} N={N} K={K} {dtype}", flush=True)
+        A, B, As, Bs = _operands(M, N, K, seed=100 + i, dev=dev)
+        out, ref, ws_n = _both(A, B, As, Bs, dtype)
+        used.append(ws_n)
+        assert torch.equal(out, ref)
+    assert used[0] > used[1] > 0 and used[2] > 0 and used[3] == 0
+    assert max(used) <= SCRATCH_BYTES
+
+
+def test_noalloc_refuses_plans_beyond_the_scratch(dev):
+    """A 128x128 grid just below the CU count split four ways needs more
+    partial storage than the scratch holds: refused before any launch, with
+    the limit named."""
+    lib = _native.load()
+    M, N, K = 1920, 2176, 4096       # 15 x 17 = 255 tiles, 4 K-splits on 256 CUs
+    need = lib.fp8b_gemm_workspace_size(M, N, K, 128, 128)
+    if need <= SCRATCH_BYTES:
+        pytest.skip(f"this device's plan needs only {need} bytes of partials")
+    A = torch.zeros(M, K, dtype=torch.float8_e4m3fn, device=dev)
+    B = torch.zeros(N, K, dtype=torch.float8_e4m3fn, device=dev)
+    As = torch.ones(M, K // 128, device=dev)
+    Bs = torch.ones(N // 128 + 1, K // 128, device=dev)
+    C = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    st = lib.fp8b_w8a8_block_matmul_noalloc(*_args(A, B, As, Bs, C, _native.BF16),
+                                            torch.cuda.current_stream().cuda_stream)
+    assert st == 6 and b"FP8B_NOALLOC_SCRATCH_BYTES" in lib.fp8b_last_error()
+
+
+def test_noalloc_argument_errors_match(dev):
+    lib = _native.load()
+    st = lib.fp8b_w8a8_block_matmul_noalloc(None, 64, None, 128, None, 1, 1, None, 1, 1, None,
+                                            128, _native.BF16, 4, 128, 128, 128, 128, None)
+    assert st == 2 and b"bad dims" in lib.fp8b_last_error()
+    st = lib.fp8b_w8a8_block_matmul_noalloc(None, 128, None, 128, None, 1, 1, None, 1, 1, None,
+                                            128, _native.BF16, 0, 128, 128, 128, 128, None)
+    assert st == 0
