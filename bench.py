@@ -375,6 +375,35 @@ def secondary(torch, fp8, synthetic, dev):
     res["harness_inputs"] = harness
     log(f"harness inputs: {harness}")
 
+    # Context for the fraction of peak: the vendor library's plain fp8 GEMM
+    # (torch._scaled_mm -> hipBLASLt, one per-tensor scale, no per-K-block
+    # scale products) on the same operand bytes. It does less arithmetic than
+    # the block-scaled path, so it bounds from above what a block-scaled
+    # kernel with the same tiles can reach on this chip under its power limit.
+    vendor = {}
+    one = torch.ones((), device=dev)
+    for (M, N, K) in ((4096, 4096, 8192), (2048, 2048, 4096)):
+        x_ = _gpu_acts(M, K, 70, dev, torch)
+        A_, As_ = fp8.act_quant(x_, 128)
+        W_, Bs_ = _gpu_weights(N, K, 71, dev, torch, synthetic)
+        try:
+            f_v = lambda: torch._scaled_mm(A_, W_.t(), scale_a=one, scale_b=one,
+                                           out_dtype=torch.bfloat16)
+            ms_v = time_events(f_v, 50, 200, torch)
+        except Exception as e:  # the vendor op is context only
+            vendor[f"{M}x{N}x{K}"] = {"error": str(e)[:120]}
+            continue
+        ms_b = time_events(lambda: fp8.w8a8_block_fp8_matmul(A_, W_, As_, Bs_, [128, 128],
+                                                             torch.bfloat16), 50, 200, torch)
+        fl = 2.0 * M * N * K
+        vendor[f"{M}x{N}x{K}"] = {"hipblaslt_plain_fp8_us": round(ms_v * 1e3, 2),
+                                  "hipblaslt_plain_fp8_TFLOP/s": round(fl / ms_v / 1e9, 1),
+                                  "block_fp8_us": round(ms_b * 1e3, 2),
+                                  "block_fp8_TFLOP/s": round(fl / ms_b / 1e9, 1)}
+        del x_, A_, As_, W_, Bs_
+    res["vendor_plain_fp8_context"] = vendor
+    log(f"vendor plain fp8 context: {vendor}")
+
     # deep-gemm layout (one weight scale per row and K-block, block_n = 1):
     # the headline shape and the decode shape (5 weight copies, as above)
     from hf_kernels_helion_amd import deep_gemm_helion as dg

@@ -1771,7 +1771,9 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
     case CFG_128x128: {
       if (pipe_ok(a, p)) {
         dim3 grid(a.tiles_m * a.tiles_n, 1, p.splits);
-        gemm_pipe128_kernel<64, 32, false><<<grid, 512, 0, st>>>(a);
+        // 32x64 wave tiles (two activation and four weight fragments per
+        // K-block) measured 3-6% faster than 64x32 on 2048x2048x4096
+        gemm_pipe128_kernel<32, 64, false><<<grid, 512, 0, st>>>(a);
       } else {
         launch_cfg<128, 128, 64, 64>(a, p.splits, st);
       }
