@@ -49,8 +49,8 @@ def parse():
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--only", default=None,
                    help="profile helper: run only one workload "
-                        "(gemm|act_quant|decode|decode_fused|weight_quant|mlp|mlp_il|medium|small|deep_gemm|"
-                        "deep_decode|copy)"
+                        "(gemm|act_quant|decode|decode_fused|weight_quant|mlp|mlp_il|mlp_gateup|"
+                        "mlp_down|medium|small|deep_gemm|deep_decode|copy)"
                         " for --steps steps and exit without JSON")
     return p.parse_args()
 
@@ -491,7 +491,8 @@ def run_only(what, steps, warmup, torch, fp8, synthetic, dev):
     """Run one workload for profiling (rocprofv3) without the other legs."""
     shapes = {"gemm": (4096, 4096, 8192), "medium": (2048, 2048, 4096),
               "small": (512, 512, 2048), "decode": (32, 4096, 14336),
-              "decode_fused": (32, 4096, 14336)}
+              "decode_fused": (32, 4096, 14336), "mlp_gateup": (3001, 28672, 4096),
+              "mlp_down": (3001, 4096, 14336)}
     if what in shapes:
         M, N, K = shapes[what]
         x = _gpu_acts(M, K, 41, dev, torch)

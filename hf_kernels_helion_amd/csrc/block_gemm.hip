@@ -366,6 +366,87 @@ gemm_bs128_kernel(GemmArgs a) {
   epilogue16<WM, WN>(a, smem + wid * WM * EPI_PITCH, acc, m0 + wm * WM, n0 + wn * WN, lane);
 }
 
+// Epilogue of a wave's WM x WN accumulator tile at rows mw.., columns nw..
+// (lane: row lane & 15 and columns 4*(lane>>4)..+3 of each 16x16 sub-tile):
+// fp32 partials to the split-K workspace or fp32 C directly, 16-bit outputs
+// staged through LDS by epilogue16. Every wave of the workgroup must call it
+// (the 16-bit path has a barrier); the operand stages in smem must be dead.
+template <int WM, int WN>
+__device__ __forceinline__ void tile_epilogue(const GemmArgs& a, uint8_t* smem,
+                                              const v4f (&acc)[WM / 16][WN / 16], int mw,
+                                              int nw, int wid, int lane, int split) {
+  constexpr int FM = WM / 16, FN = WN / 16;
+  constexpr int EPI_PITCH = WN * 2 + 16;
+  const bool to_ws = gridDim.z > 1;
+  if (to_ws || a.out_dtype == FP8B_F32) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int m = mw + i * 16 + (lane & 15);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int n = nw + j * 16 + 4 * (lane >> 4);
+        store4(a, m, n, acc[i][j], to_ws, split);
+      }
+    }
+    return;
+  }
+  epilogue16<WM, WN>(a, smem + wid * WM * EPI_PITCH, acc, mw, nw, lane);
+}
+
+// SWIGLU epilogue of a BM x 256 tile whose columns 0..127 are gate columns
+// and 128..255 the matching up columns (8 waves of WM x 64, wave w at rows
+// WM*(w/4), columns 64*(w%4)): the waves stage their bf16 tiles in LDS as
+// epilogue16 does, then thread t takes tile row 32p + t/16 in pass p and
+// output columns 8(t%16)..+7 of the row's 128-wide group, forms
+// silu(gate) * up in bf16 (silu_mul_bf16x8) and quantises the group
+// (quant_row16_8): e4m3fn codes to C [M, N/2], the scale to Sq. Every thread
+// of the workgroup must call it.
+template <int BM, int WM, int WN>
+__device__ __forceinline__ void swiglu_epilogue(const GemmArgs& a, uint8_t* smem,
+                                                const v4f (&acc)[WM / 16][WN / 16], int m0,
+                                                int tn, int wid, int lane) {
+  constexpr int NWN = 4, EPI_PITCH = WN * 2 + 16;
+  static_assert(WN == 64 && BM % 32 == 0, "a 256-column tile of 64-column waves");
+  const int tid = threadIdx.x;
+  stage16<WM, WN>(smem + wid * WM * EPI_PITCH, acc, lane, true);
+  __syncthreads();
+  // Gate values of row r, columns 8(t%16).. sit in wave (r/WM, (t%16)/8)'s
+  // staging area, the up values two waves further.
+  const int sub = tid & 15;
+  const int cb = (sub & 7) * 16;
+  const int half = sub >> 3;
+  uint8_t* qout = reinterpret_cast<uint8_t*>(a.C) + tn * 128 + sub * 8;
+  // All LDS reads first (the accumulators are dead, so registers are
+  // plentiful), then the rows' arithmetic back to back.
+  constexpr int NP = BM / 32;
+  v4i gv[NP], uv[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int r = p * 32 + (tid >> 4);
+    const uint8_t* row = smem + (r % WM) * EPI_PITCH + cb;
+    const int wg = (r / WM) * NWN + half;
+    gv[p] = *reinterpret_cast<const v4i*>(row + wg * WM * EPI_PITCH);
+    uv[p] = *reinterpret_cast<const v4i*>(row + (wg + 2) * WM * EPI_PITCH);
+  }
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int r = p * 32 + (tid >> 4);
+    float v[8];
+    const v4i h = silu_mul_bf16x8(gv[p], uv[p], v);
+    uint32_t w0, w1;
+    float scale;
+    quant_row16_8(v, max_mag_bf16x8(h), w0, w1, scale);
+    const int m = m0 + r;
+    if (m < a.M) {
+      v2i packed;
+      packed[0] = (int)w0;
+      packed[1] = (int)w1;
+      *reinterpret_cast<v2i*>(qout + (int64_t)m * a.ldc) = packed;
+      if (sub == 0) a.Sq[(int64_t)m * a.sq_sm + (int64_t)tn * a.sq_sg] = scale;
+    }
+  }
+}
+
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
 // vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
 template <int N>
@@ -702,60 +783,245 @@ __global__ void __launch_bounds__(512) gemm_pipe256_kernel(GemmArgs a) {
   __syncthreads();
 
   if constexpr (SWIGLU) {
-    stage16<WM, WN>(smem + wid * WM * EPI_PITCH, acc, lane, true);
+    swiglu_epilogue<BM, WM, WN>(a, smem, acc, m0, tn, wid, lane);
+    return;
+  }
+  tile_epilogue<WM, WN>(a, smem, acc, m0 + wm * WM, n0 + wn * WN, wid, lane, split);
+}
+
+// ---------------------------------------------------------------------------
+// Pipelined 192x256 kernel: the scheme of gemm_pipe256_kernel on a tile of
+// 192 activation rows, for grids that 256x256 tiles leave with a partial last
+// wave while 192-row tiles fill whole waves (M = 3001: the gate/up GEMM of
+// the MLP has 16 x 112 = 7 x 256 tiles against 12 x 112 = 5.25 waves, the
+// down projection 16 x 16 = 256 against 192). Per output the arithmetic is
+// the other kernels' (one zero-accumulator MFMA per 16x16 sub-tile and
+// K-block, folded as acc + dot * (As * Bs) in K order), so the result bits
+// are the same as on any unsplit plan.
+//   * 8 waves of 96x64 (2 x 4): six activation and four weight fragments,
+//     24 MFMAs per K-block, all six activation fragments in registers
+//     (no slot reuse inside a K-block).
+//   * MFMA order: rows 0-1 column-major in pairs, rows 2-3 row-major, rows
+//     4-5 column-major in pairs. Rows 4-5 and weight fragment 3 of a K-block
+//     are read at its MFMAs 0-3; one barrier per K-block before MFMA 16 (every
+//     wave has read the whole current stage, and its DMA of the next stage has
+//     landed); after it the next K-block's rows 0-3 and weight fragments 0-2
+//     are read into the registers their last use just freed, and the DMA of
+//     K-block kb+2 goes into the released stage, one instruction per MFMA.
+//   * Stage: 192 + 256 rows of 128 bytes (56 KiB) in the block layout of
+//     gemm_pipe256_kernel (A blocks 0-23, B blocks 24-55), two stages; scale
+//     windows of 8 K-blocks as there.
+// SWIGLU: the gate/up epilogue of gemm_pipe256_kernel on 192-row tiles.
+// Preconditions: those of gemm_pipe256_kernel (pipe_ok), block_n = 128.
+// ---------------------------------------------------------------------------
+template <bool SWIGLU = false>
+__global__ void __launch_bounds__(512) gemm_pipe192_kernel(GemmArgs a) {
+  constexpr int BM = 192, BN = 256, WM = 96, WN = 64, NWN = BN / WN, NW = 8;
+  constexpr int FM = WM / 16, FN = WN / 16;       // 6 activation, 4 weight fragments
+  constexpr int NP = FM * FN;                     // 24 MFMAs per K-block
+  constexpr int STAGE = (BM + BN) * 128;          // 56 KiB
+  constexpr int LPW = (BM + BN) / 8 / NW;         // 7 wave-loads per wave per K-block
+  constexpr int A_LOADS = BM / 64;                // wave-loads i < 3 bring A rows
+  constexpr int WIN_SA = BM * 32;
+  constexpr int WIN = WIN_SA + 256;
+  constexpr int SW_OFF = 2 * STAGE;
+  constexpr int EPI_PITCH = WN * 2 + 16;
+  constexpr int EPI = NW * WM * EPI_PITCH;
+  constexpr int SMEM = (2 * STAGE + 2 * WIN > EPI) ? 2 * STAGE + 2 * WIN : EPI;
+  constexpr int BAR = 16;                         // MFMA index of the barrier
+  static_assert(SMEM <= 160 * 1024, "LDS budget");
+  static_assert(LPW <= NP - BAR, "one DMA instruction per MFMA after the barrier");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wid / NWN, wn = wid % NWN;
+
+  int tm, tn;
+  tile_of_bid((int)blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  const int split = blockIdx.z;
+  const int kb_begin = split * a.kb_per_split;
+  const int kb_end = min(kb_begin + a.kb_per_split, a.KB);
+  const int nkb = kb_end - kb_begin;
+
+  const uint32_t lds0 = lds_u32(smem);
+  const int r8 = lane >> 3;
+  const uint8_t* a_base = a.A + (int64_t)m0 * a.lda;
+  const uint8_t* b_base = a.B + (int64_t)n0 * a.ldb;
+  const int a_lim = a.M - 1 - m0, b_lim = a.N - 1 - n0;
+  // wave-load L = wid + 8i: stage block L (A blocks 0..23, B blocks 24..55)
+  auto issue_op = [&](int kb, int stage, int i) {
+    const int L = wid + i * NW;
+    const uint32_t lds = lds0 + stage * STAGE + L * 1024;
+    const int Lr = i < A_LOADS ? L : L - BM / 8;
+    const int row = (Lr >> 3) * 64 + r8 * 8 + (Lr & 7);
+    const int c16 = ((lane & 7) ^ (Lr & 7)) * 16;
+    if (i < A_LOADS) {
+      const uint32_t voff = (uint32_t)min(row, a_lim) * (uint32_t)a.lda + c16;
+      dma16_soff(voff, a_base + (int64_t)kb * 128, lds);
+    } else {
+      const uint32_t voff = (uint32_t)min(row, b_lim) * (uint32_t)a.ldb + c16;
+      dma16_soff(voff, b_base + (int64_t)kb * 128, lds);
+    }
+  };
+  // Scale window of 8 K-blocks: waves 0..5 bring As rows 32w..32w+31, wave 7
+  // the Bs rows of the tile's two 128-column blocks.
+  const float* saw_src =
+      a.As + (int64_t)min(m0 + min(wid * 32 + (lane >> 1), BM - 1), a.M - 1) * a.as_sm +
+      4 * (lane & 1);
+  const float* sbw_src =
+      a.Bs + (int64_t)min((n0 >> 7) + min(lane >> 1, 1), (a.N - 1) >> 7) * a.bs_sn + 4 * (lane & 1);
+  auto issue_win = [&](int kb0, int wbuf) {
+    const int kk = (kb0 + 4 * (lane & 1) < kb_end) ? kb0 : kb0 - 4 * (lane & 1);
+    const uint32_t lb = lds0 + SW_OFF + wbuf * WIN;
+    if (wid < BM / 32) dma16_ptr(saw_src + kk, lb + wid * 1024);
+    if (wid == NW - 1 && lane < 4) dma16_ptr(sbw_src + kk, lb + WIN_SA);
+  };
+
+  const int r7 = lane & 7, g2 = 2 * (lane >> 4);
+  const int slo = (g2 ^ r7) << 4, shi = ((g2 + 1) ^ r7) << 4;
+  const int q_off = (lane & 7) * 1024 + ((lane >> 3) & 1) * 128;
+  // 16-row fragment F of an operand: block 8*(F/4) + q%8, segment 2*(F%4) + q/8
+  auto frag_off = [](int f) { return (f >> 2) * 8192 + (f & 3) * 256; };
+  auto rdx = [&](int stage, int i) {
+    return lds_frag2(smem + stage * STAGE + q_off + frag_off(wm * FM + i), slo, shi);
+  };
+  auto rdw = [&](int stage, int j) {
+    return lds_frag2(smem + stage * STAGE + BM * 128 + q_off + frag_off(wn * FN + j), slo, shi);
+  };
+  const int sa_off = SW_OFF + (wm * WM + (lane & 15)) * 32;
+  const int sb_off = SW_OFF + WIN_SA + ((wn * WN) >> 7) * 32;
+  auto rdsa = [&](int rel, int i) {
+    const int o = ((rel >> 3) & 1) * WIN + (rel & 7) * 4;
+    return *reinterpret_cast<const float*>(smem + sa_off + o + i * 512);
+  };
+  auto rdsb = [&](int rel) {
+    const int o = ((rel >> 3) & 1) * WIN + (rel & 7) * 4;
+    return *reinterpret_cast<const float*>(smem + sb_off + o);
+  };
+
+  v4f acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  constexpr int ORD_I[NP] = {0, 1, 0, 1, 0, 1, 0, 1, 2, 2, 2, 2,
+                             3, 3, 3, 3, 4, 5, 4, 5, 4, 5, 4, 5};
+  constexpr int ORD_J[NP] = {0, 0, 1, 1, 2, 2, 3, 3, 0, 1, 2, 3,
+                             0, 1, 2, 3, 0, 0, 1, 1, 2, 2, 3, 3};
+  v8i w[FN], xs[FM];
+  float sc[FM], sa_t[FM], sb_n = 0.f;
+  v4f r1 = v4f{0.f, 0.f, 0.f, 0.f}, r2 = r1;  // results of MFMAs p-1 and p-2
+
+  if (nkb > 0) {
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) issue_op(kb_begin, 0, i);
+    issue_win(kb_begin, 0);
+    if (nkb > 1) {
+#pragma unroll
+      for (int i = 0; i < LPW; ++i) issue_op(kb_begin + 1, 1, i);
+      wait_vmcnt<LPW>();
+    } else {
+      wait_vmcnt<0>();
+    }
     __syncthreads();
-    // Thread t: tile row 32p + t/16 in pass p, output columns 8(t%16)..+7 of
-    // the group; its gate values sit in wave (row/128, (t%16)/8)'s staging
-    // area, the up values two waves further.
-    const int sub = tid & 15;
-    const int cb = (sub & 7) * 16;
-    const int half = sub >> 3;
-    uint8_t* qout = reinterpret_cast<uint8_t*>(a.C) + tn * 128 + sub * 8;
-    // All LDS reads first (the accumulators are dead, so registers are
-    // plentiful), then the eight rows' arithmetic back to back.
-    constexpr int NP = BM / 32;
-    v4i gv[NP], uv[NP];
+    w[0] = rdw(0, 0); w[1] = rdw(0, 1); w[2] = rdw(0, 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { xs[i] = rdx(0, i); sa_t[i] = rdsa(0, i); }
+    sb_n = rdsb(0);
+  }
+
+  // One K-block. KIND 0: steady state (reads the next K-block, DMA of
+  // kb+2); 1: next K-block exists but no kb+2; 2: last K-block. Empty asm
+  // statements and sched_barrier keep the MFMAs, reads and folds in the
+  // written order, as in gemm_pipe256_kernel.
+  auto body = [&](int kb, auto tag) {
+    constexpr int KIND = decltype(tag)::value;
+    const int rel = kb - kb_begin;
+    const int s = rel & 1;
+    const float sb = sb_n;
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
-      const int r = p * 32 + (tid >> 4);
-      const uint8_t* row = smem + (r & (WM - 1)) * EPI_PITCH + cb;
-      const int wg = (r / WM) * NWN + half;
-      gv[p] = *reinterpret_cast<const v4i*>(row + wg * WM * EPI_PITCH);
-      uv[p] = *reinterpret_cast<const v4i*>(row + (wg + 2) * WM * EPI_PITCH);
-    }
-#pragma unroll
-    for (int p = 0; p < NP; ++p) {
-      const int r = p * 32 + (tid >> 4);
-      float v[8];
-      const v4i h = silu_mul_bf16x8(gv[p], uv[p], v);
-      uint32_t w0, w1;
-      float scale;
-      quant_row16_8(v, max_mag_bf16x8(h), w0, w1, scale);
-      const int m = m0 + r;
-      if (m < a.M) {
-        v2i packed;
-        packed[0] = (int)w0;
-        packed[1] = (int)w1;
-        *reinterpret_cast<v2i*>(qout + (int64_t)m * a.ldc) = packed;
-        if (sub == 0) a.Sq[(int64_t)m * a.sq_sm + (int64_t)tn * a.sq_sg] = scale;
+      const int i = ORD_I[p], j = ORD_J[p];
+      if (p == BAR && KIND < 2) {
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (KIND == 0 && ((rel + 2) & 7) == 0) issue_win(kb + 2, ((rel + 2) >> 3) & 1);
       }
+      v4f res = mfma16x16x128(w[j], xs[i]);
+      asm volatile("" : "+v"(res));
+      __builtin_amdgcn_sched_barrier(0);
+      // this K-block's last fragments and activation scales
+      if (p == 0) w[3] = rdw(s, 3);
+      if (p == 1) { xs[4] = rdx(s, 4); sa_t[4] = rdsa(rel, 4); }
+      if (p == 3) { xs[5] = rdx(s, 5); sa_t[5] = rdsa(rel, 5); }
+      // scale of row i, just before the fold of its first MFMA
+      if (p == 1) { sc[0] = sa_t[0] * sb; sc[1] = sa_t[1] * sb; }
+      if (p == 9) sc[2] = sa_t[2] * sb;
+      if (p == 13) sc[3] = sa_t[3] * sb;
+      if (p == 17) { sc[4] = sa_t[4] * sb; sc[5] = sa_t[5] * sb; }
+      // after the barrier: the next K-block's first fragments (stage s^1)
+      // and the DMA of K-block kb+2 into stage s
+      if (KIND < 2 && p >= BAR) {
+        if (KIND == 0 && p - BAR < LPW) issue_op(kb + 2, s, p - BAR);
+        if (p == BAR) { xs[0] = rdx(s ^ 1, 0); sb_n = rdsb(rel + 1); sa_t[0] = rdsa(rel + 1, 0); }
+        if (p == BAR + 1) { xs[1] = rdx(s ^ 1, 1); sa_t[1] = rdsa(rel + 1, 1); }
+        if (p == BAR + 2) w[0] = rdw(s ^ 1, 0);
+        if (p == BAR + 3) { xs[2] = rdx(s ^ 1, 2); sa_t[2] = rdsa(rel + 1, 2); }
+        if (p == BAR + 4) w[1] = rdw(s ^ 1, 1);
+        if (p == BAR + 5) { xs[3] = rdx(s ^ 1, 3); sa_t[3] = rdsa(rel + 1, 3); }
+        if (p == BAR + 6) w[2] = rdw(s ^ 1, 2);
+      }
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      if (p >= 2) {
+        const int qi = ORD_I[p - 2], qj = ORD_J[p - 2];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[qi][qj][e] = fmaf(r2[e], sc[qi], acc[qi][qj][e]);
+        asm volatile("" : "+v"(acc[qi][qj]));
+      } else {
+        // the previous K-block's last two MFMAs: rows 4 and 5, column 3
+        // (their scales are rewritten only at MFMA 17)
+        const int qi = FM - 2 + p;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[qi][3][e] = fmaf(r2[e], sc[qi], acc[qi][3][e]);
+        asm volatile("" : "+v"(acc[qi][3]));
+      }
+      r2 = r1;
+      r1 = res;
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
     }
+  };
+
+  // sc starts at zero so the first K-block's two "previous" folds add 0.
+#pragma unroll
+  for (int i = 0; i < FM; ++i) sc[i] = 0.f;
+  int kb = kb_begin;
+  for (; kb + 2 < kb_end; ++kb) body(kb, PipeKind<0>{});
+  if (kb + 1 < kb_end) {
+    body(kb, PipeKind<1>{});
+    ++kb;
+  }
+  if (kb < kb_end) {
+    body(kb, PipeKind<2>{});
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[FM - 2][3][e] = fmaf(r2[e], sc[FM - 2], acc[FM - 2][3][e]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[FM - 1][3][e] = fmaf(r1[e], sc[FM - 1], acc[FM - 1][3][e]);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  if constexpr (SWIGLU) {
+    swiglu_epilogue<BM, WM, WN>(a, smem, acc, m0, tn, wid, lane);
     return;
   }
-  const bool to_ws = gridDim.z > 1;
-  if (to_ws || a.out_dtype == FP8B_F32) {
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      const int m = m0 + wm * WM + i * 16 + (lane & 15);
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int n = n0 + wn * WN + j * 16 + 4 * (lane >> 4);
-        store4(a, m, n, acc[i][j], to_ws, split);
-      }
-    }
-    return;
-  }
-  epilogue16<WM, WN>(a, smem + wid * WM * EPI_PITCH, acc, m0 + wm * WM, n0 + wn * WN, lane);
+  tile_epilogue<WM, WN>(a, smem, acc, m0 + wm * WM, n0 + wn * WN, wid, lane, split);
 }
 
 // ---------------------------------------------------------------------------
@@ -1004,21 +1270,7 @@ __global__ void __launch_bounds__((128 / WM) * (128 / WN) * 64) gemm_pipe128_ker
   }
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
   __syncthreads();
-
-  const bool to_ws = gridDim.z > 1;
-  if (to_ws || a.out_dtype == FP8B_F32) {
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      const int m = m0 + wm * WM + i * 16 + (lane & 15);
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int n = n0 + wn * WN + j * 16 + 4 * (lane >> 4);
-        store4(a, m, n, acc[i][j], to_ws, split);
-      }
-    }
-    return;
-  }
-  epilogue16<WM, WN>(a, smem + wid * WM * EPI_PITCH, acc, m0 + wm * WM, n0 + wn * WN, lane);
+  tile_epilogue<WM, WN>(a, smem, acc, m0 + wm * WM, n0 + wn * WN, wid, lane, split);
 }
 
 // s_waitcnt vmcnt(n) for a run-time n in [0, 15].
@@ -1432,10 +1684,11 @@ namespace {
 // Tile configurations of the MFMA path.
 enum TileCfg {
   CFG_256x256 = 0,
-  CFG_128x128 = 1,
-  CFG_64x128 = 2,
-  CFG_SKINNY = 3,
-  CFG_DECODE = 4,
+  CFG_192x256 = 1,
+  CFG_128x128 = 2,
+  CFG_64x128 = 3,
+  CFG_SKINNY = 4,
+  CFG_DECODE = 5,
   CFG_COUNT
 };
 
@@ -1467,7 +1720,8 @@ int device_cu_count() {
 //   FP8B_DECODE=0   M <= 48 always takes the skinny kernel (no split-K
 //                   decode kernel; per-row scales then take the 128x128 path);
 //   FP8B_PIPE=0     no pipelined kernels (gemm_bs128_kernel instead);
-//   FP8B_TAIL128=0  no 128x128 quarters for a small last wave of 256x256 tiles.
+//   FP8B_TAIL128=0  no 128x128 quarters for a small last wave of 256x256 tiles;
+//   FP8B_TILE192=0  no 192x256 tiles.
 bool env_flag_on(const char* name) {
   const char* e = getenv(name);
   return !(e && e[0] == '0');
@@ -1483,6 +1737,37 @@ bool use_pipelined_kernels() {
 bool use_tail128() {
   static const bool v = env_flag_on("FP8B_TAIL128");
   return v;
+}
+bool use_tile192() {
+  static const bool v = env_flag_on("FP8B_TILE192");
+  return v;
+}
+
+// Fraction of the CU slots a grid of t tiles keeps busy over its waves.
+double wave_fill(int64_t t, int cus) {
+  const int64_t waves = (t + cus - 1) / cus;
+  return waves > 0 ? (double)t / (double)(waves * cus) : 0.0;
+}
+
+// 192x256 tiles instead of 256x256 when they fill the waves clearly better
+// (at least one full wave, fill at least 0.1 higher) and the 256x256 grid
+// cannot run a small last wave as 128x128 quarters (tail_quarters). Measured
+// at steady clock, M = 3001: the down projection (N = 4096, K = 14336: 256
+// tiles against 192) 157.8 against 160.3 us; the gate/up GEMM with SiLU·up
+// and act-quant in its epilogue plus the down projection 517.7 against 528.4
+// us; but the plain gate/up GEMM (N = 28672: 1792 tiles against 5 waves and
+// 64 tiles as quarters) 331.4 against 320.3 us, since 192-row tiles move
+// 17% more operand bytes per output.
+bool prefer_192(int64_t t256, int64_t t192, int cus, bool tail_quarters) {
+  return use_tile192() && !tail_quarters && t192 >= cus &&
+         wave_fill(t192, cus) >= wave_fill(t256, cus) + 0.1;
+}
+
+// Whether launch_pipe256 runs the last partial wave of an unsplit grid of t
+// 256x256 tiles as 128x128 quarters (at most a quarter of the CUs left).
+bool tail_quarters(int64_t t, int cus) {
+  const int64_t rest = t % cus;
+  return use_tail128() && t >= cus && rest > 0 && 4 * rest <= cus;
 }
 
 // Grids of fewer 256x256 tiles than CUs: one partial wave of 256x256 tiles
@@ -1540,6 +1825,10 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
     p.cfg = CFG_64x128; p.bm = 64; p.bn = 128;
   } else if (tiles(256, 256) >= cus || prefer_256(tiles(256, 256), tiles(128, 128), cus)) {
     p.cfg = CFG_256x256; p.bm = 256; p.bn = 256;
+    if (!per_row && prefer_192(tiles(256, 256), tiles(192, 256), cus,
+                               tail_quarters(tiles(256, 256), cus))) {
+      p.cfg = CFG_192x256; p.bm = 192;
+    }
   } else {
     p.cfg = CFG_128x128; p.bm = 128; p.bn = 128;
   }
@@ -1595,11 +1884,10 @@ bool pipe_ok(const GemmArgs& a, const Plan& p) {
 // gemm_pipe256_kernel.
 template <bool PR>
 void launch_pipe256(const GemmArgs& a, hipStream_t st) {
-  const bool tail_on = use_tail128();
   const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
-  const int64_t cus = device_cu_count();
+  const int cus = device_cu_count();
   const int64_t full = tiles / cus * cus, rest = tiles - full;
-  if (!tail_on || full == 0 || rest == 0 || 4 * rest > cus || a.kb_per_split < a.KB) {
+  if (!tail_quarters(tiles, cus) || a.kb_per_split < a.KB) {
     gemm_pipe256_kernel<PR><<<(unsigned)tiles, 512, 0, st>>>(a);
     return;
   }
@@ -1723,6 +2011,12 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
     p.cfg = CFG_SKINNY; p.bn = 16; p.splits = 1; p.kb_per_split = (int)(K / 128);
   }
   GemmArgs a = make_args(p);
+  // 192x256 tiles exist only as a pipelined kernel: without its
+  // preconditions the grid goes back to 256x256 tiles.
+  if (p.cfg == CFG_192x256 && !pipe_ok(a, p)) {
+    p.cfg = CFG_256x256; p.bm = 256;
+    a = make_args(p);
+  }
   if (per_row) {
     if (p.cfg == CFG_DECODE) {
       const dim3 grid((unsigned)((N + 127) / 128), 1, (unsigned)p.splits);
@@ -1768,6 +2062,9 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
       }
       break;
     }
+    case CFG_192x256:
+      gemm_pipe192_kernel<false><<<(unsigned)(a.tiles_m * a.tiles_n), 512, 0, st>>>(a);
+      break;
     case CFG_128x128: {
       if (pipe_ok(a, p)) {
         dim3 grid(a.tiles_m * a.tiles_n, 1, p.splits);
@@ -1962,7 +2259,10 @@ extern "C" int fp8b_gate_up_silu_quant(const void* A, int64_t lda, const void* B
   a.lda = lda; a.ldb = ldb; a.as_sm = as_sm; a.as_sk = 1; a.bs_sn = bs_sn; a.bs_sk = 1;
   a.ldc = ldq; a.M = (int)M; a.N = (int)N; a.K = (int)K; a.KB = (int)(K / 128);
   a.kb_per_split = a.KB;
-  a.tiles_m = (int)((M + 255) / 256);
+  const int cus = device_cu_count();
+  const bool tile192 =
+      prefer_192(((M + 255) / 256) * (N / 256), ((M + 191) / 192) * (N / 256), cus, false);
+  a.tiles_m = (int)(tile192 ? (M + 191) / 192 : (M + 255) / 256);
   a.tiles_n = (int)(N / 256);
   a.out_dtype = FP8B_BF16;
   a.vec_store = 0;
@@ -1973,7 +2273,10 @@ extern "C" int fp8b_gate_up_silu_quant(const void* A, int64_t lda, const void* B
     set_error("fp8b_gate_up_silu_quant: too many tiles");
     return FP8B_ERR_DIMS;
   }
-  gemm_pipe256_kernel<false, true><<<(unsigned)tiles, 512, 0, (hipStream_t)stream>>>(a);
+  if (tile192)
+    gemm_pipe192_kernel<true><<<(unsigned)tiles, 512, 0, (hipStream_t)stream>>>(a);
+  else
+    gemm_pipe256_kernel<false, true><<<(unsigned)tiles, 512, 0, (hipStream_t)stream>>>(a);
   if (hipGetLastError() != hipSuccess) {
     set_error("fp8b_gate_up_silu_quant: kernel launch failed");
     return FP8B_ERR_LAUNCH;

@@ -354,6 +354,40 @@ def test_gemm_partial_last_wave_on_128_tiles(M, N, K, block_n, dev):
                                rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("M,N,K", [(3001, 4096, 14336), (1500, 8192, 4096), (3001, 8192, 1024)])
+def test_gemm_192_row_tiles_equal_other_plans(M, N, K, dev):
+    """Grids whose 256x256 tiles leave a partial last wave too large for
+    128x128 quarters while 192x256 tiles fill whole waves (3001 x 4096: 256
+    tiles against 192; 1500 x 8192: 256 against 192; 3001 x 8192: 512
+    against 384) run gemm_pipe192_kernel, ragged last tile row included. Per
+    output its arithmetic is that of every unsplit MFMA plan, so row slices of
+    1024 (which run the 128x128 kernel) give the same bits; sampled rows
+    against the oracle. (The gate/up GEMM with the SiLU epilogue on 192-row
+    tiles is checked against the plain GEMM in test_gpu_mlp.py.)"""
+    from hf_kernels_helion_amd import _native
+    print(f"gemm 192-row tiles M={M} N={N} K={K}", flush=True)
+    x = synthetic.activations(M, K, seed=M + 2 * N, outlier_frac=0.01)
+    q, s = fp8.act_quant(x.to(dev), 128)
+    W, Bs = synthetic.weights(N, K, seed=N + 3)
+    W, Bs = W.to(dev), Bs.to(dev)
+    out = fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [128, 128], torch.bfloat16)
+    lib = _native.load()
+    slices = [(r0, r0 + 1024) for r0 in range(0, M - 1024, 1024)] + [(M - 1024, M)]
+    for r0, r1 in slices:
+        assert lib.fp8b_gemm_workspace_size(r1 - r0, N, K, 128, 128) == 0
+        part = fp8.w8a8_block_fp8_matmul(q[r0:r1], W, s[r0:r1], Bs, [128, 128], torch.bfloat16)
+        torch.testing.assert_close(out[r0:r1], part, rtol=0, atol=0)
+    rows = torch.tensor([0, 191, 192, M // 2, M - 1])
+    orc = oracle.block_gemm(_u8(q.cpu()[rows]), _u8(W.cpu()), s.cpu()[rows].numpy(),
+                            Bs.cpu().numpy())
+    torch.testing.assert_close(out[rows.to(dev)].float().cpu(),
+                               torch.from_numpy(orc).to(torch.bfloat16).float(),
+                               rtol=RTOL, atol=ATOL)
+    # fp32 output through the same kernel's fp32 epilogue
+    out32 = fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [128, 128], torch.float32)
+    assert torch.equal(out32.to(torch.bfloat16), out)
+
+
 def _one_hot_rows(N, K, dev):
     """B [N,K] e4m3fn with row n = 1.0 at k < 8(n+1) and 0 elsewhere, so that
     with A = 1.0 and unit scales C[m,n] = 8(n+1) exactly."""
