@@ -1566,6 +1566,126 @@ __global__ void __launch_bounds__(512) gemm_skinny_kernel(GemmArgs a) {
   }
 }
 
+// Small-grid GEMM (grids of 128x128 tiles that would leave most CUs idle,
+// e.g. 512x512x2048): one workgroup per 32x32 output tile, so the grid
+// spreads the operand stream over up to 16x more CUs than 128x128 tiles,
+// with no workspace and no second kernel. Each of its NW waves takes a
+// contiguous range of the K-blocks and streams the tile's 32 activation and
+// 32 weight rows (eight 1 KiB DMA instructions per K-block, the chunk
+// swizzle of gemm_bs128_kernel) and their scales (one 4-byte DMA lane per
+// activation row, the weight block's scale in lanes 32..63) through a
+// private ring of NS LDS slots, so the only waits in the loop are vmcnt
+// waits on its own DMA. Per K-block: four 16x16x128 MFMAs (weights as the A
+// operand), each folded as acc + dot * (As * Bs). With NW = 1 that is the
+// arithmetic of every other unsplit plan, bit for bit; with NW > 1 the NW
+// partial tiles are summed through LDS in wave order (deterministic), which
+// keeps more K-blocks in flight per CU: the loop is bound by DMA latency.
+template <int NW, int NS>
+__global__ void __launch_bounds__(64 * NW) gemm_tiny_kernel(GemmArgs a) {
+  constexpr int ROWS = 64;                    // 32 activation rows, then 32 weight rows
+  constexpr int SCALE_OFF = ROWS * 128;       // sa rows 0..31, sb in slots 32..63
+  constexpr int SLOT = SCALE_OFF + 256;
+  constexpr int PER_KB = ROWS / 8 + 1;        // DMA instructions per K-block
+  // at most NS K-blocks of DMA are outstanding per wave: within the 6-bit vmcnt
+  static_assert(PER_KB * NS <= 63, "vmcnt is a 6-bit counter");
+  static_assert(NW == 1 || NW * NS * SLOT >= NW * 16 * 64 * 4, "partials reuse the ring");
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[NW][NS][SLOT];
+  const int lane = threadIdx.x & 63;
+  // wave index as a scalar, so K ranges and loop conditions are uniform
+  const int wid = NW == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int tm, tn;
+  tile_of_bid((int)blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
+  const int m0 = tm * 32, n0 = tn * 32;
+  const int kb0 = (int)((int64_t)a.KB * wid / NW);
+  const int kb1 = (int)((int64_t)a.KB * (wid + 1) / NW);
+
+  // load L brings rows 8L..8L+7 of the slot; lane i the logical chunk
+  // (i&7) ^ (r&7) of row 8L + (i>>3), so chunk c of row r sits in slot c^(r&7)
+  const uint8_t* src[ROWS / 8];
+#pragma unroll
+  for (int L = 0; L < ROWS / 8; ++L) {
+    const int r = L * 8 + (lane >> 3);
+    const int chunk = (lane & 7) ^ (r & 7);
+    src[L] = r < 32 ? a.A + (int64_t)min(m0 + r, a.M - 1) * a.lda + chunk * 16
+                    : a.B + (int64_t)min(n0 + r - 32, a.N - 1) * a.ldb + chunk * 16;
+  }
+  const float* ssrc = lane < 32 ? a.As + (int64_t)min(m0 + lane, a.M - 1) * a.as_sm
+                                : a.Bs + (int64_t)(min(n0, a.N - 1) >> 7) * a.bs_sn;
+  const int64_t sstep = lane < 32 ? a.as_sk : a.bs_sk;
+  auto issue = [&](int kb, int slot) {
+    uint8_t* dst = &ring[wid][slot][0];
+#pragma unroll
+    for (int L = 0; L < ROWS / 8; ++L) lds_dma16(src[L] + (int64_t)kb * 128, dst + L * 1024);
+    lds_dma4(ssrc + (int64_t)kb * sstep, dst + SCALE_OFF);
+  };
+
+  const int row = lane & 15, c0 = 2 * (lane >> 4), r7 = row & 7;
+  v4f acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  for (int u = 0; u < NS && kb0 + u < kb1; ++u) issue(kb0 + u, u);
+  for (int kb = kb0; kb < kb1; ++kb) {
+    const int slot = (kb - kb0) % NS;
+    // the DMAs of the next NS-1 K-blocks were issued after this slot's
+    // (fewer near the end of the range: then wait for all)
+    if (kb + NS - 1 < kb1) wait_vmcnt<PER_KB * (NS - 1)>();
+    else wait_vmcnt<0>();
+    const uint8_t* sl = &ring[wid][slot][0];
+    const float sb = *reinterpret_cast<const float*>(sl + SCALE_OFF + 32 * 4);
+    v8i x[2], w[2];
+    float sc[2];
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      x[f] = lds_frag(sl + (f * 16 + row) * 128, c0, r7);
+      w[f] = lds_frag(sl + (32 + f * 16 + row) * 128, c0, r7);
+      sc[f] = *reinterpret_cast<const float*>(sl + SCALE_OFF + (f * 16 + row) * 4) * sb;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const v4f t = mfma16x16x128(w[j], x[i]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[i][j][e] = fmaf(t[e], sc[i], acc[i][j][e]);
+      }
+    // the MFMAs consumed the slot's fragments (their reads are complete):
+    // refill it
+    if (kb + NS < kb1) issue(kb + NS, slot);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  if constexpr (NW == 1) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        store4(a, m0 + i * 16 + row, n0 + j * 16 + 4 * (lane >> 4), acc[i][j], false, 0);
+  } else {
+    // partial tiles reuse the ring: [wave][i][j][e][lane] floats; wave q
+    // then sums sub-tile (q / 2, q % 2) of every wave in wave order
+    __syncthreads();
+    float* part = reinterpret_cast<float*>(&ring[0][0][0]);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) part[(((wid * 2 + i) * 2 + j) * 4 + e) * 64 + lane] = acc[i][j][e];
+    __syncthreads();
+    for (int q = wid; q < 4; q += NW) {
+      const int i = q >> 1, j = q & 1;
+      v4f sum = {0.f, 0.f, 0.f, 0.f};
+      for (int w = 0; w < NW; ++w)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sum[e] += part[(((w * 2 + i) * 2 + j) * 4 + e) * 64 + lane];
+      store4(a, m0 + i * 16 + row, n0 + j * 16 + 4 * (lane >> 4), sum, false, 0);
+    }
+  }
+}
+
 // Sum split-K partials in split order and convert: 4 outputs per thread. The
 // partial loads go out eight splits at a time before any is added, so the
 // kernel costs about one memory latency per eight splits.
@@ -1689,6 +1809,7 @@ enum TileCfg {
   CFG_64x128 = 3,
   CFG_SKINNY = 4,
   CFG_DECODE = 5,
+  CFG_TINY = 6,
   CFG_COUNT
 };
 
@@ -1721,7 +1842,8 @@ int device_cu_count() {
 //                   decode kernel; per-row scales then take the 128x128 path);
 //   FP8B_PIPE=0     no pipelined kernels (gemm_bs128_kernel instead);
 //   FP8B_TAIL128=0  no 128x128 quarters for a small last wave of 256x256 tiles;
-//   FP8B_TILE192=0  no 192x256 tiles.
+//   FP8B_TILE192=0  no 192x256 tiles;
+//   FP8B_TINY=0     no one-wave 32x32 tiles for small grids.
 bool env_flag_on(const char* name) {
   const char* e = getenv(name);
   return !(e && e[0] == '0');
@@ -1740,6 +1862,10 @@ bool use_tail128() {
 }
 bool use_tile192() {
   static const bool v = env_flag_on("FP8B_TILE192");
+  return v;
+}
+bool use_tiny() {
+  static const bool v = env_flag_on("FP8B_TINY");
   return v;
 }
 
@@ -1780,6 +1906,16 @@ bool prefer_256(int64_t t256, int64_t t128, int cus) {
   if (t256 * 2 <= cus) return false;
   const int64_t w256 = (t256 + cus - 1) / cus, w128 = (t128 + cus - 1) / cus;
   return 71 * w128 > 175 * w256;
+}
+
+// Grids for gemm_tiny_kernel: at most 8 tiles of 32x32 per CU and at most
+// 128 tile K-blocks per CU. Measured (HIP-graph replay, against the
+// 128x128 kernel split along K within one wave of workgroups): 512x512x2048
+// 4.6 against 11.7 us, 512x512x7168 7.9 against 16.0, 768x768x4096 11.1
+// against 16.5, 2048x1024x2048 14.1 against 20.7; past 128 K-blocks per CU
+// the split 128x128 grid wins (1024x2048x4096: 24.6 against 23.2).
+bool tiny_grid(int64_t t32, int KB, int cus) {
+  return t32 <= 8 * (int64_t)cus && t32 * KB <= 128 * (int64_t)cus;
 }
 
 // per_row: weight scales per output row (block_n = 1, the deep-gemm layout);
@@ -1829,18 +1965,29 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
                                tail_quarters(tiles(256, 256), cus))) {
       p.cfg = CFG_192x256; p.bm = 192;
     }
+  } else if (!per_row && use_tiny() && tiny_grid(tiles(32, 32), KB, cus)) {
+    p.cfg = CFG_TINY; p.bm = 32; p.bn = 32;
+    p.splits = 1;
+    p.kb_per_split = KB;
+    return p;
   } else {
     p.cfg = CFG_128x128; p.bm = 128; p.bn = 128;
   }
   const int64_t t = tiles(p.bm, p.bn);
-  // Grids with fewer tiles than CUs split K until there are about two
-  // workgroups per CU, keeping at least four K-blocks per split. Grids that
-  // already cover the CUs are not split: the fp32 partials would cost more
-  // HBM traffic than the extra occupancy recovers.
+  // Grids with fewer tiles than CUs split K, keeping at least four K-blocks
+  // per split: 128x128 grids while the split grid still fits one wave of
+  // workgroups (one per CU, by its LDS; a second wave costs more than the
+  // idle CUs: 1536x1536x4096 40.2 us split in two, 24.2 unsplit), 64x128
+  // grids (four waves, three workgroups per CU) until there are about two
+  // workgroups per CU. Grids that already cover the CUs are not split: the
+  // fp32 partials would cost more HBM traffic than the extra occupancy
+  // recovers.
   int splits = 1;
   // (a partial wave of 256x256 tiles chosen by prefer_256 is not split: the
   // fp32 partials of a long-K grid cost more than the idle CUs)
-  if (t < cus && p.cfg != CFG_256x256)
+  if (t < cus && p.cfg == CFG_128x128)
+    while (t * splits * 2 <= cus && KB / (splits * 2) >= 4) splits *= 2;
+  else if (t < cus && p.cfg != CFG_256x256)
     while (t * splits < 2 * cus && KB / (splits * 2) >= 4) splits *= 2;
   p.kb_per_split = (KB + splits - 1) / splits;
   // Split sizes in whole scale half-windows (multiples of 4 K-blocks) keep
@@ -1899,6 +2046,19 @@ void launch_pipe256(const GemmArgs& a, hipStream_t st) {
   r.tiles_m = (a.M + 127) / 128;
   r.tiles_n = (a.N + 127) / 128;
   gemm_pipe128_kernel<64, 32, PR><<<(unsigned)(4 * rest), 512, 0, st>>>(r);
+}
+
+// gemm_tiny_kernel with as many waves per tile as keep about eight waves
+// per CU resident (two K-block slots per wave: 8448 B each). Measured per
+// waves x slots on 512x512x2048: 8x2 4.6 us, 4x2 4.6, 2x2 5.8, 1x7 8.1;
+// on 2048x1024x2048 (eight tiles per CU): 1x2 13.3, 2x2 16.2, 8x2 23.1.
+void launch_tiny(const GemmArgs& a, hipStream_t st) {
+  const int64_t t = (int64_t)a.tiles_m * a.tiles_n;
+  const int cus = device_cu_count();
+  if (t <= cus) gemm_tiny_kernel<8, 2><<<(unsigned)t, 512, 0, st>>>(a);
+  else if (t <= 2 * (int64_t)cus) gemm_tiny_kernel<4, 2><<<(unsigned)t, 256, 0, st>>>(a);
+  else if (t <= 4 * (int64_t)cus) gemm_tiny_kernel<2, 2><<<(unsigned)t, 128, 0, st>>>(a);
+  else gemm_tiny_kernel<1, 2><<<(unsigned)t, 64, 0, st>>>(a);
 }
 
 template <int BM, int BN, int WM, int WN>
@@ -2011,6 +2171,10 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
     p.cfg = CFG_SKINNY; p.bn = 16; p.splits = 1; p.kb_per_split = (int)(K / 128);
   }
   GemmArgs a = make_args(p);
+  if ((int64_t)a.tiles_m * a.tiles_n >= (int64_t(1) << 31)) {
+    set_error("fp8b_w8a8_block_matmul: too many output tiles for one launch");
+    return FP8B_ERR_DIMS;
+  }
   // 192x256 tiles exist only as a pipelined kernel: without its
   // preconditions the grid goes back to 256x256 tiles.
   if (p.cfg == CFG_192x256 && !pipe_ok(a, p)) {
@@ -2064,6 +2228,9 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
     }
     case CFG_192x256:
       gemm_pipe192_kernel<false><<<(unsigned)(a.tiles_m * a.tiles_n), 512, 0, st>>>(a);
+      break;
+    case CFG_TINY:
+      launch_tiny(a, st);
       break;
     case CFG_128x128: {
       if (pipe_ok(a, p)) {

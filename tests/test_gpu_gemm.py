@@ -390,6 +390,77 @@ def test_gemm_192_row_tiles_equal_other_plans(M, N, K, dev):
     assert torch.equal(out32.to(torch.bfloat16), out)
 
 
+# Small-grid shapes and the waves per 32x32 tile gemm_tiny_kernel runs them
+# with on a 256-CU MI355X (8: at most one tile per CU; 4: two; 2: four; 1:
+# up to eight), ragged edges, one K-block (seven of eight waves idle) and a
+# long K included.
+SMALL_GRIDS = [(512, 512, 2048), (500, 300, 1024), (65, 96, 4096), (100, 2000, 7168),
+               (256, 1024, 128), (512, 1024, 2048), (1024, 512, 7168), (768, 768, 4096),
+               (2048, 1024, 2048), (1000, 2000, 1024)]
+
+
+@pytest.mark.parametrize("M,N,K", SMALL_GRIDS)
+def test_gemm_small_grid_tiles(M, N, K, dev):
+    """Grids of at most eight 32x32 tiles per CU (512 x 512 and the like) run
+    gemm_tiny_kernel: one workgroup per 32x32 tile whose waves split K and
+    sum their partial tiles in wave order, no workspace. Sampled rows
+    against the oracle; the same bits on a second call, with column-major
+    activation scales and through the fp32 epilogue. With one wave per tile
+    (eight tiles per CU) the arithmetic is that of every unsplit plan, so
+    the same rows inside a 32768-row grid give the same bits."""
+    from hf_kernels_helion_amd import _native
+    print(f"gemm small-grid tiles M={M} N={N} K={K}", flush=True)
+    lib = _native.load()
+    assert lib.fp8b_gemm_workspace_size(M, N, K, 128, 128) == 0
+    x = synthetic.activations(M, K, seed=M + 5 * N, outlier_frac=0.01)
+    q, s = fp8.act_quant(x.to(dev), 128)
+    W, Bs = synthetic.weights(N, K, seed=N + 7)
+    W, Bs = W.to(dev), Bs.to(dev)
+    out = fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [128, 128], torch.bfloat16)
+    rows = torch.tensor(sorted({0, 31, 32, M // 2, M - 1}))
+    orc = oracle.block_gemm(_u8(q.cpu()[rows]), _u8(W.cpu()), s.cpu()[rows].numpy(),
+                            Bs.cpu().numpy())
+    torch.testing.assert_close(out[rows.to(dev)].float().cpu(),
+                               torch.from_numpy(orc).to(torch.bfloat16).float(),
+                               rtol=RTOL, atol=ATOL)
+    again = fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [128, 128], torch.bfloat16)
+    assert torch.equal(again, out)
+    s_cm = torch.empty_strided(s.shape, (1, M), dtype=s.dtype, device=dev).copy_(s)
+    out_cm = fp8.w8a8_block_fp8_matmul(q, W, s_cm, Bs, [128, 128], torch.bfloat16)
+    assert torch.equal(out_cm, out)
+    out32 = fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [128, 128], torch.float32)
+    assert torch.equal(out32.to(torch.bfloat16), out)
+    tiles32 = ((M + 31) // 32) * ((N + 31) // 32)
+    if tiles32 > 4 * 256:
+        big = 32768
+        reps = (big + M - 1) // M
+        qb = q.repeat(reps, 1)[:big].contiguous()
+        sb = s.repeat(reps, 1)[:big].contiguous()
+        assert lib.fp8b_gemm_workspace_size(big, N, K, 128, 128) == 0
+        ref = fp8.w8a8_block_fp8_matmul(qb, W, sb, Bs, [128, 128], torch.bfloat16)
+        assert torch.equal(out, ref[:M])
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 512, 2048), (256, 1024, 128), (512, 1024, 2048),
+                                   (768, 768, 4096), (2048, 1024, 2048)])
+def test_gemm_small_grid_exact_integers(M, N, K, dev):
+    """Small-integer fp8 operands and power-of-two scales: every MFMA dot,
+    fold and sum of partial tiles is exact, so each small-grid configuration
+    (8, 4, 2 and 1 waves per tile) must give the exact product bit for bit."""
+    print(f"gemm small-grid exact M={M} N={N} K={K}", flush=True)
+    g = torch.Generator().manual_seed(M + N + K)
+    A = torch.randint(-3, 4, (M, K), generator=g).float().to(torch.float8_e4m3fn)
+    B = torch.randint(-3, 4, (N, K), generator=g).float().to(torch.float8_e4m3fn)
+    As = torch.exp2(torch.randint(-2, 3, (M, K // 128), generator=g).float())
+    Bs = torch.exp2(torch.randint(-2, 3, (N // 128, K // 128), generator=g).float())
+    out = fp8.w8a8_block_fp8_matmul(A.to(dev), B.to(dev), As.to(dev), Bs.to(dev), [128, 128])
+    Ad = A.double() * As.double().repeat_interleave(128, 1)
+    Bd = B.double() * Bs.double().repeat_interleave(128, 0).repeat_interleave(128, 1)
+    exact = Ad @ Bd.T
+    assert exact.abs().max() < 2 ** 20
+    assert torch.equal(out.cpu().double(), exact)
+
+
 def _one_hot_rows(N, K, dev):
     """B [N,K] e4m3fn with row n = 1.0 at k < 8(n+1) and 0 elsewhere, so that
     with A = 1.0 and unit scales C[m,n] = 8(n+1) exactly."""

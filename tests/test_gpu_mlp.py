@@ -95,15 +95,19 @@ def test_fp8_mlp_chain_ragged(dev):
 
 def _gate_up_chain(xq, xs, w13, s13, M):
     """h = bf16 GEMM, then silu_and_mul_quant: the two-kernel reference of
-    gate_up_silu_quant. Small M is padded to 256 rows (zero activations) so
-    that the GEMM runs on the unsplit MFMA kernels whose per-output
-    arithmetic (one MFMA and one scale FMA per K-block, in K order) the fused
-    kernel shares; rows are independent, so the first M rows are the ones of
-    the unpadded problem."""
-    if M < 256:
-        pad = 256 - M
+    gate_up_silu_quant. M below 4096 is padded to 16384 rows (zero
+    activations) so that the GEMM grid covers the CUs and runs an unsplit
+    tiled kernel (no split-K, no small-grid kernel) whose per-output
+    arithmetic (one MFMA and one scale FMA per K-block, in K order) the
+    fused kernel shares; rows are independent, so the first M rows are the
+    ones of the unpadded problem."""
+    from hf_kernels_helion_amd import _native
+    if M < 4096:
+        pad = 16384 - M
         xq = torch.cat([xq, torch.zeros(pad, xq.shape[1], dtype=xq.dtype, device=xq.device)])
         xs = torch.cat([xs, torch.full((pad, xs.shape[1]), 1.0, device=xs.device)])
+    assert _native.load().fp8b_gemm_workspace_size(xq.shape[0], w13.shape[0], xq.shape[1],
+                                                   128, 128) == 0
     h = fp8.w8a8_block_fp8_matmul(xq, w13, xs, s13, [128, 128], torch.bfloat16)
     q, s = fp8.silu_and_mul_quant(h, 128)
     return q[:M], s[:M], h[:M]

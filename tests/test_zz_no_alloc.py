@@ -2,8 +2,9 @@
 against fp8b_w8a8_block_matmul with a caller workspace, through the C ABI:
 bit for bit (same kernels, same summation order), on calls in a row that
 reuse the library's scratch array with a smaller problem second, on the
-split-K 128x128 and decode plans and a plan without split-K; plans whose
-partials exceed the scratch size are refused with FP8B_ERR_WORKSPACE."""
+split-K 128x128 and decode plans and a plan without split-K; the scratch
+holds the partials of every plan on this device (plans whose partials would
+exceed it are refused with FP8B_ERR_WORKSPACE)."""
 import pytest
 import torch
 
@@ -55,7 +56,7 @@ def test_noalloc_equals_workspace_entry_point_twice(dtype, dev):
     """Two calls in a row through the scratch array, the second smaller (so
     the scratch still holds the first call's partials beyond the second's),
     then a decode shape and an unsplit one."""
-    shapes = [(300, 1024, 8192), (100, 512, 2048), (32, 4096, 14336), (1024, 4096, 1024)]
+    shapes = [(1024, 2048, 4096), (300, 1024, 16384), (32, 4096, 14336), (1024, 4096, 1024)]
     used = []
     for i, (M, N, K) in enumerate(shapes):
         print(f"noalloc M={M} N={N} K={K} {dtype}", flush=True)
@@ -67,19 +68,30 @@ def test_noalloc_equals_workspace_entry_point_twice(dtype, dev):
     assert max(used) <= SCRATCH_BYTES
 
 
-def test_noalloc_refuses_plans_beyond_the_scratch(dev):
-    """A 128x128 grid just below the CU count split four ways needs more
-    partial storage than the scratch holds: refused before any launch, with
-    the limit named."""
+def test_noalloc_scratch_holds_every_split_plan(dev):
+    """Split-K plans keep their grids within about one wave of workgroups:
+    128x128 grids at most one per CU (16 MiB of fp32 partials on 256 CUs),
+    64x128 grids (M <= 64) under four per CU (under 32 MiB), decode grids
+    under two per CU. Sweeps the worst cases of each over N at a long K: on
+    this device every plan fits the scratch array, or (a device with more
+    CUs) the largest is refused before any launch, with the limit named."""
     lib = _native.load()
-    M, N, K = 1920, 2176, 4096       # 15 x 17 = 255 tiles, 4 K-splits on 256 CUs
-    need = lib.fp8b_gemm_workspace_size(M, N, K, 128, 128)
-    if need <= SCRATCH_BYTES:
-        pytest.skip(f"this device's plan needs only {need} bytes of partials")
+    K = 131072
+    worst, shape = 0, None
+    for M in (1, 16, 32, 48, 49, 64, 65, 128, 129, 256, 1000):
+        for N in range(128, 40064, 128):
+            need = lib.fp8b_gemm_workspace_size(M, N, K, 128, 128)
+            if need > worst:
+                worst, shape = need, (M, N)
+    print(f"largest split-K partials: {worst} bytes at M, N = {shape}, K = {K}", flush=True)
+    assert worst > 0
+    if worst <= SCRATCH_BYTES:
+        return
+    M, N = shape
     A = torch.zeros(M, K, dtype=torch.float8_e4m3fn, device=dev)
     B = torch.zeros(N, K, dtype=torch.float8_e4m3fn, device=dev)
     As = torch.ones(M, K // 128, device=dev)
-    Bs = torch.ones(N // 128 + 1, K // 128, device=dev)
+    Bs = torch.ones((N + 127) // 128, K // 128, device=dev)
     C = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
     st = lib.fp8b_w8a8_block_matmul_noalloc(*_args(A, B, As, Bs, C, _native.BF16),
                                             torch.cuda.current_stream().cuda_stream)
