@@ -392,11 +392,12 @@ def test_gemm_192_row_tiles_equal_other_plans(M, N, K, dev):
 
 # Small-grid shapes and the waves per 32x32 tile gemm_tiny_kernel runs them
 # with on a 256-CU MI355X (8: at most one tile per CU; 4: two; 2: four; 1:
-# up to eight), ragged edges, one K-block (seven of eight waves idle) and a
-# long K included.
+# up to eight), ragged edges, one K-block (seven of eight waves idle), a
+# long K and 49..64 rows (just above the decode kernels) included.
 SMALL_GRIDS = [(512, 512, 2048), (500, 300, 1024), (65, 96, 4096), (100, 2000, 7168),
                (256, 1024, 128), (512, 1024, 2048), (1024, 512, 7168), (768, 768, 4096),
-               (2048, 1024, 2048), (1000, 2000, 1024)]
+               (2048, 1024, 2048), (1000, 2000, 1024), (64, 4096, 4096), (49, 500, 2048),
+               (56, 14336, 4096)]
 
 
 @pytest.mark.parametrize("M,N,K", SMALL_GRIDS)
