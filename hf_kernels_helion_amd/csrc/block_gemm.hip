@@ -1933,6 +1933,23 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
     p.kb_per_split = KB;
     return p;
   }
+  // Small grids: one workgroup per 32x32 tile over the whole K, no split-K
+  // (grids this small never take the 256x256 plans). At 49..64 rows it
+  // replaces the 64x128 tiles (64x4096x4096: 6.2 against 13.2 us), and at up
+  // to 48 rows the decode and skinny kernels once the grid has a tile per CU
+  // (32x14336x4096: 11.7 against 16.4 us; 1x8192x4096: 5.6 against 9.0), or
+  // half that with M > 16 and at most 64 K-blocks (32x4096x7168: 7.6
+  // against 11.1). The decode kernel keeps grids of fewer tiles with longer
+  // K (32x4096x14336: 15.7 against 16.8), the skinny kernel those with M <=
+  // 16 (16x4096x4096: 5.0 against 5.5).
+  const int64_t t32 = tiles(32, 32);
+  if (!per_row && use_tiny() && tiny_grid(t32, KB, cus) &&
+      (M > 48 || t32 >= cus || (2 * t32 >= cus && KB <= 64 && M > 16))) {
+    p.cfg = CFG_TINY; p.bm = 32; p.bn = 32;
+    p.splits = 1;
+    p.kb_per_split = KB;
+    return p;
+  }
   if (M <= 48 && use_decode_kernel()) {
     // Decode path: 128 output columns per workgroup; split K until the grid
     // covers the CUs.
@@ -1953,16 +1970,6 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
       p.splits = 1;
       p.kb_per_split = KB;
     }
-    return p;
-  }
-  // Small grids (M > 48): one workgroup per 32x32 tile over the whole K, no
-  // split-K (grids this small never take the 256x256 plans). At 49..64 rows
-  // it replaces the 64x128 tiles: 64x4096x4096 6.2 against 13.2 us,
-  // 56x14336x4096 15.3 against 23.6.
-  if (!per_row && use_tiny() && tiny_grid(tiles(32, 32), KB, cus)) {
-    p.cfg = CFG_TINY; p.bm = 32; p.bn = 32;
-    p.splits = 1;
-    p.kb_per_split = KB;
     return p;
   }
   if (per_row && M <= 64) {
