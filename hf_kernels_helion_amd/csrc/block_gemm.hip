@@ -1580,7 +1580,11 @@ __global__ void __launch_bounds__(512) gemm_skinny_kernel(GemmArgs a) {
 // arithmetic of every other unsplit plan, bit for bit; with NW > 1 the NW
 // partial tiles are summed through LDS in wave order (deterministic), which
 // keeps more K-blocks in flight per CU: the loop is bound by DMA latency.
-template <int NW, int NS>
+// PR: per-row weight scales (block_n = 1): lanes 32..63 of the scale DMA
+// bring the scales of the tile's 32 weight rows, and each fold multiplies
+// the activation scale by the scale of its output column, as the other
+// per-row kernels do.
+template <int NW, int NS, bool PR = false>
 __global__ void __launch_bounds__(64 * NW) gemm_tiny_kernel(GemmArgs a) {
   constexpr int ROWS = 64;                    // 32 activation rows, then 32 weight rows
   constexpr int SCALE_OFF = ROWS * 128;       // sa rows 0..31, sb in slots 32..63
@@ -1609,8 +1613,9 @@ __global__ void __launch_bounds__(64 * NW) gemm_tiny_kernel(GemmArgs a) {
     src[L] = r < 32 ? a.A + (int64_t)min(m0 + r, a.M - 1) * a.lda + chunk * 16
                     : a.B + (int64_t)min(n0 + r - 32, a.N - 1) * a.ldb + chunk * 16;
   }
+  const int64_t b_row = PR ? min(n0 + lane - 32, a.N - 1) : (min(n0, a.N - 1) >> 7);
   const float* ssrc = lane < 32 ? a.As + (int64_t)min(m0 + lane, a.M - 1) * a.as_sm
-                                : a.Bs + (int64_t)(min(n0, a.N - 1) >> 7) * a.bs_sn;
+                                : a.Bs + b_row * a.bs_sn;
   const int64_t sstep = lane < 32 ? a.as_sk : a.bs_sk;
   auto issue = [&](int kb, int slot) {
     uint8_t* dst = &ring[wid][slot][0];
@@ -1634,23 +1639,44 @@ __global__ void __launch_bounds__(64 * NW) gemm_tiny_kernel(GemmArgs a) {
     if (kb + NS - 1 < kb1) wait_vmcnt<PER_KB * (NS - 1)>();
     else wait_vmcnt<0>();
     const uint8_t* sl = &ring[wid][slot][0];
-    const float sb = *reinterpret_cast<const float*>(sl + SCALE_OFF + 32 * 4);
     v8i x[2], w[2];
-    float sc[2];
 #pragma unroll
     for (int f = 0; f < 2; ++f) {
       x[f] = lds_frag(sl + (f * 16 + row) * 128, c0, r7);
       w[f] = lds_frag(sl + (32 + f * 16 + row) * 128, c0, r7);
-      sc[f] = *reinterpret_cast<const float*>(sl + SCALE_OFF + (f * 16 + row) * 4) * sb;
     }
+    if constexpr (PR) {
+      // output (i, j, e): activation row 16i + row, weight row 16j + 4*(lane>>4) + e
+      float sa[2];
+      v4f sbv[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const v4f t = mfma16x16x128(w[j], x[i]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc[i][j][e] = fmaf(t[e], sc[i], acc[i][j][e]);
+      for (int f = 0; f < 2; ++f) {
+        sa[f] = *reinterpret_cast<const float*>(sl + SCALE_OFF + (f * 16 + row) * 4);
+        sbv[f] = *reinterpret_cast<const v4f*>(sl + SCALE_OFF + (32 + f * 16 + 4 * (lane >> 4)) * 4);
       }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const v4f t = mfma16x16x128(w[j], x[i]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[i][j][e] = fmaf(t[e], sa[i] * sbv[j][e], acc[i][j][e]);
+        }
+    } else {
+      const float sb = *reinterpret_cast<const float*>(sl + SCALE_OFF + 32 * 4);
+      float sc[2];
+#pragma unroll
+      for (int f = 0; f < 2; ++f)
+        sc[f] = *reinterpret_cast<const float*>(sl + SCALE_OFF + (f * 16 + row) * 4) * sb;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const v4f t = mfma16x16x128(w[j], x[i]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[i][j][e] = fmaf(t[e], sc[i], acc[i][j][e]);
+        }
+    }
     // the MFMAs consumed the slot's fragments (their reads are complete):
     // refill it
     if (kb + NS < kb1) issue(kb + NS, slot);
@@ -1919,8 +1945,8 @@ bool tiny_grid(int64_t t32, int KB, int cus) {
 }
 
 // per_row: weight scales per output row (block_n = 1, the deep-gemm layout);
-// only the decode kernel (M <= 48), gemm_pipe128_kernel and
-// gemm_pipe256_kernel implement it.
+// only the decode kernel (M <= 48), gemm_tiny_kernel, gemm_pipe128_kernel
+// and gemm_pipe256_kernel implement it.
 Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
   const int KB = (int)(K / 128);
   const int cus = device_cu_count();
@@ -1943,7 +1969,7 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
   // K (32x4096x14336: 15.7 against 16.8), the skinny kernel those with M <=
   // 16 (16x4096x4096: 5.0 against 5.5).
   const int64_t t32 = tiles(32, 32);
-  if (!per_row && use_tiny() && tiny_grid(t32, KB, cus) &&
+  if (use_tiny() && tiny_grid(t32, KB, cus) &&
       (M > 48 || t32 >= cus || (2 * t32 >= cus && KB <= 64 && M > 16))) {
     p.cfg = CFG_TINY; p.bm = 32; p.bn = 32;
     p.splits = 1;
@@ -2064,13 +2090,14 @@ void launch_pipe256(const GemmArgs& a, hipStream_t st) {
 // per CU resident (two K-block slots per wave: 8448 B each). Measured per
 // waves x slots on 512x512x2048: 8x2 4.6 us, 4x2 4.6, 2x2 5.8, 1x7 8.1;
 // on 2048x1024x2048 (eight tiles per CU): 1x2 13.3, 2x2 16.2, 8x2 23.1.
+template <bool PR>
 void launch_tiny(const GemmArgs& a, hipStream_t st) {
   const int64_t t = (int64_t)a.tiles_m * a.tiles_n;
   const int cus = device_cu_count();
-  if (t <= cus) gemm_tiny_kernel<8, 2><<<(unsigned)t, 512, 0, st>>>(a);
-  else if (t <= 2 * (int64_t)cus) gemm_tiny_kernel<4, 2><<<(unsigned)t, 256, 0, st>>>(a);
-  else if (t <= 4 * (int64_t)cus) gemm_tiny_kernel<2, 2><<<(unsigned)t, 128, 0, st>>>(a);
-  else gemm_tiny_kernel<1, 2><<<(unsigned)t, 64, 0, st>>>(a);
+  if (t <= cus) gemm_tiny_kernel<8, 2, PR><<<(unsigned)t, 512, 0, st>>>(a);
+  else if (t <= 2 * (int64_t)cus) gemm_tiny_kernel<4, 2, PR><<<(unsigned)t, 256, 0, st>>>(a);
+  else if (t <= 4 * (int64_t)cus) gemm_tiny_kernel<2, 2, PR><<<(unsigned)t, 128, 0, st>>>(a);
+  else gemm_tiny_kernel<1, 2, PR><<<(unsigned)t, 64, 0, st>>>(a);
 }
 
 template <int BM, int BN, int WM, int WN>
@@ -2194,7 +2221,9 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
     a = make_args(p);
   }
   if (per_row) {
-    if (p.cfg == CFG_DECODE) {
+    if (p.cfg == CFG_TINY) {
+      launch_tiny<true>(a, st);
+    } else if (p.cfg == CFG_DECODE) {
       const dim3 grid((unsigned)((N + 127) / 128), 1, (unsigned)p.splits);
       const int fm = (int)((M + 15) / 16);
       if (fm <= 1) gemm_decode_kernel<1, true><<<grid, 512, 0, st>>>(a);
@@ -2242,7 +2271,7 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
       gemm_pipe192_kernel<false><<<(unsigned)(a.tiles_m * a.tiles_n), 512, 0, st>>>(a);
       break;
     case CFG_TINY:
-      launch_tiny(a, st);
+      launch_tiny<false>(a, st);
       break;
     case CFG_128x128: {
       if (pipe_ok(a, p)) {

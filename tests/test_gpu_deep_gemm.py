@@ -2,9 +2,9 @@
 gemm_fp8_fp8_bf16_nt, deep-gemm-helion/.../deep_gemm_helion/fp8.py:13-29:
 (A*As) @ (B*Bs)^T with Bs [N, K/128]) against the oracle's blockwise formula
 with block_n = 1, within the north-star tolerance (1e-2 relative, 1e-3
-absolute of the bf16 result). Covers the decode kernel (M <= 48), the 128x128
-and 256x256 pipelined kernels, split-K, the generic fallback (column-major
-As) and ragged edges."""
+absolute of the bf16 result). Covers the decode kernel (M <= 48), the
+small-grid kernel, the 128x128 and 256x256 pipelined kernels, split-K, the
+generic fallback (column-major As) and ragged edges."""
 import pytest
 import torch
 
@@ -91,3 +91,60 @@ def test_per_row_generic_fallback(dev):
     ref = oracle.block_gemm(_u8(q), _u8(Wq), s.cpu().numpy(), Bs.numpy(), (1, 128))
     torch.testing.assert_close(out.float().cpu(), torch.from_numpy(ref).to(torch.bfloat16).float(),
                                rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 512, 2048), (1024, 512, 7168), (768, 768, 4096),
+                                   (2048, 1024, 2048), (32, 14336, 4096), (1, 8192, 4096),
+                                   (64, 4096, 4096), (300, 700, 1536)])
+def test_per_row_small_grid_tiles(M, N, K, dev):
+    """Small grids run gemm_tiny_kernel with per-row weight scales (8, 4, 2
+    and 1 waves per 32x32 tile, decode-sized M, ragged edges): every element
+    against torch's fp32 dequant-matmul, sampled rows against the oracle,
+    no workspace, the same bits on a second call. With one wave per tile the
+    fold order is that of the unsplit per-row plans, so the same rows inside
+    a 32768-row grid give the same bits."""
+    from hf_kernels_helion_amd import _native
+    print(f"deep-gemm per-row small grid M={M} N={N} K={K}", flush=True)
+    lib = _native.load()
+    assert lib.fp8b_gemm_workspace_size(M, N, K, 1, 128) == 0
+    x, Wq, Bs = _operands(M, N, K, seed=M + 3 * N)
+    q, s = fp8.act_quant(x.to(dev), 128)
+    Wd, Bsd = Wq.to(dev), Bs.to(dev)
+    out = dg.gemm_fp8_fp8_bf16_nt(q, Wd, s, Bsd)
+    full = (q.float() * s.repeat_interleave(128, 1)) @ (Wd.float() * Bsd.repeat_interleave(
+        128, 1)).T
+    torch.testing.assert_close(out.float(), full.to(torch.bfloat16).float(), rtol=RTOL,
+                               atol=ATOL)
+    rows = torch.tensor(sorted({r for r in (0, 31, 32, M // 2, M - 1) if r < M}))
+    ref = oracle.block_gemm(_u8(q.cpu()[rows]), _u8(Wq), s.cpu()[rows].numpy(), Bs.numpy(),
+                            (1, 128))
+    torch.testing.assert_close(out[rows.to(dev)].float().cpu(),
+                               torch.from_numpy(ref).to(torch.bfloat16).float(),
+                               rtol=RTOL, atol=ATOL)
+    assert torch.equal(dg.gemm_fp8_fp8_bf16_nt(q, Wd, s, Bsd), out)
+    if ((M + 31) // 32) * ((N + 31) // 32) > 4 * 256:
+        big = 32768
+        reps = (big + M - 1) // M
+        qb = q.repeat(reps, 1)[:big].contiguous()
+        sb = s.repeat(reps, 1)[:big].contiguous()
+        assert lib.fp8b_gemm_workspace_size(big, N, K, 1, 128) == 0
+        assert torch.equal(dg.gemm_fp8_fp8_bf16_nt(qb, Wd, sb, Bsd)[:M], out)
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 4096, 32768), (1024, 2048, 4096), (3000, 1000, 2048)])
+def test_per_row_128_tiles_split_and_unsplit(M, N, K, dev):
+    """Grids past the small-grid range on the per-row 128x128 kernel: split
+    along K (64 rows, 8 splits; 1024 x 2048, 2 splits) and unsplit (3000 x
+    1000: 192 tiles). Every element against torch's fp32 dequant-matmul."""
+    from hf_kernels_helion_amd import _native
+    print(f"deep-gemm per-row 128x128 tiles M={M} N={N} K={K}", flush=True)
+    need = _native.load().fp8b_gemm_workspace_size(M, N, K, 1, 128)
+    assert (need > 0) == (M <= 1024)
+    x, Wq, Bs = _operands(M, N, K, seed=11)
+    q, s = fp8.act_quant(x.to(dev), 128)
+    Wd, Bsd = Wq.to(dev), Bs.to(dev)
+    out = dg.gemm_fp8_fp8_bf16_nt(q, Wd, s, Bsd)
+    full = (q.float() * s.repeat_interleave(128, 1)) @ (Wd.float() * Bsd.repeat_interleave(
+        128, 1)).T
+    torch.testing.assert_close(out.float(), full.to(torch.bfloat16).float(), rtol=RTOL,
+                               atol=ATOL)
