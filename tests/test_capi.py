@@ -115,6 +115,27 @@ def test_workspace_size_zero_for_unsupported_blocks():
     assert lib.fp8b_gemm_workspace_size(0, 4096, 14336, 128, 128) == 0
 
 
+def test_plans_split_k_only_within_one_wave():
+    """The tile planner through the split-K workspace it asks for, on 256 CUs
+    (MI355X, and the count assumed without a device): small grids run one
+    workgroup per 32x32 tile and need no partials, for block and per-row
+    weight scales; 128x128 grids split K only while the split grid still
+    fits one workgroup per CU; the decode plan keeps its 8-way split."""
+    lib = _native.load()
+
+    def ws(M, N, K, block_n=128):
+        return lib.fp8b_gemm_workspace_size(M, N, K, block_n, 128)
+
+    for shape in [(512, 512, 2048), (64, 4096, 4096), (32, 14336, 4096), (1, 8192, 4096),
+                  (2048, 1024, 2048), (768, 768, 4096), (65, 96, 4096)]:
+        assert ws(*shape) == 0 and ws(*shape, block_n=1) == 0, shape
+    assert ws(1536, 1536, 4096) == 0                      # 144 tiles: two ways would need two waves
+    assert ws(1024, 2048, 4096) == 2 * 1024 * 2048 * 4    # 128 tiles, two ways
+    assert ws(1024, 1024, 8192) == 4 * 1024 * 1024 * 4    # 64 tiles, four ways
+    assert ws(32, 4096, 14336) == 8 * 32 * 4096 * 4       # decode: 32 column tiles x 8
+    assert ws(4096, 4096, 8192) == 0
+
+
 def test_status_to_runtime_error():
     with pytest.raises(RuntimeError, match="FP8B_ERR_DIMS"):
         _native.check(2, "probe")
