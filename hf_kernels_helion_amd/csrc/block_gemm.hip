@@ -455,6 +455,14 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// Before a wave refills an LDS slot by DMA without a barrier: its own LDS
+// reads of that slot must have completed. The compiler waits for a ds_read
+// only where the value is used, which can be after the refill is issued
+// (then the DMA's write can overtake the pending read).
+__device__ __forceinline__ void lds_reads_done() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
 // ---------------------------------------------------------------------------
 // Pipelined 256x256 kernel (the large-GEMM path).
 //
@@ -1538,8 +1546,11 @@ __global__ void __launch_bounds__(512) gemm_skinny_kernel(GemmArgs a) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc[f][r] = fmaf(t[r], sc, acc[f][r]);
         }
-        // The MFMAs above consumed the slot (its LDS reads are complete): refill it.
-        if (kb + u + SK < kb1) issue(kb + u + SK, u);
+        // refill the slot once this wave's reads of it are complete
+        if (kb + u + SK < kb1) {
+          lds_reads_done();
+          issue(kb + u + SK, u);
+        }
       }
     }
   }
@@ -1567,39 +1578,41 @@ __global__ void __launch_bounds__(512) gemm_skinny_kernel(GemmArgs a) {
 }
 
 // Small-grid GEMM (grids of 128x128 tiles that would leave most CUs idle,
-// e.g. 512x512x2048): one workgroup per 32x32 output tile, so the grid
-// spreads the operand stream over up to 16x more CUs than 128x128 tiles,
-// with no workspace and no second kernel. Each of its NW waves takes a
-// contiguous range of the K-blocks and streams the tile's 32 activation and
-// 32 weight rows (eight 1 KiB DMA instructions per K-block, the chunk
-// swizzle of gemm_bs128_kernel) and their scales (one 4-byte DMA lane per
-// activation row, the weight block's scale in lanes 32..63) through a
-// private ring of NS LDS slots, so the only waits in the loop are vmcnt
-// waits on its own DMA. Per K-block: four 16x16x128 MFMAs (weights as the A
-// operand), each folded as acc + dot * (As * Bs). With NW = 1 that is the
-// arithmetic of every other unsplit plan, bit for bit; with NW > 1 the NW
-// partial tiles are summed through LDS in wave order (deterministic), which
-// keeps more K-blocks in flight per CU: the loop is bound by DMA latency.
-// PR: per-row weight scales (block_n = 1): lanes 32..63 of the scale DMA
-// bring the scales of the tile's 32 weight rows, and each fold multiplies
-// the activation scale by the scale of its output column, as the other
-// per-row kernels do.
-template <int NW, int NS, bool PR = false>
+// e.g. 512x512x2048): one workgroup per TM x TN output tile (TM = 16*FM,
+// TN = 16*FN: 32x32 or 64x64), so the grid spreads the operand stream over
+// many more CUs than 128x128 tiles, with no workspace and no second kernel.
+// Each of its NW waves takes a contiguous range of the K-blocks and streams
+// the tile's TM activation and TN weight rows ((TM+TN)/8 DMA instructions of
+// 1 KiB per K-block, the chunk swizzle of gemm_bs128_kernel) and their
+// scales (4-byte DMA lanes: the TM activation rows' scales, then TN weight
+// scales: the block's, or each weight row's with PR) through a private ring
+// of NS LDS slots, so the only waits in the loop are vmcnt waits on its own
+// DMA. Per K-block: FM x FN 16x16x128 MFMAs (weights as the A operand), each
+// folded as acc + dot * (As * Bs), or dot * (As * Bs[n]) per output column
+// with PR, as the other kernels do. With NW = 1 that is the arithmetic of
+// every other unsplit plan, bit for bit; with NW > 1 the NW partial tiles
+// are summed through LDS in wave order (deterministic), which keeps more
+// K-blocks in flight per CU: the loop is bound by DMA latency.
+template <int FM, int FN, int NW, int NS, bool PR = false>
 __global__ void __launch_bounds__(64 * NW) gemm_tiny_kernel(GemmArgs a) {
-  constexpr int ROWS = 64;                    // 32 activation rows, then 32 weight rows
-  constexpr int SCALE_OFF = ROWS * 128;       // sa rows 0..31, sb in slots 32..63
-  constexpr int SLOT = SCALE_OFF + 256;
-  constexpr int PER_KB = ROWS / 8 + 1;        // DMA instructions per K-block
+  constexpr int TM = 16 * FM, TN = 16 * FN;
+  constexpr int ROWS = TM + TN;               // activation rows, then weight rows
+  constexpr int SCALES = TM + TN;             // sa of the TM rows, then TN weight scales
+  constexpr int SDMA = (SCALES + 63) / 64;    // 4-byte DMA instructions per K-block
+  constexpr int SCALE_OFF = ROWS * 128;
+  constexpr int SLOT = SCALE_OFF + SDMA * 256;
+  constexpr int PER_KB = ROWS / 8 + SDMA;     // DMA instructions per K-block
+  static_assert(SCALES % 64 == 0 && TM <= 128 && TN <= 128, "tile shape");
   // at most NS K-blocks of DMA are outstanding per wave: within the 6-bit vmcnt
   static_assert(PER_KB * NS <= 63, "vmcnt is a 6-bit counter");
-  static_assert(NW == 1 || NW * NS * SLOT >= NW * 16 * 64 * 4, "partials reuse the ring");
+  static_assert(NW == 1 || NS * SLOT >= FM * FN * 4 * 64 * 4, "partials reuse the ring");
   __shared__ __attribute__((aligned(1024))) uint8_t ring[NW][NS][SLOT];
   const int lane = threadIdx.x & 63;
   // wave index as a scalar, so K ranges and loop conditions are uniform
   const int wid = NW == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int tm, tn;
   tile_of_bid((int)blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
-  const int m0 = tm * 32, n0 = tn * 32;
+  const int m0 = tm * TM, n0 = tn * TN;
   const int kb0 = (int)((int64_t)a.KB * wid / NW);
   const int kb1 = (int)((int64_t)a.KB * (wid + 1) / NW);
 
@@ -1610,26 +1623,35 @@ __global__ void __launch_bounds__(64 * NW) gemm_tiny_kernel(GemmArgs a) {
   for (int L = 0; L < ROWS / 8; ++L) {
     const int r = L * 8 + (lane >> 3);
     const int chunk = (lane & 7) ^ (r & 7);
-    src[L] = r < 32 ? a.A + (int64_t)min(m0 + r, a.M - 1) * a.lda + chunk * 16
-                    : a.B + (int64_t)min(n0 + r - 32, a.N - 1) * a.ldb + chunk * 16;
+    src[L] = r < TM ? a.A + (int64_t)min(m0 + r, a.M - 1) * a.lda + chunk * 16
+                    : a.B + (int64_t)min(n0 + r - TM, a.N - 1) * a.ldb + chunk * 16;
   }
-  const int64_t b_row = PR ? min(n0 + lane - 32, a.N - 1) : (min(n0, a.N - 1) >> 7);
-  const float* ssrc = lane < 32 ? a.As + (int64_t)min(m0 + lane, a.M - 1) * a.as_sm
-                                : a.Bs + b_row * a.bs_sn;
-  const int64_t sstep = lane < 32 ? a.as_sk : a.bs_sk;
+  // scale entry e = 64 d + lane of DMA d: e < TM the activation row m0 + e,
+  // else weight scale e - TM (the block's, or weight row n0 + e - TM with PR)
+  const float* ssrc[SDMA];
+  int64_t sstep[SDMA];
+#pragma unroll
+  for (int d = 0; d < SDMA; ++d) {
+    const int e = d * 64 + lane;
+    const int64_t b_row = PR ? min(n0 + e - TM, a.N - 1) : (min(n0, a.N - 1) >> 7);
+    ssrc[d] = e < TM ? a.As + (int64_t)min(m0 + e, a.M - 1) * a.as_sm : a.Bs + b_row * a.bs_sn;
+    sstep[d] = e < TM ? a.as_sk : a.bs_sk;
+  }
   auto issue = [&](int kb, int slot) {
     uint8_t* dst = &ring[wid][slot][0];
 #pragma unroll
     for (int L = 0; L < ROWS / 8; ++L) lds_dma16(src[L] + (int64_t)kb * 128, dst + L * 1024);
-    lds_dma4(ssrc + (int64_t)kb * sstep, dst + SCALE_OFF);
+#pragma unroll
+    for (int d = 0; d < SDMA; ++d)
+      lds_dma4(ssrc[d] + (int64_t)kb * sstep[d], dst + SCALE_OFF + d * 256);
   };
 
   const int row = lane & 15, c0 = 2 * (lane >> 4), r7 = row & 7;
-  v4f acc[2][2];
+  v4f acc[FM][FN];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < FN; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
   for (int u = 0; u < NS && kb0 + u < kb1; ++u) issue(kb0 + u, u);
   for (int kb = kb0; kb < kb1; ++kb) {
@@ -1639,74 +1661,76 @@ __global__ void __launch_bounds__(64 * NW) gemm_tiny_kernel(GemmArgs a) {
     if (kb + NS - 1 < kb1) wait_vmcnt<PER_KB * (NS - 1)>();
     else wait_vmcnt<0>();
     const uint8_t* sl = &ring[wid][slot][0];
-    v8i x[2], w[2];
+    const float* sv = reinterpret_cast<const float*>(sl + SCALE_OFF);
+    v8i x[FM], w[FN];
 #pragma unroll
-    for (int f = 0; f < 2; ++f) {
-      x[f] = lds_frag(sl + (f * 16 + row) * 128, c0, r7);
-      w[f] = lds_frag(sl + (32 + f * 16 + row) * 128, c0, r7);
-    }
+    for (int f = 0; f < FM; ++f) x[f] = lds_frag(sl + (f * 16 + row) * 128, c0, r7);
+#pragma unroll
+    for (int f = 0; f < FN; ++f) w[f] = lds_frag(sl + (TM + f * 16 + row) * 128, c0, r7);
     if constexpr (PR) {
       // output (i, j, e): activation row 16i + row, weight row 16j + 4*(lane>>4) + e
-      float sa[2];
-      v4f sbv[2];
+      float sa[FM];
+      v4f sbv[FN];
 #pragma unroll
-      for (int f = 0; f < 2; ++f) {
-        sa[f] = *reinterpret_cast<const float*>(sl + SCALE_OFF + (f * 16 + row) * 4);
-        sbv[f] = *reinterpret_cast<const v4f*>(sl + SCALE_OFF + (32 + f * 16 + 4 * (lane >> 4)) * 4);
-      }
+      for (int f = 0; f < FM; ++f) sa[f] = sv[f * 16 + row];
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int f = 0; f < FN; ++f)
+        sbv[f] = *reinterpret_cast<const v4f*>(sv + TM + f * 16 + 4 * (lane >> 4));
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
           const v4f t = mfma16x16x128(w[j], x[i]);
 #pragma unroll
           for (int e = 0; e < 4; ++e) acc[i][j][e] = fmaf(t[e], sa[i] * sbv[j][e], acc[i][j][e]);
         }
     } else {
-      const float sb = *reinterpret_cast<const float*>(sl + SCALE_OFF + 32 * 4);
-      float sc[2];
+      const float sb = sv[TM];
+      float sc[FM];
 #pragma unroll
-      for (int f = 0; f < 2; ++f)
-        sc[f] = *reinterpret_cast<const float*>(sl + SCALE_OFF + (f * 16 + row) * 4) * sb;
+      for (int f = 0; f < FM; ++f) sc[f] = sv[f * 16 + row] * sb;
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < FN; ++j) {
           const v4f t = mfma16x16x128(w[j], x[i]);
 #pragma unroll
           for (int e = 0; e < 4; ++e) acc[i][j][e] = fmaf(t[e], sc[i], acc[i][j][e]);
         }
     }
-    // the MFMAs consumed the slot's fragments (their reads are complete):
-    // refill it
-    if (kb + NS < kb1) issue(kb + NS, slot);
+    // refill the slot once this wave's reads of it are complete
+    if (kb + NS < kb1) {
+      lds_reads_done();
+      issue(kb + NS, slot);
+    }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   if constexpr (NW == 1) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < FN; ++j)
         store4(a, m0 + i * 16 + row, n0 + j * 16 + 4 * (lane >> 4), acc[i][j], false, 0);
   } else {
     // partial tiles reuse the ring: [wave][i][j][e][lane] floats; wave q
-    // then sums sub-tile (q / 2, q % 2) of every wave in wave order
+    // then sums sub-tiles q, q + NW, ... of every wave in wave order
     __syncthreads();
     float* part = reinterpret_cast<float*>(&ring[0][0][0]);
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < FN; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) part[(((wid * 2 + i) * 2 + j) * 4 + e) * 64 + lane] = acc[i][j][e];
+        for (int e = 0; e < 4; ++e)
+          part[(((wid * FM + i) * FN + j) * 4 + e) * 64 + lane] = acc[i][j][e];
     __syncthreads();
-    for (int q = wid; q < 4; q += NW) {
-      const int i = q >> 1, j = q & 1;
+    for (int q = wid; q < FM * FN; q += NW) {
+      const int i = q / FN, j = q % FN;
       v4f sum = {0.f, 0.f, 0.f, 0.f};
       for (int w = 0; w < NW; ++w)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sum[e] += part[(((w * 2 + i) * 2 + j) * 4 + e) * 64 + lane];
+        for (int e = 0; e < 4; ++e) sum[e] += part[(((w * FM + i) * FN + j) * 4 + e) * 64 + lane];
       store4(a, m0 + i * 16 + row, n0 + j * 16 + 4 * (lane >> 4), sum, false, 0);
     }
   }
@@ -1968,6 +1992,21 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
   // against 11.1). The decode kernel keeps grids of fewer tiles with longer
   // K (32x4096x14336: 15.7 against 16.8), the skinny kernel those with M <=
   // 16 (16x4096x4096: 5.0 against 5.5).
+  // Mid-size grids (about one to two 64x64 tiles per CU, 16..64 K-blocks):
+  // the same kernel on 64x64 tiles, against split 128x128 grids or 32x32
+  // tiles: 1024x2048x4096 19.1 against 22.8 us, 2048x1024x2048 12.5 against
+  // 14.0, 960x1024x4096 12.1 against 14.6, 1024x1024x8192 19.5 against
+  // 24.2; outside that band it lost (1024x2048x14336 52.3 against 47.6,
+  // 1536x1536x4096 with 576 tiles 33.8 against 24.3, 768x768x4096 with 144
+  // tiles 11.6 against 11.1).
+  const int64_t t64 = tiles(64, 64);
+  if (M > 64 && use_tiny() && KB >= 16 && KB <= 64 &&
+      ((t64 > cus && t64 <= 2 * (int64_t)cus) || (8 * t64 >= 7 * (int64_t)cus && t64 <= cus))) {
+    p.cfg = CFG_TINY; p.bm = 64; p.bn = 64;
+    p.splits = 1;
+    p.kb_per_split = KB;
+    return p;
+  }
   const int64_t t32 = tiles(32, 32);
   if (use_tiny() && tiny_grid(t32, KB, cus) &&
       (M > 48 || t32 >= cus || (2 * t32 >= cus && KB <= 64 && M > 16))) {
@@ -2087,17 +2126,23 @@ void launch_pipe256(const GemmArgs& a, hipStream_t st) {
 }
 
 // gemm_tiny_kernel with as many waves per tile as keep about eight waves
-// per CU resident (two K-block slots per wave: 8448 B each). Measured per
-// waves x slots on 512x512x2048: 8x2 4.6 us, 4x2 4.6, 2x2 5.8, 1x7 8.1;
-// on 2048x1024x2048 (eight tiles per CU): 1x2 13.3, 2x2 16.2, 8x2 23.1.
+// per CU resident (two K-block slots per wave: 8448 B each for 32x32
+// tiles). Measured per waves x slots on 512x512x2048: 8x2 4.6 us, 4x2 4.6,
+// 2x2 5.8, 1x7 8.1; on 2048x1024x2048 (eight tiles per CU): 1x2 13.3, 2x2
+// 16.2, 8x2 23.1. 64x64 tiles (16896 B per slot): four waves for up to one
+// tile per CU, else two (1024x2048x4096: 2x2 19.1 us, 4x2 22.0, 1x2 28.9,
+// 2x3 33.0).
 template <bool PR>
-void launch_tiny(const GemmArgs& a, hipStream_t st) {
+void launch_tiny(const GemmArgs& a, int tile, hipStream_t st) {
   const int64_t t = (int64_t)a.tiles_m * a.tiles_n;
   const int cus = device_cu_count();
-  if (t <= cus) gemm_tiny_kernel<8, 2, PR><<<(unsigned)t, 512, 0, st>>>(a);
-  else if (t <= 2 * (int64_t)cus) gemm_tiny_kernel<4, 2, PR><<<(unsigned)t, 256, 0, st>>>(a);
-  else if (t <= 4 * (int64_t)cus) gemm_tiny_kernel<2, 2, PR><<<(unsigned)t, 128, 0, st>>>(a);
-  else gemm_tiny_kernel<1, 2, PR><<<(unsigned)t, 64, 0, st>>>(a);
+  if (tile == 64) {
+    if (t <= cus) gemm_tiny_kernel<4, 4, 4, 2, PR><<<(unsigned)t, 256, 0, st>>>(a);
+    else gemm_tiny_kernel<4, 4, 2, 2, PR><<<(unsigned)t, 128, 0, st>>>(a);
+  } else if (t <= cus) gemm_tiny_kernel<2, 2, 8, 2, PR><<<(unsigned)t, 512, 0, st>>>(a);
+  else if (t <= 2 * (int64_t)cus) gemm_tiny_kernel<2, 2, 4, 2, PR><<<(unsigned)t, 256, 0, st>>>(a);
+  else if (t <= 4 * (int64_t)cus) gemm_tiny_kernel<2, 2, 2, 2, PR><<<(unsigned)t, 128, 0, st>>>(a);
+  else gemm_tiny_kernel<2, 2, 1, 2, PR><<<(unsigned)t, 64, 0, st>>>(a);
 }
 
 template <int BM, int BN, int WM, int WN>
@@ -2222,7 +2267,7 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
   }
   if (per_row) {
     if (p.cfg == CFG_TINY) {
-      launch_tiny<true>(a, st);
+      launch_tiny<true>(a, p.bm, st);
     } else if (p.cfg == CFG_DECODE) {
       const dim3 grid((unsigned)((N + 127) / 128), 1, (unsigned)p.splits);
       const int fm = (int)((M + 15) / 16);
@@ -2271,7 +2316,7 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
       gemm_pipe192_kernel<false><<<(unsigned)(a.tiles_m * a.tiles_n), 512, 0, st>>>(a);
       break;
     case CFG_TINY:
-      launch_tiny<false>(a, st);
+      launch_tiny<false>(a, p.bm, st);
       break;
     case CFG_128x128: {
       if (pipe_ok(a, p)) {

@@ -95,7 +95,8 @@ def test_per_row_generic_fallback(dev):
 
 @pytest.mark.parametrize("M,N,K", [(512, 512, 2048), (1024, 512, 7168), (768, 768, 4096),
                                    (2048, 1024, 2048), (32, 14336, 4096), (1, 8192, 4096),
-                                   (64, 4096, 4096), (300, 700, 1536)])
+                                   (64, 4096, 4096), (300, 700, 1536), (1024, 2048, 4096),
+                                   (960, 1024, 4096)])
 def test_per_row_small_grid_tiles(M, N, K, dev):
     """Small grids run gemm_tiny_kernel with per-row weight scales (8, 4, 2
     and 1 waves per 32x32 tile, decode-sized M, ragged edges): every element
@@ -122,7 +123,9 @@ def test_per_row_small_grid_tiles(M, N, K, dev):
                                torch.from_numpy(ref).to(torch.bfloat16).float(),
                                rtol=RTOL, atol=ATOL)
     assert torch.equal(dg.gemm_fp8_fp8_bf16_nt(q, Wd, s, Bsd), out)
-    if ((M + 31) // 32) * ((N + 31) // 32) > 4 * 256:
+    t64 = -(-M // 64) * -(-N // 64)
+    band64 = M > 64 and 16 <= K // 128 <= 64 and (256 < t64 <= 512 or 224 <= t64 <= 256)
+    if not band64 and ((M + 31) // 32) * ((N + 31) // 32) > 4 * 256:
         big = 32768
         reps = (big + M - 1) // M
         qb = q.repeat(reps, 1)[:big].contiguous()
@@ -131,10 +134,10 @@ def test_per_row_small_grid_tiles(M, N, K, dev):
         assert torch.equal(dg.gemm_fp8_fp8_bf16_nt(qb, Wd, sb, Bsd)[:M], out)
 
 
-@pytest.mark.parametrize("M,N,K", [(64, 4096, 32768), (1024, 2048, 4096), (3000, 1000, 2048)])
+@pytest.mark.parametrize("M,N,K", [(64, 4096, 32768), (1024, 2048, 14336), (3000, 1000, 2048)])
 def test_per_row_128_tiles_split_and_unsplit(M, N, K, dev):
     """Grids past the small-grid range on the per-row 128x128 kernel: split
-    along K (64 rows, 8 splits; 1024 x 2048, 2 splits) and unsplit (3000 x
+    along K (64 rows, 8 splits; 1024 x 2048 x 14336, 2 splits) and unsplit (3000 x
     1000: 192 tiles). Every element against torch's fp32 dequant-matmul."""
     from hf_kernels_helion_amd import _native
     print(f"deep-gemm per-row 128x128 tiles M={M} N={N} K={K}", flush=True)

@@ -393,12 +393,22 @@ def test_gemm_192_row_tiles_equal_other_plans(M, N, K, dev):
 # Small-grid shapes and the waves per 32x32 tile gemm_tiny_kernel runs them
 # with on a 256-CU MI355X (8: at most one tile per CU; 4: two; 2: four; 1:
 # up to eight), ragged edges, one K-block (seven of eight waves idle), a
-# long K, 49..64 rows and decode-sized M (1, 17, 24, 32) included.
+# long K, 49..64 rows, decode-sized M (1, 17, 24, 32), and the 64x64-tile
+# band (two waves per tile for 1024 x 2048, four for 960 x 1024).
 SMALL_GRIDS = [(512, 512, 2048), (500, 300, 1024), (65, 96, 4096), (100, 2000, 7168),
                (256, 1024, 128), (512, 1024, 2048), (1024, 512, 7168), (768, 768, 4096),
                (2048, 1024, 2048), (1000, 2000, 1024), (64, 4096, 4096), (49, 500, 2048),
                (56, 14336, 4096), (32, 14336, 4096), (1, 8192, 4096), (24, 4096, 4096),
-               (17, 8192, 1024)]
+               (17, 8192, 1024), (1024, 2048, 4096), (960, 1024, 4096), (1000, 1800, 2048)]
+
+
+def _one_wave_per_tile(M, N, K):
+    """Whether the planner (256 CUs) runs this small grid with one wave per
+    tile: 32x32 tiles, more than four per CU, and not the 64x64 band."""
+    t64 = -(-M // 64) * -(-N // 64)
+    kb = K // 128
+    band64 = M > 64 and 16 <= kb <= 64 and (256 < t64 <= 512 or 224 <= t64 <= 256)
+    return not band64 and -(-M // 32) * -(-N // 32) > 4 * 256
 
 
 @pytest.mark.parametrize("M,N,K", SMALL_GRIDS)
@@ -432,8 +442,7 @@ def test_gemm_small_grid_tiles(M, N, K, dev):
     assert torch.equal(out_cm, out)
     out32 = fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [128, 128], torch.float32)
     assert torch.equal(out32.to(torch.bfloat16), out)
-    tiles32 = ((M + 31) // 32) * ((N + 31) // 32)
-    if tiles32 > 4 * 256:
+    if _one_wave_per_tile(M, N, K):
         big = 32768
         reps = (big + M - 1) // M
         qb = q.repeat(reps, 1)[:big].contiguous()
@@ -443,12 +452,34 @@ def test_gemm_small_grid_tiles(M, N, K, dev):
         assert torch.equal(out, ref[:M])
 
 
+@pytest.mark.parametrize("M,N,K", [(1024, 512, 7168), (512, 512, 2048), (768, 768, 4096),
+                                   (1024, 2048, 4096), (960, 1024, 4096), (32, 14336, 4096)])
+def test_gemm_small_grid_repeatable(M, N, K, dev):
+    """The small-grid kernel refills each wave's LDS slots without a barrier,
+    so a refill issued before that wave's reads of the slot complete would
+    race them. Sixteen calls, alternating row- and column-major activation
+    scales (different DMA timing), must give the same bits."""
+    print(f"gemm small-grid repeatable M={M} N={N} K={K}", flush=True)
+    x = synthetic.activations(M, K, seed=M + 5 * N, outlier_frac=0.01)
+    q, s = fp8.act_quant(x.to(dev), 128)
+    W, Bs = synthetic.weights(N, K, seed=N + 7)
+    W, Bs = W.to(dev), Bs.to(dev)
+    s_cm = torch.empty_strided(s.shape, (1, M), dtype=s.dtype, device=dev).copy_(s)
+    first = fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [128, 128], torch.bfloat16)
+    for i in range(16):
+        out = fp8.w8a8_block_fp8_matmul(q, W, s_cm if i % 2 == 0 else s, Bs, [128, 128],
+                                        torch.bfloat16)
+        assert torch.equal(out, first), f"call {i}"
+
+
 @pytest.mark.parametrize("M,N,K", [(512, 512, 2048), (256, 1024, 128), (512, 1024, 2048),
-                                   (768, 768, 4096), (2048, 1024, 2048)])
+                                   (768, 768, 4096), (2048, 1024, 1024), (1024, 2048, 2048),
+                                   (1024, 1024, 4096)])
 def test_gemm_small_grid_exact_integers(M, N, K, dev):
     """Small-integer fp8 operands and power-of-two scales: every MFMA dot,
     fold and sum of partial tiles is exact, so each small-grid configuration
-    (8, 4, 2 and 1 waves per tile) must give the exact product bit for bit."""
+    (8, 4, 2 and 1 waves per 32x32 tile; 2 and 4 per 64x64 tile) must give
+    the exact product bit for bit."""
     print(f"gemm small-grid exact M={M} N={N} K={K}", flush=True)
     g = torch.Generator().manual_seed(M + N + K)
     A = torch.randint(-3, 4, (M, K), generator=g).float().to(torch.float8_e4m3fn)
