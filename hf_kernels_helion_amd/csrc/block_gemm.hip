@@ -1602,7 +1602,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_tiny_kernel(GemmArgs a) {
   constexpr int SCALE_OFF = ROWS * 128;
   constexpr int SLOT = SCALE_OFF + SDMA * 256;
   constexpr int PER_KB = ROWS / 8 + SDMA;     // DMA instructions per K-block
-  static_assert(SCALES % 64 == 0 && TM <= 128 && TN <= 128, "tile shape");
+  static_assert(TM <= 128 && TN <= 128, "tile shape");
   // at most NS K-blocks of DMA are outstanding per wave: within the 6-bit vmcnt
   static_assert(PER_KB * NS <= 63, "vmcnt is a 6-bit counter");
   static_assert(NW == 1 || NS * SLOT >= FM * FN * 4 * 64 * 4, "partials reuse the ring");
@@ -1627,7 +1627,8 @@ __global__ void __launch_bounds__(64 * NW) gemm_tiny_kernel(GemmArgs a) {
                     : a.B + (int64_t)min(n0 + r - TM, a.N - 1) * a.ldb + chunk * 16;
   }
   // scale entry e = 64 d + lane of DMA d: e < TM the activation row m0 + e,
-  // else weight scale e - TM (the block's, or weight row n0 + e - TM with PR)
+  // else weight scale e - TM (the block's, or weight row n0 + e - TM with PR;
+  // entries past TM + TN repeat a valid address and are not read)
   const float* ssrc[SDMA];
   int64_t sstep[SDMA];
 #pragma unroll
@@ -1968,6 +1969,54 @@ bool tiny_grid(int64_t t32, int KB, int cus) {
   return t32 <= 8 * (int64_t)cus && t32 * KB <= 128 * (int64_t)cus;
 }
 
+// Tile of gemm_tiny_kernel for a small grid, or false when the grid is not
+// one (grids this small never take the 256x256 plans). Measured in HIP-graph
+// replay against the plans they replace:
+//  * 64x64 tiles for a band of mid-size grids, M > 64 with 16..64 K-blocks
+//    and about one to two tiles per CU: 1024x2048x4096 19.1 against 22.8 us
+//    (split 128x128), 2048x1024x2048 12.5 against 14.0, 960x1024x4096 12.1
+//    against 14.6, 1024x1024x8192 19.5 against 24.2. Outside it they lost:
+//    1024x2048x14336 52.3 against 47.6, 1536x1536x4096 (576 tiles, a second
+//    partial round) 33.8 against 24.3, 768x768x4096 (144 tiles) 11.6
+//    against 11.1.
+//  * 32x32 tiles (tiny_grid): M > 48, replacing the split 128x128 and the
+//    64x128 tiles (512x512x2048 4.6 against 11.7 us, 64x4096x4096 6.2
+//    against 13.2); at up to 48 rows, replacing the decode and skinny
+//    kernels, once the grid has a tile per CU (32x14336x4096 11.7 against
+//    16.4; 1x8192x4096 5.6 against 9.0), or, when 32x16 tiles do not fit
+//    either, half that with M > 16 and at most 64 K-blocks.
+//  * 32x16 tiles at 9..32 rows and at least 16 K-blocks when they fill 3/4
+//    to all of the CUs once and 32x32 tiles would not fill them:
+//    32x4096x14336 14.1 against 15.7 us (decode kernel + split-K sum),
+//    12x4096x14336 11.6 against 14.2, 16x4096x7168 6.2 against 9.0,
+//    32x4096x4096 5.1 against 5.6 (32x32 tiles). The decode kernel keeps
+//    fewer tiles with long K (32x2048x14336: 12.0 against 11.9), the skinny
+//    kernel M <= 8 and short K (16x4096x1024: 3.3 against 3.7).
+bool small_grid_tile(int64_t M, int64_t N, int KB, int cus, int& tm, int& tn) {
+  auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+  const int64_t c = cus;
+  const int64_t t64 = tiles(64, 64), t32 = tiles(32, 32), t16 = tiles(32, 16);
+  tm = 32;
+  if (M > 64 && KB >= 16 && KB <= 64 &&
+      ((t64 > c && t64 <= 2 * c) || (8 * t64 >= 7 * c && t64 <= c))) {
+    tm = tn = 64;
+    return true;
+  }
+  if (tiny_grid(t32, KB, cus) && (M > 48 || t32 >= c)) {
+    tn = 32;
+    return true;
+  }
+  if (M > 8 && M <= 32 && KB >= 16 && t16 <= c && 4 * t16 >= 3 * c && t16 * KB <= 128 * c) {
+    tn = 16;
+    return true;
+  }
+  if (tiny_grid(t32, KB, cus) && 2 * t32 >= c && KB <= 64 && M > 16) {
+    tn = 32;
+    return true;
+  }
+  return false;
+}
+
 // per_row: weight scales per output row (block_n = 1, the deep-gemm layout);
 // only the decode kernel (M <= 48), gemm_tiny_kernel, gemm_pipe128_kernel
 // and gemm_pipe256_kernel implement it.
@@ -1983,34 +2032,9 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
     p.kb_per_split = KB;
     return p;
   }
-  // Small grids: one workgroup per 32x32 tile over the whole K, no split-K
-  // (grids this small never take the 256x256 plans). At 49..64 rows it
-  // replaces the 64x128 tiles (64x4096x4096: 6.2 against 13.2 us), and at up
-  // to 48 rows the decode and skinny kernels once the grid has a tile per CU
-  // (32x14336x4096: 11.7 against 16.4 us; 1x8192x4096: 5.6 against 9.0), or
-  // half that with M > 16 and at most 64 K-blocks (32x4096x7168: 7.6
-  // against 11.1). The decode kernel keeps grids of fewer tiles with longer
-  // K (32x4096x14336: 15.7 against 16.8), the skinny kernel those with M <=
-  // 16 (16x4096x4096: 5.0 against 5.5).
-  // Mid-size grids (about one to two 64x64 tiles per CU, 16..64 K-blocks):
-  // the same kernel on 64x64 tiles, against split 128x128 grids or 32x32
-  // tiles: 1024x2048x4096 19.1 against 22.8 us, 2048x1024x2048 12.5 against
-  // 14.0, 960x1024x4096 12.1 against 14.6, 1024x1024x8192 19.5 against
-  // 24.2; outside that band it lost (1024x2048x14336 52.3 against 47.6,
-  // 1536x1536x4096 with 576 tiles 33.8 against 24.3, 768x768x4096 with 144
-  // tiles 11.6 against 11.1).
-  const int64_t t64 = tiles(64, 64);
-  if (M > 64 && use_tiny() && KB >= 16 && KB <= 64 &&
-      ((t64 > cus && t64 <= 2 * (int64_t)cus) || (8 * t64 >= 7 * (int64_t)cus && t64 <= cus))) {
-    p.cfg = CFG_TINY; p.bm = 64; p.bn = 64;
-    p.splits = 1;
-    p.kb_per_split = KB;
-    return p;
-  }
-  const int64_t t32 = tiles(32, 32);
-  if (use_tiny() && tiny_grid(t32, KB, cus) &&
-      (M > 48 || t32 >= cus || (2 * t32 >= cus && KB <= 64 && M > 16))) {
-    p.cfg = CFG_TINY; p.bm = 32; p.bn = 32;
+  int tm = 0, tn = 0;
+  if (use_tiny() && small_grid_tile(M, N, KB, cus, tm, tn)) {
+    p.cfg = CFG_TINY; p.bm = tm; p.bn = tn;
     p.splits = 1;
     p.kb_per_split = KB;
     return p;
@@ -2133,10 +2157,12 @@ void launch_pipe256(const GemmArgs& a, hipStream_t st) {
 // tile per CU, else two (1024x2048x4096: 2x2 19.1 us, 4x2 22.0, 1x2 28.9,
 // 2x3 33.0).
 template <bool PR>
-void launch_tiny(const GemmArgs& a, int tile, hipStream_t st) {
+void launch_tiny(const GemmArgs& a, int tile_n, hipStream_t st) {
   const int64_t t = (int64_t)a.tiles_m * a.tiles_n;
   const int cus = device_cu_count();
-  if (tile == 64) {
+  if (tile_n == 16) {
+    gemm_tiny_kernel<2, 1, 8, 2, PR><<<(unsigned)t, 512, 0, st>>>(a);
+  } else if (tile_n == 64) {
     if (t <= cus) gemm_tiny_kernel<4, 4, 4, 2, PR><<<(unsigned)t, 256, 0, st>>>(a);
     else gemm_tiny_kernel<4, 4, 2, 2, PR><<<(unsigned)t, 128, 0, st>>>(a);
   } else if (t <= cus) gemm_tiny_kernel<2, 2, 8, 2, PR><<<(unsigned)t, 512, 0, st>>>(a);
@@ -2267,7 +2293,7 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
   }
   if (per_row) {
     if (p.cfg == CFG_TINY) {
-      launch_tiny<true>(a, p.bm, st);
+      launch_tiny<true>(a, p.bn, st);
     } else if (p.cfg == CFG_DECODE) {
       const dim3 grid((unsigned)((N + 127) / 128), 1, (unsigned)p.splits);
       const int fm = (int)((M + 15) / 16);
@@ -2316,7 +2342,7 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
       gemm_pipe192_kernel<false><<<(unsigned)(a.tiles_m * a.tiles_n), 512, 0, st>>>(a);
       break;
     case CFG_TINY:
-      launch_tiny<false>(a, p.bm, st);
+      launch_tiny<false>(a, p.bn, st);
       break;
     case CFG_128x128: {
       if (pipe_ok(a, p)) {

@@ -144,10 +144,13 @@ def test_gemm_empty_shapes(dev):
     assert out.shape == (0, 128)
 
 
-def test_gemm_decode_shape_splitk(dev):
-    """M=32, N=4096, K=14336 (split-K path) against the oracle on all rows."""
-    print("gemm decode 32x4096x14336", flush=True)
-    A, B, As, Bs = _operands(32, 4096, 14336, seed=21)
+@pytest.mark.parametrize("N", [4096, 2048])
+def test_gemm_decode_shape(N, dev):
+    """M=32, K=14336 against the oracle on all rows: N = 4096 (the decode
+    config, 256 tiles of 32x16 on the small-grid kernel) and N = 2048 (the
+    split-K decode kernel and its sum)."""
+    print(f"gemm decode 32x{N}x14336", flush=True)
+    A, B, As, Bs = _operands(32, N, 14336, seed=21)
     out = fp8.w8a8_block_fp8_matmul(A.to(dev), B.to(dev), As.to(dev), Bs.to(dev), [128, 128],
                                     torch.bfloat16)
     _check(out, A, B, As, Bs)
@@ -260,12 +263,12 @@ def test_gemm_golden_fixture(dev):
 
 
 @pytest.mark.parametrize("M,N,K", [(4096, 4096, 1024), (512, 512, 2048), (32, 4096, 14336),
-                                   (3001, 4096, 4096)])
+                                   (32, 2048, 14336), (3001, 4096, 4096), (2048, 2048, 4096)])
 def test_gemm_power_of_two_row_scaling(M, N, K, dev):
     """Scaling the activation scales of one row by 2^k scales that fp32
     output row by exactly 2^k and leaves every other row bit-identical, on
-    each kernel family (256x256 pipelined, 128x128 pipelined, split-K decode,
-    partial-wave 256x256)."""
+    each kernel family (256x256 pipelined, small-grid 32x32 and 32x16 tiles,
+    split-K decode, partial-wave 256x256, 128x128 pipelined)."""
     print(f"gemm 2^k row scaling M={M} N={N} K={K}", flush=True)
     A, B, As, Bs = [t.to(dev) for t in _operands(M, N, K, seed=7 + M, kind="harness")]
     out = fp8.w8a8_block_fp8_matmul(A, B, As, Bs, [128, 128], torch.float32)
@@ -393,13 +396,15 @@ def test_gemm_192_row_tiles_equal_other_plans(M, N, K, dev):
 # Small-grid shapes and the waves per 32x32 tile gemm_tiny_kernel runs them
 # with on a 256-CU MI355X (8: at most one tile per CU; 4: two; 2: four; 1:
 # up to eight), ragged edges, one K-block (seven of eight waves idle), a
-# long K, 49..64 rows, decode-sized M (1, 17, 24, 32), and the 64x64-tile
-# band (two waves per tile for 1024 x 2048, four for 960 x 1024).
+# long K, 49..64 rows, decode-sized M (1, 17, 24, 32), the 64x64-tile band
+# (two waves per tile for 1024 x 2048, four for 960 x 1024) and 32x16 tiles
+# (decode shapes with N = 4096).
 SMALL_GRIDS = [(512, 512, 2048), (500, 300, 1024), (65, 96, 4096), (100, 2000, 7168),
                (256, 1024, 128), (512, 1024, 2048), (1024, 512, 7168), (768, 768, 4096),
                (2048, 1024, 2048), (1000, 2000, 1024), (64, 4096, 4096), (49, 500, 2048),
                (56, 14336, 4096), (32, 14336, 4096), (1, 8192, 4096), (24, 4096, 4096),
-               (17, 8192, 1024), (1024, 2048, 4096), (960, 1024, 4096), (1000, 1800, 2048)]
+               (17, 8192, 1024), (1024, 2048, 4096), (960, 1024, 4096), (1000, 1800, 2048),
+               (32, 4096, 14336), (12, 4096, 14336), (16, 4096, 7168)]
 
 
 def _one_wave_per_tile(M, N, K):
@@ -474,12 +479,12 @@ def test_gemm_small_grid_repeatable(M, N, K, dev):
 
 @pytest.mark.parametrize("M,N,K", [(512, 512, 2048), (256, 1024, 128), (512, 1024, 2048),
                                    (768, 768, 4096), (2048, 1024, 1024), (1024, 2048, 2048),
-                                   (1024, 1024, 4096)])
+                                   (1024, 1024, 4096), (32, 4096, 4096), (16, 4096, 7168)])
 def test_gemm_small_grid_exact_integers(M, N, K, dev):
     """Small-integer fp8 operands and power-of-two scales: every MFMA dot,
     fold and sum of partial tiles is exact, so each small-grid configuration
-    (8, 4, 2 and 1 waves per 32x32 tile; 2 and 4 per 64x64 tile) must give
-    the exact product bit for bit."""
+    (8, 4, 2 and 1 waves per 32x32 tile; 2 and 4 per 64x64 tile; 8 per
+    32x16 tile) must give the exact product bit for bit."""
     print(f"gemm small-grid exact M={M} N={N} K={K}", flush=True)
     g = torch.Generator().manual_seed(M + N + K)
     A = torch.randint(-3, 4, (M, K), generator=g).float().to(torch.float8_e4m3fn)
