@@ -1971,7 +1971,9 @@ bool tiny_grid(int64_t t32, int KB, int cus) {
 
 // Tile of gemm_tiny_kernel for a small grid, or false when the grid is not
 // one (grids this small never take the 256x256 plans). Measured in HIP-graph
-// replay against the plans they replace:
+// replay against the plans they replace; for M <= 64 with the weights
+// streamed from HBM (each launch of the graph on another weight copy, 600 MB
+// of copies past the 256 MB MALL, as a decode step over a model's layers):
 //  * 64x64 tiles for a band of mid-size grids, M > 64 with 16..64 K-blocks
 //    and about one to two tiles per CU: 1024x2048x4096 19.1 against 22.8 us
 //    (split 128x128), 2048x1024x2048 12.5 against 14.0, 960x1024x4096 12.1
@@ -1979,19 +1981,20 @@ bool tiny_grid(int64_t t32, int KB, int cus) {
 //    1024x2048x14336 52.3 against 47.6, 1536x1536x4096 (576 tiles, a second
 //    partial round) 33.8 against 24.3, 768x768x4096 (144 tiles) 11.6
 //    against 11.1.
-//  * 32x32 tiles (tiny_grid): M > 48, replacing the split 128x128 and the
-//    64x128 tiles (512x512x2048 4.6 against 11.7 us, 64x4096x4096 6.2
-//    against 13.2); at up to 48 rows, replacing the decode and skinny
-//    kernels, once the grid has a tile per CU (32x14336x4096 11.7 against
-//    16.4; 1x8192x4096 5.6 against 9.0), or, when 32x16 tiles do not fit
-//    either, half that with M > 16 and at most 64 K-blocks.
-//  * 32x16 tiles at 9..32 rows and at least 16 K-blocks when they fill 3/4
-//    to all of the CUs once and 32x32 tiles would not fill them:
-//    32x4096x14336 14.1 against 15.7 us (decode kernel + split-K sum),
-//    12x4096x14336 11.6 against 14.2, 16x4096x7168 6.2 against 9.0,
-//    32x4096x4096 5.1 against 5.6 (32x32 tiles). The decode kernel keeps
-//    fewer tiles with long K (32x2048x14336: 12.0 against 11.9), the skinny
-//    kernel M <= 8 and short K (16x4096x1024: 3.3 against 3.7).
+//  * 32x32 tiles (tiny_grid) for M > 64, replacing the split 128x128 plan
+//    (512x512x2048 4.6 against 11.7 us); at 49..64 rows up to 64 K-blocks,
+//    replacing the 64x128 tiles (64x2048x4096 8.1 against 12.6; at 112
+//    K-blocks 24.2 against 23.6); at up to 48 rows up to 32 K-blocks,
+//    replacing the decode and skinny kernels, once the grid has a tile per
+//    CU (32x14336x4096 16.4 against 19.2; 1x8192x4096 9.5 against 11.3;
+//    48x7168x2048 7.3 against 11.4), or half that with M > 16. Longer K
+//    keeps the decode kernel's deeper weight stream (32x8192x14336 29.6
+//    against 26.8, 32x16384x7168 31.1 against 26.9).
+//  * 32x16 tiles at 9..32 rows and 16..64 K-blocks when they fill 3/4 to all
+//    of the CUs once and 32x32 tiles would not fill them: 32x4096x4096 7.4
+//    against 8.2 (skinny), 16x4096x7168 9.2 against 10.9 and 32x4096x7168
+//    11.5 against 12.1 (decode + split-K sum); at 112 K-blocks the decode
+//    kernel wins (32x4096x14336: 16.7 against 21.6).
 bool small_grid_tile(int64_t M, int64_t N, int KB, int cus, int& tm, int& tn) {
   auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
   const int64_t c = cus;
@@ -2002,19 +2005,15 @@ bool small_grid_tile(int64_t M, int64_t N, int KB, int cus, int& tm, int& tn) {
     tm = tn = 64;
     return true;
   }
-  if (tiny_grid(t32, KB, cus) && (M > 48 || t32 >= c)) {
-    tn = 32;
-    return true;
-  }
-  if (M > 8 && M <= 32 && KB >= 16 && t16 <= c && 4 * t16 >= 3 * c && t16 * KB <= 128 * c) {
+  tn = 32;
+  if (M > 64) return tiny_grid(t32, KB, cus);
+  if (M > 48) return tiny_grid(t32, KB, cus) && KB <= 64;
+  if (tiny_grid(t32, KB, cus) && t32 >= c && KB <= 32) return true;
+  if (M > 8 && M <= 32 && KB >= 16 && KB <= 64 && t16 <= c && 4 * t16 >= 3 * c) {
     tn = 16;
     return true;
   }
-  if (tiny_grid(t32, KB, cus) && 2 * t32 >= c && KB <= 64 && M > 16) {
-    tn = 32;
-    return true;
-  }
-  return false;
+  return tiny_grid(t32, KB, cus) && 2 * t32 >= c && KB <= 32 && M > 16;
 }
 
 // per_row: weight scales per output row (block_n = 1, the deep-gemm layout);

@@ -127,13 +127,14 @@ def test_plans_split_k_only_within_one_wave():
         return lib.fp8b_gemm_workspace_size(M, N, K, block_n, 128)
 
     for shape in [(512, 512, 2048), (64, 4096, 4096), (32, 14336, 4096), (1, 8192, 4096),
-                  (2048, 1024, 2048), (768, 768, 4096), (65, 96, 4096), (32, 4096, 14336)]:
+                  (2048, 1024, 2048), (768, 768, 4096), (65, 96, 4096), (32, 4096, 4096)]:
         assert ws(*shape) == 0 and ws(*shape, block_n=1) == 0, shape
     assert ws(1536, 1536, 4096) == 0                      # 144 tiles: two ways would need two waves
     assert ws(1024, 2048, 14336) == 2 * 1024 * 2048 * 4   # 128 tiles, two ways
     assert ws(1024, 1024, 16384) == 4 * 1024 * 1024 * 4   # 64 tiles, four ways
     assert ws(1024, 2048, 4096) == 0 and ws(960, 1024, 4096) == 0   # 64x64 tiles
     assert ws(32, 2048, 14336) == 16 * 32 * 2048 * 4      # decode: 16 column tiles x 16
+    assert ws(32, 4096, 14336) == 8 * 32 * 4096 * 4       # decode: 32 column tiles x 8
     assert ws(4096, 4096, 8192) == 0
 
 
