@@ -1981,10 +1981,13 @@ bool tiny_grid(int64_t t32, int KB, int cus) {
 //    1024x2048x14336 52.3 against 47.6, 1536x1536x4096 (576 tiles, a second
 //    partial round) 33.8 against 24.3, 768x768x4096 (144 tiles) 11.6
 //    against 11.1.
-//  * 32x32 tiles (tiny_grid) for M > 64, replacing the split 128x128 plan
-//    (512x512x2048 4.6 against 11.7 us); at 49..64 rows up to 64 K-blocks,
-//    replacing the 64x128 tiles (64x2048x4096 8.1 against 12.6; at 112
-//    K-blocks 24.2 against 23.6); at up to 48 rows up to 32 K-blocks,
+//  * 32x32 tiles (tiny_grid) up to 64 K-blocks for M > 64, replacing the
+//    split 128x128 plan (512x512x2048 5.2 against 12.9 us, 128x4096x4096
+//    12.0 against 19.8, 256x7168x2048 14.4 against 21.3; at 224 K-blocks
+//    38.6 against 21.7 for 128x1024x28672, at 112 20.9 against 19.2 for
+//    128x2048x14336), and at 49..64 rows, replacing the 64x128 tiles
+//    (64x2048x4096 8.1 against 12.6; at 112 K-blocks 24.2 against 23.6);
+//    at up to 48 rows up to 32 K-blocks,
 //    replacing the decode and skinny kernels, once the grid has a tile per
 //    CU (32x14336x4096 16.4 against 19.2; 1x8192x4096 9.5 against 11.3;
 //    48x7168x2048 7.3 against 11.4), or half that with M > 16. Longer K
@@ -2006,7 +2009,6 @@ bool small_grid_tile(int64_t M, int64_t N, int KB, int cus, int& tm, int& tn) {
     return true;
   }
   tn = 32;
-  if (M > 64) return tiny_grid(t32, KB, cus);
   if (M > 48) return tiny_grid(t32, KB, cus) && KB <= 64;
   if (tiny_grid(t32, KB, cus) && t32 >= c && KB <= 32) return true;
   if (M > 8 && M <= 32 && KB >= 16 && KB <= 64 && t16 <= c && 4 * t16 >= 3 * c) {
