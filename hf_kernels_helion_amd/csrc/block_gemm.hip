@@ -50,10 +50,12 @@ struct GemmArgs {
   int tiles_m, tiles_n;
   int out_dtype;     // fp8b_dtype; ignored when writing split-K partials
   int vec_store;     // 1 if 4 consecutive outputs can be stored as one vector
-  // gemm_pipe128_kernel only: when rem_base >= 0, workgroup w computes
-  // quarter w % 4 of 256x256 tile rem_base + w / 4 of a rem_tiles_m x
-  // rem_tiles_n grid (the tiles a gemm_pipe256_kernel launch of rem_base
-  // workgroups left), instead of 128x128 tile w.
+  // gemm_pipe128_kernel and gemm_tiny_kernel only: when rem_base >= 0,
+  // workgroup w computes quarter w % 4 of tile rem_base + w / 4 of a
+  // rem_tiles_m x rem_tiles_n grid of tiles twice as large (the tiles a
+  // launch of rem_base workgroups on that grid left), instead of tile w:
+  // 128x128 quarters of gemm_pipe256_kernel's tiles, 64x64 quarters of
+  // gemm_pipe128_kernel's.
   int rem_base, rem_tiles_m, rem_tiles_n;
   // gemm_pipe256_kernel<false, true> only (the gate/up GEMM that writes
   // silu(gate) * up quantised): C is the e4m3fn output [M, N/2] (row stride
@@ -1611,8 +1613,16 @@ __global__ void __launch_bounds__(64 * NW) gemm_tiny_kernel(GemmArgs a) {
   // wave index as a scalar, so K ranges and loop conditions are uniform
   const int wid = NW == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int tm, tn;
-  tile_of_bid((int)blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
+  if (a.rem_base >= 0) {
+    // a quarter of one of the tiles of twice the size a launch left
+    tile_of_bid(a.rem_base + (int)blockIdx.x / 4, a.rem_tiles_m, a.rem_tiles_n, tm, tn);
+    tm = 2 * tm + (((int)blockIdx.x >> 1) & 1);
+    tn = 2 * tn + ((int)blockIdx.x & 1);
+  } else {
+    tile_of_bid((int)blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
+  }
   const int m0 = tm * TM, n0 = tn * TN;
+  if (m0 >= a.M || n0 >= a.N) return;  // a quarter past the matrix edge (whole workgroup)
   const int kb0 = (int)((int64_t)a.KB * wid / NW);
   const int kb1 = (int)((int64_t)a.KB * (wid + 1) / NW);
 
@@ -1894,7 +1904,8 @@ int device_cu_count() {
 //   FP8B_PIPE=0     no pipelined kernels (gemm_bs128_kernel instead);
 //   FP8B_TAIL128=0  no 128x128 quarters for a small last wave of 256x256 tiles;
 //   FP8B_TILE192=0  no 192x256 tiles;
-//   FP8B_TINY=0     no one-wave 32x32 tiles for small grids.
+//   FP8B_TINY=0     no small-grid kernel (32x32, 32x16, 64x64 tiles);
+//   FP8B_TAIL64=0   no 64x64 quarters for a small last wave of 128x128 tiles.
 bool env_flag_on(const char* name) {
   const char* e = getenv(name);
   return !(e && e[0] == '0');
@@ -1917,6 +1928,10 @@ bool use_tile192() {
 }
 bool use_tiny() {
   static const bool v = env_flag_on("FP8B_TINY");
+  return v;
+}
+bool use_tail64() {
+  static const bool v = env_flag_on("FP8B_TAIL64");
   return v;
 }
 
@@ -2172,6 +2187,40 @@ void launch_tiny(const GemmArgs& a, int tile_n, hipStream_t st) {
   else gemm_tiny_kernel<2, 2, 1, 2, PR><<<(unsigned)t, 64, 0, st>>>(a);
 }
 
+// Whether an unsplit grid of t 128x128 tiles runs its last partial wave as
+// 64x64 quarters on gemm_tiny_kernel: when the quarters fit one per CU.
+// Measured (64 tiles left after full waves): 2048x2560x4096 37.9 against
+// 45.3 us, 1536x3072x4096 37.0 against 45.4, 2048x2560x14336 109.0 against
+// 140.0; with 80 or 128 tiles left (two quarters per CU) no gain
+// (3584x1536x4096 45.3 against 45.5, 2000x2600x2048 27.8 against 27.0).
+bool tail64(int64_t t, int cus) {
+  const int64_t rest = t % cus;
+  return use_tiny() && use_tail64() && t >= cus && rest > 0 && 4 * rest <= cus;
+}
+
+// One grid of 128x128 tiles on gemm_pipe128_kernel. When an unsplit grid
+// leaves a last partial wave that tail64 accepts, that wave's tiles run as
+// 64x64 quarters on gemm_tiny_kernel (four waves per quarter, one quarter
+// per CU): 2048x2560x4096 has 320 tiles, one full wave and 64 left.
+template <int WM, int WN, bool PR>
+void launch_pipe128(const GemmArgs& a, int splits, hipStream_t st) {
+  const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
+  const int cus = device_cu_count();
+  if (splits > 1 || !tail64(tiles, cus)) {
+    gemm_pipe128_kernel<WM, WN, PR><<<dim3((unsigned)tiles, 1, splits), 512, 0, st>>>(a);
+    return;
+  }
+  const int64_t full = tiles / cus * cus, rest = tiles - full;
+  gemm_pipe128_kernel<WM, WN, PR><<<(unsigned)full, 512, 0, st>>>(a);
+  GemmArgs r = a;
+  r.rem_base = (int)full;
+  r.rem_tiles_m = a.tiles_m;
+  r.rem_tiles_n = a.tiles_n;
+  r.tiles_m = (a.M + 63) / 64;
+  r.tiles_n = (a.N + 63) / 64;
+  gemm_tiny_kernel<4, 4, 4, 2, PR><<<(unsigned)(4 * rest), 256, 0, st>>>(r);
+}
+
 template <int BM, int BN, int WM, int WN>
 void launch_cfg(const GemmArgs& a, int splits, hipStream_t st) {
   dim3 grid(a.tiles_m * a.tiles_n, 1, splits);
@@ -2302,9 +2351,8 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
       else if (fm == 2) gemm_decode_kernel<2, true><<<grid, 512, 0, st>>>(a);
       else gemm_decode_kernel<3, true><<<grid, 512, 0, st>>>(a);
     } else if (pipe_ok(a, p)) {
-      dim3 grid(a.tiles_m * a.tiles_n, 1, p.splits);
       if (p.cfg == CFG_256x256) launch_pipe256<true>(a, st);
-      else gemm_pipe128_kernel<64, 32, true><<<grid, 512, 0, st>>>(a);
+      else launch_pipe128<64, 32, true>(a, p.splits, st);
     } else {
       return run_generic();
     }
@@ -2347,10 +2395,9 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
       break;
     case CFG_128x128: {
       if (pipe_ok(a, p)) {
-        dim3 grid(a.tiles_m * a.tiles_n, 1, p.splits);
         // 32x64 wave tiles (two activation and four weight fragments per
         // K-block) measured 3-6% faster than 64x32 on 2048x2048x4096
-        gemm_pipe128_kernel<32, 64, false><<<grid, 512, 0, st>>>(a);
+        launch_pipe128<32, 64, false>(a, p.splits, st);
       } else {
         launch_cfg<128, 128, 64, 64>(a, p.splits, st);
       }

@@ -331,10 +331,10 @@ def test_gemm_partial_last_wave_on_128_tiles(M, N, K, block_n, dev):
     per-output arithmetic of every unsplit MFMA plan is the same (one MFMA per
     K-block, folded as acc + dot * (As * Bs) in K order), so the result must
     equal, bit for bit, the same rows computed by separate calls on row
-    slices of 1024 (the last one ending at row M) whose grids have no tail
-    and no split-K. Covers the MLP gate/up shape (1344 tiles), quarters past
-    the M or N edge (4224 = 16.5 tiles), a ragged last row of tiles, and
-    per-row weight scales."""
+    slices (the last one ending at row M) whose grids have no split-K and
+    no tail run on other kernels. Covers the MLP gate/up shape (1344
+    tiles), quarters past the M or N edge (4224 = 16.5 tiles), a ragged last
+    row of tiles, and per-row weight scales."""
     from hf_kernels_helion_amd import _native
     print(f"gemm 128x128 tail M={M} N={N} K={K} block_n={block_n}", flush=True)
     x = synthetic.activations(M, K, seed=M + N)
@@ -343,7 +343,10 @@ def test_gemm_partial_last_wave_on_128_tiles(M, N, K, block_n, dev):
     W, Bs = W.to(dev), Bs.to(dev)
     out = fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [block_n, 128], torch.bfloat16)
     lib = _native.load()
-    slices = [(r0, r0 + 1024) for r0 in range(0, M - 1024, 1024)] + [(M - 1024, M)]
+    # slices whose 128x128 grids end in whole waves or in a last wave too
+    # large for 64x64 quarters (4224 columns: 1280 rows, 330 tiles)
+    h = 1280 if N == 4224 else 1024
+    slices = [(r0, r0 + h) for r0 in range(0, M - h, h)] + [(M - h, M)]
     for r0, r1 in slices:
         assert lib.fp8b_gemm_workspace_size(r1 - r0, N, K, block_n, 128) == 0
         part = fp8.w8a8_block_fp8_matmul(q[r0:r1], W, s[r0:r1], Bs, [block_n, 128],
@@ -355,6 +358,49 @@ def test_gemm_partial_last_wave_on_128_tiles(M, N, K, block_n, dev):
     torch.testing.assert_close(out[rows.to(dev)].float().cpu(),
                                torch.from_numpy(orc).to(torch.bfloat16).float(),
                                rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("M,N,K,block_n", [(2048, 2560, 4096, 128), (1950, 2560, 2048, 128),
+                                           (1024, 5120, 1024, 128), (2048, 2560, 2048, 1)])
+def test_gemm_128_tiles_last_wave_as_64_quarters(M, N, K, block_n, dev):
+    """Grids of 128x128 tiles (one per CU per wave) that leave at most a
+    quarter of the CUs for a last wave run that wave's tiles as 64x64
+    quarters on the small-grid kernel (320 tiles: 256 + 64 as 256 quarters):
+    every element against torch's fp32 dequant-matmul, sampled rows against
+    the oracle; 1950 rows leaves quarters wholly past the M edge (skipped by
+    their workgroups); per-row weight scales too. Exact small-integer
+    operands give the exact product."""
+    from hf_kernels_helion_amd import _native
+    print(f"gemm 128x128 tiles, 64x64 last wave M={M} N={N} K={K} block_n={block_n}",
+          flush=True)
+    assert _native.load().fp8b_gemm_workspace_size(M, N, K, block_n, 128) == 0
+    x = synthetic.activations(M, K, seed=M + 3 * N, outlier_frac=0.01)
+    q, s = fp8.act_quant(x.to(dev), 128)
+    W, Bs = synthetic.weights(N, K, seed=N + 11, block_n=block_n)
+    W, Bs = W.to(dev), Bs.to(dev)
+    out = fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [block_n, 128], torch.bfloat16)
+    full = (q.float() * s.repeat_interleave(128, 1)) @ (
+        W.float() * Bs.repeat_interleave(block_n, 0)[:N].repeat_interleave(128, 1)[:, :K]).T
+    torch.testing.assert_close(out.float(), full.to(torch.bfloat16).float(), rtol=RTOL,
+                               atol=ATOL)
+    rows = torch.tensor([0, 1023, M // 2, M - 1])
+    orc = oracle.block_gemm(_u8(q.cpu()[rows]), _u8(W.cpu()), s.cpu()[rows].numpy(),
+                            Bs.cpu().numpy(), (block_n, 128))
+    torch.testing.assert_close(out[rows.to(dev)].float().cpu(),
+                               torch.from_numpy(orc).to(torch.bfloat16).float(),
+                               rtol=RTOL, atol=ATOL)
+    g = torch.Generator().manual_seed(M + N)
+    Ai = torch.randint(-3, 4, (M, K), generator=g).float().to(torch.float8_e4m3fn)
+    Bi = torch.randint(-3, 4, (N, K), generator=g).float().to(torch.float8_e4m3fn)
+    Asi = torch.exp2(torch.randint(-2, 3, (M, K // 128), generator=g).float())
+    Bsi = torch.exp2(torch.randint(-2, 3, ((N + block_n - 1) // block_n, K // 128),
+                                   generator=g).float())
+    outi = fp8.w8a8_block_fp8_matmul(Ai.to(dev), Bi.to(dev), Asi.to(dev), Bsi.to(dev),
+                                     [block_n, 128])
+    exact = (Ai.double() * Asi.double().repeat_interleave(128, 1)) @ (
+        Bi.double() * Bsi.double().repeat_interleave(block_n, 0)[:N].repeat_interleave(
+            128, 1)).T
+    assert torch.equal(outi.cpu().double(), exact)
 
 
 @pytest.mark.parametrize("M,N,K", [(3001, 4096, 14336), (1500, 8192, 4096), (3001, 8192, 1024),
