@@ -618,10 +618,9 @@ def _random_shapes(n, seed):
 @pytest.mark.parametrize("M,N,K,block_n,dtype", _random_shapes(48, 2024))
 def test_gemm_random_shapes(M, N, K, block_n, dtype, dev):
     """A seeded sweep over shapes (M 1-699, N 1-1999, K 128-4096), weight
-    block sizes 128 and 1 (per-row) and output dtypes: every plan the tile
-    selector can pick (skinny, split-K decode, 32/64x128, 128x128 with and
-    without split-K, partial waves) against torch's fp32 dequant-matmul of
-    the same operands, within the north-star tolerance."""
+    block sizes 128 and 1 (per-row) and output dtypes: the small-grid,
+    skinny, split-K decode, 64x128 and 128x128 plans against torch's fp32
+    dequant-matmul of the same operands, within the north-star tolerance."""
     print(f"gemm random M={M} N={N} K={K} block_n={block_n} {dtype}", flush=True)
     x = synthetic.activations(M, K, seed=M * 31 + N)
     q, s = fp8.act_quant(x.to(dev), 128)
@@ -633,3 +632,35 @@ def test_gemm_random_shapes(M, N, K, block_n, dtype, dev):
     sbf = (Bs if block_n == 1 else Bs.repeat_interleave(128, 0)[:N]).repeat_interleave(128, 1)
     full = (q.float() * saf) @ (W.float() * sbf[:, :K]).T
     torch.testing.assert_close(out.float(), full.to(dtype).float(), rtol=RTOL, atol=ATOL)
+
+
+def _random_shapes_large(n, seed):
+    g = torch.Generator().manual_seed(seed)
+    shapes = []
+    for _ in range(n):
+        M = int(torch.randint(1, 4097, (1,), generator=g))
+        N = int(torch.randint(1, 6145, (1,), generator=g))
+        KB = int(torch.randint(1, 65, (1,), generator=g))
+        block_n = 1 if int(torch.randint(0, 4, (1,), generator=g)) == 0 else 128
+        shapes.append((M, N, 128 * KB, block_n))
+    return shapes
+
+
+@pytest.mark.parametrize("M,N,K,block_n", _random_shapes_large(24, 2025))
+def test_gemm_random_shapes_large(M, N, K, block_n, dev):
+    """A seeded sweep over larger shapes (M up to 4096, N up to 6144, K up
+    to 8192): the small-grid tilings (32x16, 32x32, 64x64), 128x128 grids
+    with split-K or with their last wave as 64x64 quarters, 192- and
+    256-row tiles and their quarters, against torch's fp32 dequant-matmul of
+    the same operands, within the north-star tolerance."""
+    print(f"gemm random large M={M} N={N} K={K} block_n={block_n}", flush=True)
+    x = synthetic.activations(M, K, seed=M * 7 + N)
+    q, s = fp8.act_quant(x.to(dev), 128)
+    W, Bs = synthetic.weights(N, K, seed=N * 13 + K, block_n=block_n)
+    W, Bs = W.to(dev), Bs.to(dev)
+    out = fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [block_n, 128], torch.bfloat16)
+    saf = s.repeat_interleave(128, 1)[:, :K]
+    sbf = (Bs if block_n == 1 else Bs.repeat_interleave(128, 0)[:N]).repeat_interleave(128, 1)
+    full = (q.float() * saf) @ (W.float() * sbf[:, :K]).T
+    torch.testing.assert_close(out.float(), full.to(torch.bfloat16).float(), rtol=RTOL,
+                               atol=ATOL)
