@@ -484,6 +484,16 @@ weight_quant_vec_kernel(const T* __restrict__ W, int64_t ldw, uint8_t* __restric
   const bool block_inf = m == 0x7F800000u;
   const float scale = block_nan ? __uint_as_float(0x7FC00000u)
                                 : fmaxf(__uint_as_float(m), kAmaxFloor) / kFp8Max;
+  // bf16 weights: the quotients without division instructions, as the
+  // act-quant kernels form them (div_by_scale with recip_of_scale; exact
+  // for bf16 values and scales of bf16 magnitudes, checked exhaustively in
+  // tests/fastdiv_check.c and tests/scale_recip_check.c); fp32 weights keep
+  // the IEEE division.
+  const float recip = recip_of_scale(scale);
+  auto quot = [&](float x) {
+    if constexpr (VPL == 8) return div_by_scale(x, scale, recip);
+    else return x / scale;
+  };
 #pragma unroll
   for (int i = 0; i < NL; ++i) {
     uint32_t b[VPL / 4];
@@ -495,10 +505,10 @@ weight_quant_vec_kernel(const T* __restrict__ W, int64_t ldw, uint8_t* __restric
         b[c] = inf_block_code(v[i][4 * c]) | (inf_block_code(v[i][4 * c + 1]) << 8) |
                (inf_block_code(v[i][4 * c + 2]) << 16) | (inf_block_code(v[i][4 * c + 3]) << 24);
       } else {
-        int p = __builtin_amdgcn_cvt_pk_fp8_f32(v[i][4 * c] / scale, v[i][4 * c + 1] / scale,
-                                                0, false);
-        p = __builtin_amdgcn_cvt_pk_fp8_f32(v[i][4 * c + 2] / scale, v[i][4 * c + 3] / scale,
-                                            p, true);
+        int p = __builtin_amdgcn_cvt_pk_fp8_f32(quot(v[i][4 * c]), quot(v[i][4 * c + 1]), 0,
+                                                false);
+        p = __builtin_amdgcn_cvt_pk_fp8_f32(quot(v[i][4 * c + 2]), quot(v[i][4 * c + 3]), p,
+                                            true);
         b[c] = (uint32_t)p;
       }
     }
