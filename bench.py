@@ -49,7 +49,8 @@ def parse():
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--only", default=None,
                    help="profile helper: run only one workload "
-                        "(gemm|act_quant|decode|decode_fused|weight_quant|mlp|mlp_il|mlp_gateup|"
+                        "(gemm|act_quant|decode|decode_fused|weight_quant|weight_quant_bf16|mlp|"
+                        "mlp_il|mlp_gateup|"
                         "mlp_down|medium|small|deep_gemm|deep_decode|copy)"
                         " for --steps steps and exit without JSON")
     return p.parse_args()
@@ -530,12 +531,18 @@ def run_only(what, steps, warmup, torch, fp8, synthetic, dev):
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
         fn = lambda: dst.copy_(src)
-    elif what == "weight_quant":
-        wsrc = [torch.randn(4096, 14336, device=dev) * 0.02 for _ in range(2)]
+    elif what in ("weight_quant", "weight_quant_bf16"):
+        # as the bench legs: two fp32 or four bf16 inputs (470 MB) rotate past
+        # the MALL
+        if what == "weight_quant":
+            wsrc = [torch.randn(4096, 14336, device=dev) * 0.02 for _ in range(2)]
+        else:
+            wsrc = [(torch.randn(4096, 14336, device=dev) * 0.02).to(torch.bfloat16)
+                    for _ in range(4)]
         it = [0]
 
         def fn():
-            i = it[0] = (it[0] + 1) % 2
+            i = it[0] = (it[0] + 1) % len(wsrc)
             return fp8.quantize_weight(wsrc[i])
     elif what == "act_quant":
         # four input sets (384 MB with outputs) rotate past the MALL, as in
