@@ -1644,7 +1644,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_tiny_kernel(GemmArgs a) {
 #pragma unroll
   for (int d = 0; d < SDMA; ++d) {
     const int e = d * 64 + lane;
-    const int64_t b_row = PR ? min(n0 + e - TM, a.N - 1) : (min(n0, a.N - 1) >> 7);
+    const int64_t b_row = PR ? min(max(n0 + e - TM, 0), a.N - 1) : (min(n0, a.N - 1) >> 7);
     ssrc[d] = e < TM ? a.As + (int64_t)min(m0 + e, a.M - 1) * a.as_sm : a.Bs + b_row * a.bs_sn;
     sstep[d] = e < TM ? a.as_sk : a.bs_sk;
   }
