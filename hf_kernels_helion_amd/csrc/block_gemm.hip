@@ -1306,7 +1306,7 @@ __device__ __forceinline__ void wait_vmcnt_rt(int n) {
 }
 
 // ---------------------------------------------------------------------------
-// Decode GEMM (M <= 16*FM <= 48): bound by the weight stream from HBM. A
+// Decode GEMM (M <= 16*FM <= 64): bound by the weight stream from HBM. A
 // 512-thread workgroup owns 128 weight rows (output columns n0..n0+127) and a
 // K-range of kb_per_split K-blocks; grid.z splits K so that the grid covers
 // the CUs (partials go to the workspace and splitk_reduce_kernel sums them
@@ -1318,7 +1318,7 @@ __device__ __forceinline__ void wait_vmcnt_rt(int n) {
 // scales arrive per window of 8 K-blocks by 4-byte DMA (any strides; the
 // activation scales slot-major, 32 rows per slot).
 // Preconditions (checked by the host, decode_offsets_ok): the 32-bit DMA
-// offsets row * ldb + 127 (row <= 127) and row * lda + 127 (row <= 47) fit.
+// offsets row * ldb + 127 (row <= 127) and row * lda + 127 (row < 16*FM) fit.
 // ---------------------------------------------------------------------------
 template <int FM, bool PR = false, int NSX = 0> struct DecodeCfg {
   static constexpr int NW = 8, BN = 128, AR = 16 * FM;
@@ -1867,10 +1867,9 @@ enum TileCfg {
   CFG_256x256 = 0,
   CFG_192x256 = 1,
   CFG_128x128 = 2,
-  CFG_64x128 = 3,
-  CFG_SKINNY = 4,
-  CFG_DECODE = 5,
-  CFG_TINY = 6,
+  CFG_SKINNY = 3,
+  CFG_DECODE = 4,
+  CFG_TINY = 5,
   CFG_COUNT
 };
 
@@ -2034,7 +2033,7 @@ bool small_grid_tile(int64_t M, int64_t N, int KB, int cus, int& tm, int& tn) {
 }
 
 // per_row: weight scales per output row (block_n = 1, the deep-gemm layout);
-// only the decode kernel (M <= 48), gemm_tiny_kernel, gemm_pipe128_kernel
+// only the decode kernel (M <= 48 for them), gemm_tiny_kernel, gemm_pipe128_kernel
 // and gemm_pipe256_kernel implement it.
 Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
   const int KB = (int)(K / 128);
@@ -2055,7 +2054,15 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
     p.kb_per_split = KB;
     return p;
   }
-  if (M <= 48 && use_decode_kernel()) {
+  // 49..64 rows beyond the small-grid rules (weights streamed from HBM):
+  // the decode kernel with 64 activation rows for few or many 128-column
+  // tiles, else 128x128 tiles (half of each tile's rows idle) instead of the
+  // 64x128 tiles of the non-pipelined kernel: 64x4096x14336 19.3 us decode
+  // (21.7 on 128x128 tiles, 23.5 on 64x128), 64x57344x2048 26.4 (33.7,
+  // 28.2), 56x14336x14336 57.3 (51.7, 66.4), 64x28672x4096 33.5 (33.4, 44.1).
+  const int64_t t128n = (N + 127) / 128;
+  const bool decode64 = !per_row && M <= 64 && (t128n <= 32 || t128n >= cus);
+  if (use_decode_kernel() && (M <= 48 || decode64)) {
     // Decode path: 128 output columns per workgroup; split K until the grid
     // covers the CUs.
     p.cfg = CFG_DECODE; p.bm = (int)(((M + 15) / 16) * 16); p.bn = 128;
@@ -2070,17 +2077,15 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
     // 8.2 us skinny; 1..8x4096x14336: 14.7-15.0 against 13.2-13.6; but
     // 32x4096x14336: 16.1 against 21.5, 16x4096x14336 even, and 8x14336x4096
     // with 3 splits 16.7 against 20.6).
-    if (!per_row && (p.kb_per_split <= 4 || (M <= 8 && p.splits >= 8))) {
+    if (!per_row && M <= 48 && (p.kb_per_split <= 4 || (M <= 8 && p.splits >= 8))) {
       p.cfg = CFG_SKINNY; p.bn = 16;
       p.splits = 1;
       p.kb_per_split = KB;
     }
     return p;
   }
-  if (per_row && M <= 64) {
+  if (M <= 64) {
     p.cfg = CFG_128x128; p.bm = 128; p.bn = 128;
-  } else if (M <= 64) {
-    p.cfg = CFG_64x128; p.bm = 64; p.bn = 128;
   } else if (tiles(256, 256) >= cus || prefer_256(tiles(256, 256), tiles(128, 128), cus)) {
     p.cfg = CFG_256x256; p.bm = 256; p.bn = 256;
     if (!per_row && prefer_192(tiles(256, 256), tiles(192, 256), cus,
@@ -2091,21 +2096,17 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
     p.cfg = CFG_128x128; p.bm = 128; p.bn = 128;
   }
   const int64_t t = tiles(p.bm, p.bn);
-  // Grids with fewer tiles than CUs split K, keeping at least four K-blocks
-  // per split: 128x128 grids while the split grid still fits one wave of
-  // workgroups (one per CU, by its LDS; a second wave costs more than the
-  // idle CUs: 1536x1536x4096 40.2 us split in two, 24.2 unsplit), 64x128
-  // grids (four waves, three workgroups per CU) until there are about two
-  // workgroups per CU. Grids that already cover the CUs are not split: the
-  // fp32 partials would cost more HBM traffic than the extra occupancy
-  // recovers.
+  // Grids of 128x128 tiles with fewer tiles than CUs split K, keeping at
+  // least four K-blocks per split, while the split grid still fits one wave
+  // of workgroups (one per CU, by its LDS; a second wave costs more than the
+  // idle CUs: 1536x1536x4096 40.2 us split in two, 24.2 unsplit). Grids that
+  // already cover the CUs are not split: the fp32 partials would cost more
+  // HBM traffic than the extra occupancy recovers. (A partial wave of
+  // 256x256 tiles chosen by prefer_256 is not split either: the fp32
+  // partials of a long-K grid cost more than the idle CUs.)
   int splits = 1;
-  // (a partial wave of 256x256 tiles chosen by prefer_256 is not split: the
-  // fp32 partials of a long-K grid cost more than the idle CUs)
   if (t < cus && p.cfg == CFG_128x128)
     while (t * splits * 2 <= cus && KB / (splits * 2) >= 4) splits *= 2;
-  else if (t < cus && p.cfg != CFG_256x256)
-    while (t * splits < 2 * cus && KB / (splits * 2) >= 4) splits *= 2;
   p.kb_per_split = (KB + splits - 1) / splits;
   // Split sizes in whole scale half-windows (multiples of 4 K-blocks) keep
   // the pipelined kernels usable.
@@ -2116,9 +2117,10 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
 }
 
 // 32-bit DMA offsets of gemm_decode_kernel: weight rows up to 127 of a tile
-// (row * ldb + 127) and activation rows up to 47 (row * lda + 127).
-bool decode_offsets_ok(int64_t lda, int64_t ldb) {
-  return 127 * ldb + 128 <= (int64_t(1) << 32) && 47 * lda + 128 <= (int64_t(1) << 32);
+// (row * ldb + 127) and activation rows up to 16*FM - 1 (row * lda + 127).
+bool decode_offsets_ok(int64_t lda, int64_t ldb, int64_t M) {
+  const int64_t rows = (M + 15) / 16 * 16;
+  return 127 * ldb + 128 <= (int64_t(1) << 32) && (rows - 1) * lda + 128 <= (int64_t(1) << 32);
 }
 
 bool mfma_path_ok(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N,
@@ -2324,10 +2326,10 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
 
   // Leading dimensions too large for the decode kernel's 32-bit DMA offsets:
   // the skinny kernel (64-bit addresses, no workspace) or, for per-row
-  // scales, the generic kernel.
+  // scales and more than 48 rows, the generic kernel.
   Plan p = p0;
-  if (p.cfg == CFG_DECODE && !decode_offsets_ok(lda, ldb)) {
-    if (per_row) return run_generic();
+  if (p.cfg == CFG_DECODE && !decode_offsets_ok(lda, ldb, M)) {
+    if (per_row || M > 48) return run_generic();
     p.cfg = CFG_SKINNY; p.bn = 16; p.splits = 1; p.kb_per_split = (int)(K / 128);
   }
   GemmArgs a = make_args(p);
@@ -2371,11 +2373,13 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
       if ((int64_t)grid.x * grid.z > device_cu_count()) {
         if (fm <= 1) gemm_decode_kernel<1, false, 3><<<grid, 512, 0, st>>>(a);
         else if (fm == 2) gemm_decode_kernel<2, false, 3><<<grid, 512, 0, st>>>(a);
-        else gemm_decode_kernel<3, false, 3><<<grid, 512, 0, st>>>(a);
+        else if (fm == 3) gemm_decode_kernel<3, false, 3><<<grid, 512, 0, st>>>(a);
+        else gemm_decode_kernel<4, false, 3><<<grid, 512, 0, st>>>(a);
       } else {
         if (fm <= 1) gemm_decode_kernel<1, false><<<grid, 512, 0, st>>>(a);
         else if (fm == 2) gemm_decode_kernel<2, false><<<grid, 512, 0, st>>>(a);
-        else gemm_decode_kernel<3, false><<<grid, 512, 0, st>>>(a);
+        else if (fm == 3) gemm_decode_kernel<3, false><<<grid, 512, 0, st>>>(a);
+        else gemm_decode_kernel<4, false><<<grid, 512, 0, st>>>(a);
       }
       break;
     }
@@ -2403,7 +2407,9 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
       }
       break;
     }
-    default: launch_cfg<64, 128, 32, 64>(a, p.splits, st); break;
+    default:
+      set_error("fp8b_w8a8_block_matmul: no kernel for this plan");
+      return FP8B_ERR_LAUNCH;
   }
   if (hipGetLastError() != hipSuccess) {
     set_error("fp8b_w8a8_block_matmul: MFMA kernel launch failed");

@@ -135,6 +135,9 @@ def test_plans_split_k_only_within_one_wave():
     assert ws(1024, 2048, 4096) == 0 and ws(960, 1024, 4096) == 0   # 64x64 tiles
     assert ws(32, 2048, 14336) == 16 * 32 * 2048 * 4      # decode: 16 column tiles x 16
     assert ws(32, 4096, 14336) == 8 * 32 * 4096 * 4       # decode: 32 column tiles x 8
+    assert ws(64, 4096, 14336) == 8 * 64 * 4096 * 4       # decode with 64 rows
+    assert ws(56, 14336, 14336) == 2 * 56 * 14336 * 4     # 112 tiles of 128x128, two ways
+    assert ws(64, 28672, 4096) == 0                       # 224 tiles of 128x128
     assert ws(4096, 4096, 8192) == 0
 
 

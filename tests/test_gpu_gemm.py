@@ -360,6 +360,41 @@ def test_gemm_partial_last_wave_on_128_tiles(M, N, K, block_n, dev):
                                rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("M,N,K", [(64, 4096, 14336), (64, 57344, 2048), (56, 14336, 14336),
+                                   (64, 28672, 4096), (50, 2048, 14336)])
+def test_gemm_49_to_64_rows_past_small_grids(M, N, K, dev):
+    """49..64 rows beyond the small-grid rules: the decode kernel with 64
+    activation rows (few or many 128-column tiles: split-K over the CUs, or
+    448 workgroups two per CU) or 128x128 tiles with half their rows idle
+    (split-K 2 ways, or one partial wave). Every element against torch's
+    fp32 dequant-matmul, sampled rows against the oracle; unit-scale small
+    integers give the exact product."""
+    print(f"gemm 49..64 rows M={M} N={N} K={K}", flush=True)
+    x = synthetic.activations(M, K, seed=M + N, outlier_frac=0.01)
+    q, s = fp8.act_quant(x.to(dev), 128)
+    W, Bs = synthetic.weights(N, K, seed=N + 5)
+    W, Bs = W.to(dev), Bs.to(dev)
+    out = fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [128, 128], torch.bfloat16)
+    full = (q.float() * s.repeat_interleave(128, 1)) @ (
+        W.float() * Bs.repeat_interleave(128, 0)[:N].repeat_interleave(128, 1)[:, :K]).T
+    torch.testing.assert_close(out.float(), full.to(torch.bfloat16).float(), rtol=RTOL,
+                               atol=ATOL)
+    rows = torch.tensor([0, M // 2, M - 1])
+    orc = oracle.block_gemm(_u8(q.cpu()[rows]), _u8(W.cpu()), s.cpu()[rows].numpy(),
+                            Bs.cpu().numpy())
+    torch.testing.assert_close(out[rows.to(dev)].float().cpu(),
+                               torch.from_numpy(orc).to(torch.bfloat16).float(),
+                               rtol=RTOL, atol=ATOL)
+    g = torch.Generator().manual_seed(M * N)
+    Ai = torch.randint(-3, 4, (M, K), generator=g).float().to(torch.float8_e4m3fn)
+    Bi = torch.randint(-3, 4, (N, K), generator=g).float().to(torch.float8_e4m3fn)
+    outi = fp8.w8a8_block_fp8_matmul(Ai.to(dev), Bi.to(dev),
+                                     torch.ones(M, K // 128, device=dev),
+                                     torch.ones((N + 127) // 128, K // 128, device=dev),
+                                     [128, 128])
+    assert torch.equal(outi.cpu().double(), Ai.double() @ Bi.double().T)
+
+
 @pytest.mark.parametrize("M,N,K,block_n", [(2048, 2560, 4096, 128), (1950, 2560, 2048, 128),
                                            (1024, 5120, 1024, 128), (2048, 2560, 2048, 1)])
 def test_gemm_128_tiles_last_wave_as_64_quarters(M, N, K, block_n, dev):
