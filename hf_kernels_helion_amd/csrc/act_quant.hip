@@ -70,6 +70,34 @@ act_quant_g128_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   }
 }
 
+// Rows of fewer than 16 groups (K below 2048): the 16-lane rows of a block
+// take consecutive (row, group) pairs of the flattened [M x groups_per_row]
+// index space, so none idles (the row-mapped kernel leaves 16 - groups of
+// its 16). Same arithmetic per group.
+__global__ void __launch_bounds__(256)
+act_quant_g128_flat_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                           uint8_t* __restrict__ q, int64_t ldq,
+                           float* __restrict__ s, int64_t ssm, int64_t ssg,
+                           uint32_t slots, uint32_t groups_per_row) {
+  const uint32_t sub = threadIdx.x & 15u;
+  const uint32_t slot = blockIdx.x * 16u + (threadIdx.x >> 4);
+  if (slot >= slots) return;  // uniform across the 16-lane row
+  const uint32_t m = slot / groups_per_row, g = slot - m * groups_per_row;
+  const v4i raw = __builtin_nontemporal_load(
+      reinterpret_cast<const v4i*>(x + (int64_t)m * ldx + g * 128u + sub * 8u));
+  float v[8];
+  const uint32_t mag = unpack_bf16x8(raw, v);
+  uint32_t w0, w1;
+  float scale;
+  quant_row16_8(v, mag, w0, w1, scale);
+  v2i packed;
+  packed[0] = (int)w0;
+  packed[1] = (int)w1;
+  __builtin_nontemporal_store(packed,
+                              reinterpret_cast<v2i*>(q + (int64_t)m * ldq + g * 128u + sub * 8u));
+  if (sub == 0) s[(int64_t)m * ssm + (int64_t)g * ssg] = scale;
+}
+
 // Groups per block column of the fast kernels: 16*U with U in {4, 2, 1},
 // the largest that divides the groups of a row (no idle lanes at the row's
 // end), and 1 when there are few groups in all (decode: spread them over
@@ -189,6 +217,33 @@ silu_mul_quant_g128_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   }
 }
 
+// silu_mul_quant_g128_kernel for rows of fewer than 16 groups (d below
+// 2048), mapped as act_quant_g128_flat_kernel is.
+__global__ void __launch_bounds__(256)
+silu_mul_quant_g128_flat_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                uint8_t* __restrict__ q, int64_t ldq,
+                                float* __restrict__ s, int64_t ssm, int64_t ssg,
+                                uint32_t slots, uint32_t groups_per_row, int64_t d) {
+  const uint32_t sub = threadIdx.x & 15u;
+  const uint32_t slot = blockIdx.x * 16u + (threadIdx.x >> 4);
+  if (slot >= slots) return;  // uniform across the 16-lane row
+  const uint32_t m = slot / groups_per_row, g = slot - m * groups_per_row;
+  const uint16_t* xg = x + (int64_t)m * ldx + g * 128u + sub * 8u;
+  const v4i gr = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(xg));
+  const v4i ur = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(xg + d));
+  float v[8];
+  const v4i h = silu_mul_bf16x8(gr, ur, v);
+  uint32_t w0, w1;
+  float scale;
+  quant_row16_8(v, max_mag_bf16x8(h), w0, w1, scale);
+  v2i packed;
+  packed[0] = (int)w0;
+  packed[1] = (int)w1;
+  __builtin_nontemporal_store(packed,
+                              reinterpret_cast<v2i*>(q + (int64_t)m * ldq + g * 128u + sub * 8u));
+  if (sub == 0) s[(int64_t)m * ssm + (int64_t)g * ssg] = scale;
+}
+
 __global__ void __launch_bounds__(64)
 silu_mul_quant_generic_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                               uint8_t* __restrict__ q, int64_t ldq,
@@ -250,7 +305,12 @@ extern "C" int fp8b_act_quant(const void* x, int64_t ldx, void* q, int64_t ldq,
   const bool fast = group == 128 && K % 128 == 0 && ldx % 8 == 0 && ldq % 8 == 0 &&
                     aligned(x, 16) && aligned(q, 8) && M * gpr < (int64_t(1) << 31) &&
                     K < (int64_t(1) << 32);
-  if (fast) {
+  if (fast && gpr < 16) {
+    const int64_t slots = M * gpr;
+    act_quant_g128_flat_kernel<<<(unsigned)((slots + 15) / 16), 256, 0, st>>>(
+        (const uint16_t*)x, ldx, (uint8_t*)q, ldq, s, s_stride_m, s_stride_g, (uint32_t)slots,
+        (uint32_t)gpr);
+  } else if (fast) {
     const int U = g128_unroll(M, gpr);
     const dim3 grid((unsigned)((gpr + 16 * U - 1) / (16 * U)), (unsigned)std::min<int64_t>(M, 65535));
     auto launch = [&](auto kernel) {
@@ -316,7 +376,12 @@ extern "C" int fp8b_silu_and_mul_quant(const void* x, int64_t ldx, void* q, int6
   const bool fast = group == 128 && d % 128 == 0 && ldx % 8 == 0 && ldq % 8 == 0 &&
                     aligned(x, 16) && aligned(q, 8) && M * gpr < (int64_t(1) << 31) &&
                     d < (int64_t(1) << 31);
-  if (fast) {
+  if (fast && gpr < 16) {
+    const int64_t slots = M * gpr;
+    silu_mul_quant_g128_flat_kernel<<<(unsigned)((slots + 15) / 16), 256, 0, st>>>(
+        (const uint16_t*)x, ldx, (uint8_t*)q, ldq, s, s_stride_m, s_stride_g, (uint32_t)slots,
+        (uint32_t)gpr, d);
+  } else if (fast) {
     const int U = g128_unroll(M, gpr);
     const dim3 grid((unsigned)((gpr + 16 * U - 1) / (16 * U)), (unsigned)std::min<int64_t>(M, 65535));
     auto launch = [&](auto kernel) {

@@ -42,13 +42,16 @@ def test_silu_and_mul_3d(dev):
 
 @pytest.mark.parametrize("M,d,group", [(3001, 14336, 128), (5, 384, 128), (9, 200, 64),
                                        (4, 256, 256), (70000, 256, 128), (512, 4096, 128),
-                                       (256, 8192, 128), (1000, 8192, 128)])
+                                       (256, 8192, 128), (1000, 8192, 128), (4097, 1920, 128),
+                                       (28672, 128, 128)])
 def test_silu_and_mul_quant_equals_two_ops(M, d, group, dev):
     """Fused kernel == silu_and_mul then act_quant, bit for bit, and its codes
     and scales are oracle.act_quant of the GPU's bf16 silu_and_mul output.
     d = 14336 runs silu_mul_quant_g128_kernel<1>, d = 4096 with 512 rows <2>,
     d = 8192 with 256 or more rows <4> (16*U groups per block column, U the
-    largest of 4, 2, 1 dividing the row's groups, 1 below 16384 groups)."""
+    largest of 4, 2, 1 dividing the row's groups, 1 below 16384 groups);
+    rows of fewer than 16 groups (d = 384, 256, 1920, 128) the flat-mapped
+    kernel."""
     print(f"silu_and_mul_quant M={M} d={d} group={group}", flush=True)
     x = (synthetic.activations(M, 2 * d, seed=M + d) * 2).to(dev)
     q, s = fp8.silu_and_mul_quant(x, group)
@@ -93,7 +96,7 @@ def test_fp8_mlp_chain_ragged(dev):
                                rtol=1e-2, atol=1e-3)
 
 
-def _gate_up_chain(xq, xs, w13, s13, M):
+def _gate_up_chain(xq, xs, w13, s13, M, pad=True):
     """h = bf16 GEMM, then silu_and_mul_quant: the two-kernel reference of
     gate_up_silu_quant. M below 4096 is padded to 16384 rows (zero
     activations) so that the GEMM grid covers the CUs and runs an unsplit
@@ -102,7 +105,7 @@ def _gate_up_chain(xq, xs, w13, s13, M):
     fused kernel shares; rows are independent, so the first M rows are the
     ones of the unpadded problem."""
     from hf_kernels_helion_amd import _native
-    if M < 4096:
+    if pad and M < 4096:
         pad = 16384 - M
         xq = torch.cat([xq, torch.zeros(pad, xq.shape[1], dtype=xq.dtype, device=xq.device)])
         xs = torch.cat([xs, torch.full((pad, xs.shape[1]), 1.0, device=xs.device)])
@@ -114,7 +117,8 @@ def _gate_up_chain(xq, xs, w13, s13, M):
 
 
 @pytest.mark.parametrize("M,I,H", [(1, 128, 512), (5, 256, 1024), (200, 384, 512),
-                                   (257, 512, 512), (3001, 1024, 512), (3001, 14336, 4096)])
+                                   (257, 512, 512), (600, 384, 512), (513, 512, 1024),
+                                   (3001, 1024, 512), (3001, 14336, 4096)])
 def test_gate_up_silu_quant_equals_chain(M, I, H, dev):
     """GEMM + SiLU·up + act-quant in one kernel == bf16 GEMM then
     silu_and_mul_quant, fp8 codes and scales bit for bit; the bf16 GEMM is
@@ -128,6 +132,10 @@ def test_gate_up_silu_quant_equals_chain(M, I, H, dev):
     wi, si = fp8.interleave_gate_up(w13d, s13d)
     q, s = fp8.gate_up_silu_quant(xq, xs, wi, si)
     assert q.shape == (M, I) and s.shape == (M, I // 128)
+    if M < fp8.mlp.FUSED_GATE_UP_MIN_ROWS:
+        # the chain itself on the interleaved weights: the same GEMM plan
+        # for M rows, columns permuted
+        q_ref, s_ref, _ = _gate_up_chain(xq, xs, w13d, s13d, M, pad=False)
     assert torch.equal(q.view(torch.uint8), q_ref.view(torch.uint8))
     assert torch.equal(s.view(torch.int32), s_ref.view(torch.int32))
     rows = torch.arange(0, M, max(1, M // 16))
@@ -141,9 +149,10 @@ def test_gate_up_silu_quant_equals_chain(M, I, H, dev):
 
 def test_gate_up_silu_quant_strided_outputs_and_repeat(dev):
     """A second call on the same buffers gives the same bits (no state kept
-    between calls), and a row-strided A/As view is read correctly."""
+    between calls), and a row-strided A/As view is read correctly by the
+    fused kernel (600 rows)."""
     print("gate_up_silu_quant strided", flush=True)
-    M, I, H = 300, 256, 512
+    M, I, H = 600, 256, 512
     x = synthetic.activations(M, 2 * H, seed=3)
     xq_full, xs_full = fp8.act_quant(x.to(dev), 128)
     xq, xs = xq_full[:, :H], xs_full[:, : H // 128]           # row strides 2H, 2H/128
@@ -171,12 +180,13 @@ def test_fp8_mlp_interleaved_equals_default(dev):
     assert torch.equal(y, y2)
 
 
-@pytest.mark.parametrize("interleaved", [False, True])
-def test_fp8_mlp_graph_replays(interleaved, dev):
+@pytest.mark.parametrize("interleaved,M", [(False, 300), (True, 300), (True, 600)])
+def test_fp8_mlp_graph_replays(interleaved, M, dev):
     """The MLP chain captured in a HIP graph (a serving loop's form): every
-    replay, with eager work in between, equals the eager result."""
-    print(f"fp8 mlp graph interleaved={interleaved}", flush=True)
-    M, H, I = 300, 512, 1024
+    replay, with eager work in between, equals the eager result (interleaved
+    at 300 rows: the two-op route; at 600: the fused kernel)."""
+    print(f"fp8 mlp graph interleaved={interleaved} M={M}", flush=True)
+    H, I = 512, 1024
     x = synthetic.activations(M, H, seed=51).to(dev)
     w13, s13 = synthetic.weights(2 * I, H, seed=52)
     w2, s2 = synthetic.weights(H, I, seed=53)
@@ -231,9 +241,10 @@ def test_silu_fast_path_same_bits(dev):
 
 def test_gate_up_silu_quant_nonfinite_rows(dev):
     """Rows whose activation scale makes h overflow to +-inf (and a NaN
-    scale): the epilogue's non-finite groups equal the chain's, bit for bit."""
+    scale): the fused epilogue's non-finite groups equal the chain's, bit
+    for bit (600 rows: the fused kernel)."""
     print("gate_up_silu_quant non-finite", flush=True)
-    M, I, H = 300, 256, 512
+    M, I, H = 600, 256, 512
     x = synthetic.activations(M, H, seed=61)
     w13, s13 = synthetic.weights(2 * I, H, seed=62)
     xq, xs = fp8.act_quant(x.to(dev), 128)
