@@ -72,7 +72,9 @@ def fp8_mlp(x: torch.Tensor, w_gate_up: torch.Tensor, s_gate_up: torch.Tensor,
     (bit-identical result, one more bf16 round trip through HBM).
     ``gate_up_interleaved=True``: (w_gate_up, s_gate_up) come from
     ``interleave_gate_up`` and the gate/up GEMM, SiLU·up and its quantisation
-    run as one kernel (same result)."""
+    run as one kernel from FUSED_GATE_UP_MIN_ROWS rows (the same bits as the
+    default chain whenever its gate/up GEMM runs unsplit; below that many
+    rows the default chain's ops on the interleaved layout, the same bits)."""
     bn, bk = int(block_size[0]), int(block_size[1])
     lead = x.shape[:-1]
     x2 = x.reshape(-1, x.shape[-1])
