@@ -188,7 +188,9 @@ __device__ __forceinline__ void epilogue16(const GemmArgs& a, uint8_t* wbase,
     if (m >= a.M || n >= a.N) continue;
     uint16_t* dst = C + (int64_t)m * a.ldc + n;
     if (n + 8 <= a.N && a.vec_store) {
-      *reinterpret_cast<v4i*>(dst) = v;
+      // streaming store: 0.5-1.4% on 4096x4096x8192 and 3001x28672x4096
+      // (steady and graph replay, eight alternating runs), no loss seen
+      __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(dst));
     } else {
       for (int e = 0; e < 8 && n + e < a.N; ++e)
         dst[e] = (uint16_t)(((uint32_t)v[e >> 1]) >> ((e & 1) * 16));
