@@ -699,3 +699,34 @@ def test_gemm_random_shapes_large(M, N, K, block_n, dev):
     full = (q.float() * saf) @ (W.float() * sbf[:, :K]).T
     torch.testing.assert_close(out.float(), full.to(torch.bfloat16).float(), rtol=RTOL,
                                atol=ATOL)
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 512, 2048), (1024, 2048, 14336), (2048, 2560, 4096),
+                                   (32, 4096, 14336), (4096, 4096, 1024), (64, 4096, 14336)])
+def test_gemm_graph_replays(M, N, K, dev):
+    """The GEMM captured in a HIP graph on each plan family (small-grid
+    tiles; split-K 128x128 with its sum; a 128x128 grid whose last wave runs
+    as 64x64 quarters; the split-K decode kernel; 256x256 tiles; the decode
+    kernel with 64 rows): every replay, with eager work in between, equals
+    the eager result."""
+    print(f"gemm graph M={M} N={N} K={K}", flush=True)
+    x = synthetic.activations(M, K, seed=M + N + K)
+    q, s = fp8.act_quant(x.to(dev), 128)
+    W, Bs = synthetic.weights(N, K, seed=N + 1)
+    W, Bs = W.to(dev), Bs.to(dev)
+    f = lambda: fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [128, 128], torch.bfloat16)
+    eager = f()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        f()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = f()
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        f()  # eager work between replays
+        torch.cuda.synchronize()
