@@ -57,6 +57,11 @@ def gate_up_silu_quant(xq: torch.Tensor, xs: torch.Tensor, w_il: torch.Tensor,
     m = xq.shape[0]
     if m >= FUSED_GATE_UP_MIN_ROWS or m == 0:
         return ops.gate_up_silu_quant(xq, w_il, xs, s_il)
+    # the fused kernel's shape contract, for both routes
+    if xq.dim() != 2 or w_il.dim() != 2 or w_il.shape[0] % 256 != 0 or \
+            xq.shape[1] % 512 != 0 or xq.shape[1] == 0:
+        raise RuntimeError("gate_up_silu_quant: I must be a multiple of 128 and K a positive "
+                           f"multiple of 512 (A {tuple(xq.shape)}, B {tuple(w_il.shape)})")
     i = w_il.shape[0] // 2
     h = ops.w8a8_block_fp8_matmul_dtype(xq, w_il, xs, s_il, 128, 128, torch.bfloat16)
     # rows of 256 columns: gate block | up block
