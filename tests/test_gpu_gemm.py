@@ -677,28 +677,31 @@ def _random_shapes_large(n, seed):
         N = int(torch.randint(1, 6145, (1,), generator=g))
         KB = int(torch.randint(1, 65, (1,), generator=g))
         block_n = 1 if int(torch.randint(0, 4, (1,), generator=g)) == 0 else 128
-        shapes.append((M, N, 128 * KB, block_n))
+        dtype = [torch.bfloat16, torch.float32, torch.float16][int(torch.randint(0, 3, (1,),
+                                                                                  generator=g))]
+        shapes.append((M, N, 128 * KB, block_n, dtype))
     return shapes
 
 
-@pytest.mark.parametrize("M,N,K,block_n", _random_shapes_large(24, 2025))
-def test_gemm_random_shapes_large(M, N, K, block_n, dev):
+@pytest.mark.parametrize("M,N,K,block_n,dtype", _random_shapes_large(24, 2025))
+def test_gemm_random_shapes_large(M, N, K, block_n, dtype, dev):
     """A seeded sweep over larger shapes (M up to 4096, N up to 6144, K up
-    to 8192): the small-grid tilings (32x16, 32x32, 64x64), 128x128 grids
-    with split-K or with their last wave as 64x64 quarters, 192- and
-    256-row tiles and their quarters, against torch's fp32 dequant-matmul of
-    the same operands, within the north-star tolerance."""
-    print(f"gemm random large M={M} N={N} K={K} block_n={block_n}", flush=True)
+    to 8192) and output dtypes: the small-grid tilings (32x16, 32x32,
+    64x64), 128x128 grids with split-K or with their last wave as 64x64
+    quarters, 192- and 256-row tiles and their quarters, against torch's
+    fp32 dequant-matmul of the same operands, within the north-star
+    tolerance."""
+    print(f"gemm random large M={M} N={N} K={K} block_n={block_n} {dtype}", flush=True)
     x = synthetic.activations(M, K, seed=M * 7 + N)
     q, s = fp8.act_quant(x.to(dev), 128)
     W, Bs = synthetic.weights(N, K, seed=N * 13 + K, block_n=block_n)
     W, Bs = W.to(dev), Bs.to(dev)
-    out = fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [block_n, 128], torch.bfloat16)
+    out = fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [block_n, 128], dtype)
+    assert out.dtype == dtype and out.shape == (M, N)
     saf = s.repeat_interleave(128, 1)[:, :K]
     sbf = (Bs if block_n == 1 else Bs.repeat_interleave(128, 0)[:N]).repeat_interleave(128, 1)
     full = (q.float() * saf) @ (W.float() * sbf[:, :K]).T
-    torch.testing.assert_close(out.float(), full.to(torch.bfloat16).float(), rtol=RTOL,
-                               atol=ATOL)
+    torch.testing.assert_close(out.float(), full.to(dtype).float(), rtol=RTOL, atol=ATOL)
 
 
 @pytest.mark.parametrize("M,N,K", [(512, 512, 2048), (1024, 2048, 14336), (2048, 2560, 4096),
