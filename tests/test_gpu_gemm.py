@@ -654,7 +654,7 @@ def _random_shapes(n, seed):
 def test_gemm_random_shapes(M, N, K, block_n, dtype, dev):
     """A seeded sweep over shapes (M 1-699, N 1-1999, K 128-4096), weight
     block sizes 128 and 1 (per-row) and output dtypes: the small-grid,
-    skinny, split-K decode, 64x128 and 128x128 plans against torch's fp32
+    skinny, split-K decode and 128x128 plans against torch's fp32
     dequant-matmul of the same operands, within the north-star tolerance."""
     print(f"gemm random M={M} N={N} K={K} block_n={block_n} {dtype}", flush=True)
     x = synthetic.activations(M, K, seed=M * 31 + N)
