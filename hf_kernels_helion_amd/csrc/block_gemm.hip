@@ -1037,6 +1037,226 @@ __global__ void __launch_bounds__(512) gemm_pipe192_kernel(GemmArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Pipelined 256x128 kernel: the scheme of gemm_pipe192_kernel on tiles of 256
+// activation rows by one 128-column weight block, for grids where 256x256
+// tiles leave CUs idle while 128x128 tiles need extra waves (M x N = 2048 x
+// 4096: 128 tiles of 256x256, 512 of 128x128, 256 of 256x128 on 256 CUs).
+// Per output the arithmetic is the other kernels' (one zero-accumulator MFMA
+// per 16x16 sub-tile and K-block, folded as acc + dot * (As * Bs) in K
+// order), so the result bits are those of any unsplit plan.
+//   * 8 waves of 64x64 (4 x 2): four activation and four weight fragments,
+//     16 MFMAs per K-block.
+//   * MFMA order: rows 0-1, then rows 2-3, each pair column-major. Weight
+//     fragment 3 and rows 2-3 of a K-block are read at its MFMAs 0-3; one
+//     barrier per K-block before MFMA 8 (every wave has read the whole
+//     current stage, and its DMA of the next stage has landed); after it the
+//     next K-block's rows 0-1 and weight fragments 0-2 are read into the
+//     registers their last use just freed, and the DMA of K-block kb+2 goes
+//     into the released stage, one instruction per MFMA.
+//   * Stage: 256 + 128 rows of 128 bytes (48 KiB) in the block layout of
+//     gemm_pipe256_kernel (A blocks 0-31, B blocks 32-47), two stages; scale
+//     windows of 8 K-blocks as there, with the tile's single weight-scale row
+//     (one scale per K-block for all 128 columns).
+// Preconditions: those of gemm_pipe256_kernel (pipe_ok), block_n = 128.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(512) gemm_pipe256x128_kernel(GemmArgs a) {
+  constexpr int BM = 256, BN = 128, WM = 64, WN = 64, NWN = BN / WN, NW = 8;
+  constexpr int FM = WM / 16, FN = WN / 16;       // 4 activation, 4 weight fragments
+  constexpr int NP = FM * FN;                     // 16 MFMAs per K-block
+  constexpr int STAGE = (BM + BN) * 128;          // 48 KiB
+  constexpr int LPW = (BM + BN) / 8 / NW;         // 6 wave-loads per wave per K-block
+  constexpr int A_LOADS = BM / 64;                // wave-loads i < 4 bring A rows
+  constexpr int WIN_SA = BM * 32;
+  constexpr int WIN = WIN_SA + 256;
+  constexpr int SW_OFF = 2 * STAGE;
+  constexpr int EPI_PITCH = WN * 2 + 16;
+  constexpr int EPI = NW * WM * EPI_PITCH;
+  constexpr int SMEM = (2 * STAGE + 2 * WIN > EPI) ? 2 * STAGE + 2 * WIN : EPI;
+  constexpr int BAR = 8;                          // MFMA index of the barrier
+  static_assert(SMEM <= 160 * 1024, "LDS budget");
+  static_assert(LPW <= NP - BAR, "one DMA instruction per MFMA after the barrier");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wid / NWN, wn = wid % NWN;
+
+  int tm, tn;
+  tile_of_bid((int)blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  const int split = blockIdx.z;
+  const int kb_begin = split * a.kb_per_split;
+  const int kb_end = min(kb_begin + a.kb_per_split, a.KB);
+  const int nkb = kb_end - kb_begin;
+
+  const uint32_t lds0 = lds_u32(smem);
+  const int r8 = lane >> 3;
+  const uint8_t* a_base = a.A + (int64_t)m0 * a.lda;
+  const uint8_t* b_base = a.B + (int64_t)n0 * a.ldb;
+  const int a_lim = a.M - 1 - m0, b_lim = a.N - 1 - n0;
+  // wave-load L = wid + 8i: stage block L (A blocks 0..31, B blocks 32..47)
+  auto issue_op = [&](int kb, int stage, int i) {
+    const int L = wid + i * NW;
+    const uint32_t lds = lds0 + stage * STAGE + L * 1024;
+    const int Lr = i < A_LOADS ? L : L - BM / 8;
+    const int row = (Lr >> 3) * 64 + r8 * 8 + (Lr & 7);
+    const int c16 = ((lane & 7) ^ (Lr & 7)) * 16;
+    if (i < A_LOADS) {
+      const uint32_t voff = (uint32_t)min(row, a_lim) * (uint32_t)a.lda + c16;
+      dma16_soff(voff, a_base + (int64_t)kb * 128, lds);
+    } else {
+      const uint32_t voff = (uint32_t)min(row, b_lim) * (uint32_t)a.ldb + c16;
+      dma16_soff(voff, b_base + (int64_t)kb * 128, lds);
+    }
+  };
+  // Scale window of 8 K-blocks: wave w brings As rows 32w..32w+31 (two lanes
+  // per row, 4 K-blocks each); lanes 0-1 of wave 7 also bring the tile's Bs
+  // row. A half-window past kb_end re-reads the first half (KB is a multiple
+  // of 4), so no lane reads past the row.
+  const float* saw_src =
+      a.As + (int64_t)min(m0 + wid * 32 + (lane >> 1), a.M - 1) * a.as_sm + 4 * (lane & 1);
+  const float* sbw_src = a.Bs + (int64_t)(n0 >> 7) * a.bs_sn + 4 * (lane & 1);
+  auto issue_win = [&](int kb0, int wbuf) {
+    const int kk = (kb0 + 4 * (lane & 1) < kb_end) ? kb0 : kb0 - 4 * (lane & 1);
+    const uint32_t lb = lds0 + SW_OFF + wbuf * WIN;
+    dma16_ptr(saw_src + kk, lb + wid * 1024);
+    if (wid == NW - 1 && lane < 2) dma16_ptr(sbw_src + kk, lb + WIN_SA);
+  };
+
+  const int r7 = lane & 7, g2 = 2 * (lane >> 4);
+  const int slo = (g2 ^ r7) << 4, shi = ((g2 + 1) ^ r7) << 4;
+  const int q_off = (lane & 7) * 1024 + ((lane >> 3) & 1) * 128;
+  // 16-row fragment F of an operand: block 8*(F/4) + q%8, segment 2*(F%4) + q/8
+  auto frag_off = [](int f) { return (f >> 2) * 8192 + (f & 3) * 256; };
+  auto rdx = [&](int stage, int i) {
+    return lds_frag2(smem + stage * STAGE + q_off + frag_off(wm * FM + i), slo, shi);
+  };
+  auto rdw = [&](int stage, int j) {
+    return lds_frag2(smem + stage * STAGE + BM * 128 + q_off + frag_off(wn * FN + j), slo, shi);
+  };
+  const int sa_off = SW_OFF + (wm * WM + (lane & 15)) * 32;
+  auto rdsa = [&](int rel, int i) {
+    const int o = ((rel >> 3) & 1) * WIN + (rel & 7) * 4;
+    return *reinterpret_cast<const float*>(smem + sa_off + o + i * 512);
+  };
+  auto rdsb = [&](int rel) {
+    const int o = ((rel >> 3) & 1) * WIN + (rel & 7) * 4;
+    return *reinterpret_cast<const float*>(smem + SW_OFF + WIN_SA + o);
+  };
+
+  v4f acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  constexpr int ORD_I[NP] = {0, 1, 0, 1, 0, 1, 0, 1, 2, 3, 2, 3, 2, 3, 2, 3};
+  constexpr int ORD_J[NP] = {0, 0, 1, 1, 2, 2, 3, 3, 0, 0, 1, 1, 2, 2, 3, 3};
+  v8i w[FN], xs[FM];
+  float sc[FM], sa_t[FM], sb_n = 0.f;
+  v4f r1 = v4f{0.f, 0.f, 0.f, 0.f}, r2 = r1;  // results of MFMAs p-1 and p-2
+
+  if (nkb > 0) {
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) issue_op(kb_begin, 0, i);
+    issue_win(kb_begin, 0);
+    if (nkb > 1) {
+#pragma unroll
+      for (int i = 0; i < LPW; ++i) issue_op(kb_begin + 1, 1, i);
+      wait_vmcnt<LPW>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    __syncthreads();
+    w[0] = rdw(0, 0); w[1] = rdw(0, 1); w[2] = rdw(0, 2);
+    xs[0] = rdx(0, 0); xs[1] = rdx(0, 1);
+    sa_t[0] = rdsa(0, 0); sa_t[1] = rdsa(0, 1);
+    sb_n = rdsb(0);
+  }
+
+  // One K-block. KIND 0: steady state (reads the next K-block, DMA of
+  // kb+2); 1: next K-block exists but no kb+2; 2: last K-block. Empty asm
+  // statements and sched_barrier keep the MFMAs, reads and folds in the
+  // written order, as in gemm_pipe256_kernel.
+  auto body = [&](int kb, auto tag) {
+    constexpr int KIND = decltype(tag)::value;
+    const int rel = kb - kb_begin;
+    const int s = rel & 1;
+    const float sb = sb_n;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int i = ORD_I[p], j = ORD_J[p];
+      if (p == BAR && KIND < 2) {
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (KIND == 0 && ((rel + 2) & 7) == 0) issue_win(kb + 2, ((rel + 2) >> 3) & 1);
+      }
+      v4f res = mfma16x16x128(w[j], xs[i]);
+      asm volatile("" : "+v"(res));
+      __builtin_amdgcn_sched_barrier(0);
+      // this K-block's last weight fragment, rows 2-3 and their scales
+      if (p == 0) w[3] = rdw(s, 3);
+      if (p == 1) { xs[2] = rdx(s, 2); sa_t[2] = rdsa(rel, 2); }
+      if (p == 3) { xs[3] = rdx(s, 3); sa_t[3] = rdsa(rel, 3); }
+      // scale of row i, just before the fold of its first MFMA
+      if (p == 1) { sc[0] = sa_t[0] * sb; sc[1] = sa_t[1] * sb; }
+      if (p == 9) { sc[2] = sa_t[2] * sb; sc[3] = sa_t[3] * sb; }
+      // after the barrier: the next K-block's rows 0-1 and weight fragments
+      // 0-2 (stage s^1) and the DMA of K-block kb+2 into stage s
+      if (KIND < 2 && p >= BAR) {
+        if (KIND == 0 && p - BAR < LPW) issue_op(kb + 2, s, p - BAR);
+        if (p == BAR) { xs[0] = rdx(s ^ 1, 0); sb_n = rdsb(rel + 1); sa_t[0] = rdsa(rel + 1, 0); }
+        if (p == BAR + 1) { xs[1] = rdx(s ^ 1, 1); sa_t[1] = rdsa(rel + 1, 1); }
+        if (p == BAR + 2) w[0] = rdw(s ^ 1, 0);
+        if (p == BAR + 4) w[1] = rdw(s ^ 1, 1);
+        if (p == BAR + 6) w[2] = rdw(s ^ 1, 2);
+      }
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      if (p >= 2) {
+        const int qi = ORD_I[p - 2], qj = ORD_J[p - 2];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[qi][qj][e] = fmaf(r2[e], sc[qi], acc[qi][qj][e]);
+        asm volatile("" : "+v"(acc[qi][qj]));
+      } else {
+        // the previous K-block's last two MFMAs: rows 2 and 3, column 3
+        // (their scales are rewritten only at MFMA 9)
+        const int qi = FM - 2 + p;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[qi][3][e] = fmaf(r2[e], sc[qi], acc[qi][3][e]);
+        asm volatile("" : "+v"(acc[qi][3]));
+      }
+      r2 = r1;
+      r1 = res;
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // sc starts at zero so the first K-block's two "previous" folds add 0.
+#pragma unroll
+  for (int i = 0; i < FM; ++i) sc[i] = 0.f;
+  int kb = kb_begin;
+  for (; kb + 2 < kb_end; ++kb) body(kb, PipeKind<0>{});
+  if (kb + 1 < kb_end) {
+    body(kb, PipeKind<1>{});
+    ++kb;
+  }
+  if (kb < kb_end) {
+    body(kb, PipeKind<2>{});
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[FM - 2][3][e] = fmaf(r2[e], sc[FM - 2], acc[FM - 2][3][e]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[FM - 1][3][e] = fmaf(r1[e], sc[FM - 1], acc[FM - 1][3][e]);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  tile_epilogue<WM, WN>(a, smem, acc, m0 + wm * WM, n0 + wn * WN, wid, lane, split);
+}
+
+// ---------------------------------------------------------------------------
 // Pipelined 128x128 kernel (grids below one 256x256 tile per CU, and the
 // split-K path). Waves of WM x WN (two per SIMD for 64x32); with half the operand
 // reuse of a 256x256 tile this size is bound by the operand stream, so it
@@ -1872,6 +2092,7 @@ enum TileCfg {
   CFG_SKINNY = 3,
   CFG_DECODE = 4,
   CFG_TINY = 5,
+  CFG_256x128 = 6,
   CFG_COUNT
 };
 
@@ -1906,7 +2127,8 @@ int device_cu_count() {
 //   FP8B_TAIL128=0  no 128x128 quarters for a small last wave of 256x256 tiles;
 //   FP8B_TILE192=0  no 192x256 tiles;
 //   FP8B_TINY=0     no small-grid kernel (32x32, 32x16, 64x64 tiles);
-//   FP8B_TAIL64=0   no 64x64 quarters for a small last wave of 128x128 tiles.
+//   FP8B_TAIL64=0   no 64x64 quarters for a small last wave of 128x128 tiles;
+//   FP8B_TILE256X128=0  no 256x128 tiles.
 bool env_flag_on(const char* name) {
   const char* e = getenv(name);
   return !(e && e[0] == '0');
@@ -1935,6 +2157,10 @@ bool use_tail64() {
   static const bool v = env_flag_on("FP8B_TAIL64");
   return v;
 }
+bool use_tile256x128() {
+  static const bool v = env_flag_on("FP8B_TILE256X128");
+  return v;
+}
 
 // Fraction of the CU slots a grid of t tiles keeps busy over its waves.
 double wave_fill(int64_t t, int cus) {
@@ -1961,6 +2187,22 @@ bool prefer_192(int64_t t256, int64_t t192, int cus, bool tail_quarters) {
 bool tail_quarters(int64_t t, int cus) {
   const int64_t rest = t % cus;
   return use_tail128() && t >= cus && rest > 0 && 4 * rest <= cus;
+}
+
+// 256x128 tiles (gemm_pipe256x128_kernel) when they fit in one wave of
+// workgroups while 128x128 tiles would need two or more. Per K-block on one
+// CU a 256x128 tile takes ~0.9-1.0 us, a 128x128 tile ~0.7 and a 256x256
+// tile ~1.75. Measured at steady clock against the plan each replaces (bits
+// unchanged where that plan was unsplit): 2048x4096x4096 34.8 against 47.1
+// us (two waves of 128x128 tiles), 768x7168x4096 29.4 against 45.3,
+// 1024x8192x14336 106.7 against 143.3, 256x28672x4096 33.5 against 45.9,
+// 768x6144x14336 94.3 against 101.7. Outside the rule they lost: half a
+// wave of them against one wave of 128x128 tiles (2048x2048x4096 30.1
+// against 25.3), two waves against one of 256x256 tiles (2048x6144x4096
+// 61.2 against 47.1), three against two (4096x6144x14336 313.9 against
+// 306.8).
+bool prefer_256x128(int64_t t2x1, int64_t t128, int cus) {
+  return use_tile256x128() && t128 > cus && t2x1 <= cus;
 }
 
 // Grids of fewer 256x256 tiles than CUs: one partial wave of 256x256 tiles
@@ -2088,6 +2330,8 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
   }
   if (M <= 64) {
     p.cfg = CFG_128x128; p.bm = 128; p.bn = 128;
+  } else if (!per_row && prefer_256x128(tiles(256, 128), tiles(128, 128), cus)) {
+    p.cfg = CFG_256x128; p.bm = 256; p.bn = 128;
   } else if (tiles(256, 256) >= cus || prefer_256(tiles(256, 256), tiles(128, 128), cus)) {
     p.cfg = CFG_256x256; p.bm = 256; p.bn = 256;
     if (!per_row && prefer_192(tiles(256, 256), tiles(192, 256), cus,
@@ -2339,10 +2583,14 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
     set_error("fp8b_w8a8_block_matmul: too many output tiles for one launch");
     return FP8B_ERR_DIMS;
   }
-  // 192x256 tiles exist only as a pipelined kernel: without its
-  // preconditions the grid goes back to 256x256 tiles.
+  // 192x256 and 256x128 tiles exist only as pipelined kernels: without
+  // their preconditions the grid goes back to 256x256 or 128x128 tiles.
   if (p.cfg == CFG_192x256 && !pipe_ok(a, p)) {
     p.cfg = CFG_256x256; p.bm = 256;
+    a = make_args(p);
+  }
+  if (p.cfg == CFG_256x128 && !pipe_ok(a, p)) {
+    p.cfg = CFG_128x128; p.bm = 128;
     a = make_args(p);
   }
   if (per_row) {
@@ -2395,6 +2643,9 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
     }
     case CFG_192x256:
       gemm_pipe192_kernel<false><<<(unsigned)(a.tiles_m * a.tiles_n), 512, 0, st>>>(a);
+      break;
+    case CFG_256x128:
+      gemm_pipe256x128_kernel<<<(unsigned)(a.tiles_m * a.tiles_n), 512, 0, st>>>(a);
       break;
     case CFG_TINY:
       launch_tiny<false>(a, p.bn, st);

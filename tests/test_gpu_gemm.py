@@ -474,6 +474,79 @@ def test_gemm_192_row_tiles_equal_other_plans(M, N, K, dev):
     assert torch.equal(out32.to(torch.bfloat16), out)
 
 
+def _tiles(M, N, bm, bn):
+    return -(-M // bm) * -(-N // bn)
+
+
+def _is_256x128_grid(M, N, cus):
+    """The planner's rule for 256x128 tiles: they fit one wave of workgroups
+    while 128x128 tiles would need more than one."""
+    return _tiles(M, N, 128, 128) > cus >= _tiles(M, N, 256, 128)
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 4096, 4096), (1000, 6144, 2048), (768, 7000, 1024),
+                                   (256, 28672, 1024), (1537, 4096, 1024), (4096, 2048, 7168)])
+def test_gemm_256x128_tiles(M, N, K, dev):
+    """Grids whose 256x128 tiles fit one wave of workgroups while 128x128
+    tiles need two or more run gemm_pipe256x128_kernel (ragged last tile row
+    and column, a last tile row of one row): sampled rows against the oracle,
+    and bit for bit against row slices that run the unsplit 128x128 plan
+    (every unsplit MFMA plan folds the same products in the same K order);
+    fp32 and fp16 outputs through the kernel's other epilogues."""
+    from hf_kernels_helion_amd import _native
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if not _is_256x128_grid(M, N, cus):
+        pytest.skip(f"{M}x{N} is not a 256x128 grid on {cus} CUs")
+    print(f"gemm 256x128 tiles M={M} N={N} K={K}", flush=True)
+    x = synthetic.activations(M, K, seed=M + 5 * N, outlier_frac=0.01)
+    q, s = fp8.act_quant(x.to(dev), 128)
+    W, Bs = synthetic.weights(N, K, seed=N + 7)
+    W, Bs = W.to(dev), Bs.to(dev)
+    out = fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [128, 128], torch.bfloat16)
+    lib = _native.load()
+    # slices of whole 128-row tiles filling between half a wave and one wave
+    # of 128x128 tiles: neither split nor another tiling
+    h = 128 * (cus // -(-N // 128))
+    assert h < M and _tiles(h, N, 128, 128) * 2 > cus
+    slices = [(r0, r0 + h) for r0 in range(0, M - h, h)] + [(M - h, M)]
+    for r0, r1 in slices:
+        assert lib.fp8b_gemm_workspace_size(r1 - r0, N, K, 128, 128) == 0
+        part = fp8.w8a8_block_fp8_matmul(q[r0:r1], W, s[r0:r1], Bs, [128, 128], torch.bfloat16)
+        torch.testing.assert_close(out[r0:r1], part, rtol=0, atol=0)
+    rows = torch.tensor(sorted({r for r in (0, 255, 256, M // 2, M - 1) if r < M}))
+    orc = oracle.block_gemm(_u8(q.cpu()[rows]), _u8(W.cpu()), s.cpu()[rows].numpy(),
+                            Bs.cpu().numpy())
+    torch.testing.assert_close(out[rows.to(dev)].float().cpu(),
+                               torch.from_numpy(orc).to(torch.bfloat16).float(),
+                               rtol=RTOL, atol=ATOL)
+    out32 = fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [128, 128], torch.float32)
+    assert torch.equal(out32.to(torch.bfloat16), out)
+    out16 = fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [128, 128], torch.float16)
+    assert torch.equal(out32.to(torch.float16), out16)
+
+
+def test_gemm_256x128_tiles_exact_integers(dev):
+    """gemm_pipe256x128_kernel on small-integer operands with power-of-two
+    scales per activation row and weight block (every product and partial
+    sum exact in fp32): the whole fp32 output equals the float64 product,
+    ragged last tile row and column included."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    M, N, K = 1800, 4000, 1024
+    if not _is_256x128_grid(M, N, cus):
+        pytest.skip(f"{M}x{N} is not a 256x128 grid on {cus} CUs")
+    print(f"gemm 256x128 exact M={M} N={N} K={K}", flush=True)
+    g = torch.Generator().manual_seed(17)
+    A = torch.randint(-4, 5, (M, K), generator=g).float().to(torch.float8_e4m3fn)
+    B = torch.randint(-4, 5, (N, K), generator=g).float().to(torch.float8_e4m3fn)
+    As = torch.exp2(torch.randint(-2, 3, (M, K // 128), generator=g).float())
+    Bs = torch.exp2(torch.randint(-2, 3, ((N + 127) // 128, K // 128), generator=g).float())
+    out = fp8.w8a8_block_fp8_matmul(A.to(dev), B.to(dev), As.to(dev), Bs.to(dev), [128, 128],
+                                    torch.float32)
+    exact = (A.double() * As.double().repeat_interleave(128, 1)) @ (
+        B.double() * Bs.double().repeat_interleave(128, 0)[:N].repeat_interleave(128, 1)).T
+    assert torch.equal(out.cpu().double(), exact)
+
+
 # Small-grid shapes and the waves per 32x32 tile gemm_tiny_kernel runs them
 # with on a 256-CU MI355X (8: at most one tile per CU; 4: two; 2: four; 1:
 # up to eight), ragged edges, one K-block (seven of eight waves idle), a
@@ -683,14 +756,32 @@ def _random_shapes_large(n, seed):
     return shapes
 
 
-@pytest.mark.parametrize("M,N,K,block_n,dtype", _random_shapes_large(24, 2025))
+def _random_256x128_shapes(n, seed, cus=256):
+    """Random grids that the planner gives 256x128 tiles on a 256-CU device
+    (K a multiple of 512 for three in four: the pipelined kernel's
+    precondition)."""
+    g = torch.Generator().manual_seed(seed)
+    shapes = []
+    while len(shapes) < n:
+        M = int(torch.randint(129, 4097, (1,), generator=g))
+        N = int(torch.randint(129, 16385, (1,), generator=g))
+        KB = int(torch.randint(1, 13, (1,), generator=g)) * (4 if len(shapes) % 4 else 1)
+        dtype = [torch.bfloat16, torch.float32][len(shapes) % 2]
+        if _is_256x128_grid(M, N, cus):
+            shapes.append((M, N, 128 * KB, 128, dtype))
+    return shapes
+
+
+@pytest.mark.parametrize("M,N,K,block_n,dtype",
+                         _random_shapes_large(24, 2025) + _random_256x128_shapes(8, 7))
 def test_gemm_random_shapes_large(M, N, K, block_n, dtype, dev):
     """A seeded sweep over larger shapes (M up to 4096, N up to 6144, K up
     to 8192) and output dtypes: the small-grid tilings (32x16, 32x32,
     64x64), 128x128 grids with split-K or with their last wave as 64x64
-    quarters, 192- and 256-row tiles and their quarters, against torch's
-    fp32 dequant-matmul of the same operands, within the north-star
-    tolerance."""
+    quarters, 256x128 tiles (and the 128x128 kernel that takes their grids
+    when K is not a multiple of 512), 192- and 256-row tiles and their
+    quarters, against torch's fp32 dequant-matmul of the same operands,
+    within the north-star tolerance."""
     print(f"gemm random large M={M} N={N} K={K} block_n={block_n} {dtype}", flush=True)
     x = synthetic.activations(M, K, seed=M * 7 + N)
     q, s = fp8.act_quant(x.to(dev), 128)
@@ -705,13 +796,14 @@ def test_gemm_random_shapes_large(M, N, K, block_n, dtype, dev):
 
 
 @pytest.mark.parametrize("M,N,K", [(512, 512, 2048), (1024, 2048, 14336), (2048, 2560, 4096),
-                                   (32, 4096, 14336), (4096, 4096, 1024), (64, 4096, 14336)])
+                                   (32, 4096, 14336), (4096, 4096, 1024), (64, 4096, 14336),
+                                   (2048, 4096, 2048)])
 def test_gemm_graph_replays(M, N, K, dev):
     """The GEMM captured in a HIP graph on each plan family (small-grid
     tiles; split-K 128x128 with its sum; a 128x128 grid whose last wave runs
     as 64x64 quarters; the split-K decode kernel; 256x256 tiles; the decode
-    kernel with 64 rows): every replay, with eager work in between, equals
-    the eager result."""
+    kernel with 64 rows; 256x128 tiles): every replay, with eager work in
+    between, equals the eager result."""
     print(f"gemm graph M={M} N={N} K={K}", flush=True)
     x = synthetic.activations(M, K, seed=M + N + K)
     q, s = fp8.act_quant(x.to(dev), 128)
