@@ -2176,10 +2176,15 @@ double wave_fill(int64_t t, int cus) {
 // and act-quant in its epilogue plus the down projection 517.7 against 528.4
 // us; but the plain gate/up GEMM (N = 28672: 1792 tiles against 5 waves and
 // 64 tiles as quarters) 331.4 against 320.3 us, since 192-row tiles move
-// 17% more operand bytes per output.
+// 17% more operand bytes per output. Also when one partial wave of 256x256
+// tiles would become one wave of 192x256 tiles (a 192-row tile takes ~1.2-
+// 1.4 us per K-block on one CU against ~1.75): 384x28672x4096 45.0 against
+// 52.9 us, 1536x6144x4096 40.8 against 43.7, 768x14336x7168 71.9 against
+// 76.0; 1536x8192 (192 tiles against 256) even.
 bool prefer_192(int64_t t256, int64_t t192, int cus, bool tail_quarters) {
-  return use_tile192() && !tail_quarters && t192 >= cus &&
-         wave_fill(t192, cus) >= wave_fill(t256, cus) + 0.1;
+  if (!use_tile192()) return false;
+  if (t256 < cus && t192 <= cus) return true;
+  return !tail_quarters && t192 >= cus && wave_fill(t192, cus) >= wave_fill(t256, cus) + 0.1;
 }
 
 // Whether launch_pipe256 runs the last partial wave of an unsplit grid of t

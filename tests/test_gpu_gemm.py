@@ -439,16 +439,18 @@ def test_gemm_128_tiles_last_wave_as_64_quarters(M, N, K, block_n, dev):
 
 
 @pytest.mark.parametrize("M,N,K", [(3001, 4096, 14336), (1500, 8192, 4096), (3001, 8192, 1024),
-                                   (1500, 8064, 1024)])
+                                   (1500, 8064, 1024), (1536, 6144, 2048), (1536, 7168, 1024)])
 def test_gemm_192_row_tiles_equal_other_plans(M, N, K, dev):
     """Grids whose 256x256 tiles leave a partial last wave too large for
     128x128 quarters while 192x256 tiles fill whole waves (3001 x 4096: 256
     tiles against 192; 1500 x 8192: 256 against 192; 3001 x 8192: 512
-    against 384; 1500 x 8064: half a tile column past N) run
-    gemm_pipe192_kernel, ragged last tile row included. Per
-    output its arithmetic is that of every unsplit MFMA plan, so row slices of
-    1024 (which run the 128x128 kernel) give the same bits; sampled rows
-    against the oracle. (The gate/up GEMM with the SiLU epilogue on 192-row
+    against 384; 1500 x 8064: half a tile column past N), or one partial
+    wave of 256x256 tiles that 192x256 tiles still hold in one wave (1536 x
+    6144: 192 against 144; 1536 x 7168: 224 against 168) run
+    gemm_pipe192_kernel, ragged last tile row included. Per output its
+    arithmetic is that of every unsplit MFMA plan, so row slices of 1024
+    (which run the 128x128 or 256x128 kernels) give the same bits; sampled
+    rows against the oracle. (The gate/up GEMM with the SiLU epilogue on 192-row
     tiles is checked against the plain GEMM in test_gpu_mlp.py.)"""
     from hf_kernels_helion_amd import _native
     print(f"gemm 192-row tiles M={M} N={N} K={K}", flush=True)
