@@ -1057,8 +1057,15 @@ __global__ void __launch_bounds__(512) gemm_pipe192_kernel(GemmArgs a) {
 //     gemm_pipe256_kernel (A blocks 0-31, B blocks 32-47), two stages; scale
 //     windows of 8 K-blocks as there, with the tile's single weight-scale row
 //     (one scale per K-block for all 128 columns).
-// Preconditions: those of gemm_pipe256_kernel (pipe_ok), block_n = 128.
+// PR (per-row weight scales, block_n = 1): as in gemm_pipe256_kernel, the
+// window holds the 128 weight rows' scales slot-major (4-byte DMA lanes) and
+// each fold multiplies the row scale by the lane's four column scales, read
+// per weight fragment and K-block as one 16-byte load into the register its
+// previous value just left.
+// Preconditions: those of gemm_pipe256_kernel (pipe_ok); block_n = 128, or
+// 1 with PR.
 // ---------------------------------------------------------------------------
+template <bool PR>
 __global__ void __launch_bounds__(512) gemm_pipe256x128_kernel(GemmArgs a) {
   constexpr int BM = 256, BN = 128, WM = 64, WN = 64, NWN = BN / WN, NW = 8;
   constexpr int FM = WM / 16, FN = WN / 16;       // 4 activation, 4 weight fragments
@@ -1067,7 +1074,7 @@ __global__ void __launch_bounds__(512) gemm_pipe256x128_kernel(GemmArgs a) {
   constexpr int LPW = (BM + BN) / 8 / NW;         // 6 wave-loads per wave per K-block
   constexpr int A_LOADS = BM / 64;                // wave-loads i < 4 bring A rows
   constexpr int WIN_SA = BM * 32;
-  constexpr int WIN = WIN_SA + 256;
+  constexpr int WIN = WIN_SA + (PR ? 8 * BN * 4 : 256);
   constexpr int SW_OFF = 2 * STAGE;
   constexpr int EPI_PITCH = WN * 2 + 16;
   constexpr int EPI = NW * WM * EPI_PITCH;
@@ -1113,8 +1120,9 @@ __global__ void __launch_bounds__(512) gemm_pipe256x128_kernel(GemmArgs a) {
   };
   // Scale window of 8 K-blocks: wave w brings As rows 32w..32w+31 (two lanes
   // per row, 4 K-blocks each); lanes 0-1 of wave 7 also bring the tile's Bs
-  // row. A half-window past kb_end re-reads the first half (KB is a multiple
-  // of 4), so no lane reads past the row.
+  // row (PR: wave w brings slot w, the 128 rows' scales of K-block kb0 + w).
+  // A half-window past kb_end re-reads the first half (KB is a multiple of
+  // 4), so no lane reads past the row.
   const float* saw_src =
       a.As + (int64_t)min(m0 + wid * 32 + (lane >> 1), a.M - 1) * a.as_sm + 4 * (lane & 1);
   const float* sbw_src = a.Bs + (int64_t)(n0 >> 7) * a.bs_sn + 4 * (lane & 1);
@@ -1122,7 +1130,18 @@ __global__ void __launch_bounds__(512) gemm_pipe256x128_kernel(GemmArgs a) {
     const int kk = (kb0 + 4 * (lane & 1) < kb_end) ? kb0 : kb0 - 4 * (lane & 1);
     const uint32_t lb = lds0 + SW_OFF + wbuf * WIN;
     dma16_ptr(saw_src + kk, lb + wid * 1024);
-    if (wid == NW - 1 && lane < 2) dma16_ptr(sbw_src + kk, lb + WIN_SA);
+    if constexpr (PR) {
+      const int kbs = min(kb0 + wid, kb_end - 1);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        int row = n0 + h * 64 + lane;
+        asm volatile("" : "+v"(row));
+        dma4_ptr(a.Bs + (int64_t)min(row, a.N - 1) * a.bs_sn + kbs,
+                 lb + WIN_SA + wid * 512 + h * 256);
+      }
+    } else {
+      if (wid == NW - 1 && lane < 2) dma16_ptr(sbw_src + kk, lb + WIN_SA);
+    }
   };
 
   const int r7 = lane & 7, g2 = 2 * (lane >> 4);
@@ -1142,8 +1161,15 @@ __global__ void __launch_bounds__(512) gemm_pipe256x128_kernel(GemmArgs a) {
     return *reinterpret_cast<const float*>(smem + sa_off + o + i * 512);
   };
   auto rdsb = [&](int rel) {
+    if constexpr (PR) return 1.0f;
     const int o = ((rel >> 3) & 1) * WIN + (rel & 7) * 4;
     return *reinterpret_cast<const float*>(smem + SW_OFF + WIN_SA + o);
+  };
+  // PR: the lane's four column scales of weight fragment j at K-block rel
+  auto rdsbj = [&](int rel, int j) {
+    const int o = ((rel >> 3) & 1) * WIN + (rel & 7) * 512;
+    return *reinterpret_cast<const v4f*>(smem + SW_OFF + WIN_SA + o +
+                                         (wn * WN + j * 16 + 4 * (lane >> 4)) * 4);
   };
 
   v4f acc[FM][FN];
@@ -1156,6 +1182,9 @@ __global__ void __launch_bounds__(512) gemm_pipe256x128_kernel(GemmArgs a) {
   constexpr int ORD_J[NP] = {0, 0, 1, 1, 2, 2, 3, 3, 0, 0, 1, 1, 2, 2, 3, 3};
   v8i w[FN], xs[FM];
   float sc[FM], sa_t[FM], sb_n = 0.f;
+  v4f sbj[PR ? FN : 1];
+#pragma unroll
+  for (int j = 0; j < (PR ? FN : 1); ++j) sbj[j] = v4f{0.f, 0.f, 0.f, 0.f};
   v4f r1 = v4f{0.f, 0.f, 0.f, 0.f}, r2 = r1;  // results of MFMAs p-1 and p-2
 
   if (nkb > 0) {
@@ -1174,6 +1203,7 @@ __global__ void __launch_bounds__(512) gemm_pipe256x128_kernel(GemmArgs a) {
     xs[0] = rdx(0, 0); xs[1] = rdx(0, 1);
     sa_t[0] = rdsa(0, 0); sa_t[1] = rdsa(0, 1);
     sb_n = rdsb(0);
+    if constexpr (PR) { sbj[0] = rdsbj(0, 0); sbj[1] = rdsbj(0, 1); }
   }
 
   // One K-block. KIND 0: steady state (reads the next K-block, DMA of
@@ -1200,6 +1230,12 @@ __global__ void __launch_bounds__(512) gemm_pipe256x128_kernel(GemmArgs a) {
       if (p == 0) w[3] = rdw(s, 3);
       if (p == 1) { xs[2] = rdx(s, 2); sa_t[2] = rdsa(rel, 2); }
       if (p == 3) { xs[3] = rdx(s, 3); sa_t[3] = rdsa(rel, 3); }
+      // PR: column scales of fragments 2 and 3, each read once the previous
+      // K-block's last fold with it has been issued
+      if constexpr (PR) {
+        if (p == 0) sbj[2] = rdsbj(rel, 2);
+        if (p == 2) sbj[3] = rdsbj(rel, 3);
+      }
       // scale of row i, just before the fold of its first MFMA
       if (p == 1) { sc[0] = sa_t[0] * sb; sc[1] = sa_t[1] * sb; }
       if (p == 9) { sc[2] = sa_t[2] * sb; sc[3] = sa_t[3] * sb; }
@@ -1212,20 +1248,30 @@ __global__ void __launch_bounds__(512) gemm_pipe256x128_kernel(GemmArgs a) {
         if (p == BAR + 2) w[0] = rdw(s ^ 1, 0);
         if (p == BAR + 4) w[1] = rdw(s ^ 1, 1);
         if (p == BAR + 6) w[2] = rdw(s ^ 1, 2);
+        // PR: the next K-block's column scales of fragments 0 and 1, after
+        // this K-block's last folds with them (MFMAs 9 and 11)
+        if constexpr (PR) {
+          if (p == 12) sbj[0] = rdsbj(rel + 1, 0);
+          if (p == 14) sbj[1] = rdsbj(rel + 1, 1);
+        }
       }
       asm volatile("" ::: "memory");
       __builtin_amdgcn_sched_barrier(0);
       if (p >= 2) {
         const int qi = ORD_I[p - 2], qj = ORD_J[p - 2];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[qi][qj][e] = fmaf(r2[e], sc[qi], acc[qi][qj][e]);
+        for (int e = 0; e < 4; ++e)
+          acc[qi][qj][e] = fmaf(r2[e], PR ? sc[qi] * sbj[qj % (PR ? FN : 1)][e] : sc[qi],
+                                acc[qi][qj][e]);
         asm volatile("" : "+v"(acc[qi][qj]));
       } else {
         // the previous K-block's last two MFMAs: rows 2 and 3, column 3
-        // (their scales are rewritten only at MFMA 9)
+        // (their scales are rewritten only at MFMA 9; PR: fragment 3's
+        // column scales only at MFMA 2)
         const int qi = FM - 2 + p;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[qi][3][e] = fmaf(r2[e], sc[qi], acc[qi][3][e]);
+        for (int e = 0; e < 4; ++e)
+          acc[qi][3][e] = fmaf(r2[e], PR ? sc[qi] * sbj[PR ? 3 : 0][e] : sc[qi], acc[qi][3][e]);
         asm volatile("" : "+v"(acc[qi][3]));
       }
       r2 = r1;
@@ -1247,9 +1293,13 @@ __global__ void __launch_bounds__(512) gemm_pipe256x128_kernel(GemmArgs a) {
   if (kb < kb_end) {
     body(kb, PipeKind<2>{});
 #pragma unroll
-    for (int e = 0; e < 4; ++e) acc[FM - 2][3][e] = fmaf(r2[e], sc[FM - 2], acc[FM - 2][3][e]);
+    for (int e = 0; e < 4; ++e)
+      acc[FM - 2][3][e] =
+          fmaf(r2[e], PR ? sc[FM - 2] * sbj[PR ? 3 : 0][e] : sc[FM - 2], acc[FM - 2][3][e]);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) acc[FM - 1][3][e] = fmaf(r1[e], sc[FM - 1], acc[FM - 1][3][e]);
+    for (int e = 0; e < 4; ++e)
+      acc[FM - 1][3][e] =
+          fmaf(r1[e], PR ? sc[FM - 1] * sbj[PR ? 3 : 0][e] : sc[FM - 1], acc[FM - 1][3][e]);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
@@ -2201,7 +2251,9 @@ bool tail_quarters(int64_t t, int cus) {
 // unchanged where that plan was unsplit): 2048x4096x4096 34.8 against 47.1
 // us (two waves of 128x128 tiles), 768x7168x4096 29.4 against 45.3,
 // 1024x8192x14336 106.7 against 143.3, 256x28672x4096 33.5 against 45.9,
-// 768x6144x14336 94.3 against 101.7. Outside the rule they lost: half a
+// 768x6144x14336 94.3 against 101.7; with per-row weight scales
+// 2048x4096x4096 41.8 against 61.6, 768x7168x4096 34.3 against 54.3. Outside
+// the rule they lost: half a
 // wave of them against one wave of 128x128 tiles (2048x2048x4096 30.1
 // against 25.3), two waves against one of 256x256 tiles (2048x6144x4096
 // 61.2 against 47.1), three against two (4096x6144x14336 313.9 against
@@ -2335,7 +2387,7 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
   }
   if (M <= 64) {
     p.cfg = CFG_128x128; p.bm = 128; p.bn = 128;
-  } else if (!per_row && prefer_256x128(tiles(256, 128), tiles(128, 128), cus)) {
+  } else if (prefer_256x128(tiles(256, 128), tiles(128, 128), cus)) {
     p.cfg = CFG_256x128; p.bm = 256; p.bn = 128;
   } else if (tiles(256, 256) >= cus || prefer_256(tiles(256, 256), tiles(128, 128), cus)) {
     p.cfg = CFG_256x256; p.bm = 256; p.bn = 256;
@@ -2609,6 +2661,8 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
       else gemm_decode_kernel<3, true><<<grid, 512, 0, st>>>(a);
     } else if (pipe_ok(a, p)) {
       if (p.cfg == CFG_256x256) launch_pipe256<true>(a, st);
+      else if (p.cfg == CFG_256x128)
+        gemm_pipe256x128_kernel<true><<<(unsigned)(a.tiles_m * a.tiles_n), 512, 0, st>>>(a);
       else launch_pipe128<64, 32, true>(a, p.splits, st);
     } else {
       return run_generic();
@@ -2650,7 +2704,7 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
       gemm_pipe192_kernel<false><<<(unsigned)(a.tiles_m * a.tiles_n), 512, 0, st>>>(a);
       break;
     case CFG_256x128:
-      gemm_pipe256x128_kernel<<<(unsigned)(a.tiles_m * a.tiles_n), 512, 0, st>>>(a);
+      gemm_pipe256x128_kernel<false><<<(unsigned)(a.tiles_m * a.tiles_n), 512, 0, st>>>(a);
       break;
     case CFG_TINY:
       launch_tiny<false>(a, p.bn, st);

@@ -3,8 +3,8 @@ gemm_fp8_fp8_bf16_nt, deep-gemm-helion/.../deep_gemm_helion/fp8.py:13-29:
 (A*As) @ (B*Bs)^T with Bs [N, K/128]) against the oracle's blockwise formula
 with block_n = 1, within the north-star tolerance (1e-2 relative, 1e-3
 absolute of the bf16 result). Covers the decode kernel (M <= 48), the
-small-grid kernel, the 128x128 and 256x256 pipelined kernels, split-K, the
-generic fallback (column-major As) and ragged edges."""
+small-grid kernel, the 128x128, 256x128 and 256x256 pipelined kernels,
+split-K, the generic fallback (column-major As) and ragged edges."""
 import pytest
 import torch
 
@@ -79,6 +79,38 @@ def test_per_row_256_tiles(M, N, K, dev):
         128, 1)).T
     torch.testing.assert_close(out.float(), full.to(torch.bfloat16).float(), rtol=RTOL,
                                atol=ATOL)
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 4096, 2048), (1000, 7000, 1536), (256, 28672, 1024),
+                                   (1537, 4096, 512)])
+def test_per_row_256x128_tiles(M, N, K, dev):
+    """Grids whose 256x128 tiles fit one wave of workgroups while 128x128
+    tiles need two or more: the per-row 256x128 kernel, with ragged edges, a
+    K-block count (12) that leaves the second scale window half empty and a
+    last tile row of one row. Every element against torch's fp32
+    dequant-matmul, and bit for bit against row slices on the unsplit
+    per-row 128x128 kernel."""
+    from hf_kernels_helion_amd import _native
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    t = lambda bm, bn: -(-M // bm) * -(-N // bn)
+    if not t(128, 128) > cus >= t(256, 128):
+        pytest.skip(f"{M}x{N} is not a 256x128 grid on {cus} CUs")
+    print(f"deep-gemm per-row 256x128 tiles M={M} N={N} K={K}", flush=True)
+    x, Wq, Bs = _operands(M, N, K, seed=13)
+    q, s = fp8.act_quant(x.to(dev), 128)
+    Wd, Bsd = Wq.to(dev), Bs.to(dev)
+    out = dg.gemm_fp8_fp8_bf16_nt(q, Wd, s, Bsd)
+    full = (q.float() * s.repeat_interleave(128, 1)) @ (Wd.float() * Bsd.repeat_interleave(
+        128, 1)).T
+    torch.testing.assert_close(out.float(), full.to(torch.bfloat16).float(), rtol=RTOL,
+                               atol=ATOL)
+    lib = _native.load()
+    h = 128 * (cus // -(-N // 128))
+    slices = [(r0, r0 + h) for r0 in range(0, M - h, h)] + [(M - h, M)]
+    for r0, r1 in slices:
+        assert lib.fp8b_gemm_workspace_size(r1 - r0, N, K, 1, 128) == 0
+        part = dg.gemm_fp8_fp8_bf16_nt(q[r0:r1], Wd, s[r0:r1], Bsd)
+        assert torch.equal(out[r0:r1], part)
 
 
 def test_per_row_generic_fallback(dev):
