@@ -55,7 +55,8 @@ struct GemmArgs {
   // rem_tiles_m x rem_tiles_n grid of tiles twice as large (the tiles a
   // launch of rem_base workgroups on that grid left), instead of tile w:
   // 128x128 quarters of gemm_pipe256_kernel's tiles, 64x64 quarters of
-  // gemm_pipe128_kernel's.
+  // gemm_pipe128_kernel's. gemm_pipe256x128_kernel: column half w % 2 of
+  // tile rem_base + w / 2 of gemm_pipe256_kernel's grid.
   int rem_base, rem_tiles_m, rem_tiles_n;
   // gemm_pipe256_kernel<false, true> only (the gate/up GEMM that writes
   // silu(gate) * up quantised): C is the e4m3fn output [M, N/2] (row stride
@@ -1090,8 +1091,16 @@ __global__ void __launch_bounds__(512) gemm_pipe256x128_kernel(GemmArgs a) {
   const int wm = wid / NWN, wn = wid % NWN;
 
   int tm, tn;
-  tile_of_bid((int)blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
+  if (a.rem_base >= 0) {
+    // a 128-column half of one of the 256x256 tiles a gemm_pipe256_kernel
+    // launch left
+    tile_of_bid(a.rem_base + (int)blockIdx.x / 2, a.rem_tiles_m, a.rem_tiles_n, tm, tn);
+    tn = 2 * tn + ((int)blockIdx.x & 1);
+  } else {
+    tile_of_bid((int)blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
+  }
   const int m0 = tm * BM, n0 = tn * BN;
+  if (n0 >= a.N) return;  // a half past the matrix edge (whole workgroup)
 
   const int split = blockIdx.z;
   const int kb_begin = split * a.kb_per_split;
@@ -2244,6 +2253,13 @@ bool tail_quarters(int64_t t, int cus) {
   return use_tail128() && t >= cus && rest > 0 && 4 * rest <= cus;
 }
 
+// Whether launch_pipe256 runs that wave as 256x128 halves instead (more than
+// a quarter and at most half of the CUs left).
+bool tail_halves(int64_t t, int cus) {
+  const int64_t rest = t % cus;
+  return use_tile256x128() && t >= cus && 4 * rest > cus && 2 * rest <= cus;
+}
+
 // 256x128 tiles (gemm_pipe256x128_kernel) when they fit in one wave of
 // workgroups while 128x128 tiles would need two or more. Per K-block on one
 // CU a 256x128 tile takes ~0.9-1.0 us, a 128x128 tile ~0.7 and a 256x256
@@ -2450,13 +2466,19 @@ bool pipe_ok(const GemmArgs& a, const Plan& p) {
 // same arithmetic per output: MLP gate/up 3001x28672x4096 has 1344 tiles,
 // five full waves and 64 left; the 64 tiles take 35 us as quarters against
 // ~40 us as a sixth wave. FP8B_TAIL128=0 keeps the whole grid on
-// gemm_pipe256_kernel.
+// gemm_pipe256_kernel. With more than a quarter and at most half of the CUs
+// left, the wave runs as 256x128 halves on gemm_pipe256x128_kernel:
+// 4096x6144x14336 (384 tiles, 128 left) 298.9 against 326.0 us,
+// 2048x28672x4096 204.1 against 212.5; with per-row weight scales
+// 1536x14336x7168 (80 left) 175.6 against 208.1; block scales with 80 left
+// even (768x28672x14336 305.5 against 305.0).
 template <bool PR>
 void launch_pipe256(const GemmArgs& a, hipStream_t st) {
   const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
   const int cus = device_cu_count();
   const int64_t full = tiles / cus * cus, rest = tiles - full;
-  if (!tail_quarters(tiles, cus) || a.kb_per_split < a.KB) {
+  const bool quarters = tail_quarters(tiles, cus), halves = tail_halves(tiles, cus);
+  if ((!quarters && !halves) || a.kb_per_split < a.KB) {
     gemm_pipe256_kernel<PR><<<(unsigned)tiles, 512, 0, st>>>(a);
     return;
   }
@@ -2465,9 +2487,14 @@ void launch_pipe256(const GemmArgs& a, hipStream_t st) {
   r.rem_base = (int)full;
   r.rem_tiles_m = a.tiles_m;
   r.rem_tiles_n = a.tiles_n;
-  r.tiles_m = (a.M + 127) / 128;
-  r.tiles_n = (a.N + 127) / 128;
-  gemm_pipe128_kernel<64, 32, PR><<<(unsigned)(4 * rest), 512, 0, st>>>(r);
+  if (quarters) {
+    r.tiles_m = (a.M + 127) / 128;
+    r.tiles_n = (a.N + 127) / 128;
+    gemm_pipe128_kernel<64, 32, PR><<<(unsigned)(4 * rest), 512, 0, st>>>(r);
+  } else {
+    r.tiles_n = (a.N + 127) / 128;
+    gemm_pipe256x128_kernel<PR><<<(unsigned)(2 * rest), 512, 0, st>>>(r);
+  }
 }
 
 // gemm_tiny_kernel with as many waves per tile as keep about eight waves

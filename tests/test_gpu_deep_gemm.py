@@ -64,12 +64,13 @@ def test_per_row_full_check_and_fp32(dev):
     assert torch.equal(f32.to(torch.bfloat16), out)
 
 
-@pytest.mark.parametrize("M,N,K", [(2999, 4000, 1536), (4096, 4096, 8192)])
+@pytest.mark.parametrize("M,N,K", [(2999, 4000, 1536), (4096, 4096, 8192), (1500, 13900, 512)])
 def test_per_row_256_tiles(M, N, K, dev):
     """Grids that get 256x256 tiles: a partial wave with ragged edges and a
     K-block count (12) that leaves the second 8-block scale window half
-    empty, and the full 4096-square wave. Every element against torch's fp32
-    dequant-matmul."""
+    empty, the full 4096-square wave, and a grid whose last partial wave (74
+    of 330 tiles) runs as 256x128 halves, one of them past N. Every element
+    against torch's fp32 dequant-matmul."""
     print(f"deep-gemm per-row 256x256 tiles M={M} N={N} K={K}", flush=True)
     x, Wq, Bs = _operands(M, N, K, seed=7)
     q, s = fp8.act_quant(x.to(dev), 128)

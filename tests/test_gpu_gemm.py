@@ -527,6 +527,39 @@ def test_gemm_256x128_tiles(M, N, K, dev):
     assert torch.equal(out32.to(torch.float16), out16)
 
 
+@pytest.mark.parametrize("M,N,K", [(4096, 6144, 1024), (1500, 13900, 512), (768, 28672, 512)])
+def test_gemm_256_tiles_last_wave_as_halves(M, N, K, dev):
+    """Unsplit 256x256 grids whose last partial wave holds more than a
+    quarter and at most half of the CUs (4096 x 6144: 384 tiles, 128 left;
+    1500 x 13900: 330, 74 left, the last tile column 76 wide so its second
+    half lies past N; 768 x 28672: 336, 80 left) run that wave as 256x128
+    halves on gemm_pipe256x128_kernel: every element against torch's fp32
+    dequant-matmul, and bit for bit against row slices of 512 (other unsplit
+    plans)."""
+    from hf_kernels_helion_amd import _native
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    t, rest = _tiles(M, N, 256, 256), _tiles(M, N, 256, 256) % cus
+    if not (t >= cus and 4 * rest > cus and 2 * rest <= cus):
+        pytest.skip(f"{M}x{N} leaves no half-sized last wave on {cus} CUs")
+    print(f"gemm 256 tiles, last wave as halves M={M} N={N} K={K}", flush=True)
+    x = synthetic.activations(M, K, seed=M + 3 * N)
+    q, s = fp8.act_quant(x.to(dev), 128)
+    W, Bs = synthetic.weights(N, K, seed=N + 9)
+    W, Bs = W.to(dev), Bs.to(dev)
+    out = fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [128, 128], torch.bfloat16)
+    saf = s.repeat_interleave(128, 1)
+    sbf = Bs.repeat_interleave(128, 0)[:N].repeat_interleave(128, 1)
+    full = (q.float() * saf) @ (W.float() * sbf).T
+    torch.testing.assert_close(out.float(), full.to(torch.bfloat16).float(), rtol=RTOL,
+                               atol=ATOL)
+    lib = _native.load()
+    for r0 in range(0, M, 512):
+        r1 = min(r0 + 512, M)
+        assert lib.fp8b_gemm_workspace_size(r1 - r0, N, K, 128, 128) == 0
+        part = fp8.w8a8_block_fp8_matmul(q[r0:r1], W, s[r0:r1], Bs, [128, 128], torch.bfloat16)
+        assert torch.equal(out[r0:r1], part)
+
+
 def test_gemm_256x128_tiles_exact_integers(dev):
     """gemm_pipe256x128_kernel on small-integer operands with power-of-two
     scales per activation row and weight block (every product and partial
