@@ -51,7 +51,7 @@ def parse():
                    help="profile helper: run only one workload "
                         "(gemm|act_quant|decode|decode_fused|weight_quant|weight_quant_bf16|mlp|"
                         "mlp_il|mlp_gateup|"
-                        "mlp_down|medium|small|deep_gemm|deep_decode|copy)"
+                        "mlp_down|medium|small|prefill|deep_gemm|deep_decode|copy)"
                         " for --steps steps and exit without JSON")
     return p.parse_args()
 
@@ -493,7 +493,7 @@ def run_only(what, steps, warmup, torch, fp8, synthetic, dev):
     shapes = {"gemm": (4096, 4096, 8192), "medium": (2048, 2048, 4096),
               "small": (512, 512, 2048), "decode": (32, 4096, 14336),
               "decode_fused": (32, 4096, 14336), "mlp_gateup": (3001, 28672, 4096),
-              "mlp_down": (3001, 4096, 14336)}
+              "mlp_down": (3001, 4096, 14336), "prefill": (2048, 4096, 4096)}
     if what in shapes:
         M, N, K = shapes[what]
         x = _gpu_acts(M, K, 41, dev, torch)
