@@ -2414,7 +2414,6 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
   } else {
     p.cfg = CFG_128x128; p.bm = 128; p.bn = 128;
   }
-  const int64_t t = tiles(p.bm, p.bn);
   // Grids of 128x128 tiles with fewer tiles than CUs split K, keeping at
   // least four K-blocks per split, while the split grid still fits one wave
   // of workgroups (one per CU, by its LDS; a second wave costs more than the
@@ -2423,9 +2422,26 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
   // HBM traffic than the extra occupancy recovers. (A partial wave of
   // 256x256 tiles chosen by prefer_256 is not split either: the fp32
   // partials of a long-K grid cost more than the idle CUs.)
+  auto split_count = [&](int64_t t) {
+    int s = 1;
+    if (t < cus)
+      while (t * s * 2 <= cus && KB / (s * 2) >= 4) s *= 2;
+    return s;
+  };
+  // Long K: 256x128 tiles split twice as often instead, when each split
+  // keeps at least 28 K-blocks. Measured at steady clock: 512x4096x28672
+  // 68.9 against 81.9 us, 768x2048x14336 40.2 against 44.4, 1024x2048x14336
+  // 44.8 against 46.9, 256x8192x14336 44.4 against 47.0; shorter splits
+  // lost (512x2048x14336, 14 K-blocks each: 31.0 against 29.9), and so did
+  // N = 1024 (2048x1024x14336 54.2 against 47.1, 1024x1024x28672 56.0
+  // against 51.5).
+  if (p.cfg == CFG_128x128 && M >= 256 && N >= 1536 && tiles(128, 128) < cus &&
+      use_tile256x128() && KB / split_count(tiles(256, 128)) >= 28) {
+    p.cfg = CFG_256x128; p.bm = 256;
+  }
+  const int64_t t = tiles(p.bm, p.bn);
   int splits = 1;
-  if (t < cus && p.cfg == CFG_128x128)
-    while (t * splits * 2 <= cus && KB / (splits * 2) >= 4) splits *= 2;
+  if (p.cfg == CFG_128x128 || p.cfg == CFG_256x128) splits = split_count(t);
   p.kb_per_split = (KB + splits - 1) / splits;
   // Split sizes in whole scale half-windows (multiples of 4 K-blocks) keep
   // the pipelined kernels usable.
@@ -2689,7 +2705,7 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
     } else if (pipe_ok(a, p)) {
       if (p.cfg == CFG_256x256) launch_pipe256<true>(a, st);
       else if (p.cfg == CFG_256x128)
-        gemm_pipe256x128_kernel<true><<<(unsigned)(a.tiles_m * a.tiles_n), 512, 0, st>>>(a);
+        gemm_pipe256x128_kernel<true><<<dim3((unsigned)(a.tiles_m * a.tiles_n), 1, (unsigned)p.splits), 512, 0, st>>>(a);
       else launch_pipe128<64, 32, true>(a, p.splits, st);
     } else {
       return run_generic();
@@ -2731,7 +2747,7 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
       gemm_pipe192_kernel<false><<<(unsigned)(a.tiles_m * a.tiles_n), 512, 0, st>>>(a);
       break;
     case CFG_256x128:
-      gemm_pipe256x128_kernel<false><<<(unsigned)(a.tiles_m * a.tiles_n), 512, 0, st>>>(a);
+      gemm_pipe256x128_kernel<false><<<dim3((unsigned)(a.tiles_m * a.tiles_n), 1, (unsigned)p.splits), 512, 0, st>>>(a);
       break;
     case CFG_TINY:
       launch_tiny<false>(a, p.bn, st);

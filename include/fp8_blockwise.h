@@ -122,8 +122,9 @@ size_t fp8b_gemm_workspace_size(int64_t M, int64_t N, int64_t K,
  * one per GPU, held until the process ends. Shapes whose partials need more
  * (fp8b_gemm_workspace_size() above the limit) return FP8B_ERR_WORKSPACE;
  * on a 256-CU device no plan does (split grids stay within about one wave
- * of workgroups: at most 16 MiB of partials for 128x128 tiles, under 16 MiB
- * for the split-K decode kernel's 64-row or smaller tiles).
+ * of workgroups: at most 16 MiB of partials for 128x128 tiles, 32 MiB for
+ * 256x128 tiles, under 16 MiB for the split-K decode kernel's 64-row or
+ * smaller tiles).
  * Every call on a GPU shares that GPU's array: calls that overlap on one GPU
  * (other streams, other threads) race and must be serialised by the caller.
  * The stream must belong to the current device.

@@ -560,6 +560,28 @@ def test_gemm_256_tiles_last_wave_as_halves(M, N, K, dev):
         assert torch.equal(out[r0:r1], part)
 
 
+@pytest.mark.parametrize("M,N,K,block_n", [(512, 4096, 14336, 128), (768, 2000, 14336, 128),
+                                           (1024, 1536, 28672, 128), (512, 4096, 14336, 1)])
+def test_gemm_256x128_split_k(M, N, K, block_n, dev):
+    """Long-K grids below one wave of 128x128 tiles run 256x128 tiles split
+    along K (at least 28 K-blocks per split; a ragged last tile column;
+    per-row weight scales): every element against torch's fp32
+    dequant-matmul."""
+    from hf_kernels_helion_amd import _native
+    print(f"gemm 256x128 split-K M={M} N={N} K={K} block_n={block_n}", flush=True)
+    assert _native.load().fp8b_gemm_workspace_size(M, N, K, block_n, 128) > 0
+    x = synthetic.activations(M, K, seed=M + N)
+    q, s = fp8.act_quant(x.to(dev), 128)
+    W, Bs = synthetic.weights(N, K, seed=N + 5, block_n=block_n)
+    W, Bs = W.to(dev), Bs.to(dev)
+    out = fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [block_n, 128], torch.bfloat16)
+    saf = s.repeat_interleave(128, 1)
+    sbf = (Bs if block_n == 1 else Bs.repeat_interleave(128, 0)[:N]).repeat_interleave(128, 1)
+    full = (q.float() * saf) @ (W.float() * sbf).T
+    torch.testing.assert_close(out.float(), full.to(torch.bfloat16).float(), rtol=RTOL,
+                               atol=ATOL)
+
+
 def test_gemm_256x128_tiles_exact_integers(dev):
     """gemm_pipe256x128_kernel on small-integer operands with power-of-two
     scales per activation row and weight block (every product and partial

@@ -71,9 +71,11 @@ def test_noalloc_equals_workspace_entry_point_twice(dtype, dev):
 def test_noalloc_scratch_holds_every_split_plan(dev):
     """Split-K plans keep their grids within about one wave of workgroups:
     128x128 grids at most one per CU (16 MiB of fp32 partials on 256 CUs),
-    decode grids (at most 64 rows) under two per CU (under 16 MiB). Sweeps the worst cases of each over N at a long K: on
-    this device every plan fits the scratch array, or (a device with more
-    CUs) the largest is refused before any launch, with the limit named."""
+    256x128 grids one per CU (32 MiB), decode grids (at most 64 rows) under
+    two per CU (under 16 MiB). Sweeps the worst cases of each over N at a
+    long K: on this device every plan fits the scratch array, or (a device
+    with more CUs) the largest is refused before any launch, with the limit
+    named."""
     lib = _native.load()
     K = 131072
     worst, shape = 0, None
