@@ -120,7 +120,9 @@ def test_plans_split_k_only_within_one_wave():
     (MI355X, and the count assumed without a device): small grids run one
     workgroup per 32x32 tile and need no partials, for block and per-row
     weight scales; 128x128 grids split K only while the split grid still
-    fits one workgroup per CU; the decode plan splits K over the CUs."""
+    fits one workgroup per CU; long-K grids of 256x128 tiles split twice as
+    often, keeping 28 K-blocks per split; the decode plan splits K over the
+    CUs."""
     lib = _native.load()
 
     def ws(M, N, K, block_n=128):
@@ -130,7 +132,10 @@ def test_plans_split_k_only_within_one_wave():
                   (2048, 1024, 2048), (768, 768, 4096), (65, 96, 4096), (32, 4096, 4096)]:
         assert ws(*shape) == 0 and ws(*shape, block_n=1) == 0, shape
     assert ws(1536, 1536, 4096) == 0                      # 144 tiles: two ways would need two waves
-    assert ws(1024, 2048, 14336) == 2 * 1024 * 2048 * 4   # 128 tiles, two ways
+    assert ws(1024, 2048, 14336) == 4 * 1024 * 2048 * 4   # 64 tiles of 256x128, four ways
+    assert ws(512, 2048, 14336) == 4 * 512 * 2048 * 4     # 64 tiles of 128x128, four ways
+    #                                                       (eight 256x128 ways: 14 K-blocks)
+    assert ws(2048, 1024, 14336) == 2 * 2048 * 1024 * 4   # N = 1024: 128x128, two ways
     assert ws(1024, 1024, 16384) == 4 * 1024 * 1024 * 4   # 64 tiles, four ways
     assert ws(1024, 2048, 4096) == 0 and ws(960, 1024, 4096) == 0   # 64x64 tiles
     assert ws(32, 2048, 14336) == 16 * 32 * 2048 * 4      # decode: 16 column tiles x 16
