@@ -51,7 +51,7 @@ def parse():
                    help="profile helper: run only one workload "
                         "(gemm|act_quant|decode|decode_fused|weight_quant|weight_quant_bf16|mlp|"
                         "mlp_il|mlp_gateup|"
-                        "mlp_down|medium|small|prefill|deep_gemm|deep_decode|copy)"
+                        "mlp_down|medium|small|prefill|deep_gemm|deep_decode|copy|shapes)"
                         " for --steps steps and exit without JSON")
     return p.parse_args()
 
@@ -567,6 +567,51 @@ def run_only(what, steps, warmup, torch, fp8, synthetic, dev):
         w2, s2 = _gpu_weights(H, I, 51, dev, torch, synthetic)
         x = _gpu_acts(M, H, 52, dev, torch)
         fn = lambda: fp8.fp8_mlp(x, wi, si, w2, s2, gate_up_interleaved=True)
+    elif what == "shapes":
+        # the block-FP8 GEMM over LLM projection shapes against the vendor's
+        # plain fp8 GEMM (torch._scaled_mm -> hipBLASLt, one per-tensor
+        # scale) on the same operand bytes, weights MALL-resident, steady
+        # clock, both as HIP-graph replays of 10 calls (GPU time without the
+        # host dispatch): an upper bound for the planner's tile choices
+        one = torch.ones((), device=dev)
+
+        def time_events(fn, n, w, torch):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for _ in range(10):
+                    fn()
+            for _ in range(max(1, w // 10)):
+                g.replay()
+            torch.cuda.synchronize()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            reps = max(1, n // 10)
+            e0.record()
+            for _ in range(reps):
+                g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) / (10 * reps)
+        log(f"{'M':>5} {'N':>6} {'K':>6} {'block_us':>9} {'vendor_us':>10} {'ratio':>6}")
+        for (N, K) in ((4096, 4096), (28672, 4096), (4096, 14336), (6144, 4096), (8192, 8192),
+                       (2048, 7168), (7168, 2048)):
+            W, Bs = _gpu_weights(N, K, 80, dev, torch, synthetic)
+            for M in (256, 512, 1024, 2048, 4096, 8192):
+                A, As = fp8.act_quant(_gpu_acts(M, K, 81, dev, torch), 128)
+                f_b = lambda: fp8.w8a8_block_fp8_matmul(A, W, As, Bs, [128, 128],
+                                                        torch.bfloat16)
+                f_v = lambda: torch._scaled_mm(A, W.t(), scale_a=one, scale_b=one,
+                                               out_dtype=torch.bfloat16)
+                n = max(5, min(steps, int(3e-3 / (2.0 * M * N * K / 2e15))))
+                tb = min(time_events(f_b, n, warmup, torch) for _ in range(2))
+                tv = min(time_events(f_v, n, warmup, torch) for _ in range(2))
+                log(f"{M:5d} {N:6d} {K:6d} {tb * 1e3:9.1f} {tv * 1e3:10.1f} {tb / tv:6.2f}")
+                del A, As
+            del W, Bs
+        return
     else:
         raise SystemExit(f"unknown --only {what}")
     ms = time_events(fn, steps, warmup, torch)
