@@ -2437,9 +2437,14 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
   // 44.8 against 46.9, 256x8192x14336 44.4 against 47.0; shorter splits
   // lost (512x2048x14336, 14 K-blocks each: 31.0 against 29.9), and so did
   // N = 1024 (2048x1024x14336 54.2 against 47.1, 1024x1024x28672 56.0
-  // against 51.5).
-  if (p.cfg == CFG_128x128 && M >= 256 && N >= 1536 && tiles(128, 128) < cus &&
-      use_tile256x128() && KB / split_count(tiles(256, 128)) >= 28) {
+  // against 51.5). A full wave of 128x128 tiles with at least 112 K-blocks
+  // also runs as 256x128 tiles split in two: 1024x4096x14336 69.6 against
+  // 75.2 us, 2048x2048x14336 72.3 against 77.9 (at 64 K-blocks 3-5% slower,
+  // at 32 25-35% slower: the partials cost more than the smaller tiles
+  // save).
+  if (p.cfg == CFG_128x128 && M >= 256 && use_tile256x128() &&
+      ((N >= 1536 && tiles(128, 128) < cus && KB / split_count(tiles(256, 128)) >= 28) ||
+       (tiles(128, 128) == cus && KB >= 112))) {
     p.cfg = CFG_256x128; p.bm = 256;
   }
   const int64_t t = tiles(p.bm, p.bn);

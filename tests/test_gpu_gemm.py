@@ -448,9 +448,9 @@ def test_gemm_192_row_tiles_equal_other_plans(M, N, K, dev):
     wave of 256x256 tiles that 192x256 tiles still hold in one wave (1536 x
     6144: 192 against 144; 1536 x 7168: 224 against 168) run
     gemm_pipe192_kernel, ragged last tile row included. Per output its
-    arithmetic is that of every unsplit MFMA plan, so row slices of 1024
-    (which run the 128x128 or 256x128 kernels) give the same bits; sampled
-    rows against the oracle. (The gate/up GEMM with the SiLU epilogue on 192-row
+    arithmetic is that of every unsplit MFMA plan, so row slices of 1024 or
+    1280 (which run the 128x128 or 256x128 kernels unsplit) give the same
+    bits; sampled rows against the oracle. (The gate/up GEMM with the SiLU epilogue on 192-row
     tiles is checked against the plain GEMM in test_gpu_mlp.py.)"""
     from hf_kernels_helion_amd import _native
     print(f"gemm 192-row tiles M={M} N={N} K={K}", flush=True)
@@ -460,9 +460,11 @@ def test_gemm_192_row_tiles_equal_other_plans(M, N, K, dev):
     W, Bs = W.to(dev), Bs.to(dev)
     out = fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [128, 128], torch.bfloat16)
     lib = _native.load()
-    slices = [(r0, r0 + 1024) for r0 in range(0, M - 1024, 1024)] + [(M - 1024, M)]
+    # row slices of a height whose plan is unsplit (1024 rows of a long-K
+    # grid split along K on 256x128 tiles)
+    h = next(h for h in (1024, 1280, 1536) if lib.fp8b_gemm_workspace_size(h, N, K, 128, 128) == 0)
+    slices = [(r0, r0 + h) for r0 in range(0, M - h, h)] + [(M - h, M)]
     for r0, r1 in slices:
-        assert lib.fp8b_gemm_workspace_size(r1 - r0, N, K, 128, 128) == 0
         part = fp8.w8a8_block_fp8_matmul(q[r0:r1], W, s[r0:r1], Bs, [128, 128], torch.bfloat16)
         torch.testing.assert_close(out[r0:r1], part, rtol=0, atol=0)
     rows = torch.tensor([0, 191, 192, M // 2, M - 1])
@@ -561,11 +563,13 @@ def test_gemm_256_tiles_last_wave_as_halves(M, N, K, dev):
 
 
 @pytest.mark.parametrize("M,N,K,block_n", [(512, 4096, 14336, 128), (768, 2000, 14336, 128),
-                                           (1024, 1536, 28672, 128), (512, 4096, 14336, 1)])
+                                           (1024, 1536, 28672, 128), (512, 4096, 14336, 1),
+                                           (1024, 4096, 14336, 128), (2048, 2048, 14336, 1)])
 def test_gemm_256x128_split_k(M, N, K, block_n, dev):
     """Long-K grids below one wave of 128x128 tiles run 256x128 tiles split
     along K (at least 28 K-blocks per split; a ragged last tile column;
-    per-row weight scales): every element against torch's fp32
+    per-row weight scales), and so do full waves of 128x128 tiles with 112
+    K-blocks (split in two): every element against torch's fp32
     dequant-matmul."""
     from hf_kernels_helion_amd import _native
     print(f"gemm 256x128 split-K M={M} N={N} K={K} block_n={block_n}", flush=True)
