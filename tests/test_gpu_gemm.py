@@ -857,15 +857,16 @@ def test_gemm_random_shapes_large(M, N, K, block_n, dtype, dev):
     torch.testing.assert_close(out.float(), full.to(dtype).float(), rtol=RTOL, atol=ATOL)
 
 
-@pytest.mark.parametrize("M,N,K", [(512, 512, 2048), (1024, 2048, 14336), (2048, 2560, 4096),
+@pytest.mark.parametrize("M,N,K", [(512, 512, 2048), (300, 1024, 16384), (2048, 2560, 4096),
                                    (32, 4096, 14336), (4096, 4096, 1024), (64, 4096, 14336),
-                                   (2048, 4096, 2048)])
+                                   (2048, 4096, 2048), (1024, 2048, 14336), (4096, 6144, 1024)])
 def test_gemm_graph_replays(M, N, K, dev):
     """The GEMM captured in a HIP graph on each plan family (small-grid
     tiles; split-K 128x128 with its sum; a 128x128 grid whose last wave runs
     as 64x64 quarters; the split-K decode kernel; 256x256 tiles; the decode
-    kernel with 64 rows; 256x128 tiles): every replay, with eager work in
-    between, equals the eager result."""
+    kernel with 64 rows; 256x128 tiles, unsplit and split-K; a 256x256 grid
+    whose last wave runs as 256x128 halves): every replay, with eager work
+    in between, equals the eager result."""
     print(f"gemm graph M={M} N={N} K={K}", flush=True)
     x = synthetic.activations(M, K, seed=M + N + K)
     q, s = fp8.act_quant(x.to(dev), 128)

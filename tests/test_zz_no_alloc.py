@@ -2,7 +2,7 @@
 against fp8b_w8a8_block_matmul with a caller workspace, through the C ABI:
 bit for bit (same kernels, same summation order), on calls in a row that
 reuse the library's scratch array with a smaller problem second, on the
-split-K 128x128 and decode plans and a plan without split-K; the scratch
+split-K 256x128, 128x128 and decode plans and a plan without split-K; the scratch
 holds the partials of every plan on this device (plans whose partials would
 exceed it are refused with FP8B_ERR_WORKSPACE)."""
 import pytest
@@ -54,8 +54,10 @@ def _both(A, B, As, Bs, dtype):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_noalloc_equals_workspace_entry_point_twice(dtype, dev):
     """Two calls in a row through the scratch array, the second smaller (so
-    the scratch still holds the first call's partials beyond the second's),
-    then a decode shape and an unsplit one."""
+    the scratch still holds the first call's partials beyond the second's):
+    256x128 tiles split four ways (32 MiB of partials, the whole array),
+    then 128x128 tiles split eight ways; then a decode shape and an unsplit
+    one."""
     shapes = [(1024, 2048, 14336), (300, 1024, 16384), (32, 2048, 14336), (1024, 4096, 1024)]
     used = []
     for i, (M, N, K) in enumerate(shapes):
