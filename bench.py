@@ -575,7 +575,7 @@ def run_only(what, steps, warmup, torch, fp8, synthetic, dev):
         # host dispatch): an upper bound for the planner's tile choices
         one = torch.ones((), device=dev)
 
-        def time_events(fn, n, w, torch):
+        def graph_time_events(fn, n, w, torch):
             for _ in range(3):
                 fn()
             torch.cuda.synchronize()
@@ -606,8 +606,8 @@ def run_only(what, steps, warmup, torch, fp8, synthetic, dev):
                 f_v = lambda: torch._scaled_mm(A, W.t(), scale_a=one, scale_b=one,
                                                out_dtype=torch.bfloat16)
                 n = max(5, min(steps, int(3e-3 / (2.0 * M * N * K / 2e15))))
-                tb = min(time_events(f_b, n, warmup, torch) for _ in range(2))
-                tv = min(time_events(f_v, n, warmup, torch) for _ in range(2))
+                tb = min(graph_time_events(f_b, n, warmup, torch) for _ in range(2))
+                tv = min(graph_time_events(f_v, n, warmup, torch) for _ in range(2))
                 log(f"{M:5d} {N:6d} {K:6d} {tb * 1e3:9.1f} {tv * 1e3:10.1f} {tb / tv:6.2f}")
                 del A, As
             del W, Bs
