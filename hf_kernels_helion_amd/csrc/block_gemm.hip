@@ -2862,13 +2862,16 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // Act-quant then the block GEMM, as two launches on the caller's stream: the
 // quantiser writes (q, s) into the workspace and the GEMM reads them (plus
-// its own split-K partials, at the start of the workspace). Three one-launch
+// its own split-K partials, at the start of the workspace). Five one-launch
 // forms were built, checked bit-identical and measured slower at
 // 32x4096x14336 (a decode kernel quantising its bf16 K-blocks in LDS, 22 us
 // against 3.5 + 14.4 us; per-split prologue quantisation; quantisation shared
-// across workgroups through device-coherent memory): the act-quant's work
-// either repeats per column tile or needs a cross-XCD hand-off that costs what
-// the saved launch does.
+// across workgroups through device-coherent memory; per-K-block quantisation
+// one K-block ahead; the quantisation and the split-K sum shared through one
+// XCD's L2, 25.1 against 19.9 us per step): the act-quant's work either
+// repeats per column tile or waits on hand-offs that cost what the saved
+// launches do, and activation loads issued beside the weight stream wait
+// behind it.
 extern "C" size_t fp8b_act_quant_matmul_workspace_size(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 128 != 0) return 0;
   // GEMM workspace, then q [M,K] and s [M,K/128].
