@@ -1,5 +1,5 @@
-"""The C ABI driven the way the reference's Python side would bind it: the
-ctypes binding printed in INTEGRATION.md (it replaces the custom op of
+"""The C ABI driven the way the reference's Python side would bind it: a
+plain ctypes binding of include/fp8_blockwise.h (it replaces the custom op of
 finegrained-fp8-helion/torch-ext/finegrained_fp8_helion/op.py:8-11 and its
 call in __init__.py:12-14), loaded straight from the built
 libfp8_blockwise.so with no torch op in between, on real operands, against
@@ -18,7 +18,7 @@ pytestmark = pytest.mark.gpu
 
 RTOL, ATOL = 1e-2, 1e-3
 
-# ---- the binding, as INTEGRATION.md shows it --------------------------------
+# ---- the ctypes binding a maintainer of the reference would add -----------
 lib = ctypes.CDLL(str(_native.LIB_PATH))
 P, I = ctypes.c_void_p, ctypes.c_int64
 lib.fp8b_w8a8_block_matmul.argtypes = [P, I, P, I, P, I, I, P, I, I, P, I, ctypes.c_int,
