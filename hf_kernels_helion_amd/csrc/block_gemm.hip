@@ -1604,9 +1604,10 @@ __device__ __forceinline__ void wait_vmcnt_rt(int n) {
 template <int FM, bool PR = false, int NSX = 0> struct DecodeCfg {
   static constexpr int NW = 8, BN = 128, AR = 16 * FM;
   // measured: deeper rings only lengthen the start-up burst. NSX = 3 (grids
-  // above one workgroup per CU): the smaller ring lets two workgroups share
-  // a CU, so the whole grid is resident (32x28672x4096, 448 workgroups:
-  // 29.7 us against 33.7 with four stages).
+  // above one workgroup per CU, which the planner now makes only where one
+  // split less would leave 32 K-blocks per split): the smaller ring lets two
+  // workgroups share a CU, so the whole grid is resident (32x28672x4096
+  // split in two, 448 workgroups: 29.7 us against 33.7 with four stages).
   static constexpr int NS = NSX ? NSX : 4;
   static constexpr int STAGE = (BN + AR) * 128;
   static constexpr int ACT_LOADS = AR / 8;                 // 1 KiB wave-loads per K-block
@@ -2383,11 +2384,26 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
   const int64_t t128n = (N + 127) / 128;
   const bool decode64 = !per_row && M <= 64 && (t128n <= 32 || t128n >= cus);
   if (use_decode_kernel() && (M <= 48 || decode64)) {
-    // Decode path: 128 output columns per workgroup; split K until the grid
-    // covers the CUs.
+    // Decode path: 128 output columns per workgroup; split K as often as
+    // the grid still fits one workgroup per CU. Splitting once more, until
+    // the grid covers every CU, overfills it: the workgroups past the CU
+    // count share CUs on a shallower ring (or, with per-row scales, run as
+    // a second round), and the weight stream slows by more than the idle
+    // CUs cost (weights streamed from HBM: 32x7168x8192 17.7 against 20.3
+    // us, 8x13824x5120 17.8 against 20.3, 16x12800x14336 39.0 against
+    // 45.6, 32x18432x8192 unsplit on 144 CUs 42.8 against 47.7). Except
+    // where that leaves exactly 32 K-blocks per split on two or more
+    // splits, which measured 6-10% slower than the overfilled grid
+    // (16x12800x8192 31.7 against 29.0 us, 8x13824x8192 32.2 against 29.5;
+    // 33 or 34 K-blocks per split were no faster).
     p.cfg = CFG_DECODE; p.bm = (int)(((M + 15) / 16) * 16); p.bn = 128;
     const int64_t t = (N + 127) / 128;
-    int splits = t < cus ? (int)((cus + t - 1) / t) : 1;
+    int splits = 1;
+    if (t < cus) {
+      splits = (int)(cus / t);
+      if (!per_row && splits >= 2 && (KB + splits - 1) / splits == 32)
+        splits = (int)((cus + t - 1) / t);
+    }
     splits = std::max(1, std::min(splits, KB));
     p.kb_per_split = (KB + splits - 1) / splits;
     p.splits = (KB + p.kb_per_split - 1) / p.kb_per_split;

@@ -121,8 +121,9 @@ def test_plans_split_k_only_within_one_wave():
     workgroup per 32x32 tile and need no partials, for block and per-row
     weight scales; 128x128 grids split K only while the split grid still
     fits one workgroup per CU; long-K grids of 256x128 tiles split twice as
-    often, keeping 28 K-blocks per split; the decode plan splits K over the
-    CUs."""
+    often, keeping 28 K-blocks per split; the decode plan splits K as often
+    as the grid still fits one workgroup per CU, once more where block
+    scales would otherwise get exactly 32 K-blocks per split."""
     lib = _native.load()
 
     def ws(M, N, K, block_n=128):
@@ -141,6 +142,12 @@ def test_plans_split_k_only_within_one_wave():
     assert ws(32, 2048, 14336) == 16 * 32 * 2048 * 4      # decode: 16 column tiles x 16
     assert ws(32, 4096, 14336) == 8 * 32 * 4096 * 4       # decode: 32 column tiles x 8
     assert ws(64, 4096, 14336) == 8 * 64 * 4096 * 4       # decode with 64 rows
+    assert ws(32, 7168, 8192) == 4 * 32 * 7168 * 4        # 56 column tiles x 4, not 5
+    assert ws(32, 7168, 8192, block_n=1) == 4 * 32 * 7168 * 4
+    assert ws(16, 12800, 8192) == 3 * 16 * 12800 * 4      # 100 tiles: 2 splits of 32 -> 3
+    assert ws(16, 12800, 8192, block_n=1) == 2 * 16 * 12800 * 4   # per-row: 2
+    assert ws(8, 18432, 8192) == 0                        # 144 tiles, unsplit
+    assert ws(32, 28672, 4096) == 0                       # 224 tiles, unsplit
     assert ws(56, 14336, 14336) == 2 * 56 * 14336 * 4     # 112 tiles of 128x128, two ways
     assert ws(64, 28672, 4096) == 0                       # 224 tiles of 128x128
     assert ws(4096, 4096, 8192) == 0

@@ -64,6 +64,33 @@ def test_per_row_full_check_and_fp32(dev):
     assert torch.equal(f32.to(torch.bfloat16), out)
 
 
+@pytest.mark.parametrize("M,N,K,splits", [(32, 7168, 8192, 4), (16, 12800, 8192, 2),
+                                          (8, 18432, 8192, 1)])
+def test_per_row_decode_split_plans(M, N, K, splits, dev):
+    """The per-row decode plan splits K as often as keeps one workgroup per
+    CU (its four-stage ring holds one per CU): 56 column tiles x 4, 100 x 2
+    (32 K-blocks per split), 144 unsplit. Every element against torch's
+    fp32 dequant-matmul, sampled rows against the oracle."""
+    from hf_kernels_helion_amd import _native
+    print(f"deep-gemm per-row decode split plan M={M} N={N} K={K}", flush=True)
+    ws = _native.load().fp8b_gemm_workspace_size(M, N, K, 1, 128)
+    assert ws == (splits * M * N * 4 if splits > 1 else 0)
+    x, Wq, Bs = _operands(M, N, K, seed=N + 11)
+    q, s = fp8.act_quant(x.to(dev), 128)
+    Wd, Bsd = Wq.to(dev), Bs.to(dev)
+    out = dg.gemm_fp8_fp8_bf16_nt(q, Wd, s, Bsd)
+    full = (q.float() * s.repeat_interleave(128, 1)) @ (Wd.float() * Bsd.repeat_interleave(
+        128, 1)).T
+    torch.testing.assert_close(out.float(), full.to(torch.bfloat16).float(), rtol=RTOL,
+                               atol=ATOL)
+    rows = torch.tensor([0, M // 2, M - 1])
+    ref = oracle.block_gemm(_u8(q.cpu()[rows]), _u8(Wq), s.cpu()[rows].numpy(), Bs.numpy(),
+                            (1, 128))
+    torch.testing.assert_close(out[rows.to(dev)].float().cpu(),
+                               torch.from_numpy(ref).to(torch.bfloat16).float(),
+                               rtol=RTOL, atol=ATOL)
+
+
 @pytest.mark.parametrize("M,N,K", [(2999, 4000, 1536), (4096, 4096, 8192), (1500, 13900, 512)])
 def test_per_row_256_tiles(M, N, K, dev):
     """Grids that get 256x256 tiles: a partial wave with ragged edges and a

@@ -156,6 +156,33 @@ def test_gemm_decode_shape(N, dev):
     _check(out, A, B, As, Bs)
 
 
+@pytest.mark.parametrize("M,N,K,splits", [(32, 7168, 8192, 4), (16, 12800, 8192, 3),
+                                          (8, 18432, 8192, 1), (32, 28672, 4096, 1),
+                                          (24, 9216, 11264, 3)])
+def test_gemm_decode_split_plans(M, N, K, splits, dev):
+    """The decode plan's split counts: as many splits as keep one workgroup
+    per CU (56 column tiles x 4; 144 and 224 tiles unsplit, no sum kernel;
+    72 tiles x 3), and one split more, past the CU count on the three-stage
+    ring two workgroups per CU, where that would leave 32 K-blocks per split
+    (100 tiles x 3: 300 workgroups). Every element against torch's fp32
+    dequant-matmul, sampled rows against the oracle."""
+    from hf_kernels_helion_amd import _native
+    print(f"gemm decode split plan M={M} N={N} K={K} splits={splits}", flush=True)
+    ws = _native.load().fp8b_gemm_workspace_size(M, N, K, 128, 128)
+    assert ws == (splits * M * N * 4 if splits > 1 else 0)
+    A, B, As, Bs = _operands(M, N, K, seed=N + K, outliers=0.01)
+    Ad, Bd, Asd, Bsd = A.to(dev), B.to(dev), As.to(dev), Bs.to(dev)
+    out = fp8.w8a8_block_fp8_matmul(Ad, Bd, Asd, Bsd, [128, 128], torch.bfloat16)
+    full = (Ad.float() * Asd.repeat_interleave(128, 1)) @ (
+        Bd.float() * Bsd.repeat_interleave(128, 0)[:N].repeat_interleave(128, 1)[:, :K]).T
+    torch.testing.assert_close(out.float(), full.to(torch.bfloat16).float(), rtol=RTOL,
+                               atol=ATOL)
+    rows = torch.tensor([0, M // 2, M - 1])
+    _check(out, A[rows], B, As[rows], Bs, rows=rows)
+    assert torch.equal(fp8.w8a8_block_fp8_matmul(Ad, Bd, Asd, Bsd, [128, 128], torch.bfloat16),
+                       out)
+
+
 @pytest.mark.parametrize("M,N,K,outliers", [(2048, 2048, 4096, 0.01), (4096, 4096, 8192, 0.0)])
 def test_gemm_large_sampled_rows(M, N, K, outliers, dev):
     """Benchmark sizes: every row checked against torch's fp32 dequant-matmul
@@ -365,7 +392,7 @@ def test_gemm_partial_last_wave_on_128_tiles(M, N, K, block_n, dev):
 def test_gemm_49_to_64_rows_past_small_grids(M, N, K, dev):
     """49..64 rows beyond the small-grid rules: the decode kernel with 64
     activation rows (few or many 128-column tiles: split-K over the CUs, or
-    448 workgroups two per CU) or 128x128 tiles with half their rows idle
+    224 workgroups unsplit) or 128x128 tiles with half their rows idle
     (split-K 2 ways, or one partial wave). Every element against torch's
     fp32 dequant-matmul, sampled rows against the oracle; unit-scale small
     integers give the exact product."""
