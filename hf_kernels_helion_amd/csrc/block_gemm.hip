@@ -2320,7 +2320,9 @@ bool tiny_grid(int64_t t32, int KB, int cus) {
 //    12.0 against 19.8, 256x7168x2048 14.4 against 21.3; at 224 K-blocks
 //    38.6 against 21.7 for 128x1024x28672, at 112 20.9 against 19.2 for
 //    128x2048x14336), and at 49..64 rows, replacing the 64x128 tiles
-//    (64x2048x4096 8.1 against 12.6; at 112 K-blocks 24.2 against 23.6);
+//    (64x2048x4096 8.1 against 12.6; at 112 K-blocks 24.2 against 23.6;
+//    with block scales make_plan keeps only grids below 48 K-blocks or of at
+//    most one tile per CU here, the rest stream faster on the decode kernel);
 //    at up to 48 rows up to 32 K-blocks,
 //    replacing the decode and skinny kernels, once the grid has a tile per
 //    CU (32x14336x4096 16.4 against 19.2; 1x8192x4096 9.5 against 11.3;
@@ -2368,21 +2370,27 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
     p.kb_per_split = KB;
     return p;
   }
+  // 49..64 rows with block scales (weights streamed from HBM) take the
+  // decode kernel with 64 activation rows: level with 128x128 tiles (half
+  // of each tile's rows idle) within 2% (56x14336x14336 53.5 against 54.2
+  // us, 64x28672x4096 33.8 against 34.0, 64x18432x8192 50.1 against 49.3)
+  // and ahead of the 64x128 tiles of the non-pipelined kernel
+  // (64x4096x14336 19.3 against 23.5, 64x57344x2048 26.4 against 28.2). The
+  // small-grid kernel keeps short K and grids of at most one 32x32 tile per
+  // CU; from 48 K-blocks on a larger grid the decode kernel's weight stream
+  // is faster (64x8192x8192 22.9 against 27.0 us, 64x5120x8192 17.9 against
+  // 24.5, 64x6144x6144 17.5 against 20.4, 50x6144x8192 18.7 against 22.7;
+  // at 32 K-blocks 64x12288x4096 20.8 against 19.9, 56x11008x4096 19.9
+  // against 19.0; at 256 tiles 64x4096x8192 15.8 against 14.8).
+  const bool decode64 = !per_row && M > 48 && M <= 64 && use_decode_kernel();
+  const bool tiny_ok = !(decode64 && KB >= 48 && tiles(32, 32) > cus);
   int tm = 0, tn = 0;
-  if (use_tiny() && small_grid_tile(M, N, KB, cus, tm, tn)) {
+  if (use_tiny() && tiny_ok && small_grid_tile(M, N, KB, cus, tm, tn)) {
     p.cfg = CFG_TINY; p.bm = tm; p.bn = tn;
     p.splits = 1;
     p.kb_per_split = KB;
     return p;
   }
-  // 49..64 rows beyond the small-grid rules (weights streamed from HBM):
-  // the decode kernel with 64 activation rows for few or many 128-column
-  // tiles, else 128x128 tiles (half of each tile's rows idle) instead of the
-  // 64x128 tiles of the non-pipelined kernel: 64x4096x14336 19.3 us decode
-  // (21.7 on 128x128 tiles, 23.5 on 64x128), 64x57344x2048 26.4 (33.7,
-  // 28.2), 56x14336x14336 57.3 (51.7, 66.4), 64x28672x4096 33.5 (33.4, 44.1).
-  const int64_t t128n = (N + 127) / 128;
-  const bool decode64 = !per_row && M <= 64 && (t128n <= 32 || t128n >= cus);
   if (use_decode_kernel() && (M <= 48 || decode64)) {
     // Decode path: 128 output columns per workgroup; split K as often as
     // the grid still fits one workgroup per CU. Splitting once more, until

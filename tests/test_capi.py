@@ -148,8 +148,11 @@ def test_plans_split_k_only_within_one_wave():
     assert ws(16, 12800, 8192, block_n=1) == 2 * 16 * 12800 * 4   # per-row: 2
     assert ws(8, 18432, 8192) == 0                        # 144 tiles, unsplit
     assert ws(32, 28672, 4096) == 0                       # 224 tiles, unsplit
-    assert ws(56, 14336, 14336) == 2 * 56 * 14336 * 4     # 112 tiles of 128x128, two ways
-    assert ws(64, 28672, 4096) == 0                       # 224 tiles of 128x128
+    assert ws(56, 14336, 14336) == 2 * 56 * 14336 * 4     # decode: 112 column tiles x 2
+    assert ws(64, 28672, 4096) == 0                       # decode: 224 column tiles, unsplit
+    assert ws(64, 8192, 8192) == 4 * 64 * 8192 * 4        # decode, not 512 32x32 tiles
+    assert ws(64, 4096, 8192) == 0                        # 256 32x32 tiles (one per CU)
+    assert ws(64, 12288, 4096) == 0                       # 768 32x32 tiles of 32 K-blocks
     assert ws(4096, 4096, 8192) == 0
 
 

@@ -388,12 +388,14 @@ def test_gemm_partial_last_wave_on_128_tiles(M, N, K, block_n, dev):
 
 
 @pytest.mark.parametrize("M,N,K", [(64, 4096, 14336), (64, 57344, 2048), (56, 14336, 14336),
-                                   (64, 28672, 4096), (50, 2048, 14336)])
+                                   (64, 28672, 4096), (50, 2048, 14336), (64, 8192, 8192),
+                                   (50, 6144, 8192)])
 def test_gemm_49_to_64_rows_past_small_grids(M, N, K, dev):
     """49..64 rows beyond the small-grid rules: the decode kernel with 64
-    activation rows (few or many 128-column tiles: split-K over the CUs, or
-    224 workgroups unsplit) or 128x128 tiles with half their rows idle
-    (split-K 2 ways, or one partial wave). Every element against torch's
+    activation rows, split along K over the CUs (16, 32, 48, 64 or 112
+    column tiles), unsplit (224 column tiles), or two workgroups per CU (448);
+    64 x 8192 x 8192 and 50 x 6144 x 8192 would fit the small-grid kernel but
+    stream faster here. Every element against torch's
     fp32 dequant-matmul, sampled rows against the oracle; unit-scale small
     integers give the exact product."""
     print(f"gemm 49..64 rows M={M} N={N} K={K}", flush=True)
