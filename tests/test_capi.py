@@ -139,6 +139,9 @@ def test_plans_split_k_only_within_one_wave():
     assert ws(2048, 1024, 14336) == 2 * 2048 * 1024 * 4   # N = 1024: 128x128, two ways
     assert ws(1024, 1024, 16384) == 4 * 1024 * 1024 * 4   # 64 tiles, four ways
     assert ws(1024, 2048, 4096) == 0 and ws(960, 1024, 4096) == 0   # 64x64 tiles
+    assert ws(256, 8192, 2048) == 0                       # 512 64x64 tiles, 16 K-blocks
+    assert ws(256, 8192, 8192) == 2 * 256 * 8192 * 4      # 512 64x64 tiles of 64 K-blocks:
+    #                                                       128x128 tiles split two ways
     assert ws(32, 2048, 14336) == 16 * 32 * 2048 * 4      # decode: 16 column tiles x 16
     assert ws(32, 4096, 14336) == 8 * 32 * 4096 * 4       # decode: 32 column tiles x 8
     assert ws(64, 4096, 14336) == 8 * 64 * 4096 * 4       # decode with 64 rows
