@@ -51,7 +51,8 @@ def parse():
                    help="profile helper: run only one workload "
                         "(gemm|act_quant|decode|decode_fused|weight_quant|weight_quant_bf16|mlp|"
                         "mlp_il|mlp_gateup|"
-                        "mlp_down|medium|small|prefill|deep_gemm|deep_decode|copy|shapes)"
+                        "mlp_down|medium|small|prefill|deep_gemm|deep_decode|copy|shapes|"
+                        "shapes_streamed)"
                         " for --steps steps and exit without JSON")
     return p.parse_args()
 
@@ -611,6 +612,60 @@ def run_only(what, steps, warmup, torch, fp8, synthetic, dev):
                 log(f"{M:5d} {N:6d} {K:6d} {tb * 1e3:9.1f} {tv * 1e3:10.1f} {tb / tv:6.2f}")
                 del A, As
             del W, Bs
+        return
+    elif what == "shapes_streamed":
+        # decode and small-prefill shapes (M <= 256) with the weights streamed
+        # from HBM, as in a forward pass over a model's layers: each call of a
+        # HIP graph reads its own weight copy (about 600 MB of copies, past
+        # the 256 MB MALL). The block-FP8 GEMM against the vendor's plain fp8
+        # GEMM (torch._scaled_mm -> hipBLASLt, one per-tensor scale) on the
+        # same operand bytes; per call, best of four timed replays
+        one = torch.ones((), device=dev)
+
+        def graph_us(calls):
+            for c in calls:
+                c()
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for c in calls:
+                    c()
+            for _ in range(max(1, warmup // 10)):
+                g.replay()
+            torch.cuda.synchronize()
+            best = float("inf")
+            for _ in range(4):
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(5):
+                    g.replay()
+                e1.record()
+                torch.cuda.synchronize()
+                best = min(best, e0.elapsed_time(e1) * 1e3 / (5 * len(calls)))
+            return best
+
+        log(f"{'M':>5} {'N':>6} {'K':>6} {'copies':>6} {'block_us':>9} {'vendor_us':>10} {'ratio':>6}")
+        for (N, K) in ((4096, 4096), (28672, 4096), (4096, 14336), (6144, 4096), (8192, 8192),
+                       (7168, 2048), (7168, 8192), (11008, 4096)):
+            W0, Bs = _gpu_weights(N, K, 90, dev, torch, synthetic)
+            copies = max(2, (600 << 20) // (N * K))
+            Ws = [W0] + [W0.clone() for _ in range(copies - 1)]
+            for M in (1, 16, 32, 64, 128, 256):
+                A, As = fp8.act_quant(_gpu_acts(M, K, 91, dev, torch), 128)
+                tb = graph_us([
+                    (lambda W=W: fp8.w8a8_block_fp8_matmul(A, W, As, Bs, [128, 128],
+                                                           torch.bfloat16)) for W in Ws])
+                try:
+                    tv = graph_us([
+                        (lambda W=W: torch._scaled_mm(A, W.t(), scale_a=one, scale_b=one,
+                                                      out_dtype=torch.bfloat16)) for W in Ws])
+                except RuntimeError:
+                    tv = float("nan")  # the vendor GEMM rejects this M
+                log(f"{M:5d} {N:6d} {K:6d} {copies:6d} {tb:9.1f} {tv:10.1f} {tb / tv:6.2f}")
+                del A, As
+            del W0, Ws, Bs
+            torch.cuda.empty_cache()
         return
     else:
         raise SystemExit(f"unknown --only {what}")

@@ -2318,7 +2318,11 @@ bool tiny_grid(int64_t t32, int KB, int cus) {
 //    tiles per CU only up to 32 K-blocks (weights streamed: 256x8192x2048
 //    14.7 against 18.3, 1024x2048x4096 21.4 against 23.4; 48 and 64
 //    K-blocks lost: 256x8192x6144 36.6 against 30.9, 256x8192x8192 47.0
-//    against 38.2, 1024x2048x8192 37.3 against 33.8).
+//    against 38.2, 1024x2048x8192 37.3 against 33.8). Between one and two
+//    tiles per CU, with the weights streamed, only while N <= 16 M: wider
+//    grids of few rows lost (128x11008x4096 27.6 against 24.9, 128x11008x6144
+//    41.0 against 32.0, 256x6144x4096 24.7 against 22.7), 384x4096x4096
+//    (21.8 against 22.4) and 768x2048x4096 (20.9 against 22.0) gained.
 //  * 32x32 tiles (tiny_grid) up to 64 K-blocks for M > 64, replacing the
 //    split 128x128 plan (512x512x2048 5.2 against 12.9 us, 128x4096x4096
 //    12.0 against 19.8, 256x7168x2048 14.4 against 21.3; at 224 K-blocks
@@ -2344,7 +2348,8 @@ bool small_grid_tile(int64_t M, int64_t N, int KB, int cus, int& tm, int& tn) {
   const int64_t t64 = tiles(64, 64), t32 = tiles(32, 32), t16 = tiles(32, 16);
   tm = 32;
   if (M > 64 && KB >= 16 && KB <= 64 &&
-      ((t64 == 2 * c && KB <= 32) || (t64 > c && t64 < 2 * c && KB >= 24 && KB <= 48) ||
+      ((t64 == 2 * c && KB <= 32) ||
+       (t64 > c && t64 < 2 * c && KB >= 24 && KB <= 48 && N <= 16 * M) ||
        (8 * t64 >= 7 * c && t64 <= c))) {
     tm = tn = 64;
     return true;
