@@ -2365,7 +2365,7 @@ bool small_grid_tile(int64_t M, int64_t N, int KB, int cus, int& tm, int& tn) {
 }
 
 // per_row: weight scales per output row (block_n = 1, the deep-gemm layout);
-// only the decode kernel (M <= 48 for them), gemm_tiny_kernel, gemm_pipe128_kernel
+// the decode kernel, gemm_tiny_kernel, gemm_pipe128_kernel, gemm_pipe256x128_kernel
 // and gemm_pipe256_kernel implement it.
 Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
   const int KB = (int)(K / 128);
@@ -2379,8 +2379,10 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
     p.kb_per_split = KB;
     return p;
   }
-  // 49..64 rows with block scales (weights streamed from HBM) take the
-  // decode kernel with 64 activation rows: level with 128x128 tiles (half
+  // 49..64 rows (weights streamed from HBM) take the decode kernel with 64
+  // activation rows. Per-row scales: 64x8192x8192 24.5 against 31.3 us on
+  // the small-grid kernel, 64x4096x14336 22.3 against 26.7 on 128x128
+  // tiles, 50x6144x8192 20.7 against 26.6. Block scales: level with 128x128 tiles (half
   // of each tile's rows idle) within 2% (56x14336x14336 53.5 against 54.2
   // us, 64x28672x4096 33.8 against 34.0, 64x18432x8192 50.1 against 49.3)
   // and ahead of the 64x128 tiles of the non-pipelined kernel
@@ -2391,7 +2393,7 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
   // 24.5, 64x6144x6144 17.5 against 20.4, 50x6144x8192 18.7 against 22.7;
   // at 32 K-blocks 64x12288x4096 20.8 against 19.9, 56x11008x4096 19.9
   // against 19.0; at 256 tiles 64x4096x8192 15.8 against 14.8).
-  const bool decode64 = !per_row && M > 48 && M <= 64 && use_decode_kernel();
+  const bool decode64 = M > 48 && M <= 64 && use_decode_kernel();
   const bool tiny_ok = !(decode64 && KB >= 48 && tiles(32, 32) > cus);
   int tm = 0, tn = 0;
   if (use_tiny() && tiny_ok && small_grid_tile(M, N, KB, cus, tm, tn)) {
@@ -2742,7 +2744,8 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
       const int fm = (int)((M + 15) / 16);
       if (fm <= 1) gemm_decode_kernel<1, true><<<grid, 512, 0, st>>>(a);
       else if (fm == 2) gemm_decode_kernel<2, true><<<grid, 512, 0, st>>>(a);
-      else gemm_decode_kernel<3, true><<<grid, 512, 0, st>>>(a);
+      else if (fm == 3) gemm_decode_kernel<3, true><<<grid, 512, 0, st>>>(a);
+      else gemm_decode_kernel<4, true><<<grid, 512, 0, st>>>(a);
     } else if (pipe_ok(a, p)) {
       if (p.cfg == CFG_256x256) launch_pipe256<true>(a, st);
       else if (p.cfg == CFG_256x128)

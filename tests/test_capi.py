@@ -151,6 +151,7 @@ def test_plans_split_k_only_within_one_wave():
     assert ws(32, 7168, 8192, block_n=1) == 4 * 32 * 7168 * 4
     assert ws(16, 12800, 8192) == 3 * 16 * 12800 * 4      # 100 tiles: 2 splits of 32 -> 3
     assert ws(16, 12800, 8192, block_n=1) == 2 * 16 * 12800 * 4   # per-row: 2
+    assert ws(64, 8192, 8192, block_n=1) == 4 * 64 * 8192 * 4     # per-row decode, 64 rows
     assert ws(8, 18432, 8192) == 0                        # 144 tiles, unsplit
     assert ws(32, 28672, 4096) == 0                       # 224 tiles, unsplit
     assert ws(56, 14336, 14336) == 2 * 56 * 14336 * 4     # decode: 112 column tiles x 2

@@ -2,7 +2,7 @@
 gemm_fp8_fp8_bf16_nt, deep-gemm-helion/.../deep_gemm_helion/fp8.py:13-29:
 (A*As) @ (B*Bs)^T with Bs [N, K/128]) against the oracle's blockwise formula
 with block_n = 1, within the north-star tolerance (1e-2 relative, 1e-3
-absolute of the bf16 result). Covers the decode kernel (M <= 48), the
+absolute of the bf16 result). Covers the decode kernel (M <= 64), the
 small-grid kernel, the 128x128, 256x128 and 256x256 pipelined kernels,
 split-K, the generic fallback (column-major As) and ragged edges."""
 import pytest
@@ -65,11 +65,13 @@ def test_per_row_full_check_and_fp32(dev):
 
 
 @pytest.mark.parametrize("M,N,K,splits", [(32, 7168, 8192, 4), (16, 12800, 8192, 2),
-                                          (8, 18432, 8192, 1)])
+                                          (8, 18432, 8192, 1), (64, 4096, 14336, 8),
+                                          (50, 6144, 8192, 5), (64, 8192, 8192, 4)])
 def test_per_row_decode_split_plans(M, N, K, splits, dev):
     """The per-row decode plan splits K as often as keeps one workgroup per
     CU (its four-stage ring holds one per CU): 56 column tiles x 4, 100 x 2
-    (32 K-blocks per split), 144 unsplit. Every element against torch's
+    (32 K-blocks per split), 144 unsplit; with 49..64 rows (64 activation
+    rows per workgroup) 32 x 8, 48 x 5 and 64 x 4. Every element against torch's
     fp32 dequant-matmul, sampled rows against the oracle."""
     from hf_kernels_helion_amd import _native
     print(f"deep-gemm per-row decode split plan M={M} N={N} K={K}", flush=True)
@@ -197,10 +199,10 @@ def test_per_row_small_grid_tiles(M, N, K, dev):
         assert torch.equal(dg.gemm_fp8_fp8_bf16_nt(qb, Wd, sb, Bsd)[:M], out)
 
 
-@pytest.mark.parametrize("M,N,K", [(64, 4096, 32768), (1024, 2048, 14336), (3000, 1000, 2048)])
+@pytest.mark.parametrize("M,N,K", [(128, 4096, 32768), (1024, 2048, 14336), (3000, 1000, 2048)])
 def test_per_row_128_tiles_split_and_unsplit(M, N, K, dev):
     """Grids past the small-grid range on the per-row 128x128 kernel: split
-    along K (64 rows, 8 splits; 1024 x 2048 x 14336, 2 splits) and unsplit (3000 x
+    along K (128 rows, 8 splits; 1024 x 2048 x 14336, 2 splits) and unsplit (3000 x
     1000: 192 tiles). Every element against torch's fp32 dequant-matmul."""
     from hf_kernels_helion_amd import _native
     print(f"deep-gemm per-row 128x128 tiles M={M} N={N} K={K}", flush=True)
