@@ -2322,7 +2322,11 @@ bool tiny_grid(int64_t t32, int KB, int cus) {
 //    tiles per CU, with the weights streamed, only while N <= 16 M: wider
 //    grids of few rows lost (128x11008x4096 27.6 against 24.9, 128x11008x6144
 //    41.0 against 32.0, 256x6144x4096 24.7 against 22.7), 384x4096x4096
-//    (21.8 against 22.4) and 768x2048x4096 (20.9 against 22.0) gained.
+//    (21.8 against 22.4) and 768x2048x4096 (20.9 against 22.0) gained. At
+//    7/8 to one tile per CU past 32 K-blocks likewise: per-row 128x8192x8192
+//    33.2 against 30.7, 96x7168x8192 29.9 against 27.4 (block scales
+//    128x8192x8192 28.6 against 27.7), while 256x4096x8192 (N = 16 M) was
+//    level and 32 K-blocks gained (per-row 128x4096x4096 13.4 against 21.0).
 //  * 32x32 tiles (tiny_grid) up to 64 K-blocks for M > 64, replacing the
 //    split 128x128 plan (512x512x2048 5.2 against 12.9 us, 128x4096x4096
 //    12.0 against 19.8, 256x7168x2048 14.4 against 21.3; at 224 K-blocks
@@ -2350,7 +2354,7 @@ bool small_grid_tile(int64_t M, int64_t N, int KB, int cus, int& tm, int& tn) {
   if (M > 64 && KB >= 16 && KB <= 64 &&
       ((t64 == 2 * c && KB <= 32) ||
        (t64 > c && t64 < 2 * c && KB >= 24 && KB <= 48 && N <= 16 * M) ||
-       (8 * t64 >= 7 * c && t64 <= c))) {
+       (8 * t64 >= 7 * c && t64 <= c && (KB <= 32 || N <= 16 * M)))) {
     tm = tn = 64;
     return true;
   }

@@ -142,6 +142,9 @@ def test_plans_split_k_only_within_one_wave():
     assert ws(256, 8192, 2048) == 0                       # 512 64x64 tiles, 16 K-blocks
     assert ws(768, 2048, 4096) == 0                       # 384 64x64 tiles, N <= 16 M
     assert ws(128, 11008, 4096) > 0                       # 344 64x64 tiles, N > 16 M: split
+    assert ws(128, 8192, 8192) > 0                        # 256 64x64 tiles of 64 K-blocks,
+    #                                                       N > 16 M: split 128x128 tiles
+    assert ws(128, 4096, 4096) == 0 and ws(256, 4096, 8192) == 0    # 64x64 tiles
     assert ws(256, 8192, 8192) == 2 * 256 * 8192 * 4      # 512 64x64 tiles of 64 K-blocks:
     #                                                       128x128 tiles split two ways
     assert ws(32, 2048, 14336) == 16 * 32 * 2048 * 4      # decode: 16 column tiles x 16

@@ -192,7 +192,7 @@ def test_per_row_small_grid_tiles(M, N, K, dev):
     t64 = -(-M // 64) * -(-N // 64)
     kb = K // 128
     band64 = M > 64 and 16 <= kb <= 64 and (
-        (t64 == 512 and kb <= 32) or (256 < t64 < 512 and 24 <= kb <= 48 and N <= 16 * M) or 224 <= t64 <= 256)
+        (t64 == 512 and kb <= 32) or (256 < t64 < 512 and 24 <= kb <= 48 and N <= 16 * M) or (224 <= t64 <= 256 and (kb <= 32 or N <= 16 * M)))
     if not band64 and ((M + 31) // 32) * ((N + 31) // 32) > 4 * 256:
         big = 32768
         reps = (big + M - 1) // M

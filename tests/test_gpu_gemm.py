@@ -657,7 +657,7 @@ def _one_wave_per_tile(M, N, K):
     t64 = -(-M // 64) * -(-N // 64)
     kb = K // 128
     band64 = M > 64 and 16 <= kb <= 64 and (
-        (t64 == 512 and kb <= 32) or (256 < t64 < 512 and 24 <= kb <= 48 and N <= 16 * M) or 224 <= t64 <= 256)
+        (t64 == 512 and kb <= 32) or (256 < t64 < 512 and 24 <= kb <= 48 and N <= 16 * M) or (224 <= t64 <= 256 and (kb <= 32 or N <= 16 * M)))
     return not band64 and -(-M // 32) * -(-N // 32) > 4 * 256
 
 
