@@ -2398,15 +2398,16 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
   // at 32 K-blocks 64x12288x4096 20.8 against 19.9, 56x11008x4096 19.9
   // against 19.0; at 256 tiles 64x4096x8192 15.8 against 14.8).
   const bool decode64 = M > 48 && M <= 64 && use_decode_kernel();
-  // 17..48 rows with block scales and at least half as many 128-column
-  // tiles as CUs (at most two decode splits): the decode kernel streams the
-  // weights faster than the small-grid kernel's many 32x32 tiles
-  // (48x28672x2048 16.6 against 20.5 us, 48x32768x1024 10.9 against 12.8,
-  // 48x16384x4096 20.6 against 22.8, 17x28672x2048 14.0 against 15.1); with
+  // 17..48 rows and at least half as many 128-column tiles as CUs (at most
+  // two decode splits): the decode kernel streams the weights faster than
+  // the small-grid kernel's many 32x32 tiles (48x28672x2048 16.6 against
+  // 20.5 us, 48x32768x1024 10.9 against 12.8, 48x16384x4096 20.6 against
+  // 22.8, 17x28672x2048 14.0 against 15.1; per-row scales 48x28672x2048 17.8
+  // against 22.6, 48x16384x4096 22.4 against 27.1); with
   // fewer tiles the small-grid kernel keeps them (48x14336x2048 12.7
   // against 14.5, 32x14336x4096 17.3 against 18.4), and at one row it
   // stays ahead at any width (1x28672x4096 25.2 against 30.7).
-  const bool decode_wide = !per_row && M > 16 && M <= 48 && use_decode_kernel() &&
+  const bool decode_wide = M > 16 && M <= 48 && use_decode_kernel() &&
                            2 * ((N + 127) / 128) >= cus;
   const bool tiny_ok = !(decode64 && KB >= 48 && tiles(32, 32) > cus) && !decode_wide;
   int tm = 0, tn = 0;

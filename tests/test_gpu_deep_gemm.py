@@ -67,14 +67,16 @@ def test_per_row_full_check_and_fp32(dev):
 @pytest.mark.parametrize("M,N,K,splits", [(32, 7168, 8192, 4), (16, 12800, 8192, 2),
                                           (8, 18432, 8192, 1), (64, 4096, 14336, 8),
                                           (50, 6144, 8192, 5), (64, 8192, 8192, 4),
-                                          (48, 36864, 1024, 1), (17, 33024, 4224, 1)])
+                                          (48, 36864, 1024, 1), (17, 33024, 4224, 1),
+                                          (48, 28672, 2048, 1), (33, 16384, 4096, 2)])
 def test_per_row_decode_split_plans(M, N, K, splits, dev):
     """The per-row decode plan splits K as often as keeps one workgroup per
     CU (its four-stage ring holds one per CU): 56 column tiles x 4, 100 x 2
     (32 K-blocks per split), 144 unsplit; with 49..64 rows (64 activation
     rows per workgroup) 32 x 8, 48 x 5 and 64 x 4; past one workgroup per CU
     (288 and 258 column tiles, unsplit) two share a CU on the three-stage
-    ring. Every element against torch's
+    ring; 17..48 rows on 224 and 128 column tiles take it over the small-grid
+    kernel. Every element against torch's
     fp32 dequant-matmul, sampled rows against the oracle."""
     from hf_kernels_helion_amd import _native
     print(f"deep-gemm per-row decode split plan M={M} N={N} K={K}", flush=True)
