@@ -2407,8 +2407,15 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
   // fewer tiles the small-grid kernel keeps them (48x14336x2048 12.7
   // against 14.5, 32x14336x4096 17.3 against 18.4), and at one row it
   // stays ahead at any width (1x28672x4096 25.2 against 30.7).
-  const bool decode_wide = M > 16 && M <= 48 && use_decode_kernel() &&
-                           2 * ((N + 127) / 128) >= cus;
+  // Up to 16 rows only where the decode grid is unsplit (more than half as
+  // many column tiles as CUs) and K short: 1x28672x2048 13.1 against 14.1,
+  // 16x28672x2048 13.6 against 14.8, 4x32768x1536 11.7 against 12.4; at 128
+  // tiles (two splits) and at 32 K-blocks the small-grid kernel stays ahead
+  // (8x16384x2048 9.1 against 11.5, 16x28672x4096 26.4 against 30.0).
+  const int64_t t128 = (N + 127) / 128;
+  const bool decode_wide =
+      use_decode_kernel() && ((M > 16 && M <= 48 && 2 * t128 >= cus) ||
+                              (M <= 16 && 2 * t128 > cus && KB <= 16));
   const bool tiny_ok = !(decode64 && KB >= 48 && tiles(32, 32) > cus) && !decode_wide;
   int tm = 0, tn = 0;
   if (use_tiny() && tiny_ok && small_grid_tile(M, N, KB, cus, tm, tn)) {

@@ -159,14 +159,16 @@ def test_gemm_decode_shape(N, dev):
 @pytest.mark.parametrize("M,N,K,splits", [(32, 7168, 8192, 4), (16, 12800, 8192, 3),
                                           (8, 18432, 8192, 1), (32, 28672, 4096, 1),
                                           (24, 9216, 11264, 3), (48, 28672, 2048, 1),
-                                          (48, 16384, 4096, 2)])
+                                          (48, 16384, 4096, 2), (1, 28672, 2048, 1),
+                                          (16, 32768, 1536, 1)])
 def test_gemm_decode_split_plans(M, N, K, splits, dev):
     """The decode plan's split counts: as many splits as keep one workgroup
     per CU (56 column tiles x 4; 144 and 224 tiles unsplit, no sum kernel;
     72 tiles x 3), and one split more, past the CU count on the three-stage
     ring two workgroups per CU, where that would leave 32 K-blocks per split
-    (100 tiles x 3: 300 workgroups); 17..48 rows on 224 and 128 column tiles
-    take it over the small-grid kernel. Every element against torch's fp32
+    (100 tiles x 3: 300 workgroups); 17..48 rows on 224 and 128 column tiles,
+    and 1..16 rows on more than 128 with short K, take it over the
+    small-grid kernel. Every element against torch's fp32
     dequant-matmul, sampled rows against the oracle."""
     from hf_kernels_helion_amd import _native
     print(f"gemm decode split plan M={M} N={N} K={K} splits={splits}", flush=True)
