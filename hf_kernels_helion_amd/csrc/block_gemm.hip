@@ -1589,9 +1589,9 @@ __device__ __forceinline__ void wait_vmcnt_rt(int n) {
 // ---------------------------------------------------------------------------
 // Decode GEMM (M <= 16*FM <= 64): bound by the weight stream from HBM. A
 // 512-thread workgroup owns 128 weight rows (output columns n0..n0+127) and a
-// K-range of kb_per_split K-blocks; grid.z splits K so that the grid covers
-// the CUs (partials go to the workspace and splitk_reduce_kernel sums them
-// in split order). Each K-block stages 128 weight rows (a wave owns 16) and
+// K-range of kb_per_split K-blocks; grid.z splits K so that the grid fills
+// the CUs about once (partials go to the workspace and splitk_reduce_kernel
+// sums them in split order). Each K-block stages 128 weight rows (a wave owns 16) and
 // the 16*FM activation rows once for all 8 waves, so activations cost
 // 16*FM/128 of the weight bytes in L2->LDS traffic. NS LDS stages keep the
 // DMA of the next K-blocks in flight; the stage of K-block kb-1 is refilled
