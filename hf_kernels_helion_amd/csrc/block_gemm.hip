@@ -2582,7 +2582,9 @@ void launch_pipe256(const GemmArgs& a, hipStream_t st) {
 // per CU resident (two K-block slots per wave: 8448 B each for 32x32
 // tiles). Measured per waves x slots on 512x512x2048: 8x2 4.6 us, 4x2 4.6,
 // 2x2 5.8, 1x7 8.1; on 2048x1024x2048 (eight tiles per CU): 1x2 13.3, 2x2
-// 16.2, 8x2 23.1. 64x64 tiles (16896 B per slot): four waves for up to one
+// 16.2, 8x2 23.1. Four waves up to 2.5 tiles per CU (weights streamed,
+// 576 tiles: 96x6144x4096 17.1 against 18.7 us with two, 80x6144x4096 16.0
+// against 17.9; 672 tiles level, 768 tiles 16.7 with two against 17.0). 64x64 tiles (16896 B per slot): four waves for up to one
 // tile per CU, else two (1024x2048x4096: 2x2 19.1 us, 4x2 22.0, 1x2 28.9,
 // 2x3 33.0).
 template <bool PR>
@@ -2595,7 +2597,7 @@ void launch_tiny(const GemmArgs& a, int tile_n, hipStream_t st) {
     if (t <= cus) gemm_tiny_kernel<4, 4, 4, 2, PR><<<(unsigned)t, 256, 0, st>>>(a);
     else gemm_tiny_kernel<4, 4, 2, 2, PR><<<(unsigned)t, 128, 0, st>>>(a);
   } else if (t <= cus) gemm_tiny_kernel<2, 2, 8, 2, PR><<<(unsigned)t, 512, 0, st>>>(a);
-  else if (t <= 2 * (int64_t)cus) gemm_tiny_kernel<2, 2, 4, 2, PR><<<(unsigned)t, 256, 0, st>>>(a);
+  else if (2 * t <= 5 * (int64_t)cus) gemm_tiny_kernel<2, 2, 4, 2, PR><<<(unsigned)t, 256, 0, st>>>(a);
   else if (t <= 4 * (int64_t)cus) gemm_tiny_kernel<2, 2, 2, 2, PR><<<(unsigned)t, 128, 0, st>>>(a);
   else gemm_tiny_kernel<2, 2, 1, 2, PR><<<(unsigned)t, 64, 0, st>>>(a);
 }

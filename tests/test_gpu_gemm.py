@@ -642,7 +642,7 @@ def test_gemm_256x128_tiles_exact_integers(dev):
 
 
 # Small-grid shapes and the waves per 32x32 tile gemm_tiny_kernel runs them
-# with on a 256-CU MI355X (8: at most one tile per CU; 4: two; 2: four; 1:
+# with on a 256-CU MI355X (8: at most one tile per CU; 4: 2.5; 2: four; 1:
 # up to eight), ragged edges, one K-block (seven of eight waves idle), a
 # long K, 49..64 rows, decode-sized M (1, 17, 24, 32), the 64x64-tile band
 # (two waves per tile for 1024 x 2048, four for 960 x 1024) and 32x16 tiles
