@@ -160,6 +160,8 @@ def test_plans_split_k_only_within_one_wave():
     assert ws(48, 16384, 4096) == 2 * 48 * 16384 * 4      # decode over 32x32 tiles: 128 x 2
     assert ws(48, 16384, 4096, block_n=1) == 2 * 48 * 16384 * 4
     assert ws(8, 16384, 2048) == 0 and ws(16, 28672, 2048) == 0   # small-grid or unsplit
+    assert ws(96, 4096, 7168) > 0                         # 384 32x32 tiles of 56 K-blocks: split
+    assert ws(72, 5120, 7168) == 0 and ws(96, 4096, 4096) == 0     # 32x32 tiles
     assert ws(32, 14336, 4096) == 0                       # 448 32x32 tiles (112 columns)
     assert ws(56, 14336, 14336) == 2 * 56 * 14336 * 4     # decode: 112 column tiles x 2
     assert ws(64, 28672, 4096) == 0                       # decode: 224 column tiles, unsplit
