@@ -2362,8 +2362,9 @@ bool small_grid_tile(int64_t M, int64_t N, int KB, int cus, int& tm, int& tn) {
   // Past 48 K-blocks, 1 to 1.75 tiles per CU leave half the CUs with two
   // long tiles: the split 128x128 plan wins there (weights streamed, 384
   // tiles: 96x4096x7168 18.0 against 20.7 us, 80x4096x8192 18.0 against
-  // 21.2, 128x3072x8192 18.8 against 22.0; 480 tiles keep the small grid:
-  // 72x5120x7168 18.8 against 20.8).
+  // 21.2, 128x3072x8192 18.8 against 22.0; per-row scales 96x4096x7168 20.0
+  // against 23.9; 480 tiles keep the small grid: 72x5120x7168 18.8 against
+  // 20.8).
   if (M > 64 && KB > 48 && t32 > c && 4 * t32 <= 7 * c) return false;
   if (M > 48) return tiny_grid(t32, KB, cus) && KB <= 64;
   if (tiny_grid(t32, KB, cus) && t32 >= c && KB <= 32) return true;
