@@ -2591,7 +2591,8 @@ void launch_pipe256(const GemmArgs& a, hipStream_t st) {
 // 2x2 5.8, 1x7 8.1; on 2048x1024x2048 (eight tiles per CU): 1x2 13.3, 2x2
 // 16.2, 8x2 23.1. Four waves up to 2.5 tiles per CU (weights streamed,
 // 576 tiles: 96x6144x4096 17.1 against 18.7 us with two, 80x6144x4096 16.0
-// against 17.9; 672 tiles level, 768 tiles 16.7 with two against 17.0). 64x64 tiles (16896 B per slot): four waves for up to one
+// against 17.9, per-row 96x6144x4096 19.0 against 21.4; 672 tiles level,
+// 768 tiles 16.7 with two against 17.0). 64x64 tiles (16896 B per slot): four waves for up to one
 // tile per CU, else two (1024x2048x4096: 2x2 19.1 us, 4x2 22.0, 1x2 28.9,
 // 2x3 33.0).
 template <bool PR>
