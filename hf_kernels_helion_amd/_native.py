@@ -26,6 +26,27 @@ STATUS_NAMES = {
 # fp8b_dtype codes.
 F32, BF16, F16 = 0, 1, 2
 
+
+class PlanInfo(ctypes.Structure):
+    """fp8b_plan_info: what fp8b_w8a8_block_matmul launches for one call."""
+    _fields_ = [
+        ("kernel", ctypes.c_int),
+        ("tile_m", ctypes.c_int),
+        ("tile_n", ctypes.c_int),
+        ("splits", ctypes.c_int),
+        ("kb_per_split", ctypes.c_int),
+        ("waves", ctypes.c_int),
+        ("ring", ctypes.c_int),
+        ("workgroups", ctypes.c_int64),
+        ("tail_kernel", ctypes.c_int),
+        ("tail_tile_m", ctypes.c_int),
+        ("tail_tile_n", ctypes.c_int),
+        ("tail_workgroups", ctypes.c_int64),
+        ("reduce", ctypes.c_int),
+        ("workspace_bytes", ctypes.c_size_t),
+        ("cu_count", ctypes.c_int),
+    ]
+
 _i64 = ctypes.c_int64
 _vp = ctypes.c_void_p
 _sz = ctypes.c_size_t
@@ -41,6 +62,11 @@ SIGNATURES = {
          _i64, _i64, _i64, _i64, _i64, _vp, _sz, _vp],
     ),
     "fp8b_gemm_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64]),
+    "fp8b_gemm_plan": (ctypes.c_int, [_i64, _i64, _i64, _i64, _i64, ctypes.c_int,
+                                      ctypes.POINTER(PlanInfo)]),
+    "fp8b_kernel_name": (ctypes.c_char_p, [ctypes.c_int]),
+    "fp8b_gate_up_plan": (ctypes.c_int, [_i64, _i64, _i64, ctypes.c_int,
+                                         ctypes.POINTER(PlanInfo)]),
     "fp8b_w8a8_block_matmul_noalloc": (
         ctypes.c_int,
         [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, ctypes.c_int,
@@ -57,6 +83,8 @@ SIGNATURES = {
         [_vp, _i64, ctypes.c_int, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp],
     ),
     "fp8b_silu_and_mul": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _i64, _vp]),
+    "fp8b_silu_and_mul_typed": (
+        ctypes.c_int, [_vp, _i64, ctypes.c_int, _vp, _i64, ctypes.c_int, _i64, _i64, _vp]),
     "fp8b_silu_and_mul_quant": (
         ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _vp]),
     "fp8b_gate_up_silu_quant": (
@@ -88,6 +116,33 @@ def load() -> ctypes.CDLL:
                 fn.argtypes = args
             _lib = lib
     return _lib
+
+
+def gemm_plan(M: int, N: int, K: int, block_n: int = 128, block_k: int = 128,
+              cu_count: int = 0) -> dict:
+    """The launches of one fp8b_w8a8_block_matmul call for contiguous, aligned
+    operands (fp8b_gemm_plan), with kernel codes turned into names.
+    cu_count <= 0 asks the current device; a positive count makes no GPU call."""
+    lib = load()
+    info = PlanInfo()
+    check(lib.fp8b_gemm_plan(M, N, K, block_n, block_k, cu_count, ctypes.byref(info)),
+          "fp8b_gemm_plan")
+    return _plan_dict(lib, info)
+
+
+def gate_up_plan(M: int, I: int, K: int, cu_count: int = 0) -> dict:
+    """The launch of one fp8b_gate_up_silu_quant call (fp8b_gate_up_plan)."""
+    lib = load()
+    info = PlanInfo()
+    check(lib.fp8b_gate_up_plan(M, I, K, cu_count, ctypes.byref(info)), "fp8b_gate_up_plan")
+    return _plan_dict(lib, info)
+
+
+def _plan_dict(lib, info) -> dict:
+    out = {name: getattr(info, name) for name, _ in PlanInfo._fields_}
+    for key in ("kernel", "tail_kernel"):
+        out[key] = lib.fp8b_kernel_name(out[key]).decode()
+    return out
 
 
 def check(status: int, what: str) -> None:

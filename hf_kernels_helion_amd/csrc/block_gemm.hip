@@ -2378,9 +2378,8 @@ bool small_grid_tile(int64_t M, int64_t N, int KB, int cus, int& tm, int& tn) {
 // per_row: weight scales per output row (block_n = 1, the deep-gemm layout);
 // the decode kernel, gemm_tiny_kernel, gemm_pipe128_kernel, gemm_pipe256x128_kernel
 // and gemm_pipe256_kernel implement it.
-Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row = false) {
+Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row, int cus) {
   const int KB = (int)(K / 128);
-  const int cus = device_cu_count();
   Plan p;
   auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
   if (M <= 48 && !use_decode_kernel() && !per_row) {
@@ -2537,16 +2536,56 @@ bool mfma_path_ok(const void* A, int64_t lda, const void* B, int64_t ldb, int64_
          M < (int64_t(1) << 30) && N < (int64_t(1) << 30) && K < (int64_t(1) << 30);
 }
 
+// Operand properties the kernel choice depends on, besides the sizes.
+struct Operands {
+  int64_t lda, ldb;
+  bool mfma;    // mfma_path_ok
+  bool scales;  // As, Bs contiguous in K with 16-byte aligned rows (scale windows)
+};
+
+// Operands of a plan query: contiguous, 16-byte aligned, K-contiguous scales.
+Operands contiguous_operands(int64_t M, int64_t N, int64_t K, int64_t block_n,
+                             int64_t block_k) {
+  Operands o;
+  o.lda = K;
+  o.ldb = K;
+  const bool per_row = block_n == 1 && block_k == 128;
+  o.mfma = K > 0 && K % 16 == 0 &&
+           mfma_path_ok(nullptr, K, nullptr, K, M, N, K, per_row ? 128 : block_n, block_k);
+  o.scales = K % 512 == 0;  // K/128 scales per row: 16-byte rows when 4 | K/128
+  return o;
+}
+
 // Preconditions of the pipelined kernels: scale windows (As, Bs contiguous
 // in K, 16-byte aligned rows, K-block counts and split sizes multiples of 4)
 // and 32-bit DMA offsets within a 256-row tile. FP8B_PIPE=0 turns them off.
-bool pipe_ok(const GemmArgs& a, const Plan& p) {
+bool pipe_ok(const Operands& o, int64_t K, const Plan& p) {
   if (!use_pipelined_kernels()) return false;
-  const bool splits_ok = p.splits == 1 || a.kb_per_split % 4 == 0;
-  return a.as_sk == 1 && a.bs_sk == 1 && a.as_sm % 4 == 0 && a.bs_sn % 4 == 0 &&
-         ((uintptr_t)a.As & 15) == 0 && ((uintptr_t)a.Bs & 15) == 0 && a.KB % 4 == 0 &&
-         splits_ok && 255 * std::max(a.lda, a.ldb) + a.K < (int64_t(1) << 32);
+  const int KB = (int)(K / 128);
+  const bool splits_ok = p.splits == 1 || p.kb_per_split % 4 == 0;
+  return o.scales && KB % 4 == 0 && splits_ok &&
+         255 * std::max(o.lda, o.ldb) + K < (int64_t(1) << 32);
 }
+
+bool tail64(int64_t t, int cus);
+
+// Everything fp8b_w8a8_block_matmul launches for one call: the main kernel
+// (grid `grid` workgroups of `waves` waves, splits along K in grid.z), an
+// optional kernel for the last partial wave of the grid, and, when split,
+// splitk_reduce_kernel. resolve() derives it from the plan and the
+// operands; launch_dispatch() runs exactly it; fp8b_gemm_plan() reports it.
+struct Dispatch {
+  int kernel = FP8B_KERNEL_GENERIC;
+  int bm = 32, bn = 32;
+  int splits = 1, kb_per_split = 0;
+  int waves = 4;
+  int ring = 0;        // gemm_decode_kernel: LDS stages
+  int64_t grid = 0;    // workgroups of the main launch (all splits)
+  int tail_kernel = FP8B_KERNEL_NONE;
+  int tail_bm = 0, tail_bn = 0;
+  int64_t tail_grid = 0;
+  bool per_row = false;
+};
 
 // One unsplit grid of 256x256 tiles on gemm_pipe256_kernel. When the tiles
 // leave a last partial wave of at most a quarter of the CUs, that wave's
@@ -2560,28 +2599,23 @@ bool pipe_ok(const GemmArgs& a, const Plan& p) {
 // 2048x28672x4096 204.1 against 212.5; with per-row weight scales
 // 1536x14336x7168 (80 left) 175.6 against 208.1; block scales with 80 left
 // even (768x28672x14336 305.5 against 305.0).
-template <bool PR>
-void launch_pipe256(const GemmArgs& a, hipStream_t st) {
-  const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
-  const int cus = device_cu_count();
+void resolve_pipe256(Dispatch& d, int64_t tiles, int KB, int cus) {
+  d.kernel = FP8B_KERNEL_PIPE256;
+  d.waves = 8;
+  d.grid = tiles;
   const int64_t full = tiles / cus * cus, rest = tiles - full;
   const bool quarters = tail_quarters(tiles, cus), halves = tail_halves(tiles, cus);
-  if ((!quarters && !halves) || a.kb_per_split < a.KB) {
-    gemm_pipe256_kernel<PR><<<(unsigned)tiles, 512, 0, st>>>(a);
-    return;
-  }
-  gemm_pipe256_kernel<PR><<<(unsigned)full, 512, 0, st>>>(a);
-  GemmArgs r = a;
-  r.rem_base = (int)full;
-  r.rem_tiles_m = a.tiles_m;
-  r.rem_tiles_n = a.tiles_n;
+  if ((!quarters && !halves) || d.kb_per_split < KB) return;
+  d.grid = full;
   if (quarters) {
-    r.tiles_m = (a.M + 127) / 128;
-    r.tiles_n = (a.N + 127) / 128;
-    gemm_pipe128_kernel<64, 32, PR><<<(unsigned)(4 * rest), 512, 0, st>>>(r);
+    d.tail_kernel = FP8B_KERNEL_PIPE128;
+    d.tail_bm = d.tail_bn = 128;
+    d.tail_grid = 4 * rest;
   } else {
-    r.tiles_n = (a.N + 127) / 128;
-    gemm_pipe256x128_kernel<PR><<<(unsigned)(2 * rest), 512, 0, st>>>(r);
+    d.tail_kernel = FP8B_KERNEL_PIPE256X128;
+    d.tail_bm = 256;
+    d.tail_bn = 128;
+    d.tail_grid = 2 * rest;
   }
 }
 
@@ -2595,19 +2629,216 @@ void launch_pipe256(const GemmArgs& a, hipStream_t st) {
 // 768 tiles 16.7 with two against 17.0). 64x64 tiles (16896 B per slot): four waves for up to one
 // tile per CU, else two (1024x2048x4096: 2x2 19.1 us, 4x2 22.0, 1x2 28.9,
 // 2x3 33.0).
+int tiny_waves(int64_t t, int tile_n, int cus) {
+  if (tile_n == 16) return 8;
+  if (tile_n == 64) return t <= cus ? 4 : 2;
+  if (t <= cus) return 8;
+  if (2 * t <= 5 * (int64_t)cus) return 4;
+  if (t <= 4 * (int64_t)cus) return 2;
+  return 1;
+}
+
+// One grid of 128x128 tiles on gemm_pipe128_kernel. When an unsplit grid
+// leaves a last partial wave that tail64 accepts, that wave's tiles run as
+// 64x64 quarters on gemm_tiny_kernel (four waves per quarter, one quarter
+// per CU): 2048x2560x4096 has 320 tiles, one full wave and 64 left.
+void resolve_pipe128(Dispatch& d, int64_t tiles, int cus) {
+  d.kernel = FP8B_KERNEL_PIPE128;
+  d.waves = 8;
+  d.grid = tiles * d.splits;
+  if (d.splits > 1 || !tail64(tiles, cus)) return;
+  const int64_t full = tiles / cus * cus, rest = tiles - full;
+  d.grid = full;
+  d.tail_kernel = FP8B_KERNEL_TINY;
+  d.tail_bm = d.tail_bn = 64;
+  d.tail_grid = 4 * rest;
+}
+
+// The launches of one GEMM call (see Dispatch) on a device with `cus` CUs.
+Dispatch resolve(int64_t M, int64_t N, int64_t K, int64_t block_n, int64_t block_k, int cus,
+                 const Operands& o) {
+  Dispatch d;
+  const bool per_row = block_n == 1 && block_k == 128;
+  d.per_row = per_row;
+  if (!o.mfma) {
+    d.bm = d.bn = 32;
+    d.grid = ((N + 31) / 32) * ((M + 31) / 32);
+    return d;  // gemm_generic_kernel
+  }
+  const int KB = (int)(K / 128);
+  Plan p = make_plan(M, N, K, per_row, cus);
+  // Leading dimensions too large for the decode kernel's 32-bit DMA offsets:
+  // the skinny kernel (64-bit addresses, no workspace) or, for per-row
+  // scales and more than 48 rows, the generic kernel.
+  if (p.cfg == CFG_DECODE && !decode_offsets_ok(o.lda, o.ldb, M)) {
+    if (per_row || M > 48) {
+      d.grid = ((N + 31) / 32) * ((M + 31) / 32);
+      return d;
+    }
+    p.cfg = CFG_SKINNY; p.bn = 16; p.splits = 1; p.kb_per_split = KB;
+  }
+  const bool pipe = pipe_ok(o, K, p);
+  // 192x256 and 256x128 tiles exist only as pipelined kernels: without
+  // their preconditions the grid goes back to 256x256 or 128x128 tiles.
+  if (p.cfg == CFG_192x256 && !pipe) { p.cfg = CFG_256x256; p.bm = 256; }
+  if (p.cfg == CFG_256x128 && !pipe) { p.cfg = CFG_128x128; p.bm = 128; }
+  d.bm = p.bm;
+  d.bn = p.bn;
+  d.splits = p.splits;
+  d.kb_per_split = p.kb_per_split;
+  const int64_t tiles = ((M + p.bm - 1) / p.bm) * ((N + p.bn - 1) / p.bn);
+  switch (p.cfg) {
+    case CFG_SKINNY:
+      d.kernel = FP8B_KERNEL_SKINNY;
+      d.bm = (int)(((M + 15) / 16) * 16);
+      d.waves = 8;
+      d.grid = (N + 15) / 16;
+      break;
+    case CFG_DECODE: {
+      d.kernel = FP8B_KERNEL_DECODE;
+      d.waves = 8;
+      d.grid = ((N + 127) / 128) * p.splits;
+      // Past one workgroup per CU, the three-stage ring lets two share a CU
+      // instead of running a second, mostly empty round. Per-row scales
+      // (up to 48 rows): 32x40960x8192 91.7 against 103.0 us, 48x36864x4096
+      // 53.4 against 58.8 (grids of several rounds, e.g. 16x128256x4096, run
+      // the same).
+      const int fm = (int)((M + 15) / 16);
+      d.ring = (d.grid > cus && (!per_row || fm <= 3)) ? 3 : 4;
+      break;
+    }
+    case CFG_TINY:
+      d.kernel = FP8B_KERNEL_TINY;
+      d.waves = tiny_waves(tiles, p.bn, cus);
+      d.grid = tiles;
+      break;
+    case CFG_256x256:
+      if (pipe) {
+        resolve_pipe256(d, tiles, KB, cus);
+      } else if (per_row) {
+        d = Dispatch();
+        d.per_row = true;
+        d.grid = ((N + 31) / 32) * ((M + 31) / 32);
+      } else {
+        d.kernel = FP8B_KERNEL_BS128;
+        d.waves = 8;
+        d.grid = tiles * p.splits;
+      }
+      break;
+    case CFG_192x256:
+      d.kernel = FP8B_KERNEL_PIPE192;
+      d.waves = 8;
+      d.grid = tiles;
+      break;
+    case CFG_256x128:
+      d.kernel = FP8B_KERNEL_PIPE256X128;
+      d.waves = 8;
+      d.grid = tiles * p.splits;
+      break;
+    default:  // CFG_128x128
+      if (pipe) {
+        resolve_pipe128(d, tiles, cus);
+      } else if (per_row) {
+        d = Dispatch();
+        d.per_row = true;
+        d.grid = ((N + 31) / 32) * ((M + 31) / 32);
+      } else {
+        d.kernel = FP8B_KERNEL_BS128;
+        d.waves = 4;
+        d.grid = tiles * p.splits;
+      }
+      break;
+  }
+  return d;
+}
+
 template <bool PR>
-void launch_tiny(const GemmArgs& a, int tile_n, hipStream_t st) {
-  const int64_t t = (int64_t)a.tiles_m * a.tiles_n;
-  const int cus = device_cu_count();
-  if (tile_n == 16) {
-    gemm_tiny_kernel<2, 1, 8, 2, PR><<<(unsigned)t, 512, 0, st>>>(a);
-  } else if (tile_n == 64) {
-    if (t <= cus) gemm_tiny_kernel<4, 4, 4, 2, PR><<<(unsigned)t, 256, 0, st>>>(a);
-    else gemm_tiny_kernel<4, 4, 2, 2, PR><<<(unsigned)t, 128, 0, st>>>(a);
-  } else if (t <= cus) gemm_tiny_kernel<2, 2, 8, 2, PR><<<(unsigned)t, 512, 0, st>>>(a);
-  else if (2 * t <= 5 * (int64_t)cus) gemm_tiny_kernel<2, 2, 4, 2, PR><<<(unsigned)t, 256, 0, st>>>(a);
-  else if (t <= 4 * (int64_t)cus) gemm_tiny_kernel<2, 2, 2, 2, PR><<<(unsigned)t, 128, 0, st>>>(a);
-  else gemm_tiny_kernel<2, 2, 1, 2, PR><<<(unsigned)t, 64, 0, st>>>(a);
+void launch_tiny(const GemmArgs& a, int tile_n, int waves, int64_t grid, hipStream_t st) {
+  const unsigned g = (unsigned)grid, thr = 64u * (unsigned)waves;
+  if (tile_n == 16) gemm_tiny_kernel<2, 1, 8, 2, PR><<<g, thr, 0, st>>>(a);
+  else if (tile_n == 64 && waves == 4) gemm_tiny_kernel<4, 4, 4, 2, PR><<<g, thr, 0, st>>>(a);
+  else if (tile_n == 64) gemm_tiny_kernel<4, 4, 2, 2, PR><<<g, thr, 0, st>>>(a);
+  else if (waves == 8) gemm_tiny_kernel<2, 2, 8, 2, PR><<<g, thr, 0, st>>>(a);
+  else if (waves == 4) gemm_tiny_kernel<2, 2, 4, 2, PR><<<g, thr, 0, st>>>(a);
+  else if (waves == 2) gemm_tiny_kernel<2, 2, 2, 2, PR><<<g, thr, 0, st>>>(a);
+  else gemm_tiny_kernel<2, 2, 1, 2, PR><<<g, thr, 0, st>>>(a);
+}
+
+template <bool PR>
+void launch_decode(const GemmArgs& a, int M, int ring, int splits, hipStream_t st) {
+  const dim3 grid((unsigned)((a.N + 127) / 128), 1, (unsigned)splits);
+  const int fm = (M + 15) / 16;
+  if (ring == 3) {
+    if (fm <= 1) gemm_decode_kernel<1, PR, 3><<<grid, 512, 0, st>>>(a);
+    else if (fm == 2) gemm_decode_kernel<2, PR, 3><<<grid, 512, 0, st>>>(a);
+    else if (fm == 3 || PR) gemm_decode_kernel<3, PR, 3><<<grid, 512, 0, st>>>(a);
+    else gemm_decode_kernel<4, false, 3><<<grid, 512, 0, st>>>(a);
+  } else {
+    if (fm <= 1) gemm_decode_kernel<1, PR><<<grid, 512, 0, st>>>(a);
+    else if (fm == 2) gemm_decode_kernel<2, PR><<<grid, 512, 0, st>>>(a);
+    else if (fm == 3) gemm_decode_kernel<3, PR><<<grid, 512, 0, st>>>(a);
+    else gemm_decode_kernel<4, PR><<<grid, 512, 0, st>>>(a);
+  }
+}
+
+// Runs the main launch and the tail launch of d (not the split-K sum).
+template <bool PR>
+void launch_dispatch(const Dispatch& d, const GemmArgs& a, hipStream_t st) {
+  const dim3 grid3((unsigned)(d.grid / d.splits), 1, (unsigned)d.splits);
+  switch (d.kernel) {
+    case FP8B_KERNEL_SKINNY: {
+      const int fm = (a.M + 15) / 16;
+      if constexpr (!PR) {
+        if (fm <= 1) gemm_skinny_kernel<1><<<(unsigned)d.grid, 512, 0, st>>>(a);
+        else if (fm == 2) gemm_skinny_kernel<2><<<(unsigned)d.grid, 512, 0, st>>>(a);
+        else gemm_skinny_kernel<3><<<(unsigned)d.grid, 512, 0, st>>>(a);
+      }
+      break;
+    }
+    case FP8B_KERNEL_DECODE:
+      launch_decode<PR>(a, a.M, d.ring, d.splits, st);
+      break;
+    case FP8B_KERNEL_TINY:
+      launch_tiny<PR>(a, d.bn, d.waves, d.grid, st);
+      break;
+    case FP8B_KERNEL_PIPE256:
+      gemm_pipe256_kernel<PR><<<(unsigned)d.grid, 512, 0, st>>>(a);
+      break;
+    case FP8B_KERNEL_PIPE192:
+      if constexpr (!PR) gemm_pipe192_kernel<false><<<(unsigned)d.grid, 512, 0, st>>>(a);
+      break;
+    case FP8B_KERNEL_PIPE256X128:
+      gemm_pipe256x128_kernel<PR><<<grid3, 512, 0, st>>>(a);
+      break;
+    case FP8B_KERNEL_PIPE128:
+      // 32x64 wave tiles (two activation and four weight fragments per
+      // K-block) measured 3-6% faster than 64x32 on 2048x2048x4096; the
+      // per-row-scale grids take 64x32
+      if constexpr (PR) gemm_pipe128_kernel<64, 32, true><<<grid3, 512, 0, st>>>(a);
+      else gemm_pipe128_kernel<32, 64, false><<<grid3, 512, 0, st>>>(a);
+      break;
+    case FP8B_KERNEL_BS128:
+      if constexpr (!PR) {
+        if (d.bm == 256) gemm_bs128_kernel<256, 256, 64, 128><<<grid3, 512, 0, st>>>(a);
+        else gemm_bs128_kernel<128, 128, 64, 64><<<grid3, 256, 0, st>>>(a);
+      }
+      break;
+    default:
+      break;
+  }
+  if (d.tail_kernel == FP8B_KERNEL_NONE) return;
+  GemmArgs r = a;
+  r.rem_base = (int)d.grid;
+  r.rem_tiles_m = a.tiles_m;
+  r.rem_tiles_n = a.tiles_n;
+  r.tiles_m = (a.M + d.tail_bm - 1) / d.tail_bm;
+  r.tiles_n = (a.N + d.tail_bn - 1) / d.tail_bn;
+  if (d.tail_kernel == FP8B_KERNEL_PIPE128)
+    gemm_pipe128_kernel<64, 32, PR><<<(unsigned)d.tail_grid, 512, 0, st>>>(r);
+  else if (d.tail_kernel == FP8B_KERNEL_PIPE256X128)
+    gemm_pipe256x128_kernel<PR><<<(unsigned)d.tail_grid, 512, 0, st>>>(r);
+  else
+    gemm_tiny_kernel<4, 4, 4, 2, PR><<<(unsigned)d.tail_grid, 256, 0, st>>>(r);
 }
 
 // Whether an unsplit grid of t 128x128 tiles runs its last partial wave as
@@ -2621,33 +2852,39 @@ bool tail64(int64_t t, int cus) {
   return use_tiny() && use_tail64() && t >= cus && rest > 0 && 4 * rest <= cus;
 }
 
-// One grid of 128x128 tiles on gemm_pipe128_kernel. When an unsplit grid
-// leaves a last partial wave that tail64 accepts, that wave's tiles run as
-// 64x64 quarters on gemm_tiny_kernel (four waves per quarter, one quarter
-// per CU): 2048x2560x4096 has 320 tiles, one full wave and 64 left.
-template <int WM, int WN, bool PR>
-void launch_pipe128(const GemmArgs& a, int splits, hipStream_t st) {
-  const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
-  const int cus = device_cu_count();
-  if (splits > 1 || !tail64(tiles, cus)) {
-    gemm_pipe128_kernel<WM, WN, PR><<<dim3((unsigned)tiles, 1, splits), 512, 0, st>>>(a);
-    return;
+const char* kernel_name(int k) {
+  switch (k) {
+    case FP8B_KERNEL_NONE: return "none";
+    case FP8B_KERNEL_GENERIC: return "gemm_generic_kernel";
+    case FP8B_KERNEL_SKINNY: return "gemm_skinny_kernel";
+    case FP8B_KERNEL_DECODE: return "gemm_decode_kernel";
+    case FP8B_KERNEL_TINY: return "gemm_tiny_kernel";
+    case FP8B_KERNEL_PIPE128: return "gemm_pipe128_kernel";
+    case FP8B_KERNEL_PIPE256: return "gemm_pipe256_kernel";
+    case FP8B_KERNEL_PIPE192: return "gemm_pipe192_kernel";
+    case FP8B_KERNEL_PIPE256X128: return "gemm_pipe256x128_kernel";
+    case FP8B_KERNEL_BS128: return "gemm_bs128_kernel";
+    default: return "unknown";
   }
-  const int64_t full = tiles / cus * cus, rest = tiles - full;
-  gemm_pipe128_kernel<WM, WN, PR><<<(unsigned)full, 512, 0, st>>>(a);
-  GemmArgs r = a;
-  r.rem_base = (int)full;
-  r.rem_tiles_m = a.tiles_m;
-  r.rem_tiles_n = a.tiles_n;
-  r.tiles_m = (a.M + 63) / 64;
-  r.tiles_n = (a.N + 63) / 64;
-  gemm_tiny_kernel<4, 4, 4, 2, PR><<<(unsigned)(4 * rest), 256, 0, st>>>(r);
 }
 
-template <int BM, int BN, int WM, int WN>
-void launch_cfg(const GemmArgs& a, int splits, hipStream_t st) {
-  dim3 grid(a.tiles_m * a.tiles_n, 1, splits);
-  gemm_bs128_kernel<BM, BN, WM, WN><<<grid, (BM / WM) * (BN / WN) * 64, 0, st>>>(a);
+// Operands of a call, as resolve() sees them.
+Operands call_operands(const void* A, int64_t lda, const void* B, int64_t ldb, const float* As,
+                       int64_t as_sm, int64_t as_sk, const float* Bs, int64_t bs_sn,
+                       int64_t bs_sk, int64_t M, int64_t N, int64_t K, int64_t block_n,
+                       int64_t block_k) {
+  const bool per_row = block_n == 1 && block_k == 128;
+  Operands o;
+  o.lda = lda;
+  o.ldb = ldb;
+  o.mfma = mfma_path_ok(A, lda, B, ldb, M, N, K, per_row ? 128 : block_n, block_k);
+  o.scales = as_sk == 1 && bs_sk == 1 && as_sm % 4 == 0 && bs_sn % 4 == 0 &&
+             ((uintptr_t)As & 15) == 0 && ((uintptr_t)Bs & 15) == 0;
+  return o;
+}
+
+bool plan_args_ok(int64_t M, int64_t N, int64_t K, int64_t block_n, int64_t block_k) {
+  return M > 0 && N > 0 && K > 0 && block_n > 0 && block_k > 0;
 }
 
 }  // namespace
@@ -2658,9 +2895,42 @@ extern "C" size_t fp8b_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int6
   if (M <= 0 || N <= 0 || K <= 0 || (block_n != 128 && !per_row) || block_k != 128 ||
       K % 128 != 0)
     return 0;
-  const Plan p = make_plan(M, N, K, per_row);
+  const Plan p = make_plan(M, N, K, per_row, device_cu_count());
   if (p.splits <= 1) return 0;
   return (size_t)p.splits * (size_t)M * (size_t)N * sizeof(float);
+}
+
+extern "C" const char* fp8b_kernel_name(int kernel) { return kernel_name(kernel); }
+
+extern "C" int fp8b_gemm_plan(int64_t M, int64_t N, int64_t K, int64_t block_n, int64_t block_k,
+                              int cu_count, fp8b_plan_info* plan) {
+  if (!plan) {
+    set_error("fp8b_gemm_plan: null plan");
+    return FP8B_ERR_NULL;
+  }
+  if (!plan_args_ok(M, N, K, block_n, block_k)) {
+    set_error("fp8b_gemm_plan: need M, N, K, block_n, block_k > 0");
+    return FP8B_ERR_DIMS;
+  }
+  const int cus = cu_count > 0 ? cu_count : device_cu_count();
+  const Dispatch d = resolve(M, N, K, block_n, block_k, cus,
+                             contiguous_operands(M, N, K, block_n, block_k));
+  plan->kernel = d.kernel;
+  plan->tile_m = d.bm;
+  plan->tile_n = d.bn;
+  plan->splits = d.splits;
+  plan->kb_per_split = d.kb_per_split;
+  plan->waves = d.waves;
+  plan->ring = d.ring;
+  plan->workgroups = d.grid;
+  plan->tail_kernel = d.tail_kernel;
+  plan->tail_tile_m = d.tail_bm;
+  plan->tail_tile_n = d.tail_bn;
+  plan->tail_workgroups = d.tail_grid;
+  plan->reduce = d.splits > 1 ? 1 : 0;
+  plan->workspace_bytes = d.splits > 1 ? (size_t)d.splits * (size_t)M * (size_t)N * sizeof(float) : 0;
+  plan->cu_count = cus;
+  return FP8B_OK;
 }
 
 extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B, int64_t ldb,
@@ -2689,14 +2959,21 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
   hipStream_t st = (hipStream_t)stream;
   const size_t esz = out_dtype == FP8B_F32 ? 4 : 2;
 
-  auto run_generic = [&]() -> int {
+  // block_n = 1 (per-row weight scales, the deep-gemm layout) with
+  // block_k = 128 has MFMA kernels too.
+  const bool per_row = block_n == 1 && block_k == 128;
+  const Dispatch d = resolve(M, N, K, block_n, block_k, device_cu_count(),
+                             call_operands(A, lda, B, ldb, As, as_sm, as_sk, Bs, bs_sn, bs_sk, M,
+                                           N, K, block_n, block_k));
+
+  if (d.kernel == FP8B_KERNEL_GENERIC) {
     GenericArgs g;
     g.A = (const uint8_t*)A; g.B = (const uint8_t*)B; g.As = As; g.Bs = Bs; g.C = C;
     g.lda = lda; g.ldb = ldb; g.as_sm = as_sm; g.as_sk = as_sk; g.bs_sn = bs_sn;
     g.bs_sk = bs_sk; g.ldc = ldc; g.M = M; g.N = N; g.K = K; g.block_n = block_n;
     g.block_k = block_k; g.out_dtype = out_dtype;
     dim3 grid((unsigned)((N + 31) / 32), (unsigned)((M + 31) / 32));
-    if (grid.y > 65535) {
+    if ((M + 31) / 32 > 65535) {
       set_error("fp8b_w8a8_block_matmul: M too large for the generic kernel");
       return FP8B_ERR_DIMS;
     }
@@ -2706,15 +2983,9 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
       return FP8B_ERR_LAUNCH;
     }
     return FP8B_OK;
-  };
-  // block_n = 1 (per-row weight scales, the deep-gemm layout) with
-  // block_k = 128 has MFMA kernels too.
-  const bool per_row = block_n == 1 && block_k == 128;
-  if (!mfma_path_ok(A, lda, B, ldb, M, N, K, per_row ? 128 : block_n, block_k))
-    return run_generic();
+  }
 
-  const Plan p0 = make_plan(M, N, K, per_row);
-  const size_t need = p0.splits > 1 ? (size_t)p0.splits * M * N * sizeof(float) : 0;
+  const size_t need = d.splits > 1 ? (size_t)d.splits * M * N * sizeof(float) : 0;
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
     set_error("fp8b_w8a8_block_matmul: workspace smaller than fp8b_gemm_workspace_size()");
     return FP8B_ERR_WORKSPACE;
@@ -2723,142 +2994,41 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
     set_error("fp8b_w8a8_block_matmul: workspace must be 16-byte aligned");
     return FP8B_ERR_ALIGN;
   }
+  const int64_t tiles_m = (M + d.bm - 1) / d.bm, tiles_n = (N + d.bn - 1) / d.bn;
+  if (tiles_m * tiles_n >= (int64_t(1) << 31)) {
+    set_error("fp8b_w8a8_block_matmul: too many output tiles for one launch");
+    return FP8B_ERR_DIMS;
+  }
   // Vector stores: 4 fp32 (16 B) for fp32 C and split-K partials, 8 x 16-bit
   // (16 B) for bf16/fp16 C.
   const bool c_vec = esz == 4 ? (ldc % 4 == 0 && ((uintptr_t)C & 15) == 0)
                               : (ldc % 8 == 0 && ((uintptr_t)C & 15) == 0);
   const bool ws_vec = (N % 4 == 0);
-  auto make_args = [&](const Plan& p) {
-    GemmArgs a;
-    a.A = (const uint8_t*)A; a.B = (const uint8_t*)B; a.As = As; a.Bs = Bs; a.C = C;
-    a.ws = (float*)workspace;
-    a.lda = lda; a.ldb = ldb; a.as_sm = as_sm; a.as_sk = as_sk; a.bs_sn = bs_sn;
-    a.bs_sk = bs_sk; a.ldc = ldc; a.M = (int)M; a.N = (int)N; a.K = (int)K;
-    a.KB = (int)(K / 128);
-    a.kb_per_split = p.kb_per_split;
-    a.tiles_m = (int)((M + p.bm - 1) / p.bm);
-    a.tiles_n = (int)((N + p.bn - 1) / p.bn);
-    a.out_dtype = out_dtype;
-    a.rem_base = -1; a.rem_tiles_m = 0; a.rem_tiles_n = 0;
-    a.Sq = nullptr; a.sq_sm = 0; a.sq_sg = 0;
-    a.vec_store = (p.splits > 1) ? (ws_vec ? 1 : 0) : (c_vec ? 1 : 0);
-    return a;
-  };
+  GemmArgs a;
+  a.A = (const uint8_t*)A; a.B = (const uint8_t*)B; a.As = As; a.Bs = Bs; a.C = C;
+  a.ws = (float*)workspace;
+  a.lda = lda; a.ldb = ldb; a.as_sm = as_sm; a.as_sk = as_sk; a.bs_sn = bs_sn;
+  a.bs_sk = bs_sk; a.ldc = ldc; a.M = (int)M; a.N = (int)N; a.K = (int)K;
+  a.KB = (int)(K / 128);
+  a.kb_per_split = d.kb_per_split;
+  a.tiles_m = (int)tiles_m;
+  a.tiles_n = (int)tiles_n;
+  a.out_dtype = out_dtype;
+  a.rem_base = -1; a.rem_tiles_m = 0; a.rem_tiles_n = 0;
+  a.Sq = nullptr; a.sq_sm = 0; a.sq_sg = 0;
+  a.vec_store = (d.splits > 1) ? (ws_vec ? 1 : 0) : (c_vec ? 1 : 0);
 
-  // Leading dimensions too large for the decode kernel's 32-bit DMA offsets:
-  // the skinny kernel (64-bit addresses, no workspace) or, for per-row
-  // scales and more than 48 rows, the generic kernel.
-  Plan p = p0;
-  if (p.cfg == CFG_DECODE && !decode_offsets_ok(lda, ldb, M)) {
-    if (per_row || M > 48) return run_generic();
-    p.cfg = CFG_SKINNY; p.bn = 16; p.splits = 1; p.kb_per_split = (int)(K / 128);
-  }
-  GemmArgs a = make_args(p);
-  if ((int64_t)a.tiles_m * a.tiles_n >= (int64_t(1) << 31)) {
-    set_error("fp8b_w8a8_block_matmul: too many output tiles for one launch");
-    return FP8B_ERR_DIMS;
-  }
-  // 192x256 and 256x128 tiles exist only as pipelined kernels: without
-  // their preconditions the grid goes back to 256x256 or 128x128 tiles.
-  if (p.cfg == CFG_192x256 && !pipe_ok(a, p)) {
-    p.cfg = CFG_256x256; p.bm = 256;
-    a = make_args(p);
-  }
-  if (p.cfg == CFG_256x128 && !pipe_ok(a, p)) {
-    p.cfg = CFG_128x128; p.bm = 128;
-    a = make_args(p);
-  }
-  if (per_row) {
-    if (p.cfg == CFG_TINY) {
-      launch_tiny<true>(a, p.bn, st);
-    } else if (p.cfg == CFG_DECODE) {
-      const dim3 grid((unsigned)((N + 127) / 128), 1, (unsigned)p.splits);
-      const int fm = (int)((M + 15) / 16);
-      // Past one workgroup per CU, the three-stage ring (up to 48 rows) lets
-      // two share a CU instead of running a second, mostly empty round:
-      // 32x40960x8192 91.7 against 103.0 us, 48x36864x4096 53.4 against 58.8
-      // (grids of several rounds, e.g. 16x128256x4096, run the same).
-      if ((int64_t)grid.x * grid.z > device_cu_count() && fm <= 3) {
-        if (fm <= 1) gemm_decode_kernel<1, true, 3><<<grid, 512, 0, st>>>(a);
-        else if (fm == 2) gemm_decode_kernel<2, true, 3><<<grid, 512, 0, st>>>(a);
-        else gemm_decode_kernel<3, true, 3><<<grid, 512, 0, st>>>(a);
-      } else if (fm <= 1) gemm_decode_kernel<1, true><<<grid, 512, 0, st>>>(a);
-      else if (fm == 2) gemm_decode_kernel<2, true><<<grid, 512, 0, st>>>(a);
-      else if (fm == 3) gemm_decode_kernel<3, true><<<grid, 512, 0, st>>>(a);
-      else gemm_decode_kernel<4, true><<<grid, 512, 0, st>>>(a);
-    } else if (pipe_ok(a, p)) {
-      if (p.cfg == CFG_256x256) launch_pipe256<true>(a, st);
-      else if (p.cfg == CFG_256x128)
-        gemm_pipe256x128_kernel<true><<<dim3((unsigned)(a.tiles_m * a.tiles_n), 1, (unsigned)p.splits), 512, 0, st>>>(a);
-      else launch_pipe128<64, 32, true>(a, p.splits, st);
-    } else {
-      return run_generic();
-    }
-  } else switch (p.cfg) {
-    case CFG_SKINNY: {
-      const dim3 grid((unsigned)((N + 15) / 16));
-      const int fm = (int)((M + 15) / 16);
-      if (fm <= 1) gemm_skinny_kernel<1><<<grid, 512, 0, st>>>(a);
-      else if (fm == 2) gemm_skinny_kernel<2><<<grid, 512, 0, st>>>(a);
-      else gemm_skinny_kernel<3><<<grid, 512, 0, st>>>(a);
-      break;
-    }
-    case CFG_DECODE: {
-      const dim3 grid((unsigned)((N + 127) / 128), 1, (unsigned)p.splits);
-      const int fm = (int)((M + 15) / 16);
-      if ((int64_t)grid.x * grid.z > device_cu_count()) {
-        if (fm <= 1) gemm_decode_kernel<1, false, 3><<<grid, 512, 0, st>>>(a);
-        else if (fm == 2) gemm_decode_kernel<2, false, 3><<<grid, 512, 0, st>>>(a);
-        else if (fm == 3) gemm_decode_kernel<3, false, 3><<<grid, 512, 0, st>>>(a);
-        else gemm_decode_kernel<4, false, 3><<<grid, 512, 0, st>>>(a);
-      } else {
-        if (fm <= 1) gemm_decode_kernel<1, false><<<grid, 512, 0, st>>>(a);
-        else if (fm == 2) gemm_decode_kernel<2, false><<<grid, 512, 0, st>>>(a);
-        else if (fm == 3) gemm_decode_kernel<3, false><<<grid, 512, 0, st>>>(a);
-        else gemm_decode_kernel<4, false><<<grid, 512, 0, st>>>(a);
-      }
-      break;
-    }
-    case CFG_256x256: {
-      if (pipe_ok(a, p)) {
-        launch_pipe256<false>(a, st);
-      } else {
-        launch_cfg<256, 256, 64, 128>(a, p.splits, st);
-      }
-      break;
-    }
-    case CFG_192x256:
-      gemm_pipe192_kernel<false><<<(unsigned)(a.tiles_m * a.tiles_n), 512, 0, st>>>(a);
-      break;
-    case CFG_256x128:
-      gemm_pipe256x128_kernel<false><<<dim3((unsigned)(a.tiles_m * a.tiles_n), 1, (unsigned)p.splits), 512, 0, st>>>(a);
-      break;
-    case CFG_TINY:
-      launch_tiny<false>(a, p.bn, st);
-      break;
-    case CFG_128x128: {
-      if (pipe_ok(a, p)) {
-        // 32x64 wave tiles (two activation and four weight fragments per
-        // K-block) measured 3-6% faster than 64x32 on 2048x2048x4096
-        launch_pipe128<32, 64, false>(a, p.splits, st);
-      } else {
-        launch_cfg<128, 128, 64, 64>(a, p.splits, st);
-      }
-      break;
-    }
-    default:
-      set_error("fp8b_w8a8_block_matmul: no kernel for this plan");
-      return FP8B_ERR_LAUNCH;
-  }
+  if (per_row) launch_dispatch<true>(d, a, st);
+  else launch_dispatch<false>(d, a, st);
   if (hipGetLastError() != hipSuccess) {
     set_error("fp8b_w8a8_block_matmul: MFMA kernel launch failed");
     return FP8B_ERR_LAUNCH;
   }
-  if (p.splits > 1) {
+  if (d.splits > 1) {
     GemmArgs r = a;
     r.vec_store = (ws_vec && c_vec) ? 1 : 0;
     const int64_t quads = M * ((N + 3) / 4);
-    splitk_reduce_kernel<<<(unsigned)((quads + 255) / 256), 256, 0, st>>>(r, p.splits);
+    splitk_reduce_kernel<<<(unsigned)((quads + 255) / 256), 256, 0, st>>>(r, d.splits);
     if (hipGetLastError() != hipSuccess) {
       set_error("fp8b_w8a8_block_matmul: split-K reduce launch failed");
       return FP8B_ERR_LAUNCH;
@@ -2910,14 +3080,24 @@ extern "C" int fp8b_w8a8_block_matmul_noalloc(const void* A, int64_t lda, const 
                                               int64_t bs_sk, void* C, int64_t ldc, int out_dtype,
                                               int64_t M, int64_t N, int64_t K, int64_t block_n,
                                               int64_t block_k, void* stream) {
-  // Argument errors first, with the same codes and texts as the allocating
-  // entry point (it returns before touching the workspace for all of them).
+  // Argument and null-pointer errors first, with the same codes and texts as
+  // the allocating entry point (it returns before touching the workspace for
+  // all of them).
   if (M < 0 || N < 0 || K < 0 || lda < K || ldb < K || ldc < N || block_n <= 0 ||
       block_k <= 0 || (out_dtype != FP8B_F32 && out_dtype != FP8B_BF16 &&
-                       out_dtype != FP8B_F16) || M == 0 || N == 0)
+                       out_dtype != FP8B_F16) || M == 0 || N == 0 || !C ||
+      (K > 0 && (!A || !B || !As || !Bs)))
     return fp8b_w8a8_block_matmul(A, lda, B, ldb, As, as_sm, as_sk, Bs, bs_sn, bs_sk, C, ldc,
                                   out_dtype, M, N, K, block_n, block_k, nullptr, 0, stream);
-  const size_t need = fp8b_gemm_workspace_size(M, N, K, block_n, block_k);
+  // The plan the allocating entry point makes for these operands: the
+  // generic kernel and unsplit plans need no scratch (whatever the plan for
+  // aligned operands would need).
+  const Dispatch d = resolve(M, N, K, block_n, block_k, device_cu_count(),
+                             call_operands(A, lda, B, ldb, As, as_sm, as_sk, Bs, bs_sn, bs_sk, M,
+                                           N, K, block_n, block_k));
+  const size_t need = d.kernel != FP8B_KERNEL_GENERIC && d.splits > 1
+                          ? (size_t)d.splits * (size_t)M * (size_t)N * sizeof(float)
+                          : 0;
   if (need > (size_t)FP8B_NOALLOC_SCRATCH_BYTES) {
     set_error("fp8b_w8a8_block_matmul_noalloc: this shape's split-K partials need more than "
               "FP8B_NOALLOC_SCRATCH_BYTES (32 MiB); use fp8b_w8a8_block_matmul with a workspace");
@@ -2995,6 +3175,42 @@ extern "C" int fp8b_act_quant_matmul(const void* x, int64_t ldx, const void* B, 
                                 K, 128, 128, gemm ? workspace : nullptr, gemm, stream);
 }
 
+namespace {
+// Tile rows of the fused gate/up kernel: 192 where 192x256 tiles fill the
+// waves clearly better than 256x256 ones (prefer_192; no quarter tiles for
+// the last wave, whose SWIGLU epilogue needs whole gate/up column pairs).
+bool gate_up_tile192(int64_t M, int64_t I, int cus) {
+  const int64_t tn = 2 * I / 256;
+  return prefer_192(((M + 255) / 256) * tn, ((M + 191) / 192) * tn, cus, false);
+}
+}  // namespace
+
+extern "C" int fp8b_gate_up_plan(int64_t M, int64_t I, int64_t K, int cu_count,
+                                 fp8b_plan_info* plan) {
+  if (!plan) {
+    set_error("fp8b_gate_up_plan: null plan");
+    return FP8B_ERR_NULL;
+  }
+  if (M <= 0 || I <= 0 || I % 128 != 0 || K <= 0 || K % 512 != 0) {
+    set_error("fp8b_gate_up_plan: need M > 0, I a positive multiple of 128 and K a positive "
+              "multiple of 512");
+    return FP8B_ERR_DIMS;
+  }
+  const int cus = cu_count > 0 ? cu_count : device_cu_count();
+  const bool t192 = gate_up_tile192(M, I, cus);
+  *plan = fp8b_plan_info{};
+  plan->kernel = t192 ? FP8B_KERNEL_PIPE192 : FP8B_KERNEL_PIPE256;
+  plan->tile_m = t192 ? 192 : 256;
+  plan->tile_n = 256;
+  plan->splits = 1;
+  plan->kb_per_split = (int)(K / 128);
+  plan->waves = 8;
+  plan->workgroups = ((M + plan->tile_m - 1) / plan->tile_m) * (2 * I / 256);
+  plan->tail_kernel = FP8B_KERNEL_NONE;
+  plan->cu_count = cus;
+  return FP8B_OK;
+}
+
 extern "C" int fp8b_gate_up_silu_quant(const void* A, int64_t lda, const void* B, int64_t ldb,
                                        const float* As, int64_t as_sm, int64_t as_sk,
                                        const float* Bs, int64_t bs_sn, int64_t bs_sk, void* q,
@@ -3034,9 +3250,7 @@ extern "C" int fp8b_gate_up_silu_quant(const void* A, int64_t lda, const void* B
   a.lda = lda; a.ldb = ldb; a.as_sm = as_sm; a.as_sk = 1; a.bs_sn = bs_sn; a.bs_sk = 1;
   a.ldc = ldq; a.M = (int)M; a.N = (int)N; a.K = (int)K; a.KB = (int)(K / 128);
   a.kb_per_split = a.KB;
-  const int cus = device_cu_count();
-  const bool tile192 =
-      prefer_192(((M + 255) / 256) * (N / 256), ((M + 191) / 192) * (N / 256), cus, false);
+  const bool tile192 = gate_up_tile192(M, I, device_cu_count());
   a.tiles_m = (int)(tile192 ? (M + 191) / 192 : (M + 255) / 256);
   a.tiles_n = (int)(N / 256);
   a.out_dtype = FP8B_BF16;

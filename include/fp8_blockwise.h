@@ -112,6 +112,52 @@ int fp8b_w8a8_block_matmul(const void* A, int64_t lda,
 size_t fp8b_gemm_workspace_size(int64_t M, int64_t N, int64_t K,
                                 int64_t block_n, int64_t block_k);
 
+/* Kernels of the GEMM plans (fp8b_plan_info.kernel, .tail_kernel). */
+typedef enum fp8b_kernel {
+  FP8B_KERNEL_NONE = 0,
+  FP8B_KERNEL_GENERIC = 1,      /* SIMT fallback: any block size, unaligned operands */
+  FP8B_KERNEL_SKINNY = 2,       /* M <= 48, 16 output columns x all of K per workgroup */
+  FP8B_KERNEL_DECODE = 3,       /* M <= 64, 128 columns x a K split per workgroup */
+  FP8B_KERNEL_TINY = 4,         /* small grids: 32x32, 32x16 or 64x64 tiles */
+  FP8B_KERNEL_PIPE128 = 5,      /* pipelined 128x128 tiles */
+  FP8B_KERNEL_PIPE256 = 6,      /* pipelined 256x256 tiles */
+  FP8B_KERNEL_PIPE192 = 7,      /* pipelined 192x256 tiles */
+  FP8B_KERNEL_PIPE256X128 = 8,  /* pipelined 256x128 tiles */
+  FP8B_KERNEL_BS128 = 9         /* two-stage 128x128 / 256x256 tiles (scales not K-contiguous) */
+} fp8b_kernel;
+
+/* What fp8b_w8a8_block_matmul launches for one call. */
+typedef struct fp8b_plan_info {
+  int kernel;              /* fp8b_kernel of the main launch                     */
+  int tile_m, tile_n;      /* its output tile (rows of A x rows of B)            */
+  int splits;              /* K splits; > 1: fp32 partials + split-K sum launch  */
+  int kb_per_split;        /* 128-wide K-blocks per split                        */
+  int waves;               /* 64-lane waves per workgroup                        */
+  int ring;                /* FP8B_KERNEL_DECODE: LDS stages (else 0)            */
+  int64_t workgroups;      /* workgroups of the main launch, all splits          */
+  int tail_kernel;         /* kernel of the grid's last partial wave, or NONE    */
+  int tail_tile_m, tail_tile_n;
+  int64_t tail_workgroups;
+  int reduce;              /* 1 when the split-K sum kernel follows              */
+  size_t workspace_bytes;  /* bytes of fp32 split-K partials (0 when unsplit)     */
+  int cu_count;            /* CUs the plan was made for                          */
+} fp8b_plan_info;
+
+/*
+ * The launches fp8b_w8a8_block_matmul makes for an M x N x K problem with
+ * contiguous, 16-byte aligned A and B and K-contiguous scale rows, on a
+ * device with cu_count CUs (cu_count <= 0: the current device's). Makes no
+ * GPU call when cu_count > 0. Plays the role of the reference's AOT
+ * heuristic tables (finegrained-fp8-helion/torch-ext/finegrained_fp8_helion/
+ * _helion_aot_fp8_cuda_sm100.py:13-28, which pick a tile config by M);
+ * no entry point of the reference reports them.
+ */
+int fp8b_gemm_plan(int64_t M, int64_t N, int64_t K, int64_t block_n, int64_t block_k,
+                   int cu_count, fp8b_plan_info* plan);
+
+/* Name of an fp8b_kernel code ("gemm_pipe256_kernel", ...; "unknown"). */
+const char* fp8b_kernel_name(int kernel);
+
 /*
  * fp8b_w8a8_block_matmul without a workspace: it allocates nothing, for
  * callers that cannot call hipMalloc (code under HIP graph capture, tight
@@ -193,6 +239,18 @@ int fp8b_silu_and_mul(const void* x, int64_t ldx, void* out, int64_t ldo,
                       int64_t M, int64_t d, void* stream);
 
 /*
+ * silu_and_mul for x and out of any of FP8B_F32, FP8B_BF16, FP8B_F16 (the
+ * reference kernel is dtype-generic, act.py:20-28):
+ *   out[m,j] = TO( TX( TX(silu(fp32 x[m,j])) * x[m,d+j] ) )
+ * with TX the type of x and TO that of out, each rounding to nearest even
+ * (silu.to(b.dtype) * b in b's dtype, then .to(out.dtype)). bf16 in and out
+ * is fp8b_silu_and_mul.
+ */
+int fp8b_silu_and_mul_typed(const void* x, int64_t ldx, int x_dtype,
+                            void* out, int64_t ldo, int out_dtype,
+                            int64_t M, int64_t d, void* stream);
+
+/*
  * silu_and_mul fused with per-token-group fp8 quantisation of its result:
  * q/s as fp8b_act_quant would produce from the bf16 output of
  * fp8b_silu_and_mul, without writing that bf16 tensor to memory.
@@ -230,6 +288,14 @@ int fp8b_gate_up_silu_quant(const void* A, int64_t lda,
                             float* s, int64_t s_stride_m, int64_t s_stride_g,
                             int64_t M, int64_t I, int64_t K,
                             void* stream);
+
+/*
+ * The launch fp8b_gate_up_silu_quant makes for M x I x K on a device with
+ * cu_count CUs (cu_count <= 0: the current device's): one unsplit grid of
+ * 192x256 or 256x256 tiles (FP8B_KERNEL_PIPE192 / FP8B_KERNEL_PIPE256).
+ * Makes no GPU call when cu_count > 0. No counterpart in the reference.
+ */
+int fp8b_gate_up_plan(int64_t M, int64_t I, int64_t K, int cu_count, fp8b_plan_info* plan);
 
 #ifdef __cplusplus
 }

@@ -109,6 +109,25 @@ def test_gate_up_silu_quant_rejects_bad_args_without_gpu():
              4, 128, 512, None) == 3                                     # ldq % 8
 
 
+def test_noalloc_reports_argument_errors_before_scratch():
+    """fp8b_w8a8_block_matmul_noalloc checks dims and null pointers before it
+    looks at the plan's partials or the scratch array (which needs a device):
+    the same codes as fp8b_w8a8_block_matmul, here without a GPU."""
+    lib = _native.load()
+    f = lib.fp8b_w8a8_block_matmul_noalloc
+    P = 1 << 20
+    # a decode shape whose plan splits K (partials in the scratch array)
+    st = f(None, 14336, P, 14336, P, 112, 1, P, 112, 1, P, 4096, _native.BF16,
+           32, 4096, 14336, 128, 128, None)
+    assert st == 1 and b"null pointer" in lib.fp8b_last_error()
+    st = f(P, 14336, P, 14336, P, 112, 1, P, 112, 1, None, 4096, _native.BF16,
+           32, 4096, 14336, 128, 128, None)
+    assert st == 1
+    st = f(P, 100, P, 14336, P, 112, 1, P, 112, 1, P, 4096, _native.BF16,
+           32, 4096, 14336, 128, 128, None)
+    assert st == 2 and b"bad dims" in lib.fp8b_last_error()
+
+
 def test_workspace_size_zero_for_unsupported_blocks():
     lib = _native.load()
     assert lib.fp8b_gemm_workspace_size(32, 4096, 14336, 64, 128) == 0

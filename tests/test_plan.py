@@ -1,0 +1,111 @@
+"""CPU checks of the GEMM planner through the C ABI's plan query
+(fp8b_gemm_plan, fp8b_gate_up_plan): the kernel, tile, K splits and grid that
+one call launches, pinned for the five BASELINE configurations, the
+reference's fp8 tuning shapes (scripts/aot_tune.py:134-136) and the MLP
+chain, on a 256-CU MI355X. The plan query makes no GPU call for a given CU
+count, so these run without a device; the GPU tests check that every plan
+computes the right result."""
+import pytest
+
+from hf_kernels_helion_amd import _native
+
+CUS = 256
+
+
+def plan(M, N, K, block_n=128):
+    return _native.gemm_plan(M, N, K, block_n, 128, cu_count=CUS)
+
+
+def brief(p):
+    t = (p["kernel"], p["tile_m"], p["tile_n"], p["splits"], p["workgroups"])
+    if p["tail_kernel"] != "none":
+        t += (p["tail_kernel"], p["tail_tile_m"], p["tail_tile_n"], p["tail_workgroups"])
+    return t
+
+
+# (M, N, K) -> (kernel, tile_m, tile_n, splits, workgroups[, tail kernel, tile, workgroups])
+PINNED = {
+    # BASELINE configs
+    (512, 512, 2048): ("gemm_tiny_kernel", 32, 32, 1, 256),
+    (2048, 2048, 4096): ("gemm_pipe128_kernel", 128, 128, 1, 256),
+    (4096, 4096, 8192): ("gemm_pipe256_kernel", 256, 256, 1, 256),
+    (32, 4096, 14336): ("gemm_decode_kernel", 32, 128, 8, 256),
+    (3001, 28672, 4096): ("gemm_pipe256_kernel", 256, 256, 1, 1280,
+                          "gemm_pipe128_kernel", 128, 128, 256),
+    (3001, 4096, 14336): ("gemm_pipe192_kernel", 192, 256, 1, 256),
+    # the reference's tuning shapes not listed above
+    (1024, 1024, 2048): ("gemm_tiny_kernel", 64, 64, 1, 256),
+    (4096, 2048, 4096): ("gemm_pipe256x128_kernel", 256, 128, 1, 256),
+    (8192, 4096, 8192): ("gemm_pipe256_kernel", 256, 256, 1, 512),
+    (8192, 8192, 8192): ("gemm_pipe256_kernel", 256, 256, 1, 1024),
+}
+
+
+@pytest.mark.parametrize("shape", sorted(PINNED))
+def test_plan_pinned(shape):
+    p = plan(*shape)
+    assert brief(p) == PINNED[shape], (shape, p)
+    assert p["cu_count"] == CUS
+    KB = shape[2] // 128
+    assert p["splits"] * p["kb_per_split"] >= KB > (p["splits"] - 1) * p["kb_per_split"]
+
+
+def test_decode_plan_details():
+    """C4: 32 column tiles of 128 x 8 K-splits of 14 K-blocks, the four-stage
+    ring, fp32 partials [8, 32, 4096] and the split-K sum."""
+    p = plan(32, 4096, 14336)
+    assert (p["kb_per_split"], p["ring"], p["reduce"]) == (14, 4, 1)
+    assert p["workspace_bytes"] == 8 * 32 * 4096 * 4
+    assert p["workspace_bytes"] == _native.load().fp8b_gemm_workspace_size(32, 4096, 14336, 128, 128)
+
+
+def test_small_grid_waves():
+    # C1: one 32x32 tile per CU, eight waves splitting its 16 K-blocks
+    assert plan(512, 512, 2048)["waves"] == 8
+    # 64x64 tiles, one per CU: four waves
+    assert plan(1024, 1024, 2048)["waves"] == 4
+
+
+@pytest.mark.parametrize("shape,expect", [
+    ((4096, 4096, 8192), ("gemm_pipe256_kernel", 256, 256, 1, 256)),
+    ((32, 4096, 14336), ("gemm_decode_kernel", 32, 128, 8, 256)),
+    ((512, 512, 2048), ("gemm_tiny_kernel", 32, 32, 1, 256)),
+])
+def test_per_row_plans(shape, expect):
+    """deep-gemm's per-row weight scales (block_n = 1) take the same tiles."""
+    assert brief(plan(*shape, block_n=1)) == expect
+
+
+def test_plans_follow_the_cu_count():
+    """The CU count is an input: on 128 CUs the decode grid splits four ways
+    and C3's 256 tiles of 256x256 are two full waves."""
+    p = _native.gemm_plan(32, 4096, 14336, cu_count=128)
+    assert (p["kernel"], p["splits"], p["workgroups"]) == ("gemm_decode_kernel", 4, 128)
+    p = _native.gemm_plan(4096, 4096, 8192, cu_count=128)
+    assert (p["kernel"], p["workgroups"], p["tail_kernel"]) == ("gemm_pipe256_kernel", 256, "none")
+
+
+def test_generic_plan_for_other_block_sizes():
+    p = plan(256, 256, 1000, block_n=64)
+    assert p["kernel"] == "gemm_generic_kernel" and p["splits"] == 1
+
+
+@pytest.mark.parametrize("M,I,K,kernel,tile_m", [
+    (3001, 14336, 4096, "gemm_pipe192_kernel", 192),   # C5: 7 full waves of 192x256 tiles
+    (1024, 8192, 512, "gemm_pipe256_kernel", 256),     # 256 tiles of 256x256: one wave
+    (2048, 14336, 512, "gemm_pipe256_kernel", 256),    # 896 tiles (0.875 fill) vs 1232 (0.96)
+    (600, 1024, 512, "gemm_pipe192_kernel", 192),      # one partial wave either way
+])
+def test_gate_up_plans(M, I, K, kernel, tile_m):
+    p = _native.gate_up_plan(M, I, K, cu_count=CUS)
+    assert (p["kernel"], p["tile_m"], p["tile_n"], p["splits"]) == (kernel, tile_m, 256, 1)
+    assert p["workgroups"] == -(-M // tile_m) * (2 * I // 256)
+
+
+def test_plan_query_rejects_bad_args():
+    import ctypes
+    lib = _native.load()
+    info = _native.PlanInfo()
+    assert lib.fp8b_gemm_plan(0, 128, 128, 128, 128, CUS, ctypes.byref(info)) == 2
+    assert lib.fp8b_gemm_plan(128, 128, 128, 128, 128, CUS, None) == 1
+    assert lib.fp8b_gate_up_plan(128, 100, 512, CUS, ctypes.byref(info)) == 2

@@ -2,9 +2,11 @@
 against fp8b_w8a8_block_matmul with a caller workspace, through the C ABI:
 bit for bit (same kernels, same summation order), on calls in a row that
 reuse the library's scratch array with a smaller problem second, on the
-split-K 256x128, 128x128 and decode plans and a plan without split-K; the scratch
-holds the partials of every plan on this device (plans whose partials would
-exceed it are refused with FP8B_ERR_WORKSPACE)."""
+split-K 256x128, 128x128 and decode plans and a plan without split-K, and
+captured in a HIP graph as the process's first calls of the entry point (the
+scratch address is resolved inside the capture); the scratch holds the
+partials of every plan on this device, for block and per-row weight scales
+(plans whose partials would exceed it are refused with FP8B_ERR_WORKSPACE)."""
 import pytest
 import torch
 
@@ -30,6 +32,67 @@ def _args(A, B, As, Bs, C, code):
     return (A.data_ptr(), A.stride(0), B.data_ptr(), B.stride(0), As.data_ptr(), As.stride(0),
             As.stride(1), Bs.data_ptr(), Bs.stride(0), Bs.stride(1), C.data_ptr(), C.stride(0),
             code, M, N, K, 128, 128)
+
+
+def _reference(A, B, As, Bs, out):
+    """fp8b_w8a8_block_matmul with a caller workspace into out (bf16)."""
+    lib = _native.load()
+    M, K = A.shape
+    N = B.shape[0]
+    ws_n = lib.fp8b_gemm_workspace_size(M, N, K, 128, 128)
+    ws = torch.empty(max(ws_n, 1), dtype=torch.uint8, device=A.device)
+    st = lib.fp8b_w8a8_block_matmul(*_args(A, B, As, Bs, out, _native.BF16),
+                                    ws.data_ptr() if ws_n else None, ws_n,
+                                    torch.cuda.current_stream().cuda_stream)
+    _native.check(st, "fp8b_w8a8_block_matmul")
+    torch.cuda.synchronize()
+    return ws_n
+
+
+def test_noalloc_in_graph_capture(dev):
+    """A decode call (split-K over 16 column tiles) and a 128x128 split-K call
+    captured in one HIP graph. First in this file, so in a fresh process (or
+    after the other test files, none of which calls this entry point) these
+    are the process's first calls of it: the scratch address is resolved
+    inside the capture. Nothing is allocated across the calls (torch's
+    allocator and the device's free memory unchanged), and every replay, with
+    eager work and synchronisation in between, equals the workspace entry
+    point bit for bit."""
+    lib = _native.load()
+    cases = [_operands(32, 2048, 14336, seed=301, dev=dev),
+             _operands(300, 1024, 16384, seed=303, dev=dev)]
+    outs = [torch.empty(c[0].shape[0], c[1].shape[0], dtype=torch.bfloat16, device=dev)
+            for c in cases]
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        alloc0 = torch.cuda.memory_allocated()
+        for c, o in zip(cases, outs):
+            st = lib.fp8b_w8a8_block_matmul_noalloc(*_args(*c, o, _native.BF16),
+                                                    side.cuda_stream)
+            _native.check(st, "fp8b_w8a8_block_matmul_noalloc (captured)")
+        assert torch.cuda.memory_allocated() == alloc0
+    torch.cuda.synchronize()
+    # eager calls leave the device's free memory as it was (torch's graph
+    # context itself releases cached blocks, so this is checked outside it)
+    free0 = torch.cuda.mem_get_info()[0]
+    for c, o in zip(cases, outs):
+        _native.check(lib.fp8b_w8a8_block_matmul_noalloc(
+            *_args(*c, o, _native.BF16), torch.cuda.current_stream().cuda_stream), "noalloc")
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free0
+    for rep in range(3):
+        print(f"noalloc graph replay {rep}", flush=True)
+        for o in outs:
+            o.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        for c, o in zip(cases, outs):
+            ref = torch.empty_like(o)
+            assert _reference(*c, ref) > 0
+            assert torch.equal(o, ref)
 
 
 def _both(A, B, As, Bs, dtype):
@@ -81,23 +144,25 @@ def test_noalloc_scratch_holds_every_split_plan(dev):
     lib = _native.load()
     K = 131072
     worst, shape = 0, None
-    for M in (1, 16, 32, 48, 49, 64, 65, 128, 129, 256, 1000):
-        for N in range(128, 40064, 128):
-            need = lib.fp8b_gemm_workspace_size(M, N, K, 128, 128)
-            if need > worst:
-                worst, shape = need, (M, N)
+    for block_n in (128, 1):
+        for M in (1, 16, 32, 48, 49, 64, 65, 128, 129, 256, 1000):
+            for N in range(128, 40064, 128):
+                need = lib.fp8b_gemm_workspace_size(M, N, K, block_n, 128)
+                if need > worst:
+                    worst, shape = need, (M, N, block_n)
     print(f"largest split-K partials: {worst} bytes at M, N = {shape}, K = {K}", flush=True)
     assert worst > 0
     if worst <= SCRATCH_BYTES:
         return
-    M, N = shape
+    M, N, block_n = shape
     A = torch.zeros(M, K, dtype=torch.float8_e4m3fn, device=dev)
     B = torch.zeros(N, K, dtype=torch.float8_e4m3fn, device=dev)
     As = torch.ones(M, K // 128, device=dev)
-    Bs = torch.ones((N + 127) // 128, K // 128, device=dev)
+    Bs = torch.ones((N + block_n - 1) // block_n, K // 128, device=dev)
     C = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
-    st = lib.fp8b_w8a8_block_matmul_noalloc(*_args(A, B, As, Bs, C, _native.BF16),
-                                            torch.cuda.current_stream().cuda_stream)
+    args = list(_args(A, B, As, Bs, C, _native.BF16))
+    args[-2] = block_n
+    st = lib.fp8b_w8a8_block_matmul_noalloc(*args, torch.cuda.current_stream().cuda_stream)
     assert st == 6 and b"FP8B_NOALLOC_SCRATCH_BYTES" in lib.fp8b_last_error()
 
 
