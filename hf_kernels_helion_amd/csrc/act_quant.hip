@@ -174,6 +174,43 @@ silu_and_mul_generic_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   out[m * ldo + j] = (uint16_t)silu_mul_bits(x[m * ldx + j], x[m * ldx + d + j]);
 }
 
+// Element type codes of the typed silu_and_mul (fp8b_dtype values).
+template <int T> __device__ __forceinline__ float load_as_f32(const void* p, int64_t i) {
+  if constexpr (T == FP8B_F32) return static_cast<const float*>(p)[i];
+  else if constexpr (T == FP8B_F16) return (float)static_cast<const _Float16*>(p)[i];
+  else return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+// f rounded to the element type T (round to nearest even), as an fp32 value.
+template <int T> __device__ __forceinline__ float round_to(float f) {
+  if constexpr (T == FP8B_F32) return f;
+  else if constexpr (T == FP8B_F16) return (float)(_Float16)f;
+  else return bf16_to_f32(f32_to_bf16_bits(f));
+}
+template <int T> __device__ __forceinline__ void store_from_f32(void* p, int64_t i, float f) {
+  if constexpr (T == FP8B_F32) static_cast<float*>(p)[i] = f;
+  else if constexpr (T == FP8B_F16) static_cast<_Float16*>(p)[i] = (_Float16)f;
+  else static_cast<uint16_t*>(p)[i] = (uint16_t)f32_to_bf16_bits(f);
+}
+
+// silu_and_mul for any pair of element types (x of type TX, out of type TO):
+// out = TO( TX( TX(silu(fp32 gate)) * up ) ), the rounding points of
+// act.py:25-28 (silu.to(b.dtype) * b computed in fp32 and rounded to b's
+// dtype, then .to(out.dtype)). One element per thread and step.
+template <int TX, int TO>
+__global__ void __launch_bounds__(256)
+silu_and_mul_typed_kernel(const void* __restrict__ x, int64_t ldx, void* __restrict__ out,
+                          int64_t ldo, int64_t M, int64_t d) {
+  const int64_t n = M * d;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * 256) {
+    const int64_t m = i / d, j = i - m * d;
+    const float a = load_as_f32<TX>(x, m * ldx + j);
+    const float b = load_as_f32<TX>(x, m * ldx + d + j);
+    const float h = round_to<TX>(round_to<TX>(silu_f32(a)) * b);
+    store_from_f32<TO>(out, m * ldo + j, h);
+  }
+}
+
 // Fused silu_and_mul + group-128 quantisation: identical arithmetic to
 // silu_and_mul_vec_kernel followed by act_quant_g128_kernel, without the
 // bf16 round trip through memory. Requires d % 128 == 0. Blocks and 16-lane
@@ -353,6 +390,47 @@ extern "C" int fp8b_silu_and_mul(const void* x, int64_t ldx, void* out, int64_t 
         (const uint16_t*)x, ldx, (uint16_t*)out, ldo, M, d);
   }
   return check_launch("fp8b_silu_and_mul: kernel launch failed");
+}
+
+namespace {
+template <int TX>
+void launch_silu_typed(const void* x, int64_t ldx, void* out, int64_t ldo, int out_dtype,
+                       int64_t M, int64_t d, hipStream_t st) {
+  const int64_t n = M * d;
+  const unsigned blocks = (unsigned)std::min<int64_t>((n + 255) / 256, 65536);
+  if (out_dtype == FP8B_F32)
+    silu_and_mul_typed_kernel<TX, FP8B_F32><<<blocks, 256, 0, st>>>(x, ldx, out, ldo, M, d);
+  else if (out_dtype == FP8B_F16)
+    silu_and_mul_typed_kernel<TX, FP8B_F16><<<blocks, 256, 0, st>>>(x, ldx, out, ldo, M, d);
+  else
+    silu_and_mul_typed_kernel<TX, FP8B_BF16><<<blocks, 256, 0, st>>>(x, ldx, out, ldo, M, d);
+}
+}  // namespace
+
+extern "C" int fp8b_silu_and_mul_typed(const void* x, int64_t ldx, int x_dtype, void* out,
+                                       int64_t ldo, int out_dtype, int64_t M, int64_t d,
+                                       void* stream) {
+  auto dtype_ok = [](int t) { return t == FP8B_F32 || t == FP8B_BF16 || t == FP8B_F16; };
+  if (!dtype_ok(x_dtype) || !dtype_ok(out_dtype)) {
+    set_error("fp8b_silu_and_mul_typed: dtypes must be FP8B_F32, FP8B_BF16 or FP8B_F16");
+    return FP8B_ERR_DTYPE;
+  }
+  if (x_dtype == FP8B_BF16 && out_dtype == FP8B_BF16)
+    return fp8b_silu_and_mul(x, ldx, out, ldo, M, d, stream);
+  if (M < 0 || d < 0 || ldx < 2 * d || ldo < d) {
+    set_error("fp8b_silu_and_mul_typed: bad dims (need ldx >= 2d, ldo >= d)");
+    return FP8B_ERR_DIMS;
+  }
+  if (M == 0 || d == 0) return FP8B_OK;
+  if (!x || !out) {
+    set_error("fp8b_silu_and_mul_typed: null pointer");
+    return FP8B_ERR_NULL;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  if (x_dtype == FP8B_F32) launch_silu_typed<FP8B_F32>(x, ldx, out, ldo, out_dtype, M, d, st);
+  else if (x_dtype == FP8B_F16) launch_silu_typed<FP8B_F16>(x, ldx, out, ldo, out_dtype, M, d, st);
+  else launch_silu_typed<FP8B_BF16>(x, ldx, out, ldo, out_dtype, M, d, st);
+  return check_launch("fp8b_silu_and_mul_typed: kernel launch failed");
 }
 
 extern "C" int fp8b_silu_and_mul_quant(const void* x, int64_t ldx, void* q, int64_t ldq,

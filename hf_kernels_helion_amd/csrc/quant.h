@@ -109,8 +109,9 @@ __device__ __forceinline__ uint32_t unpack_bf16x8(const v4i raw, float v[8]) {
   return max_mag_bf16x8(raw);
 }
 
-// silu(a) * b with the reference's rounding points: silu in fp32, rounded to
-// bf16, multiplied by the bf16 `up` value in fp32, rounded to bf16.
+// silu(a) in fp32 (silu_f32), and silu(a) * b with the reference's rounding
+// points (silu_mul_bits): silu in fp32, rounded to bf16, multiplied by the
+// bf16 `up` value in fp32, rounded to bf16.
 // silu(a) = a / (1 + e^-a) is evaluated with the hardware v_exp_f32 and
 // v_rcp_f32 instead of expf and an IEEE division (~25 instructions per
 // element, which bound the fused quantiser: 55 -> 41 us at [3001, 28672]).
@@ -121,11 +122,10 @@ __device__ __forceinline__ uint32_t unpack_bf16x8(const v4i raw, float v[8]) {
 // what the division gives (e^-a = inf -> -0 for finite a, -inf -> NaN,
 // NaN -> NaN); for a in about [-88.7, -87.3] the reciprocal is subnormal and
 // may flush, giving -0 where the division gives |silu| < 1e-36.
-__device__ __forceinline__ uint32_t silu_mul_bits(uint32_t gate_bits, uint32_t up_bits) {
+__device__ __forceinline__ float silu_f32(float a) {
   constexpr float kLog2eHi = 1.4426950216293335f;   // log2(e) rounded to fp32
   constexpr float kLog2eLo = 1.925962989091e-08f;   // log2(e) - kLog2eHi
   constexpr float kLn2 = 0.6931471805599453f;
-  const float a = bf16_to_f32(gate_bits);
   const float t = -a * kLog2eHi;
   const float r = fmaf(-a, kLog2eHi, -t) - a * kLog2eLo;  // t's residual
   const float e0 = __builtin_amdgcn_exp2f(t);
@@ -136,7 +136,11 @@ __device__ __forceinline__ uint32_t silu_mul_bits(uint32_t gate_bits, uint32_t u
   const float y = 1.0f + e;
   const float inv0 = __builtin_amdgcn_rcpf(y);
   const float inv = y < __builtin_inff() ? fmaf(inv0, fmaf(-y, inv0, 1.0f), inv0) : inv0;
-  const float silu = a * inv;
+  return a * inv;
+}
+
+__device__ __forceinline__ uint32_t silu_mul_bits(uint32_t gate_bits, uint32_t up_bits) {
+  const float silu = silu_f32(bf16_to_f32(gate_bits));
   const float silu_b = bf16_to_f32(f32_to_bf16_bits(silu));
   return f32_to_bf16_bits(silu_b * bf16_to_f32(up_bits));
 }

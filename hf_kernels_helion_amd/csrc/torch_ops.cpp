@@ -225,21 +225,35 @@ std::tuple<Tensor, Tensor> act_quant(const Tensor& x, int64_t block_size) {
   return {q.view(qshape), s.view(sshape)};
 }
 
+// out = silu(x[..., :d]) * x[..., d:] for x and out of float32, bfloat16 or
+// float16 (any pair), leading dimensions flattened as op.py:9-12 does with
+// reshape. x may have any strides (copied when its rows are not 2-D
+// addressable); out is written in place when it flattens to rows with a unit
+// inner stride, else through a contiguous temporary copied back into it (the
+// reference's reshape would write a copy and leave out untouched).
 void silu_and_mul(Tensor& out, const Tensor& x) {
   check_gpu(x, "x");
   check_gpu(out, "out");
-  TORCH_CHECK(x.scalar_type() == at::kBFloat16 && out.scalar_type() == at::kBFloat16,
-              "silu_and_mul supports bfloat16 x and out");
+  TORCH_CHECK(x.dim() >= 1 && out.dim() >= 1, "x and out must have at least one dimension");
+  const int xt = out_code(x.scalar_type()), ot = out_code(out.scalar_type());
   const int64_t d = out.size(-1);
   TORCH_CHECK(x.size(-1) == 2 * d, "x last dim must be 2*d = ", 2 * d, ", got ", x.size(-1));
-  TORCH_CHECK(out.is_contiguous() && x.is_contiguous(), "x and out must be contiguous");
   const int64_t M = d > 0 ? out.numel() / d : 0;
   TORCH_CHECK(d == 0 || x.numel() / (2 * d) == M, "x and out must have the same leading shape");
   if (M == 0 || d == 0) return;
   at::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
-  const int st = fp8b_silu_and_mul(x.data_ptr(), 2 * d, out.data_ptr(), d, M, d,
-                                   current_stream(x));
+  Tensor x2 = rows_apart(x.reshape({M, 2 * d}));
+  // out itself when it is contiguous or 2-D rows with a unit inner stride
+  // (e.g. a slice out[:, :d] of a wider buffer), else a contiguous temporary
+  const bool direct = out.is_contiguous() ||
+                      (out.dim() == 2 && out.stride(1) == 1 && out.stride(0) >= d);
+  Tensor tmp = direct ? Tensor() : at::empty({M, d}, out.options());
+  Tensor o2 = !direct ? tmp : (out.is_contiguous() ? out.view({M, d}) : out);
+  const int64_t ldo = o2.size(0) > 1 ? o2.stride(0) : d;
+  const int st = fp8b_silu_and_mul_typed(x2.data_ptr(), row_stride(x2), xt, o2.data_ptr(), ldo,
+                                         ot, M, d, current_stream(x));
   check_status(st, "silu_and_mul");
+  if (!direct) out.copy_(tmp.view(out.sizes()));
 }
 
 std::tuple<Tensor, Tensor> silu_and_mul_quant(const Tensor& x, int64_t block_size) {

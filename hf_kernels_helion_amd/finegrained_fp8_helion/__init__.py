@@ -48,8 +48,10 @@ def per_token_group_quant_fp8(x: torch.Tensor, group_size: int = 128):
 
 
 def silu_and_mul(out: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
-    """out = silu(x[..., :d]) * x[..., d:] (bf16), written into ``out``
-    (activation-helion/activation-helion/torch-ext/activation_helion/__init__.py:7-10)."""
+    """out = silu(x[..., :d]) * x[..., d:], written into ``out``
+    (activation-helion/activation-helion/torch-ext/activation_helion/__init__.py:7-10).
+    x and out may each be float32, bfloat16 or float16, with the rounding
+    points of act.py:25-28; leading dimensions are flattened (op.py:9-12)."""
     ops.silu_and_mul(out, x)
     return out
 

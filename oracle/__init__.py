@@ -18,6 +18,10 @@ Parity status of each function (how it is pinned; see tests/test_oracle.py):
       operands.
   silu_and_mul     : pinned against torch.nn.functional.silu in fp32 with the
       reference's rounding points, to 1 bf16 ulp.
+  silu_and_mul_typed : (fp32/fp16/bf16 in and out) pinned against torch's CPU
+      evaluation of act.py's expression for every dtype pair (within one ulp
+      of the output type, mostly bit-equal) and bit-equal to silu_and_mul on
+      bf16.
   quant_weight_block : pinned by the same closed forms as act_quant applied per
       128x128 block, torch's float8_e4m3fn cast of W / Bs on finite blocks, and
       the non-finite policy cases (NaN block, +-inf block, subnormal block).
@@ -31,5 +35,6 @@ from .oracle import (  # noqa: F401
     block_gemm,
     dequant_matmul,
     silu_and_mul,
+    silu_and_mul_typed,
     quant_weight_block,
 )

@@ -119,6 +119,34 @@ def silu_and_mul(x_bits: np.ndarray) -> np.ndarray:
     return out
 
 
+def _round_to(v: np.ndarray, dtype: str) -> np.ndarray:
+    """fp32 values rounded (to nearest even) to bf16, fp16 or fp32, as fp32."""
+    v = np.asarray(v, dtype=np.float32)
+    if dtype == "float32":
+        return v
+    if dtype == "float16":
+        with np.errstate(over="ignore"):
+            return v.astype(np.float16).astype(np.float32)
+    if dtype == "bfloat16":
+        return (bf16_bits(v).astype(np.uint32) << 16).view(np.float32)
+    raise ValueError(dtype)
+
+
+def silu_and_mul_typed(x: np.ndarray, x_dtype: str, out_dtype: str) -> np.ndarray:
+    """activation-helion/.../act.py:20-28 for any element types: x holds
+    x_dtype values as fp32 [M, 2d]; returns out_dtype values as fp32 [M, d]:
+    out = out_dtype(x_dtype(x_dtype(silu(a)) * b)), silu(a) = a * sigmoid(a)
+    in fp32 (sigmoid = 1 / (1 + exp(-a))), each product formed in fp32."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    d = x.shape[1] // 2
+    a, b = x[:, :d], x[:, d:]
+    with np.errstate(over="ignore"):
+        sig = np.float32(1) / (np.float32(1) + np.exp(-a))
+    silu = (a * sig).astype(np.float32)
+    h = _round_to(_round_to(silu, x_dtype) * b, x_dtype)
+    return _round_to(h, out_dtype)
+
+
 def quant_weight_block(W: np.ndarray, block=(128, 128)):
     W = np.ascontiguousarray(W, dtype=np.float32)
     N, K = W.shape

@@ -206,6 +206,24 @@ def test_gemm_large_sampled_rows(M, N, K, outliers, dev):
     torch.testing.assert_close(out.float(), full.to(torch.bfloat16).float(), rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("M,N,K", [(1024, 1024, 2048), (4096, 2048, 4096), (8192, 4096, 8192),
+                                   (8192, 8192, 8192)])
+def test_gemm_reference_tuning_shapes(M, N, K, dev):
+    """The reference's fp8 tuning shapes not covered above
+    (scripts/aot_tune.py:134-136) on its own operand recipe (:139-146: A, B =
+    e4m3fn(randn * 0.3), As, Bs ~ U(0.5, 1)), bf16 out as it requests: every
+    row against torch's fp32 dequant-matmul, a seeded sample of rows against
+    the oracle. 8192x4096x8192 and 8192x8192x8192 are two and four full
+    waves of 256x256 tiles."""
+    print(f"gemm tuning shape M={M} N={N} K={K}", flush=True)
+    A, B, As, Bs = _operands(M, N, K, seed=M + 2 * N + 3 * K, kind="harness")
+    Ad, Bd, Asd, Bsd = A.to(dev), B.to(dev), As.to(dev), Bs.to(dev)
+    out = fp8.w8a8_block_fp8_matmul(Ad, Bd, Asd, Bsd, [128, 128], torch.bfloat16)
+    _full_check(out, Ad, Bd, Asd, Bsd)
+    rows = torch.randperm(M, generator=torch.Generator().manual_seed(M))[:8]
+    _check(out, A[rows], B, As[rows], Bs, rows=rows)
+
+
 def _full_check(out, Ad, Bd, Asd, Bsd):
     """Every row against torch's fp32 dequant-matmul on the GPU."""
     M, K = Ad.shape

@@ -40,6 +40,50 @@ def test_silu_and_mul_3d(dev):
     torch.testing.assert_close(out.cpu().float(), ref.float(), rtol=2 ** -6, atol=1e-6)
 
 
+_ULP2 = {"bfloat16": 2 ** -6, "float16": 2 ** -9, "float32": 1e-5}
+
+
+@pytest.mark.parametrize("xt", ["float32", "float16", "bfloat16"])
+@pytest.mark.parametrize("ot", ["float32", "float16", "bfloat16"])
+def test_silu_and_mul_dtypes(xt, ot, dev):
+    """act.py:20-28 is dtype-generic: every pair of fp32/fp16/bf16 input and
+    output against the oracle's typed restatement. The kernel's fp32 silu is
+    a few ulps from expf's, which can move the rounded silu and product by an
+    ulp of the input type: within two ulps of the coarser type."""
+    print(f"silu_and_mul {xt} -> {ot}", flush=True)
+    M, d = 37, 300
+    x = (synthetic.activations(M, 2 * d, seed=7).float() * 3).to(getattr(torch, xt))
+    out = torch.empty(M, d, dtype=getattr(torch, ot), device=dev)
+    fp8.silu_and_mul(out, x.to(dev))
+    ref = oracle.silu_and_mul_typed(x.float().numpy(), xt, ot)
+    tol = max(_ULP2[xt], _ULP2[ot])
+    torch.testing.assert_close(out.float().cpu(), torch.from_numpy(ref), rtol=tol, atol=1e-6)
+
+
+def test_silu_and_mul_strided_layouts(dev):
+    """Leading dims flattened as op.py:9-12 does: a non-contiguous 3-D x
+    (transposed leading dims) is read correctly, out as a row slice of a
+    wider buffer is written in place, and a non-contiguous 3-D out is
+    written through (the reference's reshape would write a copy); all equal
+    the contiguous call bit for bit."""
+    print("silu_and_mul strided layouts", flush=True)
+    base = synthetic.activations(24, 512, seed=5).to(dev).view(4, 6, 512)
+    xt = base.transpose(0, 1)                       # [6, 4, 512], not contiguous
+    ref = torch.empty(6, 4, 256, dtype=torch.bfloat16, device=dev)
+    fp8.silu_and_mul(ref, xt.contiguous())
+    out = torch.empty(6, 4, 256, dtype=torch.bfloat16, device=dev)
+    fp8.silu_and_mul(out, xt)
+    assert torch.equal(out, ref)
+    wide = torch.zeros(24, 300, dtype=torch.bfloat16, device=dev)
+    fp8.silu_and_mul(wide[:, :256], xt.reshape(24, 512))
+    assert torch.equal(wide[:, :256], ref.reshape(24, 256))
+    assert torch.count_nonzero(wide[:, 256:]) == 0
+    holder = torch.zeros(4, 6, 256, dtype=torch.bfloat16, device=dev)
+    out_nc = holder.transpose(0, 1)                 # [6, 4, 256], not contiguous
+    fp8.silu_and_mul(out_nc, xt)
+    assert torch.equal(out_nc, ref)
+
+
 @pytest.mark.parametrize("M,d,group", [(3001, 14336, 128), (5, 384, 128), (9, 200, 64),
                                        (4, 256, 256), (70000, 256, 128), (512, 4096, 128),
                                        (256, 8192, 128), (1000, 8192, 128), (4097, 1920, 128),
@@ -116,14 +160,23 @@ def _gate_up_chain(xq, xs, w13, s13, M, pad=True):
     return q[:M], s[:M], h[:M]
 
 
-@pytest.mark.parametrize("M,I,H", [(1, 128, 512), (5, 256, 1024), (200, 384, 512),
-                                   (257, 512, 512), (600, 384, 512), (513, 512, 1024),
-                                   (3001, 1024, 512), (3001, 14336, 4096)])
-def test_gate_up_silu_quant_equals_chain(M, I, H, dev):
+@pytest.mark.parametrize("M,I,H,tile_m", [(1, 128, 512, None), (5, 256, 1024, None),
+                                          (200, 384, 512, None), (257, 512, 512, None),
+                                          (600, 384, 512, None), (513, 512, 1024, None),
+                                          (3001, 1024, 512, 192), (3001, 14336, 4096, 192),
+                                          (1024, 8192, 512, 256), (2048, 14336, 512, 256)])
+def test_gate_up_silu_quant_equals_chain(M, I, H, tile_m, dev):
     """GEMM + SiLU·up + act-quant in one kernel == bf16 GEMM then
     silu_and_mul_quant, fp8 codes and scales bit for bit; the bf16 GEMM is
-    checked against the oracle on a sample of rows."""
+    checked against the oracle on a sample of rows. tile_m: the fused kernel's
+    tile rows the planner must pick on a 256-CU device (192x256 tiles for the
+    M = 3001 grids, 256x256 for 1024x8192 and 2048x14336), so both fused
+    kernels stay covered."""
     print(f"gate_up_silu_quant M={M} I={I} H={H}", flush=True)
+    from hf_kernels_helion_amd import _native
+    plan = _native.gate_up_plan(M, I, H)
+    if tile_m is not None and plan["cu_count"] == 256:
+        assert plan["tile_m"] == tile_m, plan
     x = synthetic.activations(M, H, seed=M + I)
     w13, s13 = synthetic.weights(2 * I, H, seed=I + H)
     xq, xs = fp8.act_quant(x.to(dev), 128)

@@ -330,3 +330,34 @@ def test_quant_weight_block_subnormal_and_zero_blocks():
     assert Bs[0, 0] == floor and Bs[0, 1] == floor
     np.testing.assert_array_equal(Wq, _torch_e4m3(W / floor))
     assert Wq[0, 0] == 0x80 and Wq[1, 0] == 0x00 and Wq[5, 200] == 0x80
+
+
+@pytest.mark.parametrize("xt", ["float32", "float16", "bfloat16"])
+@pytest.mark.parametrize("ot", ["float32", "float16", "bfloat16"])
+def test_silu_and_mul_typed_vs_torch(xt, ot):
+    """The typed silu oracle against torch's CPU evaluation of act.py:25-28
+    ((a * sigmoid(a)).to(b.dtype) * b, then .to(out.dtype)): bit-equal for
+    fp16 and bf16 inputs; for fp32 inputs torch's vectorised sigmoid and
+    numpy's exp differ by an fp32 ulp or two, which can move the output by
+    one ulp of its type (rarely, where the product sits on a rounding
+    boundary)."""
+    g = torch.Generator().manual_seed(11)
+    x = (torch.randn(64, 512, generator=g) * 4).to(getattr(torch, xt))
+    a, b = x[:, :256], x[:, 256:]
+    ref = ((a.float() * torch.sigmoid(a.float())).to(x.dtype) * b).to(getattr(torch, ot))
+    got = oracle.silu_and_mul_typed(x.float().numpy(), xt, ot)
+    if xt == "float32":
+        ulp = {"float32": 1e-6, "float16": 2 ** -10, "bfloat16": 2 ** -7}[ot]
+        torch.testing.assert_close(torch.from_numpy(got), ref.float(), rtol=ulp, atol=1e-30)
+        assert (got == ref.float().numpy()).mean() > 0.8
+    else:
+        assert np.array_equal(got, ref.float().numpy())
+
+
+def test_silu_and_mul_typed_equals_bf16_oracle():
+    g = torch.Generator().manual_seed(12)
+    x = (torch.randn(16, 512, generator=g) * 3).to(torch.bfloat16)
+    c = oracle.silu_and_mul(x.view(torch.int16).numpy().view(np.uint16))
+    cf = (c.astype(np.uint32) << 16).view(np.float32)
+    assert np.array_equal(cf, oracle.silu_and_mul_typed(x.float().numpy(), "bfloat16",
+                                                        "bfloat16"))
