@@ -49,7 +49,8 @@ def parse():
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--only", default=None,
                    help="profile helper: run only one workload "
-                        "(gemm|act_quant|decode|decode_fused|weight_quant|weight_quant_bf16|mlp|"
+                        "(gemm|act_quant|decode|decode_graph|decode_fused|weight_quant|"
+                        "weight_quant_bf16|mlp|"
                         "mlp_il|mlp_gateup|"
                         "mlp_down|medium|small|prefill|deep_gemm|deep_decode|copy|shapes|"
                         "shapes_streamed)"
@@ -549,6 +550,30 @@ def run_only(what, steps, warmup, torch, fp8, synthetic, dev):
         else:
             W, Bs = _gpu_weights(N, K, 40, dev, torch, synthetic)
             fn = lambda: fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [128, 128], torch.bfloat16)
+    elif what == "decode_graph":
+        # the bench leg's decode step (act_quant + GEMM + split-K sum, five
+        # weight copies) as a HIP graph of five steps, replayed --steps times
+        M, N, K = 32, 4096, 14336
+        ws_ = [_gpu_weights(N, K, 20 + i, dev, torch, synthetic) for i in range(5)]
+        xd = _gpu_acts(M, K, 30, dev, torch)
+
+        def five():
+            for i in range(5):
+                q, s = fp8.act_quant(xd, 128)
+                fp8.w8a8_block_fp8_matmul(q, ws_[i][0], s, ws_[i][1], [128, 128],
+                                          torch.bfloat16)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                five()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            five()
+        ms = time_events(graph.replay, steps, warmup, torch) / 5
+        log(f"{what}: {ms * 1e3:.2f} us/step over {5 * steps} graph-replayed steps")
+        return
     elif what in ("deep_gemm", "deep_decode"):
         from hf_kernels_helion_amd import deep_gemm_helion as dg
         M, N, K, copies = (4096, 4096, 8192, 1) if what == "deep_gemm" else (32, 4096, 14336, 5)
