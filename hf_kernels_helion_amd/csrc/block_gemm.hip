@@ -2156,11 +2156,20 @@ enum TileCfg {
   CFG_COUNT
 };
 
+// What runs the last partial wave of an unsplit grid.
+enum TailKind {
+  TAIL_NONE = 0,
+  TAIL_Q128 = 1,      // 256x256 tiles: as 128x128 quarters on gemm_pipe128_kernel
+  TAIL_H256X128 = 2,  // 256x256 tiles: as 256x128 halves on gemm_pipe256x128_kernel
+  TAIL_Q64 = 3        // 128x128 tiles: as 64x64 quarters on gemm_tiny_kernel
+};
+
 struct Plan {
   int cfg;
   int bm, bn;
   int splits;
   int kb_per_split;
+  int tail;
 };
 
 // CU count of the current device, queried once per device.
@@ -2222,73 +2231,153 @@ bool use_tile256x128() {
   return v;
 }
 
-// Fraction of the CU slots a grid of t tiles keeps busy over its waves.
-double wave_fill(int64_t t, int cus) {
-  const int64_t waves = (t + cus - 1) / cus;
-  return waves > 0 ? (double)t / (double)(waves * cus) : 0.0;
+// ---------------------------------------------------------------------------
+// Cost model of the MFMA-bound plans: grids past the small-grid and decode
+// ranges, where the choice is a tile shape (256x256, 192x256, 256x128 or
+// 128x128), what runs a last partial wave, and how often to split K. Every
+// candidate is priced as the sum over its waves of workgroups (one workgroup
+// per CU for every pipelined kernel, by its LDS) of
+//   first K-block latency
+//   + K-blocks x time per K-block of the tile x the wave's power factor
+//   + the wave's output stores,
+// plus, for a K split, the fp32 partials and the split-K sum kernel; the
+// cheapest wins. Time per K-block of one tile on one CU of a fully busy
+// chip (MI355X, realistic operand bits, power-limited clock): 256x256
+// 1.72 us, 192x256 1.37, 256x128 0.95, 128x128 0.71; 64x64 quarters on the
+// small-grid kernel 0.40. A wave that keeps a fraction f of the CUs busy
+// runs each tile faster, the power limit then allowing a higher clock:
+// factor max(0.8, 1 - 0.8 (1 - f)) (a 192-tile wave of 256x256 tiles takes
+// 1.41 us per K-block). The model reproduces the measured order of the
+// plans it chooses between, e.g. (us, steady clock):
+//   3001x4096x14336   192x256 one wave 157.8 < 256x256 partial wave 160.3
+//                     < 128x128 three waves 241
+//   3001x28672x4096   256x256 + last wave as 128x128 quarters 320.3
+//                     < 192x256 seven waves 331.4
+//   2048x4096x4096    256x128 one wave 34.8 < 128x128 two waves 47.1
+//   2048x2048x4096    128x128 one wave 25.3 < 256x128 half a wave 30.1
+//   2048x6144x4096    256x256 partial wave 47.1 < 256x128 two waves 61.2
+//   4096x6144x14336   256x256 + last wave as 256x128 halves 298.9
+//                     < 256x256 two waves 326.0
+//   2048x2560x4096    128x128 + last wave as 64x64 quarters 37.9
+//                     < 128x128 two waves 45.3
+//   1024x4096x14336   256x128 split in two 69.6 < 128x128 one wave 75.2
+//   512x4096x14336    256x128 split four ways 44.4 < 128x128 split two 51.7
+// A K split is considered only while the split grid fits one wave of
+// workgroups (a second wave costs more than the idle CUs: 1536x1536x4096
+// 40.2 us split in two, 24.2 unsplit); 256x256 and 192x256 grids are never
+// split. Two exclusions the model does not reproduce, each measured on
+// several shapes with the weights streamed from HBM: 256x128 tiles are not
+// split over 8 or fewer column tiles (N = 1024: 2048x1024x14336 56.0 us
+// split four ways against 48.1 for 128x128 tiles split two ways,
+// 1536x1024x14336 49.5 against 45.8, 1280x1024x14336 47.6 against 44.7),
+// nor below 256 rows (M = 200: 200x14336x14336 82.0 split two ways against
+// 76.6 on 128x128 tiles, 200x16384x14336 86.0 against 81.6, 200x11008x14336
+// 77.5 against 74.5; unsplit they stay ahead: 200x28672x4096 47.0 against
+// 53.0 on 192x256 tiles). Per-row weight scales (one more multiply per
+// fold) slow the tiles unevenly: x1.10 for 256x256, x1.08 for 256x128,
+// x1.20 for 128x128 (fitted to 72 shapes, 69 of their 72 choices right or
+// within 2%).
+// FP8B_TILE192=0, FP8B_TILE256X128=0, FP8B_TAIL128=0 and FP8B_TAIL64=0
+// take the corresponding candidates out.
+// ---------------------------------------------------------------------------
+struct TileCost {
+  int cfg, bm, bn;
+  double kb_us;   // per K-block of one tile on one CU of a fully busy chip
+  double per_row; // factor with per-row weight scales (one more multiply per fold)
+};
+constexpr TileCost kTileCosts[] = {{CFG_256x256, 256, 256, 1.62, 1.10},
+                                   {CFG_192x256, 192, 256, 1.31, 1.0},
+                                   {CFG_256x128, 256, 128, 1.08, 1.08},
+                                   {CFG_128x128, 128, 128, 0.67, 1.20}};
+constexpr double kQuarter64KbUs = 0.40;     // 64x64 quarters on gemm_tiny_kernel
+constexpr double kFirstKbUs = 4.7;          // launch and first K-block, per wave
+constexpr double kStoreBytesPerUs = 9.4e6;  // a wave's output stores
+constexpr double kSplitSumUs = 3.1;         // split-K sum kernel and its launch
+constexpr double kSplitBytesPerUs = 7.0e6;  // fp32 partials written and read back
+
+double power_factor(int64_t active, int cus) {
+  const double f = std::min(1.0, (double)active / (double)cus);
+  return std::max(0.93, 1.0 - 0.85 * (1.0 - f));
 }
 
-// 192x256 tiles instead of 256x256 when they fill the waves clearly better
-// (at least one full wave, fill at least 0.1 higher) and the 256x256 grid
-// cannot run a small last wave as 128x128 quarters (tail_quarters). Measured
-// at steady clock, M = 3001: the down projection (N = 4096, K = 14336: 256
-// tiles against 192) 157.8 against 160.3 us; the gate/up GEMM with SiLU·up
-// and act-quant in its epilogue plus the down projection 517.7 against 528.4
-// us; but the plain gate/up GEMM (N = 28672: 1792 tiles against 5 waves and
-// 64 tiles as quarters) 331.4 against 320.3 us, since 192-row tiles move
-// 17% more operand bytes per output. Also when one partial wave of 256x256
-// tiles would become one wave of 192x256 tiles (a 192-row tile takes ~1.2-
-// 1.4 us per K-block on one CU against ~1.75): 384x28672x4096 45.0 against
-// 52.9 us, 1536x6144x4096 40.8 against 43.7, 768x14336x7168 71.9 against
-// 76.0; 1536x8192 (192 tiles against 256) even.
-bool prefer_192(int64_t t256, int64_t t192, int cus, bool tail_quarters) {
-  if (!use_tile192()) return false;
-  if (t256 < cus && t192 <= cus) return true;
-  return !tail_quarters && t192 >= cus && wave_fill(t192, cus) >= wave_fill(t256, cus) + 0.1;
+double tile_kb_us(int cfg, bool per_row = false) {
+  for (const TileCost& tc : kTileCosts)
+    if (tc.cfg == cfg) return tc.kb_us * (per_row ? tc.per_row : 1.0);
+  return 1.0;
 }
 
-// Whether launch_pipe256 runs the last partial wave of an unsplit grid of t
-// 256x256 tiles as 128x128 quarters (at most a quarter of the CUs left).
-bool tail_quarters(int64_t t, int cus) {
-  const int64_t rest = t % cus;
-  return use_tail128() && t >= cus && rest > 0 && 4 * rest <= cus;
+// One wave of `active` workgroups, each a bm x bn tile over kbs K-blocks,
+// storing out_bytes per output element.
+double wave_us(double kb_us, int bm, int bn, int64_t active, int kbs, double out_bytes,
+               int cus) {
+  return kFirstKbUs + kbs * kb_us * power_factor(active, cus) +
+         (double)active * bm * bn * out_bytes / kStoreBytesPerUs;
 }
 
-// Whether launch_pipe256 runs that wave as 256x128 halves instead (more than
-// a quarter and at most half of the CUs left).
-bool tail_halves(int64_t t, int cus) {
-  const int64_t rest = t % cus;
-  return use_tile256x128() && t >= cus && 4 * rest > cus && 2 * rest <= cus;
+// Full waves of t tiles, then the last partial wave.
+double grid_us(double kb_us, int bm, int bn, int64_t t, int kbs, double out_bytes, int cus) {
+  const int64_t full = t / cus, rest = t % cus;
+  return full * wave_us(kb_us, bm, bn, cus, kbs, out_bytes, cus) +
+         (rest ? wave_us(kb_us, bm, bn, rest, kbs, out_bytes, cus) : 0.0);
 }
 
-// 256x128 tiles (gemm_pipe256x128_kernel) when they fit in one wave of
-// workgroups while 128x128 tiles would need two or more. Per K-block on one
-// CU a 256x128 tile takes ~0.9-1.0 us, a 128x128 tile ~0.7 and a 256x256
-// tile ~1.75. Measured at steady clock against the plan each replaces (bits
-// unchanged where that plan was unsplit): 2048x4096x4096 34.8 against 47.1
-// us (two waves of 128x128 tiles), 768x7168x4096 29.4 against 45.3,
-// 1024x8192x14336 106.7 against 143.3, 256x28672x4096 33.5 against 45.9,
-// 768x6144x14336 94.3 against 101.7; with per-row weight scales
-// 2048x4096x4096 41.8 against 61.6, 768x7168x4096 34.3 against 54.3. Outside
-// the rule they lost: half a
-// wave of them against one wave of 128x128 tiles (2048x2048x4096 30.1
-// against 25.3), two waves against one of 256x256 tiles (2048x6144x4096
-// 61.2 against 47.1), three against two (4096x6144x14336 313.9 against
-// 306.8).
-bool prefer_256x128(int64_t t2x1, int64_t t128, int cus) {
-  return use_tile256x128() && t128 > cus && t2x1 <= cus;
+bool tile_enabled(int cfg, bool per_row) {
+  if (cfg == CFG_192x256) return !per_row && use_tile192();
+  if (cfg == CFG_256x128) return use_tile256x128();
+  return true;
 }
 
-// Grids of fewer 256x256 tiles than CUs: one partial wave of 256x256 tiles
-// (not split along K) still beats the 128x128 kernel when the latter needs
-// three or more waves. Measured per K-block: a 256x256 tile takes ~1.4-1.75
-// us on one CU, a 128x128 tile ~0.71 us (it reuses each operand byte half as
-// often); 3001x4096x14336: 157 us against 241, 2560x4096x8192: 87 against
-// 140, 1536x7168x4096: 48 against 75, 2560x4096x2048: 28.5 against 42.5.
-bool prefer_256(int64_t t256, int64_t t128, int cus) {
-  if (t256 * 2 <= cus) return false;
-  const int64_t w256 = (t256 + cus - 1) / cus, w128 = (t128 + cus - 1) / cus;
-  return 71 * w128 > 175 * w256;
+// The cheapest MFMA-bound plan by the cost model above.
+Plan large_tile_plan(int64_t M, int64_t N, int64_t K, bool per_row, int cus) {
+  const int KB = (int)(K / 128);
+  const double q64_us = kQuarter64KbUs * (per_row ? tile_kb_us(CFG_128x128, true) /
+                                                        tile_kb_us(CFG_128x128) : 1.0);
+  Plan best{CFG_128x128, 128, 128, 1, KB, TAIL_NONE};
+  double best_us = 1e300;
+  auto consider = [&](const Plan& p, double us) {
+    if (us < best_us) {
+      best = p;
+      best_us = us;
+    }
+  };
+  for (const TileCost& tc : kTileCosts) {
+    if (!tile_enabled(tc.cfg, per_row)) continue;
+    const int64_t tn = (N + tc.bn - 1) / tc.bn;
+    const int64_t t = ((M + tc.bm - 1) / tc.bm) * tn;
+    const double kb_us = tile_kb_us(tc.cfg, per_row);
+    consider({tc.cfg, tc.bm, tc.bn, 1, KB, TAIL_NONE},
+             grid_us(kb_us, tc.bm, tc.bn, t, KB, 2.0, cus));
+    // The last partial wave on smaller tiles (same per-output arithmetic):
+    // 256x256 tiles as 128x128 quarters or 256x128 halves, 128x128 tiles
+    // as 64x64 quarters, when the smaller tiles fit one per CU.
+    const int64_t full = t / cus, rest = t % cus;
+    if (full > 0 && rest > 0) {
+      const double base = full * wave_us(kb_us, tc.bm, tc.bn, cus, KB, 2.0, cus);
+      if (tc.cfg == CFG_256x256 && use_tail128() && 4 * rest <= cus)
+        consider({tc.cfg, tc.bm, tc.bn, 1, KB, TAIL_Q128},
+                 base + wave_us(tile_kb_us(CFG_128x128, per_row), 128, 128, 4 * rest, KB, 2.0, cus));
+      if (tc.cfg == CFG_256x256 && use_tile256x128() && 2 * rest <= cus)
+        consider({tc.cfg, tc.bm, tc.bn, 1, KB, TAIL_H256X128},
+                 base + wave_us(tile_kb_us(CFG_256x128, per_row), 256, 128, 2 * rest, KB, 2.0, cus));
+      if (tc.cfg == CFG_128x128 && use_tiny() && use_tail64() && 4 * rest <= cus)
+        consider({tc.cfg, tc.bm, tc.bn, 1, KB, TAIL_Q64},
+                 base + wave_us(q64_us, 64, 64, 4 * rest, KB, 2.0, cus));
+    }
+    // K splits, in whole scale half-windows (multiples of 4 K-blocks) so
+    // the pipelined kernels stay usable, at least four K-blocks per split.
+    if ((tc.cfg == CFG_128x128 || (tc.cfg == CFG_256x128 && tn > 8 && M >= 256)) && t < cus) {
+      for (int s = 2; t * s <= cus && KB / s >= 4; s *= 2) {
+        int kbs = (KB + s - 1) / s;
+        if (KB % 4 == 0) kbs = (kbs + 3) / 4 * 4;
+        const int splits = (KB + kbs - 1) / kbs;
+        if (t * splits > cus) break;
+        const double us = wave_us(kb_us, tc.bm, tc.bn, t * splits, kbs, 4.0, cus) +
+                          kSplitSumUs + 2.0 * splits * (double)M * N * 4.0 / kSplitBytesPerUs;
+        consider({tc.cfg, tc.bm, tc.bn, splits, kbs, TAIL_NONE}, us);
+      }
+    }
+  }
+  return best;
 }
 
 // Grids for gemm_tiny_kernel: at most 8 tiles of 32x32 per CU and at most
@@ -2380,7 +2469,7 @@ bool small_grid_tile(int64_t M, int64_t N, int KB, int cus, int& tm, int& tn) {
 // and gemm_pipe256_kernel implement it.
 Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row, int cus) {
   const int KB = (int)(K / 128);
-  Plan p;
+  Plan p{};
   auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
   if (M <= 48 && !use_decode_kernel() && !per_row) {
     // Skinny path: 16 output columns per workgroup, K split inside it.
@@ -2467,59 +2556,7 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool per_row, int cus) {
     }
     return p;
   }
-  if (M <= 64) {
-    p.cfg = CFG_128x128; p.bm = 128; p.bn = 128;
-  } else if (prefer_256x128(tiles(256, 128), tiles(128, 128), cus)) {
-    p.cfg = CFG_256x128; p.bm = 256; p.bn = 128;
-  } else if (tiles(256, 256) >= cus || prefer_256(tiles(256, 256), tiles(128, 128), cus)) {
-    p.cfg = CFG_256x256; p.bm = 256; p.bn = 256;
-    if (!per_row && prefer_192(tiles(256, 256), tiles(192, 256), cus,
-                               tail_quarters(tiles(256, 256), cus))) {
-      p.cfg = CFG_192x256; p.bm = 192;
-    }
-  } else {
-    p.cfg = CFG_128x128; p.bm = 128; p.bn = 128;
-  }
-  // Grids of 128x128 tiles with fewer tiles than CUs split K, keeping at
-  // least four K-blocks per split, while the split grid still fits one wave
-  // of workgroups (one per CU, by its LDS; a second wave costs more than the
-  // idle CUs: 1536x1536x4096 40.2 us split in two, 24.2 unsplit). Grids that
-  // already cover the CUs are not split: the fp32 partials would cost more
-  // HBM traffic than the extra occupancy recovers. (A partial wave of
-  // 256x256 tiles chosen by prefer_256 is not split either: the fp32
-  // partials of a long-K grid cost more than the idle CUs.)
-  auto split_count = [&](int64_t t) {
-    int s = 1;
-    if (t < cus)
-      while (t * s * 2 <= cus && KB / (s * 2) >= 4) s *= 2;
-    return s;
-  };
-  // Long K: 256x128 tiles split twice as often instead, when each split
-  // keeps at least 28 K-blocks. Measured at steady clock: 512x4096x28672
-  // 68.9 against 81.9 us, 768x2048x14336 40.2 against 44.4, 1024x2048x14336
-  // 44.8 against 46.9, 256x8192x14336 44.4 against 47.0; shorter splits
-  // lost (512x2048x14336, 14 K-blocks each: 31.0 against 29.9), and so did
-  // N = 1024 (2048x1024x14336 54.2 against 47.1, 1024x1024x28672 56.0
-  // against 51.5). A full wave of 128x128 tiles with at least 112 K-blocks
-  // also runs as 256x128 tiles split in two: 1024x4096x14336 69.6 against
-  // 75.2 us, 2048x2048x14336 72.3 against 77.9 (at 64 K-blocks 3-5% slower,
-  // at 32 25-35% slower: the partials cost more than the smaller tiles
-  // save).
-  if (p.cfg == CFG_128x128 && M >= 256 && use_tile256x128() &&
-      ((N >= 1536 && tiles(128, 128) < cus && KB / split_count(tiles(256, 128)) >= 28) ||
-       (tiles(128, 128) == cus && KB >= 112))) {
-    p.cfg = CFG_256x128; p.bm = 256;
-  }
-  const int64_t t = tiles(p.bm, p.bn);
-  int splits = 1;
-  if (p.cfg == CFG_128x128 || p.cfg == CFG_256x128) splits = split_count(t);
-  p.kb_per_split = (KB + splits - 1) / splits;
-  // Split sizes in whole scale half-windows (multiples of 4 K-blocks) keep
-  // the pipelined kernels usable.
-  if (splits > 1 && KB % 4 == 0) p.kb_per_split = (p.kb_per_split + 3) / 4 * 4;
-  p.splits = (KB + p.kb_per_split - 1) / p.kb_per_split;
-  if (p.splits < 1) p.splits = 1;
-  return p;
+  return large_tile_plan(M, N, K, per_row, cus);
 }
 
 // 32-bit DMA offsets of gemm_decode_kernel: weight rows up to 127 of a tile
@@ -2567,8 +2604,6 @@ bool pipe_ok(const Operands& o, int64_t K, const Plan& p) {
          255 * std::max(o.lda, o.ldb) + K < (int64_t(1) << 32);
 }
 
-bool tail64(int64_t t, int cus);
-
 // Everything fp8b_w8a8_block_matmul launches for one call: the main kernel
 // (grid `grid` workgroups of `waves` waves, splits along K in grid.z), an
 // optional kernel for the last partial wave of the grid, and, when split,
@@ -2599,15 +2634,14 @@ struct Dispatch {
 // 2048x28672x4096 204.1 against 212.5; with per-row weight scales
 // 1536x14336x7168 (80 left) 175.6 against 208.1; block scales with 80 left
 // even (768x28672x14336 305.5 against 305.0).
-void resolve_pipe256(Dispatch& d, int64_t tiles, int KB, int cus) {
+void resolve_pipe256(Dispatch& d, int64_t tiles, int KB, int tail, int cus) {
   d.kernel = FP8B_KERNEL_PIPE256;
   d.waves = 8;
   d.grid = tiles;
   const int64_t full = tiles / cus * cus, rest = tiles - full;
-  const bool quarters = tail_quarters(tiles, cus), halves = tail_halves(tiles, cus);
-  if ((!quarters && !halves) || d.kb_per_split < KB) return;
+  if ((tail != TAIL_Q128 && tail != TAIL_H256X128) || rest == 0 || d.kb_per_split < KB) return;
   d.grid = full;
-  if (quarters) {
+  if (tail == TAIL_Q128) {
     d.tail_kernel = FP8B_KERNEL_PIPE128;
     d.tail_bm = d.tail_bn = 128;
     d.tail_grid = 4 * rest;
@@ -2638,15 +2672,15 @@ int tiny_waves(int64_t t, int tile_n, int cus) {
   return 1;
 }
 
-// One grid of 128x128 tiles on gemm_pipe128_kernel. When an unsplit grid
-// leaves a last partial wave that tail64 accepts, that wave's tiles run as
-// 64x64 quarters on gemm_tiny_kernel (four waves per quarter, one quarter
-// per CU): 2048x2560x4096 has 320 tiles, one full wave and 64 left.
-void resolve_pipe128(Dispatch& d, int64_t tiles, int cus) {
+// One grid of 128x128 tiles on gemm_pipe128_kernel. When the plan gives the
+// last partial wave of an unsplit grid to 64x64 quarters, those run on
+// gemm_tiny_kernel (four waves per quarter, one quarter per CU):
+// 2048x2560x4096 has 320 tiles, one full wave and 64 left.
+void resolve_pipe128(Dispatch& d, int64_t tiles, int tail, int cus) {
   d.kernel = FP8B_KERNEL_PIPE128;
   d.waves = 8;
   d.grid = tiles * d.splits;
-  if (d.splits > 1 || !tail64(tiles, cus)) return;
+  if (d.splits > 1 || tail != TAIL_Q64 || tiles % cus == 0) return;
   const int64_t full = tiles / cus * cus, rest = tiles - full;
   d.grid = full;
   d.tail_kernel = FP8B_KERNEL_TINY;
@@ -2680,8 +2714,8 @@ Dispatch resolve(int64_t M, int64_t N, int64_t K, int64_t block_n, int64_t block
   const bool pipe = pipe_ok(o, K, p);
   // 192x256 and 256x128 tiles exist only as pipelined kernels: without
   // their preconditions the grid goes back to 256x256 or 128x128 tiles.
-  if (p.cfg == CFG_192x256 && !pipe) { p.cfg = CFG_256x256; p.bm = 256; }
-  if (p.cfg == CFG_256x128 && !pipe) { p.cfg = CFG_128x128; p.bm = 128; }
+  if (p.cfg == CFG_192x256 && !pipe) { p.cfg = CFG_256x256; p.bm = 256; p.tail = TAIL_NONE; }
+  if (p.cfg == CFG_256x128 && !pipe) { p.cfg = CFG_128x128; p.bm = 128; p.tail = TAIL_NONE; }
   d.bm = p.bm;
   d.bn = p.bn;
   d.splits = p.splits;
@@ -2714,7 +2748,7 @@ Dispatch resolve(int64_t M, int64_t N, int64_t K, int64_t block_n, int64_t block
       break;
     case CFG_256x256:
       if (pipe) {
-        resolve_pipe256(d, tiles, KB, cus);
+        resolve_pipe256(d, tiles, KB, p.tail, cus);
       } else if (per_row) {
         d = Dispatch();
         d.per_row = true;
@@ -2737,7 +2771,7 @@ Dispatch resolve(int64_t M, int64_t N, int64_t K, int64_t block_n, int64_t block
       break;
     default:  // CFG_128x128
       if (pipe) {
-        resolve_pipe128(d, tiles, cus);
+        resolve_pipe128(d, tiles, p.tail, cus);
       } else if (per_row) {
         d = Dispatch();
         d.per_row = true;
@@ -2839,17 +2873,6 @@ void launch_dispatch(const Dispatch& d, const GemmArgs& a, hipStream_t st) {
     gemm_pipe256x128_kernel<PR><<<(unsigned)d.tail_grid, 512, 0, st>>>(r);
   else
     gemm_tiny_kernel<4, 4, 4, 2, PR><<<(unsigned)d.tail_grid, 256, 0, st>>>(r);
-}
-
-// Whether an unsplit grid of t 128x128 tiles runs its last partial wave as
-// 64x64 quarters on gemm_tiny_kernel: when the quarters fit one per CU.
-// Measured (64 tiles left after full waves): 2048x2560x4096 37.9 against
-// 45.3 us, 1536x3072x4096 37.0 against 45.4, 2048x2560x14336 109.0 against
-// 140.0; with 80 or 128 tiles left (two quarters per CU) no gain
-// (3584x1536x4096 45.3 against 45.5, 2000x2600x2048 27.8 against 27.0).
-bool tail64(int64_t t, int cus) {
-  const int64_t rest = t % cus;
-  return use_tiny() && use_tail64() && t >= cus && rest > 0 && 4 * rest <= cus;
 }
 
 const char* kernel_name(int k) {
@@ -3176,12 +3199,24 @@ extern "C" int fp8b_act_quant_matmul(const void* x, int64_t ldx, const void* B, 
 }
 
 namespace {
-// Tile rows of the fused gate/up kernel: 192 where 192x256 tiles fill the
-// waves clearly better than 256x256 ones (prefer_192; no quarter tiles for
-// the last wave, whose SWIGLU epilogue needs whole gate/up column pairs).
-bool gate_up_tile192(int64_t M, int64_t I, int cus) {
+// Tile rows of the fused gate/up kernel by the GEMM cost model: 192x256
+// against 256x256 tiles, unsplit and without tail launches (the SWIGLU
+// epilogue needs each gate block and its up block in one workgroup), each
+// wave also paying the epilogue's SiLU and quantisation (~3.5 us per
+// 256x256 tile while its matrix cores idle) and storing fp8 codes for half
+// of its columns. M = 3001, I = 14336: 1792 tiles of 192x256 (seven waves)
+// against 1344 of 256x256 (six, the last of 64 tiles), 517.7 against 528.4
+// us for the gate/up + down chain.
+bool gate_up_tile192(int64_t M, int64_t I, int64_t K, int cus) {
+  if (!use_tile192()) return false;
   const int64_t tn = 2 * I / 256;
-  return prefer_192(((M + 255) / 256) * tn, ((M + 191) / 192) * tn, cus, false);
+  const int KB = (int)(K / 128);
+  auto cost = [&](int bm, double kb_us) {
+    const int64_t t = ((M + bm - 1) / bm) * tn;
+    const int64_t waves = (t + cus - 1) / cus;
+    return grid_us(kb_us, bm, 256, t, KB, 0.5, cus) + waves * 3.5 * bm / 256.0;
+  };
+  return cost(192, tile_kb_us(CFG_192x256)) < cost(256, tile_kb_us(CFG_256x256));
 }
 }  // namespace
 
@@ -3197,7 +3232,7 @@ extern "C" int fp8b_gate_up_plan(int64_t M, int64_t I, int64_t K, int cu_count,
     return FP8B_ERR_DIMS;
   }
   const int cus = cu_count > 0 ? cu_count : device_cu_count();
-  const bool t192 = gate_up_tile192(M, I, cus);
+  const bool t192 = gate_up_tile192(M, I, K, cus);
   *plan = fp8b_plan_info{};
   plan->kernel = t192 ? FP8B_KERNEL_PIPE192 : FP8B_KERNEL_PIPE256;
   plan->tile_m = t192 ? 192 : 256;
@@ -3250,7 +3285,7 @@ extern "C" int fp8b_gate_up_silu_quant(const void* A, int64_t lda, const void* B
   a.lda = lda; a.ldb = ldb; a.as_sm = as_sm; a.as_sk = 1; a.bs_sn = bs_sn; a.bs_sk = 1;
   a.ldc = ldq; a.M = (int)M; a.N = (int)N; a.K = (int)K; a.KB = (int)(K / 128);
   a.kb_per_split = a.KB;
-  const bool tile192 = gate_up_tile192(M, I, device_cu_count());
+  const bool tile192 = gate_up_tile192(M, I, K, device_cu_count());
   a.tiles_m = (int)(tile192 ? (M + 191) / 192 : (M + 255) / 256);
   a.tiles_n = (int)(N / 256);
   a.out_dtype = FP8B_BF16;

@@ -613,17 +613,22 @@ def test_gemm_256_tiles_last_wave_as_halves(M, N, K, dev):
         assert torch.equal(out[r0:r1], part)
 
 
-@pytest.mark.parametrize("M,N,K,block_n", [(512, 4096, 14336, 128), (768, 2000, 14336, 128),
-                                           (1024, 1536, 28672, 128), (512, 4096, 14336, 1),
-                                           (1024, 4096, 14336, 128), (2048, 2048, 14336, 1)])
-def test_gemm_256x128_split_k(M, N, K, block_n, dev):
-    """Long-K grids below one wave of 128x128 tiles run 256x128 tiles split
-    along K (at least 28 K-blocks per split; a ragged last tile column;
-    per-row weight scales), and so do full waves of 128x128 tiles with 112
-    K-blocks (split in two): every element against torch's fp32
-    dequant-matmul."""
+@pytest.mark.parametrize("M,N,K,block_n,splits", [(512, 4096, 14336, 128, 4),
+                                                  (768, 2000, 14336, 128, 4),
+                                                  (1024, 1536, 28672, 128, 4),
+                                                  (512, 4096, 14336, 1, 4),
+                                                  (1024, 3072, 14336, 128, 2),
+                                                  (2048, 2048, 14336, 1, 2)])
+def test_gemm_256x128_split_k(M, N, K, block_n, splits, dev):
+    """Long-K grids the planner gives 256x128 tiles split along K (a ragged
+    last tile column; per-row weight scales): every element against torch's
+    fp32 dequant-matmul. The plan is asserted through the plan query on a
+    256-CU device."""
     from hf_kernels_helion_amd import _native
     print(f"gemm 256x128 split-K M={M} N={N} K={K} block_n={block_n}", flush=True)
+    plan = _native.gemm_plan(M, N, K, block_n)
+    if plan["cu_count"] == 256:
+        assert (plan["kernel"], plan["splits"]) == ("gemm_pipe256x128_kernel", splits), plan
     assert _native.load().fp8b_gemm_workspace_size(M, N, K, block_n, 128) > 0
     x = synthetic.activations(M, K, seed=M + N)
     q, s = fp8.act_quant(x.to(dev), 128)
