@@ -129,7 +129,41 @@ def cpu_baseline(A, B, As, Bs, torch):
                    f"mean of {len(times)} iterations, {t * 1e3:.1f} ms each, "
                    f"os.cpu_count()={os.cpu_count()}, {cpu_model}"),
         "decode_32x4096x14336": cpu_decode_step(torch),
+        "mlp_chain_3001": cpu_mlp_sample(torch),
     }
+
+
+def cpu_mlp_sample(torch):
+    """The M = 3001 MLP chain on the host, on a sample of 128 of
+    its rows: CPU act-quant, dequantise-then-matmul against the gate/up
+    weights [28672, 4096], silu_and_mul, act-quant, dequantise-then-matmul
+    against the down weights [4096, 14336], as the reference's bench.py:11-14
+    does per call; whole sampled chains, mean of up to 3 (about 10 s at most)."""
+    from oracle import torch_ref
+    from hf_kernels_helion_amd.finegrained_fp8_helion import synthetic
+    R, H, I = 128, 4096, 14336
+    x = synthetic.activations(R, H, seed=52)
+    w13, s13 = synthetic.weights(2 * I, H, seed=50)
+    w2, s2 = synthetic.weights(H, I, seed=51)
+
+    def chain():
+        q, s = torch_ref.act_quant(x, 128)
+        h = torch_ref.dequant_matmul(q, w13, s, s13)
+        a = torch_ref.silu_and_mul(h)
+        q2, s2a = torch_ref.act_quant(a, 128)
+        return torch_ref.dequant_matmul(q2, w2, s2a, s2)
+    chain()  # warmup
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 and (time.perf_counter() - t_start) < 10.0:
+        t0 = time.perf_counter()
+        chain()
+        times.append(time.perf_counter() - t0)
+    t = sum(times) / len(times)
+    flop = 2.0 * R * (2 * I * H + H * I)
+    return {"ms": round(t * 1e3, 1), "TFLOP/s": round(flop / t / 1e12, 4), "rows": R,
+            "chains": len(times),
+            "sample": f"{R} of 3001 rows; the weights are dequantised on every call"}
 
 
 def cpu_decode_step(torch):
