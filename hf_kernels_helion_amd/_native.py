@@ -56,6 +56,8 @@ SIGNATURES = {
     "fp8b_version": (ctypes.c_int, []),
     "fp8b_last_error": (ctypes.c_char_p, []),
     "fp8b_act_quant": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _vp]),
+    "fp8b_act_quant_typed": (
+        ctypes.c_int, [_vp, _i64, ctypes.c_int, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _vp]),
     "fp8b_w8a8_block_matmul": (
         ctypes.c_int,
         [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, ctypes.c_int,

@@ -4,7 +4,9 @@
 // consecutive elements. A group of 128 bf16 is 256 contiguous bytes, read by
 // 16 lanes (one DPP row) with one 16-byte load each, so a wavefront covers
 // four groups per load instruction and the whole wave's request is 1 KiB of
-// consecutive memory when the four groups sit in one row.
+// consecutive memory when the four groups sit in one row. fp16 and fp32
+// inputs take the typed kernels further down (same contract on the fp32
+// values of x).
 //
 // Numerics (the contract written in include/fp8_blockwise.h):
 //   amax  = max |x| over the group, taken as the max of the 15-bit magnitude
@@ -192,6 +194,138 @@ template <int T> __device__ __forceinline__ void store_from_f32(void* p, int64_t
   else static_cast<uint16_t*>(p)[i] = (uint16_t)f32_to_bf16_bits(f);
 }
 
+// Act-quant of fp16 or fp32 inputs (the bf16 kernels above cover bf16). A
+// magnitude pattern is the element's bits without the sign: 15 of them for
+// fp16 (infinity 0x7C00), 31 for fp32 (0x7F800000); NaN patterns lie above
+// infinity, so the group's max pattern carries a NaN. The scale and its
+// reciprocal are formed by IEEE division once per group.
+template <int T> struct TypedInf;
+template <> struct TypedInf<FP8B_F16> { static constexpr uint32_t value = 0x7C00u; };
+template <> struct TypedInf<FP8B_F32> { static constexpr uint32_t value = 0x7F800000u; };
+
+template <int T> __device__ __forceinline__ uint32_t mag_bits(const void* p, int64_t i) {
+  if constexpr (T == FP8B_F32) return static_cast<const uint32_t*>(p)[i] & 0x7FFFFFFFu;
+  else return static_cast<const uint16_t*>(p)[i] & 0x7FFFu;
+}
+template <int T> __device__ __forceinline__ float mag_value(uint32_t mag) {
+  if constexpr (T == FP8B_F32) return __uint_as_float(mag);
+  else return (float)__builtin_bit_cast(_Float16, (uint16_t)mag);
+}
+// Scale of a finite group: max(amax, 1e-10) / 448, one IEEE division.
+template <int T> __device__ __forceinline__ float typed_scale(uint32_t gmag) {
+  return fmaxf(mag_value<T>(gmag), kAmaxFloor) / kFp8Max;
+}
+
+// Group 128, K % 128 == 0, 16-byte aligned rows of x, 8-byte aligned rows of
+// q: 16 lanes per group (8 elements a lane: one 16-byte load of fp16, two of
+// fp32) over the flattened (row, group) index space; a block takes 16*U
+// consecutive slots, its 16-lane row r the slots r + 16u (u < U), all loads
+// issued before any conversion. Quotients by div_by_scale from the IEEE
+// reciprocal (correctly rounded, Markstein).
+template <int T>
+__device__ __forceinline__ uint32_t load8_typed(const void* x, int64_t e0, float v[8]) {
+  uint32_t mag = 0;
+  if constexpr (T == FP8B_F32) {
+    const v4i* p = reinterpret_cast<const v4i*>(static_cast<const float*>(x) + e0);
+    const v4i r0 = __builtin_nontemporal_load(p);
+    const v4i r1 = __builtin_nontemporal_load(p + 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = __int_as_float(r0[i]);
+      v[4 + i] = __int_as_float(r1[i]);
+      mag = max(mag, max((uint32_t)r0[i] & 0x7FFFFFFFu, (uint32_t)r1[i] & 0x7FFFFFFFu));
+    }
+  } else {
+    const v4i r = __builtin_nontemporal_load(
+        reinterpret_cast<const v4i*>(static_cast<const uint16_t*>(x) + e0));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t w = (uint32_t)r[i];
+      v[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu));
+      v[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+      mag = max(mag, max(w & 0x7FFFu, (w >> 16) & 0x7FFFu));
+    }
+  }
+  return mag;
+}
+
+template <int T, int U>
+__global__ void __launch_bounds__(256)
+act_quant_typed_g128_kernel(const void* __restrict__ x, int64_t ldx,
+                            uint8_t* __restrict__ q, int64_t ldq,
+                            float* __restrict__ s, int64_t ssm, int64_t ssg,
+                            uint32_t slots, uint32_t groups_per_row) {
+  const uint32_t sub = threadIdx.x & 15u;
+  const uint32_t slot0 = blockIdx.x * 16u * U + (threadIdx.x >> 4);
+  float v[U][8];
+  uint32_t mag[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint32_t slot = min(slot0 + 16u * u, slots - 1);  // uniform per 16-lane row
+    const uint32_t m = slot / groups_per_row, g = slot - m * groups_per_row;
+    mag[u] = load8_typed<T>(x, (int64_t)m * ldx + g * 128u + sub * 8u, v[u]);
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint32_t slot = slot0 + 16u * u;
+    if (slot >= slots) break;  // uniform across the 16-lane row
+    const uint32_t m = slot / groups_per_row, g = slot - m * groups_per_row;
+    const uint32_t gmag = row16_max_u32(mag[u]);
+    uint32_t w0, w1;
+    float scale;
+    if (gmag < TypedInf<T>::value) {
+      scale = typed_scale<T>(gmag);
+      quant8_finite(v[u], scale, 1.0f / scale, w0, w1);
+    } else {
+      quant8_nonfinite(v[u], gmag > TypedInf<T>::value, w0, w1, scale);
+    }
+    v2i packed;
+    packed[0] = (int)w0;
+    packed[1] = (int)w1;
+    __builtin_nontemporal_store(
+        packed, reinterpret_cast<v2i*>(q + (int64_t)m * ldq + g * 128u + sub * 8u));
+    if (sub == 0) s[(int64_t)m * ssm + (int64_t)g * ssg] = scale;
+  }
+}
+
+// Any group size, ragged K or unaligned rows: one thread walks one group,
+// quotients by IEEE division.
+template <int T>
+__global__ void __launch_bounds__(64)
+act_quant_typed_generic_kernel(const void* __restrict__ x, int64_t ldx,
+                               uint8_t* __restrict__ q, int64_t ldq,
+                               float* __restrict__ s, int64_t ssm, int64_t ssg,
+                               int64_t M, int64_t K, int64_t group, int64_t groups_per_row) {
+  const int64_t gi = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  if (gi >= M * groups_per_row) return;
+  const int64_t m = gi / groups_per_row;
+  const int64_t g = gi - m * groups_per_row;
+  const int64_t k0 = g * group;
+  const int64_t k1 = min(k0 + group, K);
+  const int64_t row = m * ldx;
+  uint32_t gmag = 0;
+  for (int64_t k = k0; k < k1; ++k) gmag = max(gmag, mag_bits<T>(x, row + k));
+  constexpr uint32_t kInf = TypedInf<T>::value;
+  const float scale = gmag > kInf    ? __uint_as_float(0x7FC00000u)
+                      : gmag == kInf ? __uint_as_float(0x7F800000u)
+                                     : typed_scale<T>(gmag);
+  uint8_t* qr = q + m * ldq;
+  for (int64_t k = k0; k < k1; ++k) {
+    const float xv = load_as_f32<T>(x, row + k);
+    uint8_t code;
+    if (gmag > kInf) {
+      code = kFp8NaN;
+    } else if (gmag == kInf) {
+      const uint32_t u = __float_as_uint(xv);
+      code = (u & 0x7FFFFFFFu) >= 0x7F800000u ? kFp8NaN : (uint8_t)((u >> 24) & 0x80u);
+    } else {
+      code = (uint8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(xv / scale, 0.0f, 0, false) & 0xFF);
+    }
+    qr[k] = code;
+  }
+  s[m * ssm + g * ssg] = scale;
+}
+
 // silu_and_mul for any pair of element types (x of type TX, out of type TO):
 // out = TO( TX( TX(silu(fp32 gate)) * up ) ), the rounding points of
 // act.py:25-28 (silu.to(b.dtype) * b computed in fp32 and rounded to b's
@@ -363,6 +497,56 @@ extern "C" int fp8b_act_quant(const void* x, int64_t ldx, void* q, int64_t ldq,
         (const uint16_t*)x, ldx, (uint8_t*)q, ldq, s, s_stride_m, s_stride_g, M, K, group, gpr);
   }
   return check_launch("fp8b_act_quant: kernel launch failed");
+}
+
+extern "C" int fp8b_act_quant_typed(const void* x, int64_t ldx, int x_dtype, void* q,
+                                    int64_t ldq, float* s, int64_t s_stride_m,
+                                    int64_t s_stride_g, int64_t M, int64_t K, int64_t group,
+                                    void* stream) {
+  if (x_dtype != FP8B_F32 && x_dtype != FP8B_BF16 && x_dtype != FP8B_F16) {
+    set_error("fp8b_act_quant_typed: x_dtype must be FP8B_F32, FP8B_BF16 or FP8B_F16");
+    return FP8B_ERR_DTYPE;
+  }
+  if (x_dtype == FP8B_BF16)
+    return fp8b_act_quant(x, ldx, q, ldq, s, s_stride_m, s_stride_g, M, K, group, stream);
+  if (M < 0 || K < 0 || ldx < K || ldq < K) {
+    set_error("fp8b_act_quant_typed: bad dims (need M,K >= 0, ldx >= K, ldq >= K)");
+    return FP8B_ERR_DIMS;
+  }
+  if (group != 32 && group != 64 && group != 128 && group != 256) {
+    set_error("fp8b_act_quant_typed: group must be 32, 64, 128 or 256");
+    return FP8B_ERR_BLOCK;
+  }
+  if (M == 0 || K == 0) return FP8B_OK;
+  if (!x || !q || !s) {
+    set_error("fp8b_act_quant_typed: null pointer");
+    return FP8B_ERR_NULL;
+  }
+  const int64_t gpr = (K + group - 1) / group;
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t per16 = x_dtype == FP8B_F32 ? 4 : 8;  // elements per 16 bytes
+  const bool fast = group == 128 && K % 128 == 0 && ldx % per16 == 0 && ldq % 8 == 0 &&
+                    aligned(x, 16) && aligned(q, 8) && M * gpr < (int64_t(1) << 31) &&
+                    K < (int64_t(1) << 32);
+  if (fast) {
+    // 32 bytes of x in flight per lane: two groups of fp16, one of fp32
+    const int64_t slots = M * gpr;
+    if (x_dtype == FP8B_F32)
+      act_quant_typed_g128_kernel<FP8B_F32, 1><<<(unsigned)((slots + 15) / 16), 256, 0, st>>>(
+          x, ldx, (uint8_t*)q, ldq, s, s_stride_m, s_stride_g, (uint32_t)slots, (uint32_t)gpr);
+    else
+      act_quant_typed_g128_kernel<FP8B_F16, 2><<<(unsigned)((slots + 31) / 32), 256, 0, st>>>(
+          x, ldx, (uint8_t*)q, ldq, s, s_stride_m, s_stride_g, (uint32_t)slots, (uint32_t)gpr);
+  } else {
+    const unsigned blocks = (unsigned)((M * gpr + 63) / 64);
+    if (x_dtype == FP8B_F32)
+      act_quant_typed_generic_kernel<FP8B_F32><<<blocks, 64, 0, st>>>(
+          x, ldx, (uint8_t*)q, ldq, s, s_stride_m, s_stride_g, M, K, group, gpr);
+    else
+      act_quant_typed_generic_kernel<FP8B_F16><<<blocks, 64, 0, st>>>(
+          x, ldx, (uint8_t*)q, ldq, s, s_stride_m, s_stride_g, M, K, group, gpr);
+  }
+  return check_launch("fp8b_act_quant_typed: kernel launch failed");
 }
 
 extern "C" int fp8b_silu_and_mul(const void* x, int64_t ldx, void* out, int64_t ldo,

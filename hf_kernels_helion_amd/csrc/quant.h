@@ -52,6 +52,38 @@ __device__ __forceinline__ float recip_of_scale(float s) {
   return fmaf(fmaf(-s, y, 1.0f), y, y);
 }
 
+// e4m3fn codes of 8 values of a finite group (scale s, recip = RN(1/s)),
+// packed little-endian into two words.
+__device__ __forceinline__ void quant8_finite(const float v[8], float scale, float recip,
+                                              uint32_t& w0, uint32_t& w1) {
+  float y[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) y[i] = div_by_scale(v[i], scale, recip);
+  int p0 = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
+  p0 = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], p0, true);
+  int p1 = __builtin_amdgcn_cvt_pk_fp8_f32(y[4], y[5], 0, false);
+  p1 = __builtin_amdgcn_cvt_pk_fp8_f32(y[6], y[7], p1, true);
+  w0 = (uint32_t)p0;
+  w1 = (uint32_t)p1;
+}
+
+// Codes and scale of 8 values of a group whose amax is NaN (is_nan) or +inf:
+// NaN group -> every code 0x7F, scale NaN; +inf group -> 0x7F for the +-inf
+// values, signed zero for the finite ones, scale +inf.
+__device__ __forceinline__ void quant8_nonfinite(const float v[8], bool is_nan, uint32_t& w0,
+                                                 uint32_t& w1, float& scale) {
+  scale = is_nan ? __uint_as_float(0x7FC00000u) : __uint_as_float(0x7F800000u);
+  uint32_t b[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t u = __float_as_uint(v[i]);
+    const bool nonfinite = (u & 0x7FFFFFFFu) >= 0x7F800000u;
+    b[i] = (is_nan || nonfinite) ? kFp8NaN : ((u >> 24) & 0x80u);
+  }
+  w0 = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+  w1 = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+}
+
 // Quantise 8 values held by one lane of a 16-lane group of 128.
 // `mag` is the max over this lane's 8 bf16 magnitude patterns.
 __device__ __forceinline__ void quant_row16_8(const float v[8], uint32_t mag,
@@ -61,28 +93,9 @@ __device__ __forceinline__ void quant_row16_8(const float v[8], uint32_t mag,
   if (gmag < 0x7F80u) {
     const float amax = fmaxf(bf16_to_f32(gmag), kAmaxFloor);
     scale = scale_from_amax(amax);
-    const float recip = recip_of_scale(scale);
-    float y[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = div_by_scale(v[i], scale, recip);
-    int p0 = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
-    p0 = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], p0, true);
-    int p1 = __builtin_amdgcn_cvt_pk_fp8_f32(y[4], y[5], 0, false);
-    p1 = __builtin_amdgcn_cvt_pk_fp8_f32(y[6], y[7], p1, true);
-    w0 = (uint32_t)p0;
-    w1 = (uint32_t)p1;
+    quant8_finite(v, scale, recip_of_scale(scale), w0, w1);
   } else {
-    const bool is_nan = gmag > 0x7F80u;
-    scale = is_nan ? __uint_as_float(0x7FC00000u) : __uint_as_float(0x7F800000u);
-    uint32_t b[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t u = __float_as_uint(v[i]);
-      const bool nonfinite = (u & 0x7FFFFFFFu) >= 0x7F800000u;
-      b[i] = (is_nan || nonfinite) ? kFp8NaN : ((u >> 24) & 0x80u);
-    }
-    w0 = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
-    w1 = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+    quant8_nonfinite(v, gmag > 0x7F80u, w0, w1, scale);
   }
 }
 

@@ -5,18 +5,18 @@
 //   w8a8_block_fp8_matmul(A, B, As, Bs, block_n, block_k) -> fp32 Tensor
 //       (schema of finegrained-fp8-helion/torch-ext/finegrained_fp8_helion/op.py:8-11)
 //   w8a8_block_fp8_matmul_dtype(..., ScalarType output_dtype) -> Tensor
-//   act_quant(x, block_size) -> (q, s)
+//   act_quant(x, block_size) -> (q, s)   (x float32, bfloat16 or float16)
 //   silu_and_mul(Tensor(a!) out, x) -> ()
 //       (schema of activation-helion/.../torch-ext/activation_helion/op.py:15-18)
 //   silu_and_mul_quant(x, block_size) -> (q, s)
 //   gate_up_silu_quant(A, B, As, Bs) -> (q, s)   (gate/up weights interleaved)
 //   act_quant_matmul(x, B, Bs, block_n, block_k, ScalarType output_dtype) -> Tensor
+//       (act_quant then w8a8_block_fp8_matmul in one op: two launches)
 //   weight_quant(W, block_n, block_k) -> (Wq, Bs)   (128x128 blocks)
 // and, in _deep_gemm_helion_rocm_mi355x (deep-gemm-helion's op,
 // deep-gemm-helion/deep-gemm-helion/torch-ext/deep_gemm_helion/op.py:7-14):
 //   gemm_fp8_fp8_bf16_nt(A, B, As, Bs, block_k) -> bf16 Tensor
 //       (per-row weight scales Bs [N, K/block_k]: block_n = 1)
-//       (act_quant then w8a8_block_fp8_matmul, one GEMM kernel for M <= 48)
 // Each op validates its tensors (TORCH_CHECK -> RuntimeError), allocates its
 // outputs and any split-K workspace from torch's caching allocator, and calls
 // one C-ABI entry point on torch's current HIP stream. CPU tensors raise: the
@@ -199,7 +199,9 @@ void check_group(int64_t g) {
 
 std::tuple<Tensor, Tensor> act_quant(const Tensor& x, int64_t block_size) {
   check_gpu(x, "x");
-  TORCH_CHECK(x.scalar_type() == at::kBFloat16, "x must be bfloat16, got ", x.scalar_type());
+  const at::ScalarType xt = x.scalar_type();
+  TORCH_CHECK(xt == at::kBFloat16 || xt == at::kHalf || xt == at::kFloat,
+              "x must be bfloat16, float16 or float32, got ", xt);
   TORCH_CHECK(x.dim() >= 1, "x must have at least one dimension");
   check_group(block_size);
   const int64_t K = x.size(-1);
@@ -214,8 +216,9 @@ std::tuple<Tensor, Tensor> act_quant(const Tensor& x, int64_t block_size) {
   Tensor s = at::empty({M, groups}, x.options().dtype(at::kFloat));
   if (M > 0 && K > 0) {
     const int64_t ldx = row_stride(x2);
-    const int st = fp8b_act_quant(x2.data_ptr(), ldx, q.data_ptr(), K, s.data_ptr<float>(),
-                                  groups, 1, M, K, block_size, current_stream(x));
+    const int st = fp8b_act_quant_typed(x2.data_ptr(), ldx, out_code(xt), q.data_ptr(), K,
+                                        s.data_ptr<float>(), groups, 1, M, K, block_size,
+                                        current_stream(x));
     check_status(st, "act_quant");
   }
   auto qshape = lead;

@@ -33,10 +33,11 @@ def w8a8_block_fp8_matmul(A: torch.Tensor, B: torch.Tensor, As: torch.Tensor,
 
 
 def act_quant(x: torch.Tensor, block_size: int = 128):
-    """Quantise bf16 activations per 1 x block_size group to float8_e4m3fn.
+    """Quantise activations per 1 x block_size group to float8_e4m3fn.
 
-    Returns (q, s): q has x's shape, s is fp32 [..., ceil(K/block_size)] with
-    s = max(amax, 1e-10) / 448 and q = e4m3fn(x / s). The pair is the (A, As)
+    x is bfloat16, float16 or float32. Returns (q, s): q has x's shape, s is
+    fp32 [..., ceil(K/block_size)] with s = max(amax, 1e-10) / 448 and
+    q = e4m3fn(x / s), both divisions in fp32. The pair is the (A, As)
     operand of w8a8_block_fp8_matmul.
     """
     return ops.act_quant(x, int(block_size))

@@ -79,6 +79,19 @@ int fp8b_act_quant(const void* x, int64_t ldx,
                    void* stream);
 
 /*
+ * fp8b_act_quant for x of x_dtype FP8B_F32, FP8B_BF16 or FP8B_F16 (ldx in
+ * elements of x_dtype), with the same contract on the fp32 values of x (every
+ * fp16 and bf16 value is exact in fp32). FP8B_BF16 is fp8b_act_quant. No
+ * counterpart in the reference (see fp8b_act_quant); it serves callers whose
+ * activations are not bf16.
+ */
+int fp8b_act_quant_typed(const void* x, int64_t ldx, int x_dtype,
+                         void* q, int64_t ldq,
+                         float* s, int64_t s_stride_m, int64_t s_stride_g,
+                         int64_t M, int64_t K, int64_t group,
+                         void* stream);
+
+/*
  * Block-scaled w8a8 GEMM: C = A . B^T.
  *
  * Replaces the Helion kernel _w8a8_block_fp8_matmul

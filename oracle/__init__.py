@@ -11,6 +11,10 @@ Parity status of each function (how it is pinned; see tests/test_oracle.py):
   act_quant        : pinned by closed forms (s == amax/448, amax element ->
       +-448), a brute-force nearest-grid-point search, scale invariance under
       powers of two, and the non-finite policy cases.
+  act_quant_f32    : (fp32 values; fp16 inputs widened) bit-equal to act_quant
+      on bf16-representable values, and pinned by torch's CPU evaluation of
+      the contract (fp32 division, float8_e4m3fn cast) on random fp32 and
+      fp16 groups, the s == amax/448 closed form and the non-finite policy.
   block_gemm       : pinned against float64 brute force, exact small-integer
       cases (As = Bs = 1), one-hot rows, power-of-two row scaling and K-block
       permutation invariance.
@@ -32,6 +36,7 @@ from .oracle import (  # noqa: F401
     e4m3fn_from_f32,
     e4m3fn_to_f32,
     act_quant,
+    act_quant_f32,
     block_gemm,
     dequant_matmul,
     silu_and_mul,

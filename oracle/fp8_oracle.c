@@ -18,6 +18,8 @@
  *       exists (the reference consumes pre-quantised A/As,
  *       finegrained-fp8-helion/torch-ext/finegrained_fp8_helion/fp8.py:5);
  *       contract: s = max(amax,1e-10)/448, q = e4m3fn(x/s).
+ *   oracle_act_quant_f32 : the same contract on fp32 values (fp32 inputs,
+ *       and fp16 inputs widened to fp32, which is exact).
  *   oracle_block_gemm : fp8.py:24-38 -- per K-block fp32 dot, then
  *       acc = acc + (dot * As[m,kb]) * Bs[n/bn,kb] in K-block order.
  *   oracle_dequant_matmul : finegrained-fp8-helion/bench.py:11-14
@@ -103,8 +105,13 @@ float oracle_e4m3fn_to_f32(uint8_t b) {
 }
 
 /* x: bf16 bits [M, ldx]; q: [M, K] bytes; s: [M, ceil(K/group)] */
-void oracle_act_quant(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, int64_t group,
-                      uint8_t* q, float* s) {
+/* x is bf16 bits (is_f32 = 0) or fp32 values (is_f32 = 1). */
+static float act_x(const void* x, int is_f32, int64_t i) {
+  return is_f32 ? ((const float*)x)[i] : oracle_bf16_to_f32(((const uint16_t*)x)[i]);
+}
+
+static void act_quant_impl(const void* x, int is_f32, int64_t M, int64_t K, int64_t ldx,
+                           int64_t group, uint8_t* q, float* s) {
   const int64_t G = (K + group - 1) / group;
   for (int64_t m = 0; m < M; ++m) {
     for (int64_t g = 0; g < G; ++g) {
@@ -112,7 +119,7 @@ void oracle_act_quant(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, int6
       float amax = 0.0f;
       int has_nan = 0;
       for (int64_t k = k0; k < k1; ++k) {
-        const float v = oracle_bf16_to_f32(x[m * ldx + k]);
+        const float v = act_x(x, is_f32, m * ldx + k);
         if (isnan(v)) has_nan = 1;
         else if (fabsf(v) > amax) amax = fabsf(v);
       }
@@ -123,20 +130,30 @@ void oracle_act_quant(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, int6
       } else if (isinf(amax)) {
         scale = INFINITY;
         for (int64_t k = k0; k < k1; ++k) {
-          const float v = oracle_bf16_to_f32(x[m * ldx + k]);
+          const float v = act_x(x, is_f32, m * ldx + k);
           q[m * K + k] = isinf(v) ? 0x7F : (signbit(v) ? 0x80 : 0x00);
         }
       } else {
         const float am = amax < 1e-10f ? 1e-10f : amax;
         scale = am / 448.0f;
         for (int64_t k = k0; k < k1; ++k) {
-          const float v = oracle_bf16_to_f32(x[m * ldx + k]);
+          const float v = act_x(x, is_f32, m * ldx + k);
           q[m * K + k] = oracle_e4m3fn_from_f32(v / scale);
         }
       }
       s[m * G + g] = scale;
     }
   }
+}
+
+void oracle_act_quant(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, int64_t group,
+                      uint8_t* q, float* s) {
+  act_quant_impl(x, 0, M, K, ldx, group, q, s);
+}
+
+void oracle_act_quant_f32(const float* x, int64_t M, int64_t K, int64_t ldx, int64_t group,
+                          uint8_t* q, float* s) {
+  act_quant_impl(x, 1, M, K, ldx, group, q, s);
 }
 
 /* A [M,K], B [N,K] fp8 bytes; As [M,KB], Bs [NB,KB] fp32 contiguous; C fp32 [M,N].

@@ -36,11 +36,13 @@ def load() -> ctypes.CDLL:
         lib.oracle_e4m3fn_to_f32.restype = ctypes.c_float
         lib.oracle_e4m3fn_to_f32.argtypes = [ctypes.c_uint8]
         lib.oracle_act_quant.argtypes = [_P, _I, _I, _I, _I, _P, _P]
+        lib.oracle_act_quant_f32.argtypes = [_P, _I, _I, _I, _I, _P, _P]
         lib.oracle_block_gemm.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P]
         lib.oracle_dequant_matmul.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P]
         lib.oracle_silu_and_mul.argtypes = [_P, _I, _I, _P]
         lib.oracle_quant_weight_block.argtypes = [_P, _I, _I, _I, _I, _P, _P]
-        for f in ("oracle_act_quant", "oracle_block_gemm", "oracle_dequant_matmul",
+        for f in ("oracle_act_quant", "oracle_act_quant_f32", "oracle_block_gemm",
+                  "oracle_dequant_matmul",
                   "oracle_silu_and_mul", "oracle_quant_weight_block"):
             getattr(lib, f).restype = None
         _lib = lib
@@ -83,6 +85,18 @@ def act_quant(x_bits: np.ndarray, group: int = 128):
     q = np.empty((M, K), dtype=np.uint8)
     s = np.empty((M, G), dtype=np.float32)
     load().oracle_act_quant(_ptr(x), M, K, K, group, _ptr(q), _ptr(s))
+    return q, s
+
+
+def act_quant_f32(x: np.ndarray, group: int = 128):
+    """x: fp32 values [M, K] (fp16 inputs widened to fp32, which is exact) ->
+    (q uint8 [M,K], s fp32 [M, ceil(K/group)]), the act_quant contract."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    M, K = x.shape
+    G = -(-K // group)
+    q = np.empty((M, K), dtype=np.uint8)
+    s = np.empty((M, G), dtype=np.float32)
+    load().oracle_act_quant_f32(_ptr(x), M, K, K, group, _ptr(q), _ptr(s))
     return q, s
 
 

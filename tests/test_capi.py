@@ -72,6 +72,14 @@ def test_act_quant_rejects_bad_args_without_gpu():
     assert lib.fp8b_act_quant(None, 64, None, 128, None, 1, 1, 4, 128, 128, None) == 2
     assert lib.fp8b_act_quant(None, 128, None, 128, None, 1, 1, 4, 128, 128, None) == 1
     assert lib.fp8b_act_quant(None, 128, None, 128, None, 1, 1, 0, 128, 128, None) == 0
+    # typed: bad dtype, then the same checks per input type (bf16 delegates)
+    aq = lib.fp8b_act_quant_typed
+    assert aq(None, 128, 7, None, 128, None, 1, 1, 4, 128, 128, None) == 5
+    for t in (_native.F32, _native.BF16, _native.F16):
+        assert aq(None, 128, t, None, 128, None, 1, 1, 4, 128, 100, None) == 4
+        assert aq(None, 64, t, None, 128, None, 1, 1, 4, 128, 128, None) == 2
+        assert aq(None, 128, t, None, 128, None, 1, 1, 4, 128, 128, None) == 1
+        assert aq(None, 128, t, None, 128, None, 1, 1, 0, 128, 128, None) == 0
     assert lib.fp8b_silu_and_mul(None, 10, None, 8, 2, 8, None) == 2
     assert lib.fp8b_silu_and_mul_quant(None, 256, None, 128, None, 1, 1, 2, 128, 48, None) == 4
 

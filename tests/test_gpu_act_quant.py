@@ -193,3 +193,126 @@ def test_act_quant_full_size_properties(dev):
     qo, so = oracle.act_quant(_bits(x[rows]), 128)
     np.testing.assert_array_equal(q[rows.to(dev)].cpu().view(torch.uint8).numpy(), qo)
     np.testing.assert_array_equal(s[rows.to(dev)].cpu().numpy(), so)
+
+
+# ------------------------------------------------ float32 / float16 inputs
+
+def _wide(M, K, dtype, seed):
+    """Random values over many binades (each row its own magnitude); fp16
+    rows stay inside the fp16 range, subnormals included."""
+    g = torch.Generator().manual_seed(seed)
+    e = torch.randint(-24, 14, (M, 1), generator=g).float() if dtype == torch.float16 else \
+        torch.randint(-40, 40, (M, 1), generator=g).float()
+    return (torch.randn(M, K, generator=g) * torch.exp2(e)).to(dtype)
+
+
+def _assert_exact_typed(x_cpu, group, dev):
+    q, s = fp8.act_quant(x_cpu.to(dev), group)
+    torch.cuda.synchronize()
+    K = x_cpu.shape[-1]
+    qo, so = oracle.act_quant_f32(x_cpu.float().reshape(-1, K).numpy(), group)
+    np.testing.assert_array_equal(q.cpu().view(torch.uint8).numpy().reshape(qo.shape), qo)
+    np.testing.assert_array_equal(s.cpu().numpy().reshape(so.shape).view(np.uint32),
+                                  so.view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("M,K,group", [(1, 128, 128), (37, 4096, 128), (3001, 1024, 128),
+                                       (9, 14336, 128), (5, 300, 128), (7, 1000, 64),
+                                       (4, 512, 32), (3, 768, 256)])
+def test_act_quant_typed_exact(dtype, M, K, group, dev):
+    """fp32 and fp16 activations: the group-128 vector kernel (K % 128 == 0)
+    and the scalar kernel (other groups, ragged K), bit-exact against the
+    oracle's fp32-value quantiser."""
+    print(f"act_quant typed {dtype} M={M} K={K} group={group}", flush=True)
+    _assert_exact_typed(_wide(M, K, dtype, M * 3 + K + group), group, dev)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_act_quant_typed_nonfinite_and_extremes(dtype, dev):
+    print(f"act_quant typed nonfinite {dtype}", flush=True)
+    big = torch.finfo(dtype).max
+    tiny = 1e-40 if dtype == torch.float32 else 6e-8
+    x = torch.randn(6, 512).to(dtype)
+    x[0, 0:128] = 0.0
+    x[0, 5] = -0.0
+    x[0, 6] = tiny
+    x[1, 130] = float("nan")
+    x[2, 300] = float("inf")
+    x[2, 301] = -float("inf")
+    x[3, 384:512] = tiny
+    x[4, 0:128] = big
+    x[4, 1] = -1.0
+    x[5, 128:256] = x[5, 128:256].float().mul(1e-12).to(dtype)  # amax under the 1e-10 floor (fp32)
+    _assert_exact_typed(x, 128, dev)
+    _assert_exact_typed(x, 64, dev)
+
+
+def test_act_quant_typed_scale_with_all_ones_mantissa(dev):
+    """fp32 groups whose scale has an all-ones mantissa (no bf16 amax gives
+    one): the reciprocal and the quotients still match IEEE division."""
+    print("act_quant typed all-ones scale", flush=True)
+    g = np.random.default_rng(21)
+    rows = []
+    for e in range(-20, 20):
+        s_t = np.float32(np.ldexp(np.float32(2.0 - 2.0 ** -23), e))
+        center = int(np.float32(s_t * np.float32(448)).view(np.uint32))
+        for u in range(center - 3, center + 4):
+            a = np.uint32(u).view(np.float32)
+            if ((a / np.float32(448)).view(np.uint32) & 0x7FFFFF) == 0x7FFFFF:
+                r = (g.standard_normal(128) * float(a) / 4).astype(np.float32)
+                r = np.clip(r, -a, a)
+                r[g.integers(128)] = a
+                rows.append(r)
+    assert len(rows) >= 40
+    x = torch.from_numpy(np.stack(rows))
+    _assert_exact_typed(x, 128, dev)
+
+
+def test_act_quant_every_fp16_through_cvt(dev):
+    """Groups whose amax is exactly 448 have scale 1.0: every finite fp16
+    value with |x| <= 448 goes through the convert (127 per group)."""
+    print("act_quant exhaustive fp16 cvt", flush=True)
+    f = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float32)
+    vals = f[np.isfinite(f) & (np.abs(f) <= 448.0)]
+    per = 127
+    G = -(-vals.size // per)
+    padded = np.zeros(G * per, dtype=np.float32)
+    padded[: vals.size] = vals
+    grid = np.full((G, 128), 448.0, dtype=np.float32)
+    grid[:, 1:] = padded.reshape(G, per)
+    x = torch.from_numpy(grid).to(torch.float16)
+    _assert_exact_typed(x, 128, dev)
+
+
+def test_act_quant_typed_strided_and_3d(dev):
+    print("act_quant typed strided/3d", flush=True)
+    x = _wide(64, 1024, torch.float32, 5)
+    for xs in (x[:, :512], x[:, 3:515]):  # row stride 1024; the second unaligned (scalar kernel)
+        q, s = fp8.act_quant(xs.to(dev), 128)
+        qo, so = oracle.act_quant_f32(xs.contiguous().numpy(), 128)
+        np.testing.assert_array_equal(q.cpu().view(torch.uint8).numpy(), qo)
+        np.testing.assert_array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32))
+    x3 = _wide(64, 1024, torch.float16, 6).view(4, 16, 1024)
+    q3, s3 = fp8.act_quant(x3.to(dev), 128)
+    assert q3.shape == (4, 16, 1024) and s3.shape == (4, 16, 8) and q3.dtype == torch.float8_e4m3fn
+    qo, so = oracle.act_quant_f32(x3.float().reshape(64, 1024).numpy(), 128)
+    np.testing.assert_array_equal(q3.cpu().view(torch.uint8).numpy().reshape(64, 1024), qo)
+
+
+def test_act_quant_typed_entry_point_bf16_is_act_quant(dev):
+    """Through the C ABI: x_dtype = BF16 gives fp8b_act_quant's bits."""
+    from hf_kernels_helion_amd import _native
+    lib = _native.load()
+    x = synthetic.activations(33, 2048, seed=9).to(dev)
+    q1 = torch.empty(33, 2048, dtype=torch.uint8, device=dev)
+    q2 = torch.empty_like(q1)
+    s1 = torch.empty(33, 16, device=dev)
+    s2 = torch.empty_like(s1)
+    st = torch.cuda.current_stream().cuda_stream
+    assert lib.fp8b_act_quant(x.data_ptr(), 2048, q1.data_ptr(), 2048, s1.data_ptr(), 16, 1,
+                              33, 2048, 128, st) == 0
+    assert lib.fp8b_act_quant_typed(x.data_ptr(), 2048, _native.BF16, q2.data_ptr(), 2048,
+                                    s2.data_ptr(), 16, 1, 33, 2048, 128, st) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(q1, q2) and torch.equal(s1.view(torch.int32), s2.view(torch.int32))

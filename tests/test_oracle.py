@@ -163,6 +163,80 @@ def test_act_quant_nonfinite_and_zero_policy():
     assert s[3, 0] == np.float32(1.0) / np.float32(448) and np.all(q[3] == 0x7E)
 
 
+def _wide_f32(shape, seed):
+    """fp32 values over many binades (each group gets its own magnitude)."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(shape, generator=g)
+    e = torch.randint(-30, 30, (shape[0], 1), generator=g).float()
+    return (x * torch.exp2(e)).numpy()
+
+
+def test_act_quant_f32_equals_bf16_oracle_on_bf16_values():
+    x, bits = _rand_bf16((24, 640), 11, scale=2.0)
+    q, s = oracle.act_quant(bits, 128)
+    qf, sf = oracle.act_quant_f32(x.float().numpy(), 128)
+    np.testing.assert_array_equal(qf, q)
+    np.testing.assert_array_equal(sf.view(np.uint32), s.view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_act_quant_f32_matches_torch_formulation(dtype):
+    xw = torch.from_numpy(_wide_f32((48, 1024), 12))
+    if dtype == torch.float16:
+        xw = (xw * 1e-4).clamp(-6e4, 6e4).to(torch.float16)
+    q, s = oracle.act_quant_f32(xw.float().numpy(), 128)
+    tq, ts = torch_ref.act_quant(xw, 128)
+    np.testing.assert_array_equal(q, tq.view(torch.uint8).numpy())
+    np.testing.assert_array_equal(s.view(np.uint32), ts.numpy().view(np.uint32))
+
+
+def test_act_quant_f32_rounding_bruteforce_and_closed_form():
+    x = _wide_f32((8, 256), 13)
+    q, s = oracle.act_quant_f32(x, 128)
+    xg = x.reshape(8, 2, 128)
+    amax = np.abs(xg).max(axis=-1)
+    np.testing.assert_array_equal(s, np.maximum(amax, np.float32(1e-10)) / np.float32(448.0))
+    y = (xg / s[:, :, None]).astype(np.float32).ravel()
+    np.testing.assert_array_equal(q.ravel(), _nearest_e4m3_bruteforce(y))
+
+
+def test_act_quant_f32_scale_with_all_ones_mantissa():
+    """A group whose scale has an all-ones mantissa (possible for fp32 and
+    fp16 amax, never for bf16): the quotients still follow the IEEE
+    division."""
+    amax = np.float32(117440504.0)  # / 448 rounds to 262143.98... = (2 - 2^-23) * 2^17
+    s_want = amax / np.float32(448)
+    assert (s_want.view(np.uint32) & 0x7FFFFF) == 0x7FFFFF
+    g = np.random.default_rng(14)
+    x = (g.standard_normal((2, 128)) * 3e7).astype(np.float32)
+    x[:, 5] = amax
+    q, s = oracle.act_quant_f32(x, 128)
+    assert np.all(s[:, 0] == s_want)
+    np.testing.assert_array_equal(q.ravel(), _nearest_e4m3_bruteforce((x / s_want).ravel()))
+
+
+def test_act_quant_f32_nonfinite_subnormal_and_extremes():
+    x = np.zeros((5, 128), dtype=np.float32)
+    x[0, 3] = -0.0
+    x[0, 4] = np.float32(1e-40)            # subnormal, below the 1e-10 floor
+    x[1, 7] = np.nan
+    x[1, 8] = 2.0
+    x[2, 9] = np.inf
+    x[2, 10] = -3.0
+    x[2, 11] = -np.inf
+    x[3, :] = np.float32(3.4028235e38)     # FLT_MAX
+    x[3, 1] = -np.float32(1.0)
+    x[4, :] = np.float32(5e-11)            # amax below the floor
+    q, s = oracle.act_quant_f32(x, 128)
+    assert s[0, 0] == np.float32(1e-10) / np.float32(448) and q[0, 3] == 0x80 and q[0, 4] == 0
+    assert np.isnan(s[1, 0]) and np.all(q[1] == 0x7F)
+    assert np.isinf(s[2, 0]) and q[2, 9] == 0x7F and q[2, 11] == 0x7F and q[2, 10] == 0x80
+    assert s[3, 0] == np.float32(3.4028235e38) / np.float32(448) and q[3, 0] == 0x7E
+    assert q[3, 1] == 0x80  # -1 / 7.6e35 underflows to a signed fp8 zero
+    assert s[4, 0] == np.float32(1e-10) / np.float32(448)
+    np.testing.assert_array_equal(q[4], _torch_e4m3(x[4] / s[4, 0]))
+
+
 # ---------------------------------------------------------------- block GEMM
 
 def _dequant64(A, B, As, Bs, bn, bk):
