@@ -2,6 +2,8 @@
 
 Usage: python -m hf_kernels_helion_amd.build   (or build() from Python)
 The library has no torch dependency; the Python package loads it with ctypes.
+Beside it: libfp8_torch_ops.so (the torch custom ops) and _fp8_fast.so (direct
+Python bindings of the hot ops for eager calls).
 """
 from __future__ import annotations
 
@@ -16,6 +18,7 @@ CSRC = PKG_DIR / "csrc"
 LIB_DIR = PKG_DIR / "_lib"
 LIB_NAME = "libfp8_blockwise.so"
 TORCH_LIB_NAME = "libfp8_torch_ops.so"
+FAST_MODULE_NAME = "_fp8_fast.so"
 SOURCES = ["capi.cpp", "act_quant.hip", "block_gemm.hip"]
 ARCH = "gfx950"
 
@@ -76,6 +79,30 @@ def build_torch_ops(verbose: bool = False) -> Path:
     return out
 
 
+def build_fast_module(verbose: bool = False) -> Path:
+    """Compile the direct Python bindings of the hot ops (torch_fast.cpp) into
+    the extension module LIB_DIR/_fp8_fast.so; it links the op library."""
+    import sysconfig
+    import torch
+    from torch.utils import cpp_extension as ce
+    out = LIB_DIR / FAST_MODULE_NAME
+    tmp = LIB_DIR / (FAST_MODULE_NAME + ".tmp")
+    torch_lib = Path(torch.__file__).resolve().parent / "lib"
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           "-DTORCH_EXTENSION_NAME=_fp8_fast", "-DTORCH_API_INCLUDE_EXTENSION_H",
+           "-Wno-deprecated-declarations", "-fvisibility=hidden"]
+    for inc in ce.include_paths(device_type="cuda") + [sysconfig.get_paths()["include"]]:
+        cmd += ["-isystem", inc]
+    cmd += [str(CSRC / "torch_fast.cpp"), "-o", str(tmp),
+            f"-L{LIB_DIR}", "-lfp8_torch_ops", f"-L{torch_lib}", "-lc10", "-ltorch",
+            "-ltorch_cpu", "-ltorch_python", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{torch_lib}"]
+    _run(cmd, verbose)
+    os.replace(tmp, out)
+    return out
+
+
 def build(verbose: bool = False) -> Path:
     """Compile the HIP kernels into LIB_DIR/LIB_NAME and the torch op library
     beside it; returns the kernel library path."""
@@ -87,6 +114,7 @@ def build(verbose: bool = False) -> Path:
     _run(cmd, verbose)
     os.replace(tmp, out)
     build_torch_ops(verbose)
+    build_fast_module(verbose)
     return out
 
 

@@ -27,8 +27,9 @@
 #include <torch/library.h>
 
 #include "../../include/fp8_blockwise.h"
+#include "torch_ops.h"
 
-namespace {
+namespace fp8b_torch {
 
 using at::Tensor;
 
@@ -357,7 +358,9 @@ std::tuple<Tensor, Tensor> gate_up_silu_quant_cpu(const Tensor&, const Tensor&, 
   no_cpu("gate_up_silu_quant");
 }
 
-}  // namespace
+}  // namespace fp8b_torch
+
+using namespace fp8b_torch;
 
 TORCH_LIBRARY(_finegrained_fp8_helion_rocm_mi355x, m) {
   m.def("w8a8_block_fp8_matmul(Tensor A, Tensor B, Tensor As, Tensor Bs, int block_n, "

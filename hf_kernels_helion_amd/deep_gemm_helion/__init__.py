@@ -12,7 +12,7 @@ from __future__ import annotations
 
 import torch
 
-from ..finegrained_fp8_helion import op as _load_ops  # noqa: F401 (loads the op library)
+from ..finegrained_fp8_helion import op as _load_ops  # loads the op library and bindings
 from ._ops import add_op_namespace_prefix, ops
 
 
@@ -27,6 +27,10 @@ def gemm_fp8_fp8_bf16_nt(A: torch.Tensor, B: torch.Tensor, As: torch.Tensor,
 
     A [M,K] e4m3fn, B [N,K] e4m3fn, As fp32 [M, K//block_size], Bs fp32
     [N, K//block_size] (one scale per weight row and K-block)."""
+    if not torch.compiler.is_compiling():
+        out = _load_ops.fast.gemm_fp8_fp8_bf16_nt(A, B, As, Bs, int(block_size))
+        if out is not None:
+            return out
     return ops.gemm_fp8_fp8_bf16_nt(A, B, As, Bs, int(block_size))
 
 

@@ -12,6 +12,7 @@ activation-helion/activation-helion/torch-ext/activation_helion/op.py:15-23
 """
 from __future__ import annotations
 
+import importlib.util
 from pathlib import Path
 
 import torch
@@ -19,17 +20,26 @@ import torch
 from ._ops import add_op_namespace_prefix
 
 _LIB = Path(__file__).resolve().parent.parent / "_lib" / "libfp8_torch_ops.so"
+_FAST = _LIB.parent / "_fp8_fast.so"
 
 
-def _load() -> None:
-    if not _LIB.exists():
-        raise RuntimeError(
-            f"{_LIB} is missing: build the HIP kernels and op library first "
-            "(python -m hf_kernels_helion_amd.build)")
+def _load():
+    """Load the op library, then the direct bindings of its hot ops (module
+    _fp8_fast: the same C++ functions without the dispatcher, for plain eager
+    calls; each returns None when the call must take torch.ops)."""
+    for f in (_LIB, _FAST):
+        if not f.exists():
+            raise RuntimeError(
+                f"{f} is missing: build the HIP kernels and op library first "
+                "(python -m hf_kernels_helion_amd.build)")
     torch.ops.load_library(str(_LIB))
+    spec = importlib.util.spec_from_file_location("_fp8_fast", _FAST)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
 
 
-_load()
+fast = _load()
 
 
 @torch.library.register_fake(add_op_namespace_prefix("w8a8_block_fp8_matmul"))

@@ -69,6 +69,60 @@ def test_fake_impls_give_reference_shapes():
         assert q.shape == (300, 260) and s.shape == (3, 3) and s.dtype == torch.float32
 
 
+def test_public_api_under_fake_tensors_takes_the_op_route():
+    """The direct bindings decline tensor subclasses (FakeTensor here), so the
+    public functions reach the registered ops and their fake kernels."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    from hf_kernels_helion_amd import deep_gemm_helion as dg
+    from hf_kernels_helion_amd.finegrained_fp8_helion import op
+    with FakeTensorMode():
+        A, B = _fp8(7, 384), _fp8(200, 384)
+        As, Bs = torch.ones(7, 3), torch.ones(2, 3)
+        assert op.fast.w8a8_block_fp8_matmul_dtype(A, B, As, Bs, 128, 128,
+                                                   torch.bfloat16) is None
+        out = fp8.w8a8_block_fp8_matmul(A, B, As, Bs, [128, 128], torch.bfloat16)
+        assert out.shape == (7, 200) and out.dtype == torch.bfloat16
+        q, s = fp8.act_quant(torch.zeros(3, 300, dtype=torch.float16), 128)
+        assert q.shape == (3, 300) and s.shape == (3, 3)
+        q, s = fp8.silu_and_mul_quant(torch.zeros(4, 512, dtype=torch.bfloat16))
+        assert q.shape == (4, 256)
+        out = fp8.act_quant_w8a8_block_fp8_matmul(torch.zeros(7, 384, dtype=torch.bfloat16),
+                                                  B, Bs, [128, 128], torch.bfloat16)
+        assert out.shape == (7, 200)
+        out = dg.gemm_fp8_fp8_bf16_nt(A, B, As, torch.ones(200, 3))
+        assert out.shape == (7, 200) and out.dtype == torch.bfloat16
+
+
+def test_public_api_compiles_to_the_registered_op():
+    """Under torch.compile the wrappers call torch.ops (no graph break with
+    fullgraph=True): the traced graph holds the custom op."""
+    import torch._dynamo
+    seen = []
+
+    class Traced(Exception):
+        pass
+
+    def backend(gm, example_inputs):
+        seen.extend(str(n.target) for n in gm.graph.nodes if n.op == "call_function")
+
+        def run(*args):
+            raise Traced()
+        return run
+
+    def f(A, B, As, Bs, x):
+        q, s = fp8.act_quant(x, 128)
+        return fp8.w8a8_block_fp8_matmul(A, B, As, Bs, [128, 128], torch.bfloat16), q, s
+
+    torch._dynamo.reset()
+    g = torch.compile(f, backend=backend, fullgraph=True)
+    with pytest.raises(Traced):
+        g(_fp8(7, 384), _fp8(200, 384), torch.ones(7, 3), torch.ones(2, 3),
+          torch.zeros(7, 384, dtype=torch.bfloat16))
+    torch._dynamo.reset()
+    assert any("w8a8_block_fp8_matmul_dtype" in t for t in seen), seen
+    assert any("act_quant" in t for t in seen), seen
+
+
 def test_op_schemas_match_reference():
     # finegrained-fp8-helion/torch-ext/finegrained_fp8_helion/op.py:8-11 and
     # activation-helion/.../op.py:15-16
