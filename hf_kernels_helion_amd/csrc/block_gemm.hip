@@ -50,6 +50,11 @@ struct GemmArgs {
   int tiles_m, tiles_n;
   int out_dtype;     // fp8b_dtype; ignored when writing split-K partials
   int vec_store;     // 1 if 4 consecutive outputs can be stored as one vector
+  // Pipelined kernels: 1 = scale windows by 4-byte DMA lanes (any scale
+  // strides, any K-block count and split size); 0 = by 16-byte lanes (As and
+  // Bs contiguous in K with 16-byte aligned rows, K-block count and split
+  // size multiples of 4).
+  int win4;
   // gemm_pipe128_kernel and gemm_tiny_kernel only: when rem_base >= 0,
   // workgroup w computes quarter w % 4 of tile rem_base + w / 4 of a
   // rem_tiles_m x rem_tiles_n grid of tiles twice as large (the tiles a
@@ -497,9 +502,11 @@ __device__ __forceinline__ void lds_reads_done() {
 //     loads, so it neither tracks them (the kernel waits on vmcnt itself,
 //     before each barrier) nor treats them as LGKM events of unknown order,
 //     which would force lgkmcnt(0) before every fragment read.
-// Preconditions (checked by the host): As and Bs contiguous along K with row
-// strides that keep 16-byte alignment, KB and the split size multiples of 4,
-// and 255 * max(lda, ldb) + K below 2^32 for the 32-bit DMA offsets.
+// Precondition (checked by the host): 255 * max(lda, ldb) + K below 2^32 for
+// the 32-bit DMA offsets. Scale windows take 16-byte DMA lanes when As and
+// Bs are contiguous along K with 16-byte aligned rows and KB and the split
+// size are multiples of 4, else (a.win4) 4-byte lanes with every K-block
+// clamped into range (win4_rows, win4_blocks): any strides and counts.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void dma16_soff(uint32_t voff, const void* sbase, uint32_t lds) {
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
@@ -513,6 +520,32 @@ __device__ __forceinline__ void dma4_ptr(const void* g, uint32_t lds) {
   asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off"
                :: "v"(g), "{m0}"(lds) : "memory");
 }
+// Scale window of 8 K-blocks by 4-byte DMA lanes, for any scale strides and
+// K-block counts: rows r0..r0+31 (each clamped to rmax) into 32-byte row
+// slots at lds (slot s: K-block kb0 + s, clamped to kb_end - 1), four
+// instructions of 8 rows; lane i of instruction j writes row 8j + i/8, slot
+// i%8 (LDS DMA lane i lands at M0 + 4i).
+__device__ __forceinline__ void win4_rows(const float* S, int64_t sm, int64_t sk, int r0, int rmax,
+                                          int kb0, int kb_end, uint32_t lds, int lane) {
+  const int64_t kofs = (int64_t)min(kb0 + (lane & 7), kb_end - 1) * sk;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    int r = min(r0 + 8 * j + (lane >> 3), rmax);
+    asm volatile("" : "+v"(r));
+    dma4_ptr(S + (int64_t)r * sm + kofs, lds + j * 256);
+  }
+}
+// The weight-block scales of a window: nb 128-column blocks from row b0
+// (clamped to bmax), 8 slots each, lanes 0..8nb-1.
+__device__ __forceinline__ void win4_blocks(const float* S, int64_t sm, int64_t sk, int b0, int bmax,
+                                            int nb, int kb0, int kb_end, uint32_t lds, int lane) {
+  if (lane < 8 * nb) {
+    const int b = min(b0 + (lane >> 3), bmax);
+    const int kb = min(kb0 + (lane & 7), kb_end - 1);
+    dma4_ptr(S + (int64_t)b * sm + (int64_t)kb * sk, lds);
+  }
+}
+
 __device__ __forceinline__ uint32_t lds_u32(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
@@ -589,9 +622,10 @@ __global__ void __launch_bounds__(512) gemm_pipe256_kernel(GemmArgs a) {
     }
   };
   // Scale window of 8 K-blocks from kb0: wave w brings As rows 32w..32w+31
-  // (two lanes per row, 4 K-blocks each); wave 7 also brings the Bs rows of
-  // the tile's two 128-column blocks. A half-window past kb_end re-reads the
-  // first half (KB is a multiple of 4), so no lane reads past the row.
+  // (16-byte lanes: two per row, 4 K-blocks each); wave 7 also brings the Bs
+  // rows of the tile's two 128-column blocks. With 16-byte lanes a
+  // half-window past kb_end re-reads the first half (KB is then a multiple
+  // of 4), so no lane reads past the row.
   const float* saw_src =
       a.As + (int64_t)min(m0 + wid * 32 + (lane >> 1), a.M - 1) * a.as_sm + 4 * (lane & 1);
   const float* sbw_src =
@@ -599,7 +633,10 @@ __global__ void __launch_bounds__(512) gemm_pipe256_kernel(GemmArgs a) {
   auto issue_win = [&](int kb0, int wbuf) {
     const int kk = (kb0 + 4 * (lane & 1) < kb_end) ? kb0 : kb0 - 4 * (lane & 1);
     const uint32_t lb = lds0 + SW_OFF + wbuf * WIN;
-    dma16_ptr(saw_src + kk, lb + wid * 1024);
+    if (a.win4)
+      win4_rows(a.As, a.as_sm, a.as_sk, m0 + wid * 32, a.M - 1, kb0, kb_end, lb + wid * 1024, lane);
+    else
+      dma16_ptr(saw_src + kk, lb + wid * 1024);
     if constexpr (PR) {
       // wave w: slot w, rows 64h + lane for h = 0..3
       // (the row is pinned so that the addresses are formed here, once per
@@ -609,11 +646,14 @@ __global__ void __launch_bounds__(512) gemm_pipe256_kernel(GemmArgs a) {
       for (int h = 0; h < 4; ++h) {
         int row = n0 + h * 64 + lane;
         asm volatile("" : "+v"(row));
-        dma4_ptr(a.Bs + (int64_t)min(row, a.N - 1) * a.bs_sn + kbs,
+        dma4_ptr(a.Bs + (int64_t)min(row, a.N - 1) * a.bs_sn + (int64_t)kbs * a.bs_sk,
                  lb + WIN_SA + wid * 1024 + h * 256);
       }
-    } else {
-      if (wid == NW - 1 && lane < 4) dma16_ptr(sbw_src + kk, lb + WIN_SA);
+    } else if (wid == NW - 1) {
+      if (a.win4)
+        win4_blocks(a.Bs, a.bs_sn, a.bs_sk, n0 >> 7, (a.N - 1) >> 7, 2, kb0, kb_end, lb + WIN_SA, lane);
+      else if (lane < 4)
+        dma16_ptr(sbw_src + kk, lb + WIN_SA);
     }
   };
 
@@ -890,8 +930,16 @@ __global__ void __launch_bounds__(512) gemm_pipe192_kernel(GemmArgs a) {
   auto issue_win = [&](int kb0, int wbuf) {
     const int kk = (kb0 + 4 * (lane & 1) < kb_end) ? kb0 : kb0 - 4 * (lane & 1);
     const uint32_t lb = lds0 + SW_OFF + wbuf * WIN;
-    if (wid < BM / 32) dma16_ptr(saw_src + kk, lb + wid * 1024);
-    if (wid == NW - 1 && lane < 4) dma16_ptr(sbw_src + kk, lb + WIN_SA);
+    if (a.win4) {
+      if (wid < BM / 32)
+        win4_rows(a.As, a.as_sm, a.as_sk, m0 + wid * 32, a.M - 1, kb0, kb_end, lb + wid * 1024,
+                  lane);
+      if (wid == NW - 1)
+        win4_blocks(a.Bs, a.bs_sn, a.bs_sk, n0 >> 7, (a.N - 1) >> 7, 2, kb0, kb_end, lb + WIN_SA, lane);
+    } else {
+      if (wid < BM / 32) dma16_ptr(saw_src + kk, lb + wid * 1024);
+      if (wid == NW - 1 && lane < 4) dma16_ptr(sbw_src + kk, lb + WIN_SA);
+    }
   };
 
   const int r7 = lane & 7, g2 = 2 * (lane >> 4);
@@ -1130,26 +1178,32 @@ __global__ void __launch_bounds__(512) gemm_pipe256x128_kernel(GemmArgs a) {
   // Scale window of 8 K-blocks: wave w brings As rows 32w..32w+31 (two lanes
   // per row, 4 K-blocks each); lanes 0-1 of wave 7 also bring the tile's Bs
   // row (PR: wave w brings slot w, the 128 rows' scales of K-block kb0 + w).
-  // A half-window past kb_end re-reads the first half (KB is a multiple of
-  // 4), so no lane reads past the row.
+  // With 16-byte lanes a half-window past kb_end re-reads the first half (KB
+  // is then a multiple of 4), so no lane reads past the row.
   const float* saw_src =
       a.As + (int64_t)min(m0 + wid * 32 + (lane >> 1), a.M - 1) * a.as_sm + 4 * (lane & 1);
   const float* sbw_src = a.Bs + (int64_t)(n0 >> 7) * a.bs_sn + 4 * (lane & 1);
   auto issue_win = [&](int kb0, int wbuf) {
     const int kk = (kb0 + 4 * (lane & 1) < kb_end) ? kb0 : kb0 - 4 * (lane & 1);
     const uint32_t lb = lds0 + SW_OFF + wbuf * WIN;
-    dma16_ptr(saw_src + kk, lb + wid * 1024);
+    if (a.win4)
+      win4_rows(a.As, a.as_sm, a.as_sk, m0 + wid * 32, a.M - 1, kb0, kb_end, lb + wid * 1024, lane);
+    else
+      dma16_ptr(saw_src + kk, lb + wid * 1024);
     if constexpr (PR) {
       const int kbs = min(kb0 + wid, kb_end - 1);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         int row = n0 + h * 64 + lane;
         asm volatile("" : "+v"(row));
-        dma4_ptr(a.Bs + (int64_t)min(row, a.N - 1) * a.bs_sn + kbs,
+        dma4_ptr(a.Bs + (int64_t)min(row, a.N - 1) * a.bs_sn + (int64_t)kbs * a.bs_sk,
                  lb + WIN_SA + wid * 512 + h * 256);
       }
-    } else {
-      if (wid == NW - 1 && lane < 2) dma16_ptr(sbw_src + kk, lb + WIN_SA);
+    } else if (wid == NW - 1) {
+      if (a.win4)
+        win4_blocks(a.Bs, a.bs_sn, a.bs_sk, n0 >> 7, (a.N - 1) >> 7, 1, kb0, kb_end, lb + WIN_SA, lane);
+      else if (lane < 2)
+        dma16_ptr(sbw_src + kk, lb + WIN_SA);
     }
   };
 
@@ -1394,7 +1448,13 @@ __global__ void __launch_bounds__((128 / WM) * (128 / WN) * 64) gemm_pipe128_ker
   auto issue_win = [&](int kb0, int wbuf) {
     const int kk = (kb0 + 4 * (lane & 1) < kb_end) ? kb0 : kb0 - 4 * (lane & 1);
     const uint32_t lb = lds0 + SW_OFF + wbuf * WIN;
-    if (wid < BM / 32) dma16_ptr(saw_src + kk, lb + wid * 1024);
+    if (wid < BM / 32) {
+      if (a.win4)
+        win4_rows(a.As, a.as_sm, a.as_sk, m0 + wid * 32, a.M - 1, kb0, kb_end, lb + wid * 1024,
+                  lane);
+      else
+        dma16_ptr(saw_src + kk, lb + wid * 1024);
+    }
     if constexpr (PR) {
       // slot-major (slot s: the 128 rows' scales of K-block kb0 + s as
       // consecutive floats), so a lane reads its four rows in one 16-byte
@@ -1411,8 +1471,11 @@ __global__ void __launch_bounds__((128 / WM) * (128 / WN) * 64) gemm_pipe128_ker
                    lb + WIN_SA + sl * 512 + h * 256);
         }
       }
-    } else {
-      if (wid == NW - 1 && lane < 2) dma16_ptr(sbw_src + kk, lb + WIN_SA);
+    } else if (wid == NW - 1) {
+      if (a.win4)
+        win4_blocks(a.Bs, a.bs_sn, a.bs_sk, n0 >> 7, (a.N - 1) >> 7, 1, kb0, kb_end, lb + WIN_SA, lane);
+      else if (lane < 2)
+        dma16_ptr(sbw_src + kk, lb + WIN_SA);
     }
   };
   // DMA of one K-block (and, at a window start, its scale window).
@@ -2363,8 +2426,9 @@ Plan large_tile_plan(int64_t M, int64_t N, int64_t K, bool per_row, int cus) {
         consider({tc.cfg, tc.bm, tc.bn, 1, KB, TAIL_Q64},
                  base + wave_us(q64_us, 64, 64, 4 * rest, KB, 2.0, cus));
     }
-    // K splits, in whole scale half-windows (multiples of 4 K-blocks) so
-    // the pipelined kernels stay usable, at least four K-blocks per split.
+    // K splits, in whole scale half-windows (multiples of 4 K-blocks, which
+    // keep the 16-byte window lanes) when KB allows, at least four K-blocks
+    // per split.
     if ((tc.cfg == CFG_128x128 || (tc.cfg == CFG_256x128 && tn > 8 && M >= 256)) && t < cus) {
       for (int s = 2; t * s <= cus && KB / s >= 4; s *= 2) {
         int kbs = (KB + s - 1) / s;
@@ -2577,7 +2641,7 @@ bool mfma_path_ok(const void* A, int64_t lda, const void* B, int64_t ldb, int64_
 struct Operands {
   int64_t lda, ldb;
   bool mfma;    // mfma_path_ok
-  bool scales;  // As, Bs contiguous in K with 16-byte aligned rows (scale windows)
+  bool scales;  // As, Bs contiguous in K with 16-byte aligned rows (16-byte window lanes)
 };
 
 // Operands of a plan query: contiguous, 16-byte aligned, K-contiguous scales.
@@ -2593,15 +2657,17 @@ Operands contiguous_operands(int64_t M, int64_t N, int64_t K, int64_t block_n,
   return o;
 }
 
-// Preconditions of the pipelined kernels: scale windows (As, Bs contiguous
-// in K, 16-byte aligned rows, K-block counts and split sizes multiples of 4)
-// and 32-bit DMA offsets within a 256-row tile. FP8B_PIPE=0 turns them off.
-bool pipe_ok(const Operands& o, int64_t K, const Plan& p) {
-  if (!use_pipelined_kernels()) return false;
-  const int KB = (int)(K / 128);
-  const bool splits_ok = p.splits == 1 || p.kb_per_split % 4 == 0;
-  return o.scales && KB % 4 == 0 && splits_ok &&
-         255 * std::max(o.lda, o.ldb) + K < (int64_t(1) << 32);
+// Precondition of the pipelined kernels: 32-bit DMA offsets within a
+// 256-row tile. FP8B_PIPE=0 turns them off. Their scale windows take 16-byte
+// DMA lanes when As and Bs are contiguous in K with 16-byte aligned rows and
+// the K-block count and split size are multiples of 4 (win16_ok), else
+// 4-byte lanes (any strides and counts; 4.4 against 1.1 DMA instructions
+// per wave and 8 K-blocks).
+bool pipe_ok(const Operands& o, int64_t K) {
+  return use_pipelined_kernels() && 255 * std::max(o.lda, o.ldb) + K < (int64_t(1) << 32);
+}
+bool win16_ok(const Operands& o, int64_t K, int splits, int kb_per_split) {
+  return o.scales && (K / 128) % 4 == 0 && (splits == 1 || kb_per_split % 4 == 0);
 }
 
 // Everything fp8b_w8a8_block_matmul launches for one call: the main kernel
@@ -2620,6 +2686,7 @@ struct Dispatch {
   int tail_bm = 0, tail_bn = 0;
   int64_t tail_grid = 0;
   bool per_row = false;
+  bool win4 = false;   // pipelined kernels: scale windows by 4-byte DMA lanes
 };
 
 // One unsplit grid of 256x256 tiles on gemm_pipe256_kernel. When the tiles
@@ -2711,7 +2778,7 @@ Dispatch resolve(int64_t M, int64_t N, int64_t K, int64_t block_n, int64_t block
     }
     p.cfg = CFG_SKINNY; p.bn = 16; p.splits = 1; p.kb_per_split = KB;
   }
-  const bool pipe = pipe_ok(o, K, p);
+  const bool pipe = pipe_ok(o, K);
   // 192x256 and 256x128 tiles exist only as pipelined kernels: without
   // their preconditions the grid goes back to 256x256 or 128x128 tiles.
   if (p.cfg == CFG_192x256 && !pipe) { p.cfg = CFG_256x256; p.bm = 256; p.tail = TAIL_NONE; }
@@ -2720,6 +2787,7 @@ Dispatch resolve(int64_t M, int64_t N, int64_t K, int64_t block_n, int64_t block
   d.bn = p.bn;
   d.splits = p.splits;
   d.kb_per_split = p.kb_per_split;
+  d.win4 = !win16_ok(o, K, p.splits, p.kb_per_split);
   const int64_t tiles = ((M + p.bm - 1) / p.bm) * ((N + p.bn - 1) / p.bn);
   switch (p.cfg) {
     case CFG_SKINNY:
@@ -3040,6 +3108,7 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
   a.rem_base = -1; a.rem_tiles_m = 0; a.rem_tiles_n = 0;
   a.Sq = nullptr; a.sq_sm = 0; a.sq_sg = 0;
   a.vec_store = (d.splits > 1) ? (ws_vec ? 1 : 0) : (c_vec ? 1 : 0);
+  a.win4 = d.win4 ? 1 : 0;
 
   if (per_row) launch_dispatch<true>(d, a, st);
   else launch_dispatch<false>(d, a, st);
@@ -3290,6 +3359,7 @@ extern "C" int fp8b_gate_up_silu_quant(const void* A, int64_t lda, const void* B
   a.tiles_n = (int)(N / 256);
   a.out_dtype = FP8B_BF16;
   a.vec_store = 0;
+  a.win4 = 0;  // K % 512 == 0 and 16-byte aligned K-contiguous scale rows (checked above)
   a.rem_base = -1; a.rem_tiles_m = 0; a.rem_tiles_n = 0;
   a.Sq = s; a.sq_sm = s_stride_m; a.sq_sg = s_stride_g;
   const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;

@@ -242,8 +242,8 @@ def _full_check(out, Ad, Bd, Asd, Bsd):
 def test_gemm_large_tile_kernels(M, N, K, dev):
     """Grids of at least one 256x256 tile per CU: the pipelined kernel (K-block
     counts that are multiples of 4; windows of 8 K-blocks, full and half) and
-    the two-stage kernel it falls back to (K-block counts 3 and 9), with
-    ragged M and N edges; 3001x4096x8192 is a partial wave of 256x256 tiles
+    K-block counts 3 and 9 (scale windows by 4-byte lanes), with ragged M
+    and N edges; 3001x4096x8192 is a partial wave of 256x256 tiles
     (192 tiles, chosen over three waves of 128x128 tiles for long K). Every row against torch's fp32 dequant-matmul, a
     sample of rows against the oracle."""
     print(f"gemm large-tile M={M} N={N} K={K}", flush=True)
@@ -280,7 +280,7 @@ def test_gemm_mid_tile_kernels(M, N, K, dev):
 
 def test_gemm_large_tile_exact_and_fp32(dev):
     """Pipelined kernel with small-integer operands and unit scales (exact
-    result), fp32 output; and with column-major As (two-stage fallback)."""
+    result), fp32 output; and with column-major As (4-byte window lanes)."""
     print("gemm large-tile exact", flush=True)
     g = torch.Generator().manual_seed(5)
     M, N, K = 4096, 4096, 512
@@ -295,6 +295,79 @@ def test_gemm_large_tile_exact_and_fp32(dev):
     As2_t = As2.T.contiguous().T
     out2 = fp8.w8a8_block_fp8_matmul(A2, B2, As2_t, Bs2, [128, 128], torch.float32)
     _full_check(out2, A2, B2, As2, Bs2)
+
+
+# Grids of the pipelined kernels whose scale windows take 4-byte DMA lanes:
+# K-block counts (and split sizes) that are not multiples of 4 (K = 11008:
+# LLaMA-2's intermediate size; 1152, 1408), for block scales and per-row
+# weight scales, with the tails of partial waves.
+WIN4_CASES = [
+    (4096, 4096, 1408, 128, "gemm_pipe256_kernel"),
+    (4224, 4096, 1152, 128, "gemm_pipe256_kernel"),      # + 128x128 quarters
+    (4096, 6144, 1408, 128, "gemm_pipe256_kernel"),      # + 256x128 halves
+    (3001, 4096, 1408, 128, "gemm_pipe192_kernel"),
+    (2048, 4096, 1408, 128, "gemm_pipe256x128_kernel"),
+    (2048, 2048, 1408, 128, "gemm_pipe128_kernel"),
+    (512, 4096, 11008, 128, "gemm_pipe128_kernel"),      # 2 splits of 43 K-blocks
+    (128, 4096, 11008, 128, "gemm_pipe128_kernel"),      # 8 splits of 11
+    (4096, 4096, 1408, 1, "gemm_pipe256_kernel"),
+    (4224, 4096, 1152, 1, "gemm_pipe256_kernel"),
+    (2048, 4096, 1408, 1, "gemm_pipe256x128_kernel"),
+    (512, 4096, 11008, 1, "gemm_pipe256x128_kernel"),    # 4 splits of 22
+    (2048, 2048, 1408, 1, "gemm_pipe128_kernel"),
+    (128, 4096, 11008, 1, "gemm_pipe128_kernel"),
+]
+
+
+@pytest.mark.parametrize("M,N,K,block_n,kernel", WIN4_CASES)
+def test_gemm_pipelined_any_k_block_count(M, N, K, block_n, kernel, dev):
+    """The pipelined kernels with K-block counts or split sizes that are not
+    multiples of 4 (scale windows by 4-byte lanes): every row against
+    torch's fp32 dequant-matmul, a sample of rows against the oracle."""
+    from hf_kernels_helion_amd import _native
+    print(f"gemm any-KB M={M} N={N} K={K} block_n={block_n}", flush=True)
+    plan = _native.gemm_plan(M, N, K, block_n=block_n)
+    if plan["cu_count"] == 256:
+        assert plan["kernel"] == kernel, plan
+    x = synthetic.activations(M, K, seed=M + K)
+    q, s = fp8.act_quant(x.to(dev), 128)
+    W, Bs = synthetic.weights(N, K, seed=N + K, block_n=block_n)
+    W, Bs = W.to(dev), Bs.to(dev)
+    out = fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [block_n, 128], torch.bfloat16)
+    saf = s.repeat_interleave(128, 1)[:, :K]
+    sbf = (Bs if block_n == 1 else Bs.repeat_interleave(128, 0)[:N]).repeat_interleave(128, 1)
+    full = (q.float() * saf) @ (W.float() * sbf[:, :K]).T
+    torch.testing.assert_close(out.float(), full.to(torch.bfloat16).float(), rtol=RTOL,
+                               atol=ATOL)
+    rows = torch.tensor([0, M // 2, M - 1])
+    ref = oracle.block_gemm(_u8(q.cpu()[rows]), _u8(W.cpu()), s.cpu()[rows].numpy(),
+                            Bs.cpu().numpy(), (block_n, 128))
+    torch.testing.assert_close(out[rows.to(dev)].float().cpu(),
+                               torch.from_numpy(ref).to(torch.bfloat16).float(),
+                               rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("M,N,K,block_n", [(4096, 4096, 1024, 128), (2048, 2048, 2048, 128),
+                                           (3001, 4096, 1024, 128), (512, 4096, 8192, 128),
+                                           (4096, 4096, 1024, 1), (2048, 4096, 2048, 1),
+                                           (4096, 4096, 1408, 128)])
+def test_gemm_scale_layouts_same_bits(M, N, K, block_n, dev):
+    """Scales that are not K-contiguous 16-byte aligned rows (column-major,
+    or rows padded to an odd stride) take the 4-byte window lanes on the same
+    plan: the result bits equal those of contiguous scales."""
+    print(f"gemm scale layouts M={M} N={N} K={K} block_n={block_n}", flush=True)
+    x = synthetic.activations(M, K, seed=3 * M + K)
+    q, s = fp8.act_quant(x.to(dev), 128)
+    W, Bs = synthetic.weights(N, K, seed=N + 2 * K, block_n=block_n)
+    W, Bs = W.to(dev), Bs.to(dev)
+    ref = fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [block_n, 128], torch.bfloat16)
+    KB = s.shape[1]
+    s_cm = s.T.contiguous().T                                   # column-major As
+    s_pad = torch.zeros(M, KB + 1, device=dev)[:, :KB].copy_(s)  # row stride KB + 1
+    Bs_cm = Bs.T.contiguous().T
+    for As_, Bs_ in ((s_cm, Bs), (s_pad, Bs), (s, Bs_cm), (s_cm, Bs_cm)):
+        out = fp8.w8a8_block_fp8_matmul(q, W, As_, Bs_, [block_n, 128], torch.bfloat16)
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
 
 
 def test_gemm_golden_fixture(dev):
