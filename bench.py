@@ -689,8 +689,10 @@ def run_only(what, steps, warmup, torch, fp8, synthetic, dev):
             torch.cuda.synchronize()
             return e0.elapsed_time(e1) / (10 * reps)
         log(f"{'M':>5} {'N':>6} {'K':>6} {'block_us':>9} {'vendor_us':>10} {'ratio':>6}")
+        # (4096, 11008): LLaMA-2-7B's down projection, 86 K-blocks (scale
+        # windows by 4-byte lanes)
         for (N, K) in ((4096, 4096), (28672, 4096), (4096, 14336), (6144, 4096), (8192, 8192),
-                       (2048, 7168), (7168, 2048)):
+                       (2048, 7168), (7168, 2048), (4096, 11008)):
             W, Bs = _gpu_weights(N, K, 80, dev, torch, synthetic)
             for M in (256, 512, 1024, 2048, 4096, 8192):
                 A, As = fp8.act_quant(_gpu_acts(M, K, 81, dev, torch), 128)
