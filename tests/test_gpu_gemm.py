@@ -370,6 +370,47 @@ def test_gemm_scale_layouts_same_bits(M, N, K, block_n, dev):
         assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
 
 
+def _random_layout_cases(n, seed):
+    """Random shapes on the pipelined grids (M 129..4096, N 129..8192, any
+    K-block count 1..96), block or per-row weight scales, and a random scale
+    layout: contiguous, column-major, or rows padded to an odd stride."""
+    g = torch.Generator().manual_seed(seed)
+    cases = []
+    for i in range(n):
+        M = int(torch.randint(129, 4097, (1,), generator=g))
+        N = int(torch.randint(129, 8193, (1,), generator=g))
+        KB = int(torch.randint(1, 97, (1,), generator=g))
+        block_n = 1 if i % 3 == 0 else 128
+        layout = ["contiguous", "colmajor", "padded"][i % 3 if block_n == 128 else (i // 3) % 3]
+        cases.append((M, N, 128 * KB, block_n, layout))
+    return cases
+
+
+@pytest.mark.parametrize("M,N,K,block_n,layout", _random_layout_cases(18, 31))
+def test_gemm_random_shapes_and_scale_layouts(M, N, K, block_n, layout, dev):
+    """Every element against torch's fp32 dequant-matmul, within the
+    north-star tolerance, for random shapes with any K-block count and
+    scales in any of three layouts."""
+    print(f"gemm random layout M={M} N={N} K={K} block_n={block_n} {layout}", flush=True)
+    x = synthetic.activations(M, K, seed=M + 3 * N + K)
+    q, s = fp8.act_quant(x.to(dev), 128)
+    W, Bs = synthetic.weights(N, K, seed=N + K, block_n=block_n)
+    W, Bs = W.to(dev), Bs.to(dev)
+
+    def lay(t):
+        if layout == "colmajor":
+            return t.T.contiguous().T
+        if layout == "padded":
+            return torch.zeros(t.shape[0], t.shape[1] + 1, device=dev)[:, :t.shape[1]].copy_(t)
+        return t
+    out = fp8.w8a8_block_fp8_matmul(q, W, lay(s), lay(Bs), [block_n, 128], torch.bfloat16)
+    saf = s.repeat_interleave(128, 1)[:, :K]
+    sbf = (Bs if block_n == 1 else Bs.repeat_interleave(128, 0)[:N]).repeat_interleave(128, 1)
+    full = (q.float() * saf) @ (W.float() * sbf[:, :K]).T
+    torch.testing.assert_close(out.float(), full.to(torch.bfloat16).float(), rtol=RTOL,
+                               atol=ATOL)
+
+
 def test_gemm_golden_fixture(dev):
     """Float64 golden output; the fp8 MFMA sums a 128-long K-block with less
     than fp32 precision (measured ~2^-15 relative to the block's dot), so the
