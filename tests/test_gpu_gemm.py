@@ -990,8 +990,8 @@ def _random_shapes_large(n, seed):
 
 def _random_256x128_shapes(n, seed, cus=256):
     """Random grids that the planner gives 256x128 tiles on a 256-CU device
-    (K a multiple of 512 for three in four: the pipelined kernel's
-    precondition)."""
+    (K a multiple of 512 for three in four: 16-byte scale windows; the rest
+    take the 4-byte window lanes)."""
     g = torch.Generator().manual_seed(seed)
     shapes = []
     while len(shapes) < n:
@@ -1010,9 +1010,8 @@ def test_gemm_random_shapes_large(M, N, K, block_n, dtype, dev):
     """A seeded sweep over larger shapes (M up to 4096, N up to 6144, K up
     to 8192) and output dtypes: the small-grid tilings (32x16, 32x32,
     64x64), 128x128 grids with split-K or with their last wave as 64x64
-    quarters, 256x128 tiles (and the 128x128 kernel that takes their grids
-    when K is not a multiple of 512), 192- and 256-row tiles and their
-    quarters, against torch's fp32 dequant-matmul of the same operands,
+    quarters, 256x128 tiles (with 16- and 4-byte scale window lanes),
+    192- and 256-row tiles and their quarters, against torch's fp32 dequant-matmul of the same operands,
     within the north-star tolerance."""
     print(f"gemm random large M={M} N={N} K={K} block_n={block_n} {dtype}", flush=True)
     x = synthetic.activations(M, K, seed=M * 7 + N)
