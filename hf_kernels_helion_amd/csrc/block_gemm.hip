@@ -3295,9 +3295,9 @@ extern "C" int fp8b_gate_up_plan(int64_t M, int64_t I, int64_t K, int cu_count,
     set_error("fp8b_gate_up_plan: null plan");
     return FP8B_ERR_NULL;
   }
-  if (M <= 0 || I <= 0 || I % 128 != 0 || K <= 0 || K % 512 != 0) {
+  if (M <= 0 || I <= 0 || I % 128 != 0 || K <= 0 || K % 128 != 0) {
     set_error("fp8b_gate_up_plan: need M > 0, I a positive multiple of 128 and K a positive "
-              "multiple of 512");
+              "multiple of 128");
     return FP8B_ERR_DIMS;
   }
   const int cus = cu_count > 0 ? cu_count : device_cu_count();
@@ -3325,9 +3325,9 @@ extern "C" int fp8b_gate_up_silu_quant(const void* A, int64_t lda, const void* B
     set_error("fp8b_gate_up_silu_quant: bad dims (need M,I,K >= 0, lda,ldb >= K, ldq >= I)");
     return FP8B_ERR_DIMS;
   }
-  if (I % 128 != 0 || K % 512 != 0 || K == 0) {
+  if (I % 128 != 0 || K % 128 != 0 || K == 0) {
     set_error("fp8b_gate_up_silu_quant: I must be a multiple of 128 and K a positive "
-              "multiple of 512");
+              "multiple of 128");
     return FP8B_ERR_DIMS;
   }
   if (M == 0 || I == 0) return FP8B_OK;
@@ -3336,12 +3336,10 @@ extern "C" int fp8b_gate_up_silu_quant(const void* A, int64_t lda, const void* B
     return FP8B_ERR_NULL;
   }
   const int64_t N = 2 * I;
-  if (!mfma_path_ok(A, lda, B, ldb, M, N, K, 128, 128) || as_sk != 1 || bs_sk != 1 ||
-      as_sm % 4 != 0 || bs_sn % 4 != 0 || ((uintptr_t)As & 15) != 0 ||
-      ((uintptr_t)Bs & 15) != 0 || ldq % 8 != 0 || ((uintptr_t)q & 7) != 0) {
-    set_error("fp8b_gate_up_silu_quant: need 16-byte aligned A, B (lda, ldb multiples of 16), "
-              "K-contiguous 16-byte aligned As, Bs (row strides multiples of 4) and an "
-              "8-byte aligned q with ldq a multiple of 8");
+  if (!mfma_path_ok(A, lda, B, ldb, M, N, K, 128, 128) || ldq % 8 != 0 ||
+      ((uintptr_t)q & 7) != 0) {
+    set_error("fp8b_gate_up_silu_quant: need 16-byte aligned A, B (lda, ldb multiples of 16) "
+              "and an 8-byte aligned q with ldq a multiple of 8");
     return FP8B_ERR_ALIGN;
   }
   if (255 * std::max(lda, ldb) + K >= (int64_t(1) << 32)) {
@@ -3351,7 +3349,7 @@ extern "C" int fp8b_gate_up_silu_quant(const void* A, int64_t lda, const void* B
   GemmArgs a;
   a.A = (const uint8_t*)A; a.B = (const uint8_t*)B; a.As = As; a.Bs = Bs; a.C = q;
   a.ws = nullptr;
-  a.lda = lda; a.ldb = ldb; a.as_sm = as_sm; a.as_sk = 1; a.bs_sn = bs_sn; a.bs_sk = 1;
+  a.lda = lda; a.ldb = ldb; a.as_sm = as_sm; a.as_sk = as_sk; a.bs_sn = bs_sn; a.bs_sk = bs_sk;
   a.ldc = ldq; a.M = (int)M; a.N = (int)N; a.K = (int)K; a.KB = (int)(K / 128);
   a.kb_per_split = a.KB;
   const bool tile192 = gate_up_tile192(M, I, K, device_cu_count());
@@ -3359,7 +3357,13 @@ extern "C" int fp8b_gate_up_silu_quant(const void* A, int64_t lda, const void* B
   a.tiles_n = (int)(N / 256);
   a.out_dtype = FP8B_BF16;
   a.vec_store = 0;
-  a.win4 = 0;  // K % 512 == 0 and 16-byte aligned K-contiguous scale rows (checked above)
+  Operands o;
+  o.lda = lda;
+  o.ldb = ldb;
+  o.mfma = true;
+  o.scales = as_sk == 1 && bs_sk == 1 && as_sm % 4 == 0 && bs_sn % 4 == 0 &&
+             ((uintptr_t)As & 15) == 0 && ((uintptr_t)Bs & 15) == 0;
+  a.win4 = win16_ok(o, K, 1, a.KB) ? 0 : 1;
   a.rem_base = -1; a.rem_tiles_m = 0; a.rem_tiles_n = 0;
   a.Sq = s; a.sq_sm = s_stride_m; a.sq_sg = s_stride_g;
   const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;

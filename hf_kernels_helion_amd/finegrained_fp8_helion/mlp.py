@@ -52,16 +52,16 @@ def gate_up_silu_quant(xq: torch.Tensor, xs: torch.Tensor, w_il: torch.Tensor,
     (w_il, s_il) from ``interleave_gate_up``: from FUSED_GATE_UP_MIN_ROWS
     rows one kernel (bit-identical to the chain whenever the chain's GEMM
     runs unsplit), below that the chain's two ops on the interleaved layout.
-    Needs block_size (128, 128) and H % 512 == 0. Returns (q [M, I] e4m3fn,
+    Needs block_size (128, 128) and H % 128 == 0. Returns (q [M, I] e4m3fn,
     s [M, I/128] fp32)."""
     m = xq.shape[0]
     if m >= FUSED_GATE_UP_MIN_ROWS or m == 0:
         return ops.gate_up_silu_quant(xq, w_il, xs, s_il)
     # the fused kernel's shape contract, for both routes
     if xq.dim() != 2 or w_il.dim() != 2 or w_il.shape[0] % 256 != 0 or \
-            xq.shape[1] % 512 != 0 or xq.shape[1] == 0:
+            xq.shape[1] % 128 != 0 or xq.shape[1] == 0:
         raise RuntimeError("gate_up_silu_quant: I must be a multiple of 128 and K a positive "
-                           f"multiple of 512 (A {tuple(xq.shape)}, B {tuple(w_il.shape)})")
+                           f"multiple of 128 (A {tuple(xq.shape)}, B {tuple(w_il.shape)})")
     i = w_il.shape[0] // 2
     h = ops.w8a8_block_fp8_matmul_dtype(xq, w_il, xs, s_il, 128, 128, torch.bfloat16)
     # rows of 256 columns: gate block | up block

@@ -2,8 +2,8 @@
  * fp8_blockwise.h -- C ABI of the MI355X (gfx950) block-FP8 linear path.
  *
  * Two stages, each a hand-written HIP kernel family in libfp8_blockwise.so:
- *   1. per-token-group activation quantisation: bf16 [M,K] -> float8_e4m3fn
- *      [M,K] plus fp32 scales [M, ceil(K/group)], scale = amax/448;
+ *   1. per-token-group activation quantisation: bf16 (or fp16, fp32) [M,K] ->
+ *      float8_e4m3fn [M,K] plus fp32 scales [M, ceil(K/group)], scale = amax/448;
  *   2. w8a8 GEMM  C[M,N] = A[M,K] . B[N,K]^T  with A carrying per-(row, K-block)
  *      fp32 scales As and B carrying per-(N-block, K-block) fp32 scales Bs,
  *      accumulated in fp32 and stored as fp32, bf16 or fp16.
@@ -136,7 +136,7 @@ typedef enum fp8b_kernel {
   FP8B_KERNEL_PIPE256 = 6,      /* pipelined 256x256 tiles */
   FP8B_KERNEL_PIPE192 = 7,      /* pipelined 192x256 tiles */
   FP8B_KERNEL_PIPE256X128 = 8,  /* pipelined 256x128 tiles */
-  FP8B_KERNEL_BS128 = 9         /* two-stage 128x128 / 256x256 tiles (scales not K-contiguous) */
+  FP8B_KERNEL_BS128 = 9         /* two-stage 128x128 / 256x256 tiles (FP8B_PIPE=0, huge leading dims) */
 } fp8b_kernel;
 
 /* What fp8b_w8a8_block_matmul launches for one call. */
@@ -285,10 +285,10 @@ int fp8b_silu_and_mul_quant(const void* x, int64_t ldx,
  * weights interleaved in 128-row blocks: rows 256t..256t+127 of B are gate
  * rows 128t..128t+127 and rows 256t+128..256t+255 the matching up rows;
  * Bs block row 2t is gate block row t and 2t+1 up block row t.
- * A, As: as fp8b_w8a8_block_matmul (block_n = block_k = 128, As and Bs
- * contiguous in K, 16-byte aligned); q: e4m3fn [M,I] row stride ldq (a
- * multiple of 8); scale of (m, g) at s[m*s_stride_m + g*s_stride_g].
- * Needs I % 128 == 0 and K % 512 == 0.
+ * A, As: as fp8b_w8a8_block_matmul (block_n = block_k = 128, A and B
+ * 16-byte aligned with lda, ldb multiples of 16, scales of any strides);
+ * q: e4m3fn [M,I] row stride ldq (a multiple of 8); scale of (m, g) at
+ * s[m*s_stride_m + g*s_stride_g]. Needs I % 128 == 0 and K % 128 == 0.
  * No single counterpart in the reference: it composes the gate/up call of
  * w8a8_block_fp8_matmul (finegrained-fp8-helion/.../fp8.py:28-38) with
  * act.py:20-28 and the quantiser above, as fp8b_silu_and_mul_quant does.

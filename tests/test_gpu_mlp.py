@@ -164,14 +164,16 @@ def _gate_up_chain(xq, xs, w13, s13, M, pad=True):
                                           (200, 384, 512, None), (257, 512, 512, None),
                                           (600, 384, 512, None), (513, 512, 1024, None),
                                           (3001, 1024, 512, 192), (3001, 14336, 4096, 192),
-                                          (1024, 8192, 512, 256), (2048, 14336, 512, 256)])
+                                          (1024, 8192, 512, 256), (2048, 14336, 512, 256),
+                                          (1024, 2048, 640, None), (3001, 1024, 1408, 192)])
 def test_gate_up_silu_quant_equals_chain(M, I, H, tile_m, dev):
     """GEMM + SiLU·up + act-quant in one kernel == bf16 GEMM then
     silu_and_mul_quant, fp8 codes and scales bit for bit; the bf16 GEMM is
     checked against the oracle on a sample of rows. tile_m: the fused kernel's
     tile rows the planner must pick on a 256-CU device (192x256 tiles for the
     M = 3001 grids, 256x256 for 1024x8192 and 2048x14336), so both fused
-    kernels stay covered."""
+    kernels stay covered; H = 640 and 1408 (5 and 11 K-blocks) take the
+    4-byte scale window lanes."""
     print(f"gate_up_silu_quant M={M} I={I} H={H}", flush=True)
     from hf_kernels_helion_amd import _native
     plan = _native.gate_up_plan(M, I, H)
@@ -198,6 +200,23 @@ def test_gate_up_silu_quant_equals_chain(M, I, H, tile_m, dev):
     torch.testing.assert_close(h[rows.to(dev)].float().cpu(),
                                torch.from_numpy(ho).to(torch.bfloat16).float(),
                                rtol=1e-2, atol=1e-3)
+
+
+@pytest.mark.parametrize("M,I,H", [(600, 512, 1024), (1024, 1024, 1152)])
+def test_gate_up_silu_quant_scale_layouts(M, I, H, dev):
+    """Column-major or odd-stride activation and weight scales give the same
+    bits as contiguous ones (4-byte scale window lanes)."""
+    print(f"gate_up_silu_quant scale layouts M={M} I={I} H={H}", flush=True)
+    x = synthetic.activations(M, H, seed=M + 2 * I)
+    w13, s13 = synthetic.weights(2 * I, H, seed=I + 3 * H)
+    xq, xs = fp8.act_quant(x.to(dev), 128)
+    wi, si = fp8.interleave_gate_up(w13.to(dev), s13.to(dev))
+    q_ref, s_ref = fp8.ops.gate_up_silu_quant(xq, wi, xs, si)
+    pad = lambda t: torch.zeros(t.shape[0], t.shape[1] + 1, device=dev)[:, :t.shape[1]].copy_(t)
+    for xs_, si_ in ((xs.T.contiguous().T, si), (xs, si.T.contiguous().T), (pad(xs), pad(si))):
+        q, s = fp8.ops.gate_up_silu_quant(xq, wi, xs_, si_)
+        assert torch.equal(q.view(torch.uint8), q_ref.view(torch.uint8))
+        assert torch.equal(s.view(torch.int32), s_ref.view(torch.int32))
 
 
 def test_gate_up_silu_quant_strided_outputs_and_repeat(dev):

@@ -193,7 +193,7 @@ def test_interleave_gate_up_layout():
         fp8.gate_up_silu_quant(_fp8(4, 512), torch.ones(4, 4), _fp8(256, 512), torch.ones(2, 4))
     # below FUSED_GATE_UP_MIN_ROWS rows the two-op route keeps the fused
     # kernel's shape contract
-    with pytest.raises(RuntimeError, match="multiple of 512"):
-        fp8.gate_up_silu_quant(_fp8(4, 384), torch.ones(4, 3), _fp8(256, 384), torch.ones(2, 3))
+    with pytest.raises(RuntimeError, match="multiple of 128"):
+        fp8.gate_up_silu_quant(_fp8(4, 200), torch.ones(4, 2), _fp8(256, 200), torch.ones(2, 2))
     with pytest.raises(RuntimeError, match="multiple of 128"):
         fp8.gate_up_silu_quant(_fp8(4, 512), torch.ones(4, 4), _fp8(200, 512), torch.ones(2, 4))
