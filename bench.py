@@ -49,7 +49,8 @@ def parse():
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--only", default=None,
                    help="profile helper: run only one workload "
-                        "(gemm|act_quant|decode|decode_graph|decode_fused|weight_quant|"
+                        "(gemm|act_quant|decode|decode_graph|decode_graph_two_op|decode_fused|"
+                        "weight_quant|"
                         "weight_quant_bf16|mlp|"
                         "mlp_il|mlp_gateup|"
                         "mlp_down|medium|small|prefill|deep_gemm|deep_decode|copy|shapes|"
@@ -366,8 +367,10 @@ def secondary(torch, fp8, synthetic, dev):
 
     # The same five steps captured once in a HIP graph (how a decode loop is
     # served): replays cost GPU time only, without per-op host dispatch.
-    # Two forms: act_quant then the GEMM (two ops), and the fused op that
-    # quantises inside the GEMM kernel (same result bits).
+    # Two forms: the op that quantises in-op (act_quant_w8a8_block_fp8_matmul:
+    # one kernel quantises the bf16 rows inside the decode GEMM, then the
+    # split-K sum), which is the C4 step, and act_quant then the GEMM (two
+    # ops) beside it; every replay equals the eager two-op result bit for bit.
     def dec_two_op():
         outs = []
         for i in range(5):
@@ -398,16 +401,18 @@ def secondary(torch, fp8, synthetic, dev):
         t = time_events(graph.replay, 20, 5, torch) / 5
         del graph, gouts
         return t
-    ms = graph_time(dec_two_op)
-    ms_op = graph_time(dec_fused)
+    ms_two = graph_time(dec_two_op)
+    ms = graph_time(dec_fused)
     byt = 2.0 * M * K + N * K + 4.0 * (N // 128) * (K // 128) + 2.0 * M * N
     res["decode_32x4096x14336"] = {"us": round(ms * 1e3, 2), "GB/s": round(byt / ms / 1e6, 1),
                                    "pct_hbm_peak": round(100 * byt / ms / 1e6 / PEAK_HBM_GBS, 1),
-                                   "act_quant_matmul_op_us": round(ms_op * 1e3, 2),
-                                   "eager_us": round(ms_eager * 1e3, 2),
-                                   "includes": "bf16 activations in: act_quant + GEMM "
-                                               "(+ split-K reduce); HIP-graph replay of 5 steps "
-                                               "over 5 weight copies"}
+                                   "two_op_us": round(ms_two * 1e3, 2),
+                                   "eager_two_op_us": round(ms_eager * 1e3, 2),
+                                   "includes": "bf16 activations in, quantised in-op: "
+                                               "act_quant_w8a8_block_fp8_matmul (one kernel "
+                                               "+ split-K sum); two_op_us = act_quant then "
+                                               "the GEMM; HIP-graph replay of 5 steps over 5 "
+                                               "weight copies"}
     log(f"decode: {res['decode_32x4096x14336']}")
     del ws_
 
@@ -584,15 +589,20 @@ def run_only(what, steps, warmup, torch, fp8, synthetic, dev):
         else:
             W, Bs = _gpu_weights(N, K, 40, dev, torch, synthetic)
             fn = lambda: fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [128, 128], torch.bfloat16)
-    elif what == "decode_graph":
-        # the bench leg's decode step (act_quant + GEMM + split-K sum, five
-        # weight copies) as a HIP graph of five steps, replayed --steps times
+    elif what in ("decode_graph", "decode_graph_two_op"):
+        # the bench leg's decode step (five weight copies) as a HIP graph of
+        # five steps, replayed --steps times: the in-op quantising op
+        # (one kernel + split-K sum), or act_quant then the GEMM
         M, N, K = 32, 4096, 14336
         ws_ = [_gpu_weights(N, K, 20 + i, dev, torch, synthetic) for i in range(5)]
         xd = _gpu_acts(M, K, 30, dev, torch)
 
         def five():
             for i in range(5):
+                if what == "decode_graph":
+                    fp8.act_quant_w8a8_block_fp8_matmul(xd, ws_[i][0], ws_[i][1], [128, 128],
+                                                        torch.bfloat16)
+                    continue
                 q, s = fp8.act_quant(xd, 128)
                 fp8.w8a8_block_fp8_matmul(q, ws_[i][0], s, ws_[i][1], [128, 128],
                                           torch.bfloat16)

@@ -69,6 +69,8 @@ SIGNATURES = {
     "fp8b_kernel_name": (ctypes.c_char_p, [ctypes.c_int]),
     "fp8b_gate_up_plan": (ctypes.c_int, [_i64, _i64, _i64, ctypes.c_int,
                                          ctypes.POINTER(PlanInfo)]),
+    "fp8b_act_quant_matmul_plan": (ctypes.c_int, [_i64, _i64, _i64, ctypes.c_int,
+                                                  ctypes.POINTER(PlanInfo)]),
     "fp8b_w8a8_block_matmul_noalloc": (
         ctypes.c_int,
         [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, ctypes.c_int,
@@ -129,6 +131,17 @@ def gemm_plan(M: int, N: int, K: int, block_n: int = 128, block_k: int = 128,
     info = PlanInfo()
     check(lib.fp8b_gemm_plan(M, N, K, block_n, block_k, cu_count, ctypes.byref(info)),
           "fp8b_gemm_plan")
+    return _plan_dict(lib, info)
+
+
+def act_quant_matmul_plan(M: int, N: int, K: int, cu_count: int = 0) -> dict:
+    """The GEMM launch of one fp8b_act_quant_matmul call for a contiguous,
+    aligned x (fp8b_act_quant_matmul_plan): gemm_decode_quant_kernel when one
+    kernel quantises and multiplies, else the GEMM after the act-quant launch."""
+    lib = load()
+    info = PlanInfo()
+    check(lib.fp8b_act_quant_matmul_plan(M, N, K, cu_count, ctypes.byref(info)),
+          "fp8b_act_quant_matmul_plan")
     return _plan_dict(lib, info)
 
 

@@ -1811,6 +1811,233 @@ __global__ void __launch_bounds__(512) gemm_decode_kernel(GemmArgs a) {
     store4(a, f * 16 + (lane & 15), n0 + wid * 16 + 4 * (lane >> 4), acc[f], to_ws, split);
 }
 
+// ---------------------------------------------------------------------------
+// Decode GEMM with the group-128 act-quant inside it (fp8b_act_quant_matmul
+// on decode plans, M <= 32): gemm_decode_kernel's grid, K split and fold,
+// with the activations read as bf16. The waves split the work: waves 0-3
+// run the MFMAs of 32 weight rows each, waves 4-7 quantise activation rows,
+// and every wave DMAs exactly the bytes it consumes, so it waits on its own
+// vmcnt only. Stage j of the LDS ring holds weight K-block j (128 rows,
+// chunk-swizzled as in gemm_decode_kernel; MFMA wave w brings rows
+// 32w..32w+31) and the bf16 rows of activation K-block j + 1 (16*FM rows of
+// 256 bytes, unswizzled; quantiser wave q brings the rows it quantises); the
+// rows of the split's first K-block arrive ahead of the ring, in the
+// activation area of the last stage, which the ring first refills after
+// they are read. A quantiser wave keeps the next K-block's rows in
+// registers (read as soon as its own DMA of them has landed), quantises
+// them with the act-quant's own arithmetic (QE values per lane, one DPP row
+// or half-row per 128-value group: quant_row16_8 / quant_row8_16) into a
+// double-buffered fp8 slab in the MFMA fragment layout, and writes the group
+// scales beside it; the one barrier per K-block publishes the slab to the
+// MFMA waves and frees the other buffer. The quantiser's VALU work (every
+// column tile repeats it for the same rows) so runs beside the MFMA chain,
+// and no global read is a compiler-generated load whose wait would drain
+// the weight ring. Codes, scales, split and fold order equal act-quant
+// followed by gemm_decode_kernel, so the results are bit-identical to that
+// two-kernel path.
+// Preconditions (checked by the host): x 16-byte aligned with a row stride
+// (a.lda, in bytes) that is a multiple of 16, and the 32-bit DMA offsets
+// row * ldb + 127 (row <= 127) and row * a.lda + 255 (row < 16*FM) fit.
+// ---------------------------------------------------------------------------
+template <int FM, int NSX, int QE> struct DecodeQuantCfg {
+  static constexpr int BN = 128, AR = 16 * FM;
+  static constexpr int NS = NSX;
+  static constexpr int LPR = 128 / QE;                // quantiser lanes per row
+  static constexpr int QROWS = 64 / LPR;              // rows per quantiser wave
+  static constexpr int QLOADS = QROWS / 4;            // its 1 KiB bf16 wave-loads per stage
+  static constexpr int XB = BN * 128;                 // bf16 rows within a stage
+  static constexpr int STAGE = XB + AR * 256;
+  static constexpr int Q_OFF = NS * STAGE;            // fp8 slabs, 2 x AR x 128 B
+  static constexpr int S_OFF = Q_OFF + 2 * AR * 128;  // group scales, 2 x AR floats
+  static constexpr int W_OFF = S_OFF + 2 * AR * 4;    // weight-block scale windows, 2 x 8
+  static constexpr int SMEM = W_OFF + 2 * 256;
+};
+
+template <int FM, int NSX, int QE>
+__global__ void __launch_bounds__(512) gemm_decode_quant_kernel(GemmArgs a) {
+  using Cfg = DecodeQuantCfg<FM, NSX, QE>;
+  constexpr int BN = Cfg::BN, NS = Cfg::NS, AR = Cfg::AR, LPR = Cfg::LPR;
+  constexpr int QROWS = Cfg::QROWS, QLOADS = Cfg::QLOADS;
+  constexpr int STAGE = Cfg::STAGE, XB = Cfg::XB;
+  constexpr int Q_OFF = Cfg::Q_OFF, S_OFF = Cfg::S_OFF, W_OFF = Cfg::W_OFF;
+  static_assert(QE == 8 || QE == 16, "8 or 16 values per lane");
+  static_assert(4 * QROWS == AR && QLOADS >= 1, "four quantiser waves cover the rows");
+  static_assert(NS >= 2 && Cfg::SMEM <= 160 * 1024, "LDS budget");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[Cfg::SMEM];
+
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const bool mfma_wave = wid < 4;
+  const int n0 = blockIdx.x * BN;
+  const int split = blockIdx.z;
+  const int kb_begin = split * a.kb_per_split;
+  const int kb_end = min(kb_begin + a.kb_per_split, a.KB);
+  const int nkb = kb_end - kb_begin;
+  const int pro = min(NS - 1, nkb);
+
+  const uint32_t lds0 = lds_u32(smem);
+  // Quantiser wave q = wid - 4: rows QROWS*q .. +QROWS-1; lane -> row
+  // QROWS*q + lane/LPR, values QE*(lane%LPR) .. +QE-1.
+  const int q = wid - 4;
+  const int qm = q * QROWS + lane / LPR, qsub = lane % LPR;
+  // bf16 rows of K-block kb into the activation area at lds (this
+  // quantiser wave's QLOADS wave-loads: rows 4L..4L+3, sixteen lanes per
+  // 256-byte row).
+  auto issue_rows = [&](int kb, uint32_t lds) {
+#pragma unroll
+    for (int i = 0; i < QLOADS; ++i) {
+      const int L = q * QLOADS + i;
+      const uint32_t voff =
+          (uint32_t)min(L * 4 + (lane >> 4), a.M - 1) * (uint32_t)a.lda + (lane & 15) * 16;
+      dma16_soff(voff, a.A + (int64_t)kb * 256, lds + L * 1024);
+    }
+  };
+  // MFMA wave w: weight rows 32w..32w+31 of K-block kb (four wave-loads of
+  // eight lanes per 128-byte row, chunk-swizzled); wave 0 also brings the
+  // weight-block scales of K-blocks kb..kb+7 at a window start.
+  const int r8 = lane >> 3;
+  const int c16 = ((lane & 7) ^ r8) * 16;
+  const uint8_t* b_base = a.B + (int64_t)n0 * a.ldb;
+  const int b_lim = a.N - 1 - n0;
+  auto issue_weights = [&](int kb) {
+    const int rel = kb - kb_begin;
+    if (wid == 0 && (rel & 7) == 0 && lane < 8) {
+      const int kbs = min(kb + lane, kb_end - 1);
+      dma4_ptr(a.Bs + (int64_t)(n0 >> 7) * a.bs_sn + (int64_t)kbs * a.bs_sk,
+               lds0 + W_OFF + ((rel >> 3) & 1) * 256);
+    }
+    const uint32_t lds = lds0 + (rel % NS) * STAGE;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const int r = (wid * 4 + h) * 8 + r8;
+      const uint32_t voff = (uint32_t)min(r, b_lim) * (uint32_t)a.ldb + c16;
+      dma16_soff(voff, b_base + (int64_t)kb * 128, lds + (wid * 4 + h) * 1024);
+    }
+  };
+  // Stage of K-block kb, this wave's part: weights, or the rows of K-block
+  // kb + 1 (the last K-block's own again at the end of the split, unused).
+  auto issue_stage = [&](int kb) {
+    if (mfma_wave) issue_weights(kb);
+    else issue_rows(min(kb + 1, kb_end - 1), lds0 + ((kb - kb_begin) % NS) * STAGE + XB);
+  };
+  const int per_kb = mfma_wave ? 4 : QLOADS;
+  auto wait_after = [&](int n_after) { wait_vmcnt_rt(min(n_after * per_kb, 15)); };
+
+  // Quantiser: this lane's bf16 values of a row (read from LDS), and their
+  // codes into slab `buf` with the group scale beside it.
+  v4i raw[QE / 8];
+  auto read_rows = [&](const uint8_t* src) {
+#pragma unroll
+    for (int i = 0; i < QE / 8; ++i)
+      raw[i] = *reinterpret_cast<const v4i*>(src + qm * 256 + qsub * (QE * 2) + i * 16);
+  };
+  auto quantise = [&](int buf) {
+    uint8_t* qs = smem + Q_OFF + buf * (AR * 128);
+    float scale;
+    if constexpr (QE == 8) {
+      float v[8];
+      const uint32_t mag = unpack_bf16x8(raw[0], v);
+      uint32_t w0, w1;
+      quant_row16_8(v, mag, w0, w1, scale);
+      v2i packed;
+      packed[0] = (int)w0;
+      packed[1] = (int)w1;
+      *reinterpret_cast<v2i*>(qs + qm * 128 + (((qsub >> 1) ^ (qm & 7)) << 4) + (qsub & 1) * 8) =
+          packed;
+    } else {
+      float v[16];
+      const uint32_t mag = max(unpack_bf16x8(raw[0], v), unpack_bf16x8(raw[1], v + 8));
+      uint32_t w[4];
+      quant_row8_16(v, mag, w, scale);
+      v4i packed;
+      for (int i = 0; i < 4; ++i) packed[i] = (int)w[i];
+      *reinterpret_cast<v4i*>(qs + qm * 128 + ((qsub ^ (qm & 7)) << 4)) = packed;
+    }
+    if (qsub == 0) reinterpret_cast<float*>(smem + S_OFF + buf * (AR * 4))[qm] = scale;
+  };
+
+  // MFMA waves: fragment offsets of weight rows 32w + 16j + (lane & 15) and
+  // of the activation rows.
+  const int r7 = lane & 7, g2 = 2 * (lane >> 4);
+  const int slo = (g2 ^ r7) << 4, shi = ((g2 + 1) ^ r7) << 4;
+  const int w_off = (wid * 32 + (lane & 15)) * 128;
+  const int x_off = (lane & 15) * 128;
+  v4f acc[2][FM];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int f = 0; f < FM; ++f) acc[j][f] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  // Prologue. Quantiser waves: the first K-block's rows (into the last
+  // stage's activation area), then their part of the ring; once the first
+  // rows have landed (at most the ring's DMAs pending), quantise them into
+  // slab 0 and read the next K-block's rows as soon as they land. MFMA
+  // waves: their part of the ring.
+  const int x0 = (NS - 1) * STAGE + XB;
+  if (!mfma_wave) issue_rows(kb_begin, lds0 + x0);
+  for (int k = 0; k < pro; ++k) issue_stage(kb_begin + k);
+  if (!mfma_wave) {
+    wait_vmcnt_rt(min(pro * per_kb, 15));
+    read_rows(smem + x0);
+    quantise(0);
+    if (nkb > 1) {
+      wait_after(pro - 1);
+      read_rows(smem + XB);
+    }
+  }
+
+  for (int kb = kb_begin; kb < kb_end; ++kb) {
+    const int rel = kb - kb_begin;
+    // MFMA waves: their weights of K-block kb (DMAs issued after them: the
+    // stages of kb+1..kb+NS-2 that exist). The barrier publishes slab rel&1
+    // and frees slab (rel+1)&1.
+    if (mfma_wave) wait_after(min(NS - 2, kb_end - 1 - kb));
+    __syncthreads();
+    if (kb + NS - 1 < kb_end) issue_stage(kb + NS - 1);
+    if (mfma_wave) {
+      const uint8_t* st = smem + (rel % NS) * STAGE;
+      const uint8_t* qs = smem + Q_OFF + (rel & 1) * (AR * 128);
+      const float* ss = reinterpret_cast<const float*>(smem + S_OFF + (rel & 1) * (AR * 4));
+      const float sb =
+          *reinterpret_cast<const float*>(smem + W_OFF + ((rel >> 3) & 1) * 256 + (rel & 7) * 4);
+      const v8i w0 = lds_frag2(st + w_off, slo, shi);
+      const v8i w1 = lds_frag2(st + w_off + 2048, slo, shi);
+#pragma unroll
+      for (int f = 0; f < FM; ++f) {
+        const v8i x = lds_frag2(qs + x_off + f * 2048, slo, shi);
+        const float sab = ss[f * 16 + (lane & 15)] * sb;
+        const v4f t0 = mfma16x16x128(w0, x);
+        const v4f t1 = mfma16x16x128(w1, x);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          acc[0][f][r] = fmaf(t0[r], sab, acc[0][f][r]);
+          acc[1][f][r] = fmaf(t1[r], sab, acc[1][f][r]);
+        }
+      }
+    } else if (kb + 1 < kb_end) {
+      // rows of K-block kb+1 (in registers) -> slab (rel+1)&1; then the
+      // rows of kb+2 from stage rel+1 once this wave's DMA of them has
+      // landed (DMAs issued after it: the stages of kb+2..kb+NS-1 that exist)
+      quantise((rel + 1) & 1);
+      if (kb + 2 < kb_end) {
+        wait_after(min(NS - 2, kb_end - kb - 2));
+        read_rows(smem + ((rel + 1) % NS) * STAGE + XB);
+      }
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  if (mfma_wave) {
+    const bool to_ws = gridDim.z > 1;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int f = 0; f < FM; ++f)
+        store4(a, f * 16 + (lane & 15), n0 + wid * 32 + j * 16 + 4 * (lane >> 4), acc[j][f],
+               to_ws, split);
+  }
+}
+
 // Skinny GEMM (M <= 16*FM <= 48, the decode shapes): bandwidth-bound on the
 // weight stream. A 512-thread workgroup owns 16 weight rows (output columns
 // n0..n0+15) over the whole K; its 8 waves split the K-blocks into
@@ -2260,7 +2487,9 @@ int device_cu_count() {
 //   FP8B_TILE192=0  no 192x256 tiles;
 //   FP8B_TINY=0     no small-grid kernel (32x32, 32x16, 64x64 tiles);
 //   FP8B_TAIL64=0   no 64x64 quarters for a small last wave of 128x128 tiles;
-//   FP8B_TILE256X128=0  no 256x128 tiles.
+//   FP8B_TILE256X128=0  no 256x128 tiles;
+//   FP8B_FUSED_DECODE=0 fp8b_act_quant_matmul runs act-quant and the GEMM as
+//                   two kernels on decode plans too.
 bool env_flag_on(const char* name) {
   const char* e = getenv(name);
   return !(e && e[0] == '0');
@@ -2291,6 +2520,10 @@ bool use_tail64() {
 }
 bool use_tile256x128() {
   static const bool v = env_flag_on("FP8B_TILE256X128");
+  return v;
+}
+bool use_fused_decode() {
+  static const bool v = env_flag_on("FP8B_FUSED_DECODE");
   return v;
 }
 
@@ -2883,6 +3116,30 @@ void launch_decode(const GemmArgs& a, int M, int ring, int splits, hipStream_t s
   }
 }
 
+// gemm_decode_quant_kernel: the quantiser takes 8 values per lane for 16
+// rows and 16 for 32 (four waves either way). LDS stages of 16 KiB of weights
+// plus 16*FM bf16 rows, by measured step time (graph-replayed, bit-identical
+// results): 32 rows on 3 stages, 32x4096x14336 17.0 us against 18.3 with 4,
+// 19.3 with 5, 20.8 with 2 (act-quant + GEMM: 19.7); 16 rows on 4 stages,
+// 16x4096x14336 15.5 us against 16.0 with 5 (act-quant + GEMM: 18.0).
+int decode_quant_ring(int64_t M) { return M <= 16 ? 4 : 3; }
+void launch_decode_quant(const GemmArgs& a, int M, int splits, hipStream_t st) {
+  const dim3 grid((unsigned)((a.N + 127) / 128), 1, (unsigned)splits);
+  if (M <= 16) gemm_decode_quant_kernel<1, 4, 8><<<grid, 512, 0, st>>>(a);
+  else gemm_decode_quant_kernel<2, 3, 16><<<grid, 512, 0, st>>>(a);
+}
+
+// fp8b_act_quant_matmul takes gemm_decode_quant_kernel when the plan is the
+// decode kernel with one workgroup per CU (grids past the CU count run two
+// smaller-ring workgroups per CU, for which the bf16 stages do not fit), the
+// bf16 rows are 16-byte aligned, and the 32-bit DMA offsets fit.
+bool fused_decode_ok(const Dispatch& d, const void* x, int64_t ldx, int64_t ldb, int64_t M) {
+  if (!use_fused_decode() || d.kernel != FP8B_KERNEL_DECODE || d.per_row || d.ring != 4) return false;
+  if (M > 32 || ((uintptr_t)x & 15) != 0 || ldx % 8 != 0) return false;
+  const int64_t rows = (M + 15) / 16 * 16;
+  return 127 * ldb + 128 <= (int64_t(1) << 32) && (rows - 1) * 2 * ldx + 256 <= (int64_t(1) << 32);
+}
+
 // Runs the main launch and the tail launch of d (not the split-K sum).
 template <bool PR>
 void launch_dispatch(const Dispatch& d, const GemmArgs& a, hipStream_t st) {
@@ -2955,6 +3212,7 @@ const char* kernel_name(int k) {
     case FP8B_KERNEL_PIPE192: return "gemm_pipe192_kernel";
     case FP8B_KERNEL_PIPE256X128: return "gemm_pipe256x128_kernel";
     case FP8B_KERNEL_BS128: return "gemm_bs128_kernel";
+    case FP8B_KERNEL_DECODE_QUANT: return "gemm_decode_quant_kernel";
     default: return "unknown";
   }
 }
@@ -2993,19 +3251,9 @@ extern "C" size_t fp8b_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int6
 
 extern "C" const char* fp8b_kernel_name(int kernel) { return kernel_name(kernel); }
 
-extern "C" int fp8b_gemm_plan(int64_t M, int64_t N, int64_t K, int64_t block_n, int64_t block_k,
-                              int cu_count, fp8b_plan_info* plan) {
-  if (!plan) {
-    set_error("fp8b_gemm_plan: null plan");
-    return FP8B_ERR_NULL;
-  }
-  if (!plan_args_ok(M, N, K, block_n, block_k)) {
-    set_error("fp8b_gemm_plan: need M, N, K, block_n, block_k > 0");
-    return FP8B_ERR_DIMS;
-  }
-  const int cus = cu_count > 0 ? cu_count : device_cu_count();
-  const Dispatch d = resolve(M, N, K, block_n, block_k, cus,
-                             contiguous_operands(M, N, K, block_n, block_k));
+namespace {
+// The fp8b_plan_info of a Dispatch.
+void fill_plan(const Dispatch& d, int64_t M, int64_t N, int cus, fp8b_plan_info* plan) {
   plan->kernel = d.kernel;
   plan->tile_m = d.bm;
   plan->tile_n = d.bn;
@@ -3021,6 +3269,44 @@ extern "C" int fp8b_gemm_plan(int64_t M, int64_t N, int64_t K, int64_t block_n, 
   plan->reduce = d.splits > 1 ? 1 : 0;
   plan->workspace_bytes = d.splits > 1 ? (size_t)d.splits * (size_t)M * (size_t)N * sizeof(float) : 0;
   plan->cu_count = cus;
+}
+}  // namespace
+
+extern "C" int fp8b_gemm_plan(int64_t M, int64_t N, int64_t K, int64_t block_n, int64_t block_k,
+                              int cu_count, fp8b_plan_info* plan) {
+  if (!plan) {
+    set_error("fp8b_gemm_plan: null plan");
+    return FP8B_ERR_NULL;
+  }
+  if (!plan_args_ok(M, N, K, block_n, block_k)) {
+    set_error("fp8b_gemm_plan: need M, N, K, block_n, block_k > 0");
+    return FP8B_ERR_DIMS;
+  }
+  const int cus = cu_count > 0 ? cu_count : device_cu_count();
+  const Dispatch d = resolve(M, N, K, block_n, block_k, cus,
+                             contiguous_operands(M, N, K, block_n, block_k));
+  fill_plan(d, M, N, cus, plan);
+  return FP8B_OK;
+}
+
+extern "C" int fp8b_act_quant_matmul_plan(int64_t M, int64_t N, int64_t K, int cu_count,
+                                          fp8b_plan_info* plan) {
+  if (!plan) {
+    set_error("fp8b_act_quant_matmul_plan: null plan");
+    return FP8B_ERR_NULL;
+  }
+  if (!plan_args_ok(M, N, K, 128, 128) || K % 128 != 0) {
+    set_error("fp8b_act_quant_matmul_plan: need M, N, K > 0 and K % 128 == 0");
+    return FP8B_ERR_DIMS;
+  }
+  const int cus = cu_count > 0 ? cu_count : device_cu_count();
+  const Dispatch d = resolve(M, N, K, 128, 128, cus, contiguous_operands(M, N, K, 128, 128));
+  fill_plan(d, M, N, cus, plan);
+  if (fused_decode_ok(d, nullptr, K, K, M)) {
+    plan->kernel = FP8B_KERNEL_DECODE_QUANT;
+    plan->ring = decode_quant_ring(M);
+  }
+  plan->workspace_bytes = fp8b_act_quant_matmul_workspace_size(M, N, K);
   return FP8B_OK;
 }
 
@@ -3208,18 +3494,21 @@ namespace {
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 }  // namespace
 
-// Act-quant then the block GEMM, as two launches on the caller's stream: the
-// quantiser writes (q, s) into the workspace and the GEMM reads them (plus
-// its own split-K partials, at the start of the workspace). Five one-launch
-// forms were built, checked bit-identical and measured slower at
-// 32x4096x14336 (a decode kernel quantising its bf16 K-blocks in LDS, 22 us
-// against 3.5 + 14.4 us; per-split prologue quantisation; quantisation shared
-// across workgroups through device-coherent memory; per-K-block quantisation
-// one K-block ahead; the quantisation and the split-K sum shared through one
-// XCD's L2, 25.1 against 19.9 us per step): the act-quant's work either
-// repeats per column tile or waits on hand-offs that cost what the saved
-// launches do, and activation loads issued beside the weight stream wait
-// behind it.
+// Act-quant then the block GEMM. On a decode plan with M <= 32 (one
+// workgroup per CU) and 16-byte aligned bf16 rows, one launch of
+// gemm_decode_quant_kernel quantises the rows inside the GEMM with the plan's
+// split (then the split-K sum): 17.0 us per graph-replayed step at
+// 32x4096x14336 against 19.7 us for the two launches below, and 15.5 against
+// 18.0 at 16x4096x14336, bit-identical. Otherwise two launches on the
+// caller's stream: the quantiser writes (q, s) into the workspace and the GEMM
+// reads them (plus its own split-K partials, at the start of the workspace).
+// Earlier one-launch forms, measured slower and removed: quantisation by
+// every wave after its MFMAs (the per-column-tile repetition of the act-quant
+// work then sits on each K-block's critical path), per-split prologue
+// quantisation, quantisation shared across workgroups through
+// device-coherent memory or one XCD's L2 (hand-offs that cost what the saved
+// launch does), and activation loads issued beside the weight stream as
+// compiler-generated loads (their waits drain the weight ring).
 extern "C" size_t fp8b_act_quant_matmul_workspace_size(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 128 != 0) return 0;
   // GEMM workspace, then q [M,K] and s [M,K/128].
@@ -3261,6 +3550,47 @@ extern "C" int fp8b_act_quant_matmul(const void* x, int64_t ldx, const void* B, 
   const size_t gemm = fp8b_gemm_workspace_size(M, N, K, 128, 128);
   uint8_t* q = (uint8_t*)workspace + align256(gemm);
   float* s = (float*)(q + align256((size_t)M * K));
+  // The GEMM the two-kernel path would run on the quantised rows; on a
+  // decode plan one kernel quantises the bf16 rows itself with that plan's
+  // split (the same result bits).
+  const Dispatch d = resolve(M, N, K, 128, 128, device_cu_count(),
+                             call_operands(q, K, B, ldb, s, KB, 1, Bs, bs_sn, bs_sk, M, N, K,
+                                           128, 128));
+  if (fused_decode_ok(d, x, ldx, ldb, M)) {
+    hipStream_t st = (hipStream_t)stream;
+    GemmArgs a;
+    a.A = (const uint8_t*)x; a.B = (const uint8_t*)B; a.As = nullptr; a.Bs = Bs; a.C = C;
+    a.ws = (float*)workspace;
+    a.lda = 2 * ldx; a.ldb = ldb; a.as_sm = 0; a.as_sk = 0; a.bs_sn = bs_sn; a.bs_sk = bs_sk;
+    a.ldc = ldc; a.M = (int)M; a.N = (int)N; a.K = (int)K; a.KB = (int)KB;
+    a.kb_per_split = d.kb_per_split;
+    a.tiles_m = 1; a.tiles_n = (int)((N + 127) / 128);
+    a.out_dtype = out_dtype;
+    a.rem_base = -1; a.rem_tiles_m = 0; a.rem_tiles_n = 0;
+    a.Sq = nullptr; a.sq_sm = 0; a.sq_sg = 0;
+    a.win4 = 1;
+    const size_t esz = out_dtype == FP8B_F32 ? 4 : 2;
+    const bool c_vec = esz == 4 ? (ldc % 4 == 0 && ((uintptr_t)C & 15) == 0)
+                                : (ldc % 8 == 0 && ((uintptr_t)C & 15) == 0);
+    const bool ws_vec = (N % 4 == 0);
+    a.vec_store = (d.splits > 1) ? (ws_vec ? 1 : 0) : (c_vec ? 1 : 0);
+    launch_decode_quant(a, (int)M, d.splits, st);
+    if (hipGetLastError() != hipSuccess) {
+      set_error("fp8b_act_quant_matmul: fused decode kernel launch failed");
+      return FP8B_ERR_LAUNCH;
+    }
+    if (d.splits > 1) {
+      GemmArgs r = a;
+      r.vec_store = (ws_vec && c_vec) ? 1 : 0;
+      const int64_t quads = M * ((N + 3) / 4);
+      splitk_reduce_kernel<<<(unsigned)((quads + 255) / 256), 256, 0, st>>>(r, d.splits);
+      if (hipGetLastError() != hipSuccess) {
+        set_error("fp8b_act_quant_matmul: split-K reduce launch failed");
+        return FP8B_ERR_LAUNCH;
+      }
+    }
+    return FP8B_OK;
+  }
   int rc = fp8b_act_quant(x, ldx, q, K, s, KB, 1, M, K, 128, stream);
   if (rc != FP8B_OK) return rc;
   return fp8b_w8a8_block_matmul(q, K, B, ldb, s, KB, 1, Bs, bs_sn, bs_sk, C, ldc, out_dtype, M, N,

@@ -18,15 +18,18 @@ namespace fp8b {
 
 // x / s rounded to nearest even, for a group scale s > 0 (normal, finite)
 // and |x| <= 448 s, given recip = RN(1/s) from one IEEE division per group.
-// Markstein's theorem: q0 = RN(x * recip) is within one ulp of x/s, so
-// r = x - q0*s is exact in one FMA and RN(q0 + r*recip) = RN(x/s). The sign
-// is copied from x so that -0 stays -0 (q0 + r*recip would give +0). Below
-// the fp32 normal range the quotient may differ from IEEE division in its
-// last bits, but every such value converts to a signed fp8 zero.
+// Markstein's theorem: q0 = RN(x * recip) is within one ulp of x/s, so the
+// residual is exact in one FMA and RN(q0 + r*recip) = RN(x/s). The residual
+// is formed negated, n = q0*s - x, and enters the last FMA through the
+// operand's negation: for x = -0, n = +0 and q0 - n*recip = -0 + -0 = -0,
+// where the residual x - q0*s (+0) would give +0, so the sign of x survives
+// without a copysign. Below the fp32 normal range the quotient may differ
+// from IEEE division in its last bits, but every such value converts to a
+// signed fp8 zero (tests/fastdiv_check.c checks every bf16 x and amax).
 __device__ __forceinline__ float div_by_scale(float x, float s, float recip) {
   const float q0 = x * recip;
-  const float r = fmaf(-q0, s, x);
-  return __builtin_copysignf(fmaf(r, recip, q0), x);
+  const float n = fmaf(q0, s, -x);
+  return fmaf(-n, recip, q0);
 }
 
 // scale = amax / 448 rounded to nearest even without a division: with
@@ -59,9 +62,11 @@ __device__ __forceinline__ void quant8_finite(const float v[8], float scale, flo
   float y[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) y[i] = div_by_scale(v[i], scale, recip);
-  int p0 = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
+  // (the first convert of a word keeps the old high half, which the second
+  // one overwrites: any register serves as the old value)
+  int p0 = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], __float_as_int(y[0]), false);
   p0 = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], p0, true);
-  int p1 = __builtin_amdgcn_cvt_pk_fp8_f32(y[4], y[5], 0, false);
+  int p1 = __builtin_amdgcn_cvt_pk_fp8_f32(y[4], y[5], __float_as_int(y[4]), false);
   p1 = __builtin_amdgcn_cvt_pk_fp8_f32(y[6], y[7], p1, true);
   w0 = (uint32_t)p0;
   w1 = (uint32_t)p1;
@@ -96,6 +101,25 @@ __device__ __forceinline__ void quant_row16_8(const float v[8], uint32_t mag,
     quant8_finite(v, scale, recip_of_scale(scale), w0, w1);
   } else {
     quant8_nonfinite(v, gmag > 0x7F80u, w0, w1, scale);
+  }
+}
+
+// Quantise 16 values held by one lane of an 8-lane group of 128 (a DPP
+// half-row): the arithmetic of quant_row16_8 on twice the values per lane.
+// `mag` is the max over this lane's 16 bf16 magnitude patterns; w[0..3] are
+// the 16 codes, little-endian.
+__device__ __forceinline__ void quant_row8_16(const float v[16], uint32_t mag, uint32_t w[4],
+                                              float& scale) {
+  const uint32_t gmag = row8_max_u32(mag);
+  if (gmag < 0x7F80u) {
+    const float amax = fmaxf(bf16_to_f32(gmag), kAmaxFloor);
+    scale = scale_from_amax(amax);
+    const float recip = recip_of_scale(scale);
+    quant8_finite(v, scale, recip, w[0], w[1]);
+    quant8_finite(v + 8, scale, recip, w[2], w[3]);
+  } else {
+    quant8_nonfinite(v, gmag > 0x7F80u, w[0], w[1], scale);
+    quant8_nonfinite(v + 8, gmag > 0x7F80u, w[2], w[3], scale);
   }
 }
 

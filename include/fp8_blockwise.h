@@ -136,7 +136,8 @@ typedef enum fp8b_kernel {
   FP8B_KERNEL_PIPE256 = 6,      /* pipelined 256x256 tiles */
   FP8B_KERNEL_PIPE192 = 7,      /* pipelined 192x256 tiles */
   FP8B_KERNEL_PIPE256X128 = 8,  /* pipelined 256x128 tiles */
-  FP8B_KERNEL_BS128 = 9         /* two-stage 128x128 / 256x256 tiles (FP8B_PIPE=0, huge leading dims) */
+  FP8B_KERNEL_BS128 = 9,        /* two-stage 128x128 / 256x256 tiles (FP8B_PIPE=0, huge leading dims) */
+  FP8B_KERNEL_DECODE_QUANT = 10 /* fp8b_act_quant_matmul, M <= 32: act-quant inside the decode kernel */
 } fp8b_kernel;
 
 /* What fp8b_w8a8_block_matmul launches for one call. */
@@ -146,7 +147,7 @@ typedef struct fp8b_plan_info {
   int splits;              /* K splits; > 1: fp32 partials + split-K sum launch  */
   int kb_per_split;        /* 128-wide K-blocks per split                        */
   int waves;               /* 64-lane waves per workgroup                        */
-  int ring;                /* FP8B_KERNEL_DECODE: LDS stages (else 0)            */
+  int ring;                /* FP8B_KERNEL_DECODE(_QUANT): LDS stages (else 0)    */
   int64_t workgroups;      /* workgroups of the main launch, all splits          */
   int tail_kernel;         /* kernel of the grid's last partial wave, or NONE    */
   int tail_tile_m, tail_tile_n;
@@ -200,13 +201,17 @@ int fp8b_w8a8_block_matmul_noalloc(const void* A, int64_t lda,
 
 /*
  * Act-quant fused with the block GEMM: C = w8a8(act_quant(x)) against B/Bs
- * with block_n = block_k = 128, i.e. exactly fp8b_act_quant (group 128) into
- * (q, s) followed by fp8b_w8a8_block_matmul(q, B, s, Bs), with the same
- * result bits. No single counterpart in the reference: it composes the
- * quantiser above with the Helion kernel of
+ * with block_n = block_k = 128, with the result bits of fp8b_act_quant
+ * (group 128) into (q, s) followed by fp8b_w8a8_block_matmul(q, B, s, Bs).
+ * No single counterpart in the reference: it composes the quantiser above
+ * with the Helion kernel of
  * finegrained-fp8-helion/torch-ext/finegrained_fp8_helion/fp8.py:19-39 (the
- * act-quant-into-the-GEMM step for small M). Two launches on `stream`: the
- * quantiser writes (q, s) into the workspace, then the GEMM reads them.
+ * act-quant-into-the-GEMM step for small M). On decode plans with M <= 32
+ * (fp8b_act_quant_matmul_plan reports FP8B_KERNEL_DECODE_QUANT), with x
+ * 16-byte aligned and ldx % 8 == 0, one GEMM kernel reads the bf16 rows and
+ * quantises them itself (plus the split-K sum when the plan splits K);
+ * otherwise two launches on `stream`: the quantiser writes (q, s) into the
+ * workspace, then the GEMM reads them.
  * x : bf16 [M,K] row stride ldx (K % 128 == 0); B, Bs, C as in
  * fp8b_w8a8_block_matmul. workspace: fp8b_act_quant_matmul_workspace_size()
  * bytes, 256-byte aligned.
@@ -221,6 +226,18 @@ int fp8b_act_quant_matmul(const void* x, int64_t ldx,
 
 /* Bytes of device workspace fp8b_act_quant_matmul needs for these sizes. */
 size_t fp8b_act_quant_matmul_workspace_size(int64_t M, int64_t N, int64_t K);
+
+/*
+ * The GEMM launch fp8b_act_quant_matmul makes for an M x N x K problem with a
+ * contiguous, 16-byte aligned x (cu_count <= 0: the current device's CUs;
+ * no GPU call when cu_count > 0): FP8B_KERNEL_DECODE_QUANT with its split
+ * when one kernel quantises and multiplies, else the plan of the GEMM that
+ * follows the act-quant launch (as fp8b_gemm_plan). workspace_bytes is
+ * fp8b_act_quant_matmul_workspace_size(). No counterpart in the reference
+ * (a plan query like fp8b_gemm_plan).
+ */
+int fp8b_act_quant_matmul_plan(int64_t M, int64_t N, int64_t K, int cu_count,
+                               fp8b_plan_info* plan);
 
 /*
  * Offline 128x128 weight-block quantiser (the format of FP8 checkpoints:

@@ -1,6 +1,6 @@
 /* Exhaustive check of the act-quant division used by the GPU kernels
  * (hf_kernels_helion_amd/csrc/act_quant.hip, div_by_scale):
- *   y = RN(1/s); q0 = RN(x*y); r = fma(-q0, s, x); q = copysign(fma(r, y, q0), x)
+ *   y = RN(1/s); q0 = RN(x*y); n = fma(q0, s, -x); q = fma(-n, y, q0)
  * against IEEE x/s, for every finite bf16 x and every bf16 amax >= |x|, with
  * s = max(amax, 1e-10) / 448 as the kernels compute it. Every quotient that
  * differs from IEEE division must be below 2^-12 in magnitude (it converts to
@@ -37,8 +37,8 @@ int main(void) {
         const float x = bf16(xm | (sg ? 0x8000u : 0u));
         const float q = x / s;
         const float q0 = x * y;
-        const float r = fmaf(-q0, s, x);
-        const float f = copysignf(fmaf(r, y, q0), x);
+        const float n2 = fmaf(q0, s, -x);
+        const float f = fmaf(-n2, y, q0);
         ++n;
         if (bits(f) != bits(q)) {
           ++mism;

@@ -1,6 +1,7 @@
-"""GPU parity of the act-quant + GEMM op (act_quant_w8a8_block_fp8_matmul):
-bit for bit against the two public ops it composes (act_quant, then
-w8a8_block_fp8_matmul), and against the CPU oracle chain
+"""GPU parity of the act-quant + GEMM op (act_quant_w8a8_block_fp8_matmul),
+on both of its paths (one kernel that quantises inside the decode GEMM, or
+act-quant then the GEMM): bit for bit against the two public ops it composes
+(act_quant, then w8a8_block_fp8_matmul), and against the CPU oracle chain
 oracle.block_gemm(oracle.act_quant(x)) within the north-star tolerance
 (1e-2 relative, 1e-3 absolute of the oracle's result rounded to the output
 dtype)."""
@@ -58,6 +59,87 @@ def test_fused_equals_two_ops_and_oracle(M, N, K, dtype, dev):
     ref_t = torch.from_numpy(ref).to(dtype).float()
     torch.testing.assert_close(out[rows.to(dev), cols].float().cpu(), ref_t, rtol=RTOL,
                                atol=ATOL)
+
+
+# Shapes whose plan is the one-kernel path (gemm_decode_quant_kernel) on a
+# 256-CU MI355X, with the split layouts it must handle: K splits whose last
+# split has one or two K-blocks (fewer than the ring's prologue stages), a
+# ragged last column tile, 29 K-blocks per split (four scale windows), and
+# one unsplit K range; 9..32 rows (16-row and 32-row kernels).
+ONE_KERNEL = [(9, 2048, 8448), (32, 2048, 8576), (17, 4160, 7296), (9, 8192, 14464),
+              (32, 4160, 5248), (24, 4096, 14336), (31, 28672, 4096), (16, 13824, 5120)]
+
+
+def _one_kernel(M, N, K):
+    from hf_kernels_helion_amd import _native
+    return _native.act_quant_matmul_plan(M, N, K)["kernel"] == "gemm_decode_quant_kernel"
+
+
+@pytest.mark.parametrize("M,N,K", ONE_KERNEL)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_one_kernel_path_equals_two_ops(M, N, K, dtype, dev):
+    """act-quant inside the decode GEMM: the same bits as act_quant then the
+    GEMM, and the oracle chain within the north-star tolerance."""
+    print(f"one-kernel act-quant matmul M={M} N={N} K={K} {dtype}", flush=True)
+    assert _one_kernel(M, N, K)
+    x = synthetic.activations(M, K, seed=M * 7 + K, outlier_frac=0.01).to(dev)
+    W, Bs = _weights(N, K, N + 1, dev)
+    out = fp8.act_quant_w8a8_block_fp8_matmul(x, W, Bs, [128, 128], dtype)
+    _same(out, _two_op(x, W, Bs, dtype))
+    # rows of x; output columns of the first two and the last (ragged) weight
+    # blocks, with their block scales
+    rows = torch.unique(torch.tensor([0, M // 2, M - 1]))
+    lb = (N - 1) // 128
+    cols = torch.cat([torch.arange(0, 256), torch.arange(lb * 128, N)])
+    ref = _oracle_chain(x, W[cols.to(dev)], Bs[torch.tensor([0, 1, lb]).to(dev)], rows)
+    ref_t = torch.from_numpy(ref).to(dtype).float()
+    torch.testing.assert_close(out[rows.to(dev)][:, cols.to(dev)].float().cpu(), ref_t,
+                               rtol=RTOL, atol=ATOL)
+
+
+def test_one_kernel_path_nonfinite_zero_and_strided_rows(dev):
+    """NaN, +-inf and all-zero groups, a row stride past K and a 16-byte
+    offset base through the one-kernel path; a 2-byte offset base takes the
+    two-launch path (the kernel's DMA needs 16-byte aligned rows)."""
+    M, N, K = 17, 4160, 7296
+    assert _one_kernel(M, N, K)
+    big = synthetic.activations(M, K + 64, seed=11).to(dev)
+    big[2, 8 + 5] = float("nan")
+    big[7, 8 + 3000] = float("inf")
+    big[11, 8 + 6000] = -float("inf")
+    big[13, :] = 0
+    W, Bs = _weights(N, K, 12, dev)
+    for xv in (big[:, 8:K + 8], big[:, :K], big[:, 1:K + 1]):
+        out = fp8.act_quant_w8a8_block_fp8_matmul(xv, W, Bs, [128, 128], torch.float32)
+        _same(out, _two_op(xv.contiguous(), W, Bs, torch.float32))
+    out = fp8.act_quant_w8a8_block_fp8_matmul(big[:, 8:K + 8], W, Bs, [128, 128], torch.float32)
+    assert torch.equal(out[13], torch.zeros_like(out[13]))
+    assert torch.isnan(out[2]).all() and torch.isnan(out[7]).all() and torch.isnan(out[11]).all()
+
+
+def test_one_kernel_path_graph_replays(dev):
+    """Captured in a HIP graph, every replay of the one-kernel path (with
+    eager work between) equals the eager result."""
+    M, N, K = 32, 2048, 8576
+    assert _one_kernel(M, N, K)
+    x = synthetic.activations(M, K, seed=13).to(dev)
+    W, Bs = _weights(N, K, 14, dev)
+    f = lambda: fp8.act_quant_w8a8_block_fp8_matmul(x, W, Bs, [128, 128], torch.bfloat16)
+    eager = f()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        f()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = f()
+    for i in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        _same(out, eager)
+        _same(out, _two_op(x, W, Bs, torch.bfloat16))
+        torch.cuda.synchronize()
 
 
 def test_fused_nonfinite_and_zero_groups(dev):

@@ -1,5 +1,5 @@
 """CPU checks of the GEMM planner through the C ABI's plan query
-(fp8b_gemm_plan, fp8b_gate_up_plan): the kernel, tile, K splits and grid that
+(fp8b_gemm_plan, fp8b_gate_up_plan, fp8b_act_quant_matmul_plan): the kernel, tile, K splits and grid that
 one call launches, pinned for the five BASELINE configurations, the
 reference's fp8 tuning shapes (scripts/aot_tune.py:134-136) and the MLP
 chain, on a 256-CU MI355X. The plan query makes no GPU call for a given CU
@@ -102,6 +102,41 @@ def test_gate_up_plans(M, I, K, kernel, tile_m):
     assert p["workgroups"] == -(-M // tile_m) * (2 * I // 256)
 
 
+@pytest.mark.parametrize("M,N,K,kernel,splits,ring", [
+    (32, 4096, 14336, "gemm_decode_quant_kernel", 8, 3),   # C4: one kernel, same split
+    (16, 4096, 14336, "gemm_decode_quant_kernel", 8, 4),
+    (8, 13824, 5120, "gemm_decode_quant_kernel", 2, 4),
+    (32, 28672, 4096, "gemm_decode_quant_kernel", 1, 3),
+    (1, 4096, 14336, "gemm_skinny_kernel", 1, 0),          # the skinny GEMM's plan
+    (24, 7168, 8192, "gemm_decode_quant_kernel", 4, 3),
+    (33, 4096, 14336, "gemm_decode_kernel", 8, 4),         # 17+ rows of fragments: two launches
+    (64, 4096, 14336, "gemm_decode_kernel", 8, 4),
+    (3001, 4096, 14336, "gemm_pipe192_kernel", 1, 0),      # not a decode plan
+])
+def test_act_quant_matmul_plans(M, N, K, kernel, splits, ring):
+    """act_quant_w8a8_block_fp8_matmul runs one kernel (act-quant inside the
+    decode GEMM) exactly where the GEMM plan is the one-workgroup-per-CU
+    decode grid and M <= 32, with that plan's K split, so its result bits
+    equal act-quant + GEMM; elsewhere the GEMM of the two-launch path."""
+    p = _native.act_quant_matmul_plan(M, N, K, cu_count=CUS)
+    g = plan(M, N, K)
+    assert (p["kernel"], p["splits"], p["ring"]) == (kernel, splits, ring), p
+    assert (p["splits"], p["kb_per_split"], p["workgroups"]) == (
+        g["splits"], g["kb_per_split"], g["workgroups"])
+    assert p["workspace_bytes"] == _native.load().fp8b_act_quant_matmul_workspace_size(M, N, K)
+
+
+def test_act_quant_matmul_plan_grids_past_the_cus():
+    """A decode grid of more than one workgroup per CU (three-stage ring of
+    the GEMM, two workgroups per CU) keeps the two-launch path."""
+    g = plan(32, 28672, 8192)
+    p = _native.act_quant_matmul_plan(32, 28672, 8192, cu_count=CUS)
+    if g["kernel"] == "gemm_decode_kernel" and g["ring"] == 3:
+        assert p["kernel"] == "gemm_decode_kernel"
+    else:
+        assert g["workgroups"] <= CUS and p["kernel"] == "gemm_decode_quant_kernel"
+
+
 def test_plan_query_rejects_bad_args():
     import ctypes
     lib = _native.load()
@@ -109,3 +144,5 @@ def test_plan_query_rejects_bad_args():
     assert lib.fp8b_gemm_plan(0, 128, 128, 128, 128, CUS, ctypes.byref(info)) == 2
     assert lib.fp8b_gemm_plan(128, 128, 128, 128, 128, CUS, None) == 1
     assert lib.fp8b_gate_up_plan(128, 100, 512, CUS, ctypes.byref(info)) == 2
+    assert lib.fp8b_act_quant_matmul_plan(32, 4096, 200, CUS, ctypes.byref(info)) == 2
+    assert lib.fp8b_act_quant_matmul_plan(32, 4096, 256, CUS, None) == 1
