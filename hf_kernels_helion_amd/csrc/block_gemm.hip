@@ -2151,6 +2151,149 @@ __global__ void __launch_bounds__(512) gemm_skinny_kernel(GemmArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Skinny GEMM with the group-128 act-quant inside it (fp8b_act_quant_matmul
+// on skinny plans, M <= QR <= 8): gemm_skinny_kernel<1>'s grid, K ranges and
+// fold, with the activations read as bf16. Each wave streams its K-blocks
+// through a private ring of LDS slots (its 16 weight rows, chunk-swizzled;
+// the QR bf16 activation rows, unswizzled; the weight block's scale), all by
+// DMA counted by its own waits, and before each K-block's MFMA quantises
+// the slot's QR rows with the act-quant's own arithmetic (one task of 2*QR
+// values per lane: quant_row16_8 for 4 rows, quant_row8_16 for 8) into its
+// fp8 fragment buffer and scale buffer, which its MFMA then reads (LDS
+// operations of one wave complete in order). Rows QR..15 of the fragment are
+// never written and never stored. Codes, scales, K ranges, fold and the sum
+// of the eight partial tiles equal act-quant followed by gemm_skinny_kernel,
+// so the results are bit-identical to that two-kernel path.
+// Preconditions (checked by the host): M <= QR, x 16-byte aligned with a row
+// stride (a.lda, in bytes) that is a multiple of 16.
+// ---------------------------------------------------------------------------
+template <int QR>
+__global__ void __launch_bounds__(512) gemm_skinny_quant_kernel(GemmArgs a) {
+  constexpr int NWAVE = 8;
+  constexpr int SK = 3;                        // K-blocks in flight per wave
+  constexpr int QE = 2 * QR;                   // values per lane
+  constexpr int LPR = 128 / QE;                // lanes per row
+  constexpr int XLOADS = QR / 4;               // 1 KiB DMA instructions of bf16 rows
+  constexpr int X_OFF = 16 * 128;              // bf16 rows after the 16 weight rows
+  constexpr int S_OFF = X_OFF + QR * 256;      // the weight block's scale
+  constexpr int SLOT = S_OFF + 64;
+  constexpr int PER_KB = 2 + XLOADS + 1;       // DMA instructions per K-block
+  static_assert(QR == 4 || QR == 8, "4 or 8 activation rows");
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[NWAVE][SK][SLOT];
+  __shared__ __attribute__((aligned(1024))) uint8_t qbuf[NWAVE][16 * 128 + 64];
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n0 = blockIdx.x * 16;
+  const int kb0 = (int)((int64_t)a.KB * wid / NWAVE);
+  const int kb1 = (int)((int64_t)a.KB * (wid + 1) / NWAVE);
+  const int row = lane & 15;
+
+  // DMA sources: weight loads L = 0, 1 bring rows 8L..8L+7 (lane i: the
+  // logical chunk (i&7) ^ (r&7) of row 8L + (i>>3)); bf16 load L brings
+  // activation rows 4L..4L+3 (lane i: bytes 16(i&15).. of row 4L + (i>>4)).
+  const uint8_t* wsrc[2];
+#pragma unroll
+  for (int L = 0; L < 2; ++L) {
+    const int r = L * 8 + (lane >> 3);
+    wsrc[L] = a.B + (int64_t)min(n0 + r, a.N - 1) * a.ldb + ((lane & 7) ^ (r & 7)) * 16;
+  }
+  const uint8_t* xsrc[XLOADS];
+#pragma unroll
+  for (int L = 0; L < XLOADS; ++L)
+    xsrc[L] = a.A + (int64_t)min(L * 4 + (lane >> 4), a.M - 1) * a.lda + (lane & 15) * 16;
+  const float* bsrc = a.Bs + (int64_t)(min(n0, a.N - 1) >> 7) * a.bs_sn;
+  const uint32_t ring0 = lds_u32(&ring[wid][0][0]);
+
+  auto issue = [&](int kb, int slot) {
+    const uint32_t dst = ring0 + slot * SLOT;
+#pragma unroll
+    for (int L = 0; L < 2; ++L) dma16_ptr(wsrc[L] + (int64_t)kb * 128, dst + L * 1024);
+#pragma unroll
+    for (int L = 0; L < XLOADS; ++L) dma16_ptr(xsrc[L] + (int64_t)kb * 256, dst + X_OFF + L * 1024);
+    if (lane == 0) dma4_ptr(bsrc + (int64_t)kb * a.bs_sk, dst + S_OFF);
+  };
+
+  // This lane's quantiser task: row qm, values QE*qsub..+QE-1.
+  const int qm = lane / LPR, qsub = lane % LPR;
+  uint8_t* qb = &qbuf[wid][0];
+  float* qs = reinterpret_cast<float*>(qb + 16 * 128);
+  auto quantise = [&](const uint8_t* sl) {
+    float scale;
+    if constexpr (QE == 8) {
+      const v4i raw = *reinterpret_cast<const v4i*>(sl + X_OFF + qm * 256 + qsub * 16);
+      float v[8];
+      const uint32_t mag = unpack_bf16x8(raw, v);
+      uint32_t w0, w1;
+      quant_row16_8(v, mag, w0, w1, scale);
+      v2i packed;
+      packed[0] = (int)w0;
+      packed[1] = (int)w1;
+      *reinterpret_cast<v2i*>(qb + qm * 128 + (((qsub >> 1) ^ (qm & 7)) << 4) + (qsub & 1) * 8) =
+          packed;
+    } else {
+      const v4i raw0 = *reinterpret_cast<const v4i*>(sl + X_OFF + qm * 256 + qsub * 32);
+      const v4i raw1 = *reinterpret_cast<const v4i*>(sl + X_OFF + qm * 256 + qsub * 32 + 16);
+      float v[16];
+      const uint32_t mag = max(unpack_bf16x8(raw0, v), unpack_bf16x8(raw1, v + 8));
+      uint32_t w[4];
+      quant_row8_16(v, mag, w, scale);
+      v4i packed;
+      for (int i = 0; i < 4; ++i) packed[i] = (int)w[i];
+      *reinterpret_cast<v4i*>(qb + qm * 128 + ((qsub ^ (qm & 7)) << 4)) = packed;
+    }
+    if (qsub == 0) qs[qm] = scale;
+  };
+
+  const int c0 = 2 * (lane >> 4);
+  const int r7 = row & 7;
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int u = 0; u < SK; ++u)
+    if (kb0 + u < kb1) issue(kb0 + u, u);
+  for (int kb = kb0; kb < kb1; kb += SK) {
+#pragma unroll
+    for (int u = 0; u < SK; ++u) {
+      if (kb + u < kb1) {
+        // as in gemm_skinny_kernel: the next SK-1 K-blocks' DMAs were issued
+        // after this slot's, or fewer near the end of the range
+        if (kb + u + SK - 1 < kb1) wait_vmcnt<PER_KB * (SK - 1)>();
+        else wait_vmcnt<0>();
+        const uint8_t* sl = &ring[wid][u][0];
+        quantise(sl);
+        const v8i w = lds_frag(sl + row * 128, c0, r7);
+        const float sb = *reinterpret_cast<const float*>(sl + S_OFF);
+        const v8i x = lds_frag(qb + row * 128, c0, r7);
+        const float sc = qs[row] * sb;
+        const v4f t = mfma16x16x128(w, x);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] = fmaf(t[r], sc, acc[r]);
+        // refill the slot once this wave's reads of it are complete
+        if (kb + u + SK < kb1) {
+          lds_reads_done();
+          issue(kb + u + SK, u);
+        }
+      }
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  // Partial tiles reuse the ring: [wave][r][lane] floats, summed by wave 0
+  // in wave order (row m = lane & 15, columns n0 + 4*(lane>>4) + 0..3).
+  float* part = reinterpret_cast<float*>(&ring[0][0][0]);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) part[(wid * 4 + r) * 64 + lane] = acc[r];
+  __syncthreads();
+  if (wid != 0) return;
+  v4f sum = {0.f, 0.f, 0.f, 0.f};
+  for (int w = 0; w < NWAVE; ++w)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sum[r] += part[(w * 4 + r) * 64 + lane];
+  store4(a, row, n0 + 4 * (lane >> 4), sum, false, 0);
+}
+
 // Small-grid GEMM (grids of 128x128 tiles that would leave most CUs idle,
 // e.g. 512x512x2048): one workgroup per TM x TN output tile (TM = 16*FM,
 // TN = 16*FN: 32x32 or 64x64), so the grid spreads the operand stream over
@@ -3129,6 +3272,13 @@ void launch_decode_quant(const GemmArgs& a, int M, int splits, hipStream_t st) {
   else gemm_decode_quant_kernel<2, 3, 16><<<grid, 512, 0, st>>>(a);
 }
 
+// fp8b_act_quant_matmul takes gemm_skinny_quant_kernel when the plan is the
+// skinny kernel, M <= 8 and the bf16 rows are 16-byte aligned.
+bool skinny_quant_ok(const Dispatch& d, const void* x, int64_t ldx, int64_t M) {
+  return use_fused_decode() && d.kernel == FP8B_KERNEL_SKINNY && M <= 8 &&
+         ((uintptr_t)x & 15) == 0 && ldx % 8 == 0;
+}
+
 // fp8b_act_quant_matmul takes gemm_decode_quant_kernel when the plan is the
 // decode kernel with one workgroup per CU (grids past the CU count run two
 // smaller-ring workgroups per CU, for which the bf16 stages do not fit), the
@@ -3213,6 +3363,7 @@ const char* kernel_name(int k) {
     case FP8B_KERNEL_PIPE256X128: return "gemm_pipe256x128_kernel";
     case FP8B_KERNEL_BS128: return "gemm_bs128_kernel";
     case FP8B_KERNEL_DECODE_QUANT: return "gemm_decode_quant_kernel";
+    case FP8B_KERNEL_SKINNY_QUANT: return "gemm_skinny_quant_kernel";
     default: return "unknown";
   }
 }
@@ -3305,6 +3456,8 @@ extern "C" int fp8b_act_quant_matmul_plan(int64_t M, int64_t N, int64_t K, int c
   if (fused_decode_ok(d, nullptr, K, K, M)) {
     plan->kernel = FP8B_KERNEL_DECODE_QUANT;
     plan->ring = decode_quant_ring(M);
+  } else if (skinny_quant_ok(d, nullptr, K, M)) {
+    plan->kernel = FP8B_KERNEL_SKINNY_QUANT;
   }
   plan->workspace_bytes = fp8b_act_quant_matmul_workspace_size(M, N, K);
   return FP8B_OK;
@@ -3499,7 +3652,9 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 // gemm_decode_quant_kernel quantises the rows inside the GEMM with the plan's
 // split (then the split-K sum): 17.0 us per graph-replayed step at
 // 32x4096x14336 against 19.7 us for the two launches below, and 15.5 against
-// 18.0 at 16x4096x14336, bit-identical. Otherwise two launches on the
+// 18.0 at 16x4096x14336, bit-identical. On a skinny plan with M <= 8,
+// gemm_skinny_quant_kernel: 12.8 against 15.7 us at 1x4096x14336, 15.0
+// against 16.9 at 8x4096x14336. Otherwise two launches on the
 // caller's stream: the quantiser writes (q, s) into the workspace and the GEMM
 // reads them (plus its own split-K partials, at the start of the workspace).
 // Earlier one-launch forms, measured slower and removed: quantisation by
@@ -3556,6 +3711,30 @@ extern "C" int fp8b_act_quant_matmul(const void* x, int64_t ldx, const void* B, 
   const Dispatch d = resolve(M, N, K, 128, 128, device_cu_count(),
                              call_operands(q, K, B, ldb, s, KB, 1, Bs, bs_sn, bs_sk, M, N, K,
                                            128, 128));
+  if (skinny_quant_ok(d, x, ldx, M)) {
+    hipStream_t st = (hipStream_t)stream;
+    GemmArgs a;
+    a.A = (const uint8_t*)x; a.B = (const uint8_t*)B; a.As = nullptr; a.Bs = Bs; a.C = C;
+    a.ws = nullptr;
+    a.lda = 2 * ldx; a.ldb = ldb; a.as_sm = 0; a.as_sk = 0; a.bs_sn = bs_sn; a.bs_sk = bs_sk;
+    a.ldc = ldc; a.M = (int)M; a.N = (int)N; a.K = (int)K; a.KB = (int)KB;
+    a.kb_per_split = (int)KB;
+    a.tiles_m = 1; a.tiles_n = (int)((N + 15) / 16);
+    a.out_dtype = out_dtype;
+    a.rem_base = -1; a.rem_tiles_m = 0; a.rem_tiles_n = 0;
+    a.Sq = nullptr; a.sq_sm = 0; a.sq_sg = 0;
+    a.win4 = 1;
+    const size_t esz = out_dtype == FP8B_F32 ? 4 : 2;
+    a.vec_store = esz == 4 ? (ldc % 4 == 0 && ((uintptr_t)C & 15) == 0)
+                           : (ldc % 8 == 0 && ((uintptr_t)C & 15) == 0);
+    if (M <= 4) gemm_skinny_quant_kernel<4><<<(unsigned)d.grid, 512, 0, st>>>(a);
+    else gemm_skinny_quant_kernel<8><<<(unsigned)d.grid, 512, 0, st>>>(a);
+    if (hipGetLastError() != hipSuccess) {
+      set_error("fp8b_act_quant_matmul: fused skinny kernel launch failed");
+      return FP8B_ERR_LAUNCH;
+    }
+    return FP8B_OK;
+  }
   if (fused_decode_ok(d, x, ldx, ldb, M)) {
     hipStream_t st = (hipStream_t)stream;
     GemmArgs a;

@@ -1,6 +1,6 @@
 """GPU parity of the act-quant + GEMM op (act_quant_w8a8_block_fp8_matmul),
-on both of its paths (one kernel that quantises inside the decode GEMM, or
-act-quant then the GEMM): bit for bit against the two public ops it composes
+on each of its paths (one kernel that quantises inside the decode or the
+skinny GEMM, or act-quant then the GEMM): bit for bit against the two public ops it composes
 (act_quant, then w8a8_block_fp8_matmul), and against the CPU oracle chain
 oracle.block_gemm(oracle.act_quant(x)) within the north-star tolerance
 (1e-2 relative, 1e-3 absolute of the oracle's result rounded to the output
@@ -70,9 +70,55 @@ ONE_KERNEL = [(9, 2048, 8448), (32, 2048, 8576), (17, 4160, 7296), (9, 8192, 144
               (32, 4160, 5248), (24, 4096, 14336), (31, 28672, 4096), (16, 13824, 5120)]
 
 
-def _one_kernel(M, N, K):
+# Shapes whose plan is the skinny one-kernel path (gemm_skinny_quant_kernel,
+# M <= 8): 4- and 8-row forms, one K-block (seven of the eight waves have an
+# empty K range), K-block counts the eight waves split unevenly, ragged
+# 16-column tiles.
+SKINNY_ONE_KERNEL = [(1, 4096, 14336), (3, 1000, 1024), (4, 4096, 4096), (5, 2048, 8192),
+                     (8, 4096, 14336), (2, 520, 128), (7, 4096, 1920), (6, 3000, 640)]
+
+
+def _one_kernel(M, N, K, kernel="gemm_decode_quant_kernel"):
     from hf_kernels_helion_amd import _native
-    return _native.act_quant_matmul_plan(M, N, K)["kernel"] == "gemm_decode_quant_kernel"
+    return _native.act_quant_matmul_plan(M, N, K)["kernel"] == kernel
+
+
+@pytest.mark.parametrize("M,N,K", SKINNY_ONE_KERNEL)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_skinny_one_kernel_path_equals_two_ops(M, N, K, dtype, dev):
+    """act-quant inside the skinny GEMM: the same bits as act_quant then the
+    GEMM, and the oracle chain within the north-star tolerance."""
+    print(f"skinny one-kernel act-quant matmul M={M} N={N} K={K} {dtype}", flush=True)
+    assert _one_kernel(M, N, K, "gemm_skinny_quant_kernel")
+    x = synthetic.activations(M, K, seed=M * 5 + K, outlier_frac=0.01).to(dev)
+    W, Bs = _weights(N, K, N + 2, dev)
+    out = fp8.act_quant_w8a8_block_fp8_matmul(x, W, Bs, [128, 128], dtype)
+    _same(out, _two_op(x, W, Bs, dtype))
+    lb = (N - 1) // 128
+    cols = torch.cat([torch.arange(0, 128), torch.arange(lb * 128, N)])
+    ref = _oracle_chain(x, W[cols.to(dev)], Bs[torch.tensor([0, lb]).to(dev)],
+                        torch.arange(M))
+    torch.testing.assert_close(out[:, cols.to(dev)].float().cpu(),
+                               torch.from_numpy(ref).to(dtype).float(), rtol=RTOL, atol=ATOL)
+
+
+def test_skinny_one_kernel_path_nonfinite_and_strided_rows(dev):
+    """NaN, +-inf and all-zero groups, a row stride past K, a 16-byte offset
+    base, and a 2-byte offset base (two-launch path) on a skinny plan."""
+    M, N, K = 6, 3000, 2048
+    assert _one_kernel(M, N, K, "gemm_skinny_quant_kernel")
+    big = synthetic.activations(M, K + 64, seed=17).to(dev)
+    big[1, 8 + 5] = float("nan")
+    big[2, 8 + 1000] = float("inf")
+    big[3, 8 + 2000] = -float("inf")
+    big[4, :] = 0
+    W, Bs = _weights(N, K, 18, dev)
+    for xv in (big[:, 8:K + 8], big[:, :K], big[:, 1:K + 1]):
+        out = fp8.act_quant_w8a8_block_fp8_matmul(xv, W, Bs, [128, 128], torch.float32)
+        _same(out, _two_op(xv.contiguous(), W, Bs, torch.float32))
+    out = fp8.act_quant_w8a8_block_fp8_matmul(big[:, 8:K + 8], W, Bs, [128, 128], torch.float32)
+    assert torch.equal(out[4], torch.zeros_like(out[4]))
+    assert torch.isnan(out[1]).all() and torch.isnan(out[2]).all() and torch.isnan(out[3]).all()
 
 
 @pytest.mark.parametrize("M,N,K", ONE_KERNEL)
