@@ -2462,6 +2462,150 @@ __global__ void __launch_bounds__(64 * NW) gemm_tiny_kernel(GemmArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Small-grid GEMM with the group-128 act-quant inside it
+// (fp8b_act_quant_matmul on small-grid plans of 32-row tiles, M <= QR <= 8):
+// gemm_tiny_kernel<2, FN, NW, 2>'s grid, K ranges, fold and wave-order sum
+// for the first 16 rows of the tile (rows 8..31 do not exist). Each wave's
+// ring slots carry its TN weight rows (chunk-swizzled), the QR bf16
+// activation rows (unswizzled) and the weight block's scale, and the wave
+// quantises a slot's rows (one task of 2*QR values per lane, the
+// act-quant's arithmetic) into its own fragment and scale buffers right
+// before that slot's MFMAs (LDS operations of one wave complete in order).
+// Same codes, scales and sums as act-quant followed by gemm_tiny_kernel, so
+// the same output bits.
+// Preconditions (checked by the host): M <= QR, x 16-byte aligned with a row
+// stride (a.lda, in bytes) that is a multiple of 16; a.tiles_m = 1.
+// ---------------------------------------------------------------------------
+template <int FN, int NW, int QR>
+__global__ void __launch_bounds__(64 * NW) gemm_tiny_quant_kernel(GemmArgs a) {
+  constexpr int NS = 2;
+  constexpr int TN = 16 * FN;
+  constexpr int QE = 2 * QR;                   // values per lane
+  constexpr int LPR = 128 / QE;                // lanes per row
+  constexpr int WLOADS = TN / 8, XLOADS = QR / 4;
+  constexpr int X_OFF = TN * 128;              // bf16 rows after the weight rows
+  constexpr int S_OFF = X_OFF + QR * 256;      // the weight block's scale
+  constexpr int SLOT = S_OFF + 64;
+  constexpr int PER_KB = WLOADS + XLOADS + 1;  // DMA instructions per K-block
+  static_assert(QR == 4 || QR == 8, "4 or 8 activation rows");
+  static_assert(NW == 1 || NS * SLOT >= FN * 4 * 64 * 4, "partials reuse the ring");
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[NW][NS][SLOT];
+  __shared__ __attribute__((aligned(1024))) uint8_t qbuf[NW][16 * 128 + 64];
+  const int lane = threadIdx.x & 63;
+  const int wid = NW == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int tm, tn;
+  tile_of_bid((int)blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
+  const int n0 = tn * TN;
+  if (n0 >= a.N) return;
+  const int kb0 = (int)((int64_t)a.KB * wid / NW);
+  const int kb1 = (int)((int64_t)a.KB * (wid + 1) / NW);
+
+  const uint8_t* wsrc[WLOADS];
+#pragma unroll
+  for (int L = 0; L < WLOADS; ++L) {
+    const int r = L * 8 + (lane >> 3);
+    wsrc[L] = a.B + (int64_t)min(n0 + r, a.N - 1) * a.ldb + ((lane & 7) ^ (r & 7)) * 16;
+  }
+  const uint8_t* xsrc[XLOADS];
+#pragma unroll
+  for (int L = 0; L < XLOADS; ++L)
+    xsrc[L] = a.A + (int64_t)min(L * 4 + (lane >> 4), a.M - 1) * a.lda + (lane & 15) * 16;
+  const float* bsrc = a.Bs + (int64_t)(min(n0, a.N - 1) >> 7) * a.bs_sn;
+  const uint32_t ring0 = lds_u32(&ring[wid][0][0]);
+  auto issue = [&](int kb, int slot) {
+    const uint32_t dst = ring0 + slot * SLOT;
+#pragma unroll
+    for (int L = 0; L < WLOADS; ++L) dma16_ptr(wsrc[L] + (int64_t)kb * 128, dst + L * 1024);
+#pragma unroll
+    for (int L = 0; L < XLOADS; ++L) dma16_ptr(xsrc[L] + (int64_t)kb * 256, dst + X_OFF + L * 1024);
+    if (lane == 0) dma4_ptr(bsrc + (int64_t)kb * a.bs_sk, dst + S_OFF);
+  };
+
+  const int qm = lane / LPR, qsub = lane % LPR;
+  uint8_t* qb = &qbuf[wid][0];
+  float* qs = reinterpret_cast<float*>(qb + 16 * 128);
+  auto quantise = [&](const uint8_t* sl) {
+    float scale;
+    if constexpr (QE == 8) {
+      const v4i raw = *reinterpret_cast<const v4i*>(sl + X_OFF + qm * 256 + qsub * 16);
+      float v[8];
+      const uint32_t mag = unpack_bf16x8(raw, v);
+      uint32_t w0, w1;
+      quant_row16_8(v, mag, w0, w1, scale);
+      v2i packed;
+      packed[0] = (int)w0;
+      packed[1] = (int)w1;
+      *reinterpret_cast<v2i*>(qb + qm * 128 + (((qsub >> 1) ^ (qm & 7)) << 4) + (qsub & 1) * 8) =
+          packed;
+    } else {
+      const v4i raw0 = *reinterpret_cast<const v4i*>(sl + X_OFF + qm * 256 + qsub * 32);
+      const v4i raw1 = *reinterpret_cast<const v4i*>(sl + X_OFF + qm * 256 + qsub * 32 + 16);
+      float v[16];
+      const uint32_t mag = max(unpack_bf16x8(raw0, v), unpack_bf16x8(raw1, v + 8));
+      uint32_t w[4];
+      quant_row8_16(v, mag, w, scale);
+      v4i packed;
+      for (int i = 0; i < 4; ++i) packed[i] = (int)w[i];
+      *reinterpret_cast<v4i*>(qb + qm * 128 + ((qsub ^ (qm & 7)) << 4)) = packed;
+    }
+    if (qsub == 0) qs[qm] = scale;
+  };
+
+  const int row = lane & 15, c0 = 2 * (lane >> 4), r7 = row & 7;
+  v4f acc[FN];
+#pragma unroll
+  for (int j = 0; j < FN; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  for (int u = 0; u < NS && kb0 + u < kb1; ++u) issue(kb0 + u, u);
+  for (int kb = kb0; kb < kb1; ++kb) {
+    const int slot = (kb - kb0) % NS;
+    // as in gemm_tiny_kernel: the next NS-1 K-blocks' DMAs were issued after
+    // this slot's, or fewer near the end of the range
+    if (kb + NS - 1 < kb1) wait_vmcnt<PER_KB * (NS - 1)>();
+    else wait_vmcnt<0>();
+    const uint8_t* sl = &ring[wid][slot][0];
+    quantise(sl);
+    const v8i x = lds_frag(qb + row * 128, c0, r7);
+    const float sc = qs[row] * *reinterpret_cast<const float*>(sl + S_OFF);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const v8i w = lds_frag(sl + (j * 16 + row) * 128, c0, r7);
+      const v4f t = mfma16x16x128(w, x);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[j][e] = fmaf(t[e], sc, acc[j][e]);
+    }
+    // refill the slot once this wave's reads of it are complete
+    if (kb + NS < kb1) {
+      lds_reads_done();
+      issue(kb + NS, slot);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  if constexpr (NW == 1) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) store4(a, row, n0 + j * 16 + 4 * (lane >> 4), acc[j], false, 0);
+  } else {
+    // partial tiles reuse the ring: [wave][j][e][lane] floats; wave q sums
+    // sub-tiles q, q + NW, ... of every wave in wave order
+    __syncthreads();
+    float* part = reinterpret_cast<float*>(&ring[0][0][0]);
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) part[((wid * FN + j) * 4 + e) * 64 + lane] = acc[j][e];
+    __syncthreads();
+    for (int j = wid; j < FN; j += NW) {
+      v4f sum = {0.f, 0.f, 0.f, 0.f};
+      for (int w = 0; w < NW; ++w)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sum[e] += part[((w * FN + j) * 4 + e) * 64 + lane];
+      store4(a, row, n0 + j * 16 + 4 * (lane >> 4), sum, false, 0);
+    }
+  }
+}
+
 // Sum split-K partials in split order and convert: 4 outputs per thread. The
 // partial loads go out eight splits at a time before any is added, so the
 // kernel costs about one memory latency per eight splits.
@@ -3230,6 +3374,17 @@ Dispatch resolve(int64_t M, int64_t N, int64_t K, int64_t block_n, int64_t block
   return d;
 }
 
+// gemm_tiny_quant_kernel for a small-grid plan of 32 x tile_n tiles.
+template <int QR>
+void launch_tiny_quant(const GemmArgs& a, int tile_n, int waves, int64_t grid, hipStream_t st) {
+  const unsigned g = (unsigned)grid, thr = 64u * (unsigned)waves;
+  if (tile_n == 16) gemm_tiny_quant_kernel<1, 8, QR><<<g, thr, 0, st>>>(a);
+  else if (waves == 8) gemm_tiny_quant_kernel<2, 8, QR><<<g, thr, 0, st>>>(a);
+  else if (waves == 4) gemm_tiny_quant_kernel<2, 4, QR><<<g, thr, 0, st>>>(a);
+  else if (waves == 2) gemm_tiny_quant_kernel<2, 2, QR><<<g, thr, 0, st>>>(a);
+  else gemm_tiny_quant_kernel<2, 1, QR><<<g, thr, 0, st>>>(a);
+}
+
 template <bool PR>
 void launch_tiny(const GemmArgs& a, int tile_n, int waves, int64_t grid, hipStream_t st) {
   const unsigned g = (unsigned)grid, thr = 64u * (unsigned)waves;
@@ -3277,6 +3432,14 @@ void launch_decode_quant(const GemmArgs& a, int M, int splits, hipStream_t st) {
 bool skinny_quant_ok(const Dispatch& d, const void* x, int64_t ldx, int64_t M) {
   return use_fused_decode() && d.kernel == FP8B_KERNEL_SKINNY && M <= 8 &&
          ((uintptr_t)x & 15) == 0 && ldx % 8 == 0;
+}
+
+// ... and gemm_tiny_quant_kernel when the plan is one small grid of 32x16 or
+// 32x32 tiles (no tail launch), M <= 8 and the rows are 16-byte aligned.
+bool tiny_quant_ok(const Dispatch& d, const void* x, int64_t ldx, int64_t M) {
+  return use_fused_decode() && d.kernel == FP8B_KERNEL_TINY && d.tail_kernel == FP8B_KERNEL_NONE &&
+         d.bm == 32 && (d.bn == 16 || d.bn == 32) && M <= 8 && ((uintptr_t)x & 15) == 0 &&
+         ldx % 8 == 0;
 }
 
 // fp8b_act_quant_matmul takes gemm_decode_quant_kernel when the plan is the
@@ -3364,6 +3527,7 @@ const char* kernel_name(int k) {
     case FP8B_KERNEL_BS128: return "gemm_bs128_kernel";
     case FP8B_KERNEL_DECODE_QUANT: return "gemm_decode_quant_kernel";
     case FP8B_KERNEL_SKINNY_QUANT: return "gemm_skinny_quant_kernel";
+    case FP8B_KERNEL_TINY_QUANT: return "gemm_tiny_quant_kernel";
     default: return "unknown";
   }
 }
@@ -3458,6 +3622,8 @@ extern "C" int fp8b_act_quant_matmul_plan(int64_t M, int64_t N, int64_t K, int c
     plan->ring = decode_quant_ring(M);
   } else if (skinny_quant_ok(d, nullptr, K, M)) {
     plan->kernel = FP8B_KERNEL_SKINNY_QUANT;
+  } else if (tiny_quant_ok(d, nullptr, K, M)) {
+    plan->kernel = FP8B_KERNEL_TINY_QUANT;
   }
   plan->workspace_bytes = fp8b_act_quant_matmul_workspace_size(M, N, K);
   return FP8B_OK;
@@ -3654,9 +3820,11 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 // 32x4096x14336 against 19.7 us for the two launches below, and 15.5 against
 // 18.0 at 16x4096x14336, bit-identical. On a skinny plan with M <= 8,
 // gemm_skinny_quant_kernel: 12.8 against 15.7 us at 1x4096x14336, 15.0
-// against 16.9 at 8x4096x14336. Otherwise two launches on the
-// caller's stream: the quantiser writes (q, s) into the workspace and the GEMM
-// reads them (plus its own split-K partials, at the start of the workspace).
+// against 16.9 at 8x4096x14336; on a small-grid plan with M <= 8,
+// gemm_tiny_quant_kernel: 24.1 against 27.5 us at 1x28672x4096. Otherwise
+// two launches on the caller's stream: the quantiser writes (q, s) into the
+// workspace and the GEMM reads them (plus its own split-K partials, at the
+// start of the workspace).
 // Earlier one-launch forms, measured slower and removed: quantisation by
 // every wave after its MFMAs (the per-column-tile repetition of the act-quant
 // work then sits on each K-block's critical path), per-split prologue
@@ -3711,7 +3879,7 @@ extern "C" int fp8b_act_quant_matmul(const void* x, int64_t ldx, const void* B, 
   const Dispatch d = resolve(M, N, K, 128, 128, device_cu_count(),
                              call_operands(q, K, B, ldb, s, KB, 1, Bs, bs_sn, bs_sk, M, N, K,
                                            128, 128));
-  if (skinny_quant_ok(d, x, ldx, M)) {
+  if (skinny_quant_ok(d, x, ldx, M) || tiny_quant_ok(d, x, ldx, M)) {
     hipStream_t st = (hipStream_t)stream;
     GemmArgs a;
     a.A = (const uint8_t*)x; a.B = (const uint8_t*)B; a.As = nullptr; a.Bs = Bs; a.C = C;
@@ -3719,7 +3887,7 @@ extern "C" int fp8b_act_quant_matmul(const void* x, int64_t ldx, const void* B, 
     a.lda = 2 * ldx; a.ldb = ldb; a.as_sm = 0; a.as_sk = 0; a.bs_sn = bs_sn; a.bs_sk = bs_sk;
     a.ldc = ldc; a.M = (int)M; a.N = (int)N; a.K = (int)K; a.KB = (int)KB;
     a.kb_per_split = (int)KB;
-    a.tiles_m = 1; a.tiles_n = (int)((N + 15) / 16);
+    a.tiles_m = 1; a.tiles_n = (int)((N + d.bn - 1) / d.bn);
     a.out_dtype = out_dtype;
     a.rem_base = -1; a.rem_tiles_m = 0; a.rem_tiles_n = 0;
     a.Sq = nullptr; a.sq_sm = 0; a.sq_sg = 0;
@@ -3727,10 +3895,16 @@ extern "C" int fp8b_act_quant_matmul(const void* x, int64_t ldx, const void* B, 
     const size_t esz = out_dtype == FP8B_F32 ? 4 : 2;
     a.vec_store = esz == 4 ? (ldc % 4 == 0 && ((uintptr_t)C & 15) == 0)
                            : (ldc % 8 == 0 && ((uintptr_t)C & 15) == 0);
-    if (M <= 4) gemm_skinny_quant_kernel<4><<<(unsigned)d.grid, 512, 0, st>>>(a);
-    else gemm_skinny_quant_kernel<8><<<(unsigned)d.grid, 512, 0, st>>>(a);
+    if (d.kernel == FP8B_KERNEL_TINY) {
+      if (M <= 4) launch_tiny_quant<4>(a, d.bn, d.waves, d.grid, st);
+      else launch_tiny_quant<8>(a, d.bn, d.waves, d.grid, st);
+    } else if (M <= 4) {
+      gemm_skinny_quant_kernel<4><<<(unsigned)d.grid, 512, 0, st>>>(a);
+    } else {
+      gemm_skinny_quant_kernel<8><<<(unsigned)d.grid, 512, 0, st>>>(a);
+    }
     if (hipGetLastError() != hipSuccess) {
-      set_error("fp8b_act_quant_matmul: fused skinny kernel launch failed");
+      set_error("fp8b_act_quant_matmul: fused small-M kernel launch failed");
       return FP8B_ERR_LAUNCH;
     }
     return FP8B_OK;

@@ -138,7 +138,8 @@ typedef enum fp8b_kernel {
   FP8B_KERNEL_PIPE256X128 = 8,  /* pipelined 256x128 tiles */
   FP8B_KERNEL_BS128 = 9,        /* two-stage 128x128 / 256x256 tiles (FP8B_PIPE=0, huge leading dims) */
   FP8B_KERNEL_DECODE_QUANT = 10, /* fp8b_act_quant_matmul, M <= 32: act-quant inside the decode kernel */
-  FP8B_KERNEL_SKINNY_QUANT = 11  /* fp8b_act_quant_matmul, M <= 8: act-quant inside the skinny kernel */
+  FP8B_KERNEL_SKINNY_QUANT = 11, /* fp8b_act_quant_matmul, M <= 8: act-quant inside the skinny kernel */
+  FP8B_KERNEL_TINY_QUANT = 12    /* fp8b_act_quant_matmul, M <= 8: act-quant inside the small-grid kernel */
 } fp8b_kernel;
 
 /* What fp8b_w8a8_block_matmul launches for one call. */
@@ -208,8 +209,8 @@ int fp8b_w8a8_block_matmul_noalloc(const void* A, int64_t lda,
  * with the Helion kernel of
  * finegrained-fp8-helion/torch-ext/finegrained_fp8_helion/fp8.py:19-39 (the
  * act-quant-into-the-GEMM step for small M). On decode plans with M <= 32
- * and skinny plans with M <= 8 (fp8b_act_quant_matmul_plan reports
- * FP8B_KERNEL_DECODE_QUANT / FP8B_KERNEL_SKINNY_QUANT), with x 16-byte
+ * and skinny or small-grid plans with M <= 8 (fp8b_act_quant_matmul_plan
+ * reports FP8B_KERNEL_DECODE_QUANT / _SKINNY_QUANT / _TINY_QUANT), with x 16-byte
  * aligned and ldx % 8 == 0, one GEMM kernel reads the bf16 rows and
  * quantises them itself (plus the split-K sum when the plan splits K);
  * otherwise two launches on `stream`: the quantiser writes (q, s) into the
@@ -232,8 +233,9 @@ size_t fp8b_act_quant_matmul_workspace_size(int64_t M, int64_t N, int64_t K);
 /*
  * The GEMM launch fp8b_act_quant_matmul makes for an M x N x K problem with a
  * contiguous, 16-byte aligned x (cu_count <= 0: the current device's CUs;
- * no GPU call when cu_count > 0): FP8B_KERNEL_DECODE_QUANT (with its split)
- * or FP8B_KERNEL_SKINNY_QUANT when one kernel quantises and multiplies,
+ * no GPU call when cu_count > 0): FP8B_KERNEL_DECODE_QUANT (with its split),
+ * FP8B_KERNEL_SKINNY_QUANT or FP8B_KERNEL_TINY_QUANT when one kernel
+ * quantises and multiplies,
  * else the plan of the GEMM that
  * follows the act-quant launch (as fp8b_gemm_plan). workspace_bytes is
  * fp8b_act_quant_matmul_workspace_size(). No counterpart in the reference

@@ -78,18 +78,28 @@ SKINNY_ONE_KERNEL = [(1, 4096, 14336), (3, 1000, 1024), (4, 4096, 4096), (5, 204
                      (8, 4096, 14336), (2, 520, 128), (7, 4096, 1920), (6, 3000, 640)]
 
 
+# Shapes whose plan is the small-grid one-kernel path (gemm_tiny_quant_kernel,
+# M <= 8, 32-row tiles): 8, 4 and 2 waves per tile, one K-block, ragged last
+# 32-column tiles, 4- and 8-row forms.
+TINY_ONE_KERNEL = [(1, 8192, 128), (3, 8704, 1024), (1, 20992, 4096), (6, 28672, 4096),
+                   (8, 14336, 2048), (5, 8200, 512), (7, 9000, 640)]
+
+
 def _one_kernel(M, N, K, kernel="gemm_decode_quant_kernel"):
     from hf_kernels_helion_amd import _native
     return _native.act_quant_matmul_plan(M, N, K)["kernel"] == kernel
 
 
-@pytest.mark.parametrize("M,N,K", SKINNY_ONE_KERNEL)
+@pytest.mark.parametrize("M,N,K,kernel",
+                         [s + ("gemm_skinny_quant_kernel",) for s in SKINNY_ONE_KERNEL] +
+                         [s + ("gemm_tiny_quant_kernel",) for s in TINY_ONE_KERNEL])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_skinny_one_kernel_path_equals_two_ops(M, N, K, dtype, dev):
-    """act-quant inside the skinny GEMM: the same bits as act_quant then the
-    GEMM, and the oracle chain within the north-star tolerance."""
-    print(f"skinny one-kernel act-quant matmul M={M} N={N} K={K} {dtype}", flush=True)
-    assert _one_kernel(M, N, K, "gemm_skinny_quant_kernel")
+def test_small_m_one_kernel_paths_equal_two_ops(M, N, K, kernel, dtype, dev):
+    """act-quant inside the skinny or the small-grid GEMM: the same bits as
+    act_quant then the GEMM, and the oracle chain within the north-star
+    tolerance."""
+    print(f"{kernel} act-quant matmul M={M} N={N} K={K} {dtype}", flush=True)
+    assert _one_kernel(M, N, K, kernel)
     x = synthetic.activations(M, K, seed=M * 5 + K, outlier_frac=0.01).to(dev)
     W, Bs = _weights(N, K, N + 2, dev)
     out = fp8.act_quant_w8a8_block_fp8_matmul(x, W, Bs, [128, 128], dtype)
