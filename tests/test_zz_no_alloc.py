@@ -7,6 +7,8 @@ captured in a HIP graph as the process's first calls of the entry point (the
 scratch address is resolved inside the capture); the scratch holds the
 partials of every plan on this device, for block and per-row weight scales
 (plans whose partials would exceed it are refused with FP8B_ERR_WORKSPACE)."""
+import gc
+
 import pytest
 import torch
 
@@ -55,9 +57,9 @@ def test_noalloc_in_graph_capture(dev):
     after the other test files, none of which calls this entry point) these
     are the process's first calls of it: the scratch address is resolved
     inside the capture. Nothing is allocated across the calls (torch's
-    allocator and the device's free memory unchanged), and every replay, with
-    eager work and synchronisation in between, equals the workspace entry
-    point bit for bit."""
+    allocator unchanged, the device's free memory not lowered), and every
+    replay, with eager work and synchronisation in between, equals the
+    workspace entry point bit for bit."""
     lib = _native.load()
     cases = [_operands(32, 2048, 14336, seed=301, dev=dev),
              _operands(300, 1024, 16384, seed=303, dev=dev)]
@@ -75,14 +77,20 @@ def test_noalloc_in_graph_capture(dev):
             _native.check(st, "fp8b_w8a8_block_matmul_noalloc (captured)")
         assert torch.cuda.memory_allocated() == alloc0
     torch.cuda.synchronize()
-    # eager calls leave the device's free memory as it was (torch's graph
-    # context itself releases cached blocks, so this is checked outside it)
+    # eager calls take no device memory (torch's graph context itself
+    # releases cached blocks, so this is checked outside it). The runtime may
+    # hand back memory that earlier tests released (destroyed graphs, freed
+    # pools) at any synchronisation, which only raises the free figure; an
+    # allocation by the calls would lower it.
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
     free0 = torch.cuda.mem_get_info()[0]
     for c, o in zip(cases, outs):
         _native.check(lib.fp8b_w8a8_block_matmul_noalloc(
             *_args(*c, o, _native.BF16), torch.cuda.current_stream().cuda_stream), "noalloc")
     torch.cuda.synchronize()
-    assert torch.cuda.mem_get_info()[0] == free0
+    assert torch.cuda.mem_get_info()[0] >= free0
     for rep in range(3):
         print(f"noalloc graph replay {rep}", flush=True)
         for o in outs:
