@@ -2776,7 +2776,8 @@ int device_cu_count() {
 //   FP8B_TAIL64=0   no 64x64 quarters for a small last wave of 128x128 tiles;
 //   FP8B_TILE256X128=0  no 256x128 tiles;
 //   FP8B_FUSED_DECODE=0 fp8b_act_quant_matmul runs act-quant and the GEMM as
-//                   two kernels on decode plans too.
+//                   two kernels on decode, skinny and small-grid plans too;
+//   FP8B_TINY16=0   M <= 16 small grids run the 32-row tiles whole.
 bool env_flag_on(const char* name) {
   const char* e = getenv(name);
   return !(e && e[0] == '0');
@@ -2807,6 +2808,10 @@ bool use_tail64() {
 }
 bool use_tile256x128() {
   static const bool v = env_flag_on("FP8B_TILE256X128");
+  return v;
+}
+bool use_tiny16() {
+  static const bool v = env_flag_on("FP8B_TINY16");
   return v;
 }
 bool use_fused_decode() {
@@ -3388,6 +3393,20 @@ void launch_tiny_quant(const GemmArgs& a, int tile_n, int waves, int64_t grid, h
 template <bool PR>
 void launch_tiny(const GemmArgs& a, int tile_n, int waves, int64_t grid, hipStream_t st) {
   const unsigned g = (unsigned)grid, thr = 64u * (unsigned)waves;
+  // M <= 16 on 32-row tiles with block scales: the first 16 rows only (half
+  // the activation bytes per K-block; rows past M are never stored, so the
+  // same bits): 1x14336x4096 12.6 against 13.5 us, 1x28672x4096 23.2
+  // against 24.1, 16x14336x4096 14.0 against 14.6 (graph-replayed, rotating
+  // weight copies). With per-row scales it measured slower (28.4 against
+  // 26.2 us at 1x28672x4096).
+  if (!PR && a.M <= 16 && tile_n != 64 && use_tiny16()) {
+    if (tile_n == 16) gemm_tiny_kernel<1, 1, 8, 2, PR><<<g, thr, 0, st>>>(a);
+    else if (waves == 8) gemm_tiny_kernel<1, 2, 8, 2, PR><<<g, thr, 0, st>>>(a);
+    else if (waves == 4) gemm_tiny_kernel<1, 2, 4, 2, PR><<<g, thr, 0, st>>>(a);
+    else if (waves == 2) gemm_tiny_kernel<1, 2, 2, 2, PR><<<g, thr, 0, st>>>(a);
+    else gemm_tiny_kernel<1, 2, 1, 2, PR><<<g, thr, 0, st>>>(a);
+    return;
+  }
   if (tile_n == 16) gemm_tiny_kernel<2, 1, 8, 2, PR><<<g, thr, 0, st>>>(a);
   else if (tile_n == 64 && waves == 4) gemm_tiny_kernel<4, 4, 4, 2, PR><<<g, thr, 0, st>>>(a);
   else if (tile_n == 64) gemm_tiny_kernel<4, 4, 2, 2, PR><<<g, thr, 0, st>>>(a);

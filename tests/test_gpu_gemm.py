@@ -783,13 +783,16 @@ def test_gemm_256x128_tiles_exact_integers(dev):
 # up to eight), ragged edges, one K-block (seven of eight waves idle), a
 # long K, 49..64 rows, decode-sized M (1, 17, 24, 32), the 64x64-tile band
 # (two waves per tile for 1024 x 2048, four for 960 x 1024) and 32x16 tiles
-# (decode shapes with N = 4096).
+# (decode shapes with N = 4096). Up to 16 rows with block scales the kernel
+# computes only the first 16 rows of each 32-row tile (1, 3, 5, 8, 12, 13,
+# 16 rows here, with 8, 4 and 2 waves per tile and 32x16 tiles).
 SMALL_GRIDS = [(512, 512, 2048), (500, 300, 1024), (65, 96, 4096), (100, 2000, 7168),
                (256, 1024, 128), (512, 1024, 2048), (1024, 512, 7168), (768, 768, 4096),
                (2048, 1024, 2048), (1000, 2000, 1024), (64, 4096, 4096), (49, 500, 2048),
                (56, 14336, 4096), (32, 14336, 4096), (1, 8192, 4096), (24, 4096, 4096),
                (17, 8192, 1024), (1024, 2048, 4096), (960, 1024, 4096), (1000, 1800, 2048),
-               (32, 4096, 7168), (12, 4096, 4096), (16, 4096, 7168)]
+               (32, 4096, 7168), (12, 4096, 4096), (16, 4096, 7168), (1, 28672, 4096),
+               (8, 14336, 4096), (5, 8200, 512), (3, 8704, 1024), (13, 8192, 2048)]
 
 
 def _one_wave_per_tile(M, N, K):
@@ -865,12 +868,14 @@ def test_gemm_small_grid_repeatable(M, N, K, dev):
 
 @pytest.mark.parametrize("M,N,K", [(512, 512, 2048), (256, 1024, 128), (512, 1024, 2048),
                                    (768, 768, 4096), (2048, 1024, 1024), (1024, 2048, 2048),
-                                   (1024, 1024, 4096), (32, 4096, 4096), (16, 4096, 7168)])
+                                   (1024, 1024, 4096), (32, 4096, 4096), (16, 4096, 7168),
+                                   (1, 28672, 4096), (8, 14336, 512), (13, 8192, 2048)])
 def test_gemm_small_grid_exact_integers(M, N, K, dev):
     """Small-integer fp8 operands and power-of-two scales: every MFMA dot,
     fold and sum of partial tiles is exact, so each small-grid configuration
     (8, 4, 2 and 1 waves per 32x32 tile; 2 and 4 per 64x64 tile; 8 per
-    32x16 tile) must give the exact product bit for bit."""
+    32x16 tile; the 16-row form of a 32-row tile) must give the exact
+    product bit for bit."""
     print(f"gemm small-grid exact M={M} N={N} K={K}", flush=True)
     g = torch.Generator().manual_seed(M + N + K)
     A = torch.randint(-3, 4, (M, K), generator=g).float().to(torch.float8_e4m3fn)
