@@ -1812,6 +1812,64 @@ __global__ void __launch_bounds__(512) gemm_decode_kernel(GemmArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// One lane's share of quantising bf16 rows inside a GEMM kernel: row qm of
+// the rows at `src` (256 bytes each, unswizzled), values QE*qsub..+QE-1
+// (quant_load), then the act-quant's arithmetic over the 128/QE lanes of the
+// row's group (a DPP row, half-row or quad: quant_row16_8, quant_row8_16,
+// quant_row4_32) with the codes to row qm of `frag` in the MFMA fragment
+// layout (128 bytes per row, 16-byte chunk c at slot c ^ (row & 7)) and the
+// group scale to scales[qm] by the row's first lane (quant_codes). Every
+// lane of the group must call quant_codes.
+template <int QE> struct QuantRaw {
+  static_assert(QE == 8 || QE == 16 || QE == 32, "8, 16 or 32 values per lane");
+  v4i r[QE / 8];
+};
+
+template <int QE>
+__device__ __forceinline__ QuantRaw<QE> quant_load(const uint8_t* src, int qm, int qsub) {
+  QuantRaw<QE> raw;
+#pragma unroll
+  for (int i = 0; i < QE / 8; ++i)
+    raw.r[i] = *reinterpret_cast<const v4i*>(src + qm * 256 + qsub * (QE * 2) + i * 16);
+  return raw;
+}
+
+template <int QE>
+__device__ __forceinline__ void quant_codes(const QuantRaw<QE>& raw, int qm, int qsub,
+                                            uint8_t* frag, float* scales) {
+  float v[QE];
+  uint32_t mag = 0;
+#pragma unroll
+  for (int i = 0; i < QE / 8; ++i) mag = max(mag, unpack_bf16x8(raw.r[i], v + 8 * i));
+  float scale;
+  uint8_t* row = frag + qm * 128;
+  if constexpr (QE == 8) {
+    uint32_t w0, w1;
+    quant_row16_8(v, mag, w0, w1, scale);
+    v2i packed;
+    packed[0] = (int)w0;
+    packed[1] = (int)w1;
+    *reinterpret_cast<v2i*>(row + (((qsub >> 1) ^ (qm & 7)) << 4) + (qsub & 1) * 8) = packed;
+  } else if constexpr (QE == 16) {
+    uint32_t w[4];
+    quant_row8_16(v, mag, w, scale);
+    v4i packed;
+    for (int i = 0; i < 4; ++i) packed[i] = (int)w[i];
+    *reinterpret_cast<v4i*>(row + ((qsub ^ (qm & 7)) << 4)) = packed;
+  } else {
+    uint32_t w[8];
+    quant_row4_32(v, mag, w, scale);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      v4i packed;
+      for (int i = 0; i < 4; ++i) packed[i] = (int)w[4 * h + i];
+      *reinterpret_cast<v4i*>(row + (((2 * qsub + h) ^ (qm & 7)) << 4)) = packed;
+    }
+  }
+  if (qsub == 0) scales[qm] = scale;
+}
+
+// ---------------------------------------------------------------------------
 // Decode GEMM with the group-128 act-quant inside it (fp8b_act_quant_matmul
 // on decode plans, M <= 32): gemm_decode_kernel's grid, K split and fold,
 // with the activations read as bf16. The waves split the work: waves 0-3
@@ -1923,37 +1981,14 @@ __global__ void __launch_bounds__(512) gemm_decode_quant_kernel(GemmArgs a) {
   const int per_kb = mfma_wave ? 4 : QLOADS;
   auto wait_after = [&](int n_after) { wait_vmcnt_rt(min(n_after * per_kb, 15)); };
 
-  // Quantiser: this lane's bf16 values of a row (read from LDS), and their
-  // codes into slab `buf` with the group scale beside it.
-  v4i raw[QE / 8];
-  auto read_rows = [&](const uint8_t* src) {
-#pragma unroll
-    for (int i = 0; i < QE / 8; ++i)
-      raw[i] = *reinterpret_cast<const v4i*>(src + qm * 256 + qsub * (QE * 2) + i * 16);
-  };
+  // Quantiser: this lane's bf16 values of a row (read from LDS into
+  // registers), and their codes into slab `buf` with the group scale beside
+  // it.
+  QuantRaw<QE> raw;
+  auto read_rows = [&](const uint8_t* src) { raw = quant_load<QE>(src, qm, qsub); };
   auto quantise = [&](int buf) {
-    uint8_t* qs = smem + Q_OFF + buf * (AR * 128);
-    float scale;
-    if constexpr (QE == 8) {
-      float v[8];
-      const uint32_t mag = unpack_bf16x8(raw[0], v);
-      uint32_t w0, w1;
-      quant_row16_8(v, mag, w0, w1, scale);
-      v2i packed;
-      packed[0] = (int)w0;
-      packed[1] = (int)w1;
-      *reinterpret_cast<v2i*>(qs + qm * 128 + (((qsub >> 1) ^ (qm & 7)) << 4) + (qsub & 1) * 8) =
-          packed;
-    } else {
-      float v[16];
-      const uint32_t mag = max(unpack_bf16x8(raw[0], v), unpack_bf16x8(raw[1], v + 8));
-      uint32_t w[4];
-      quant_row8_16(v, mag, w, scale);
-      v4i packed;
-      for (int i = 0; i < 4; ++i) packed[i] = (int)w[i];
-      *reinterpret_cast<v4i*>(qs + qm * 128 + ((qsub ^ (qm & 7)) << 4)) = packed;
-    }
-    if (qsub == 0) reinterpret_cast<float*>(smem + S_OFF + buf * (AR * 4))[qm] = scale;
+    quant_codes<QE>(raw, qm, qsub, smem + Q_OFF + buf * (AR * 128),
+                    reinterpret_cast<float*>(smem + S_OFF + buf * (AR * 4)));
   };
 
   // MFMA waves: fragment offsets of weight rows 32w + 16j + (lane & 15) and
@@ -2219,30 +2254,7 @@ __global__ void __launch_bounds__(512) gemm_skinny_quant_kernel(GemmArgs a) {
   uint8_t* qb = &qbuf[wid][0];
   float* qs = reinterpret_cast<float*>(qb + 16 * 128);
   auto quantise = [&](const uint8_t* sl) {
-    float scale;
-    if constexpr (QE == 8) {
-      const v4i raw = *reinterpret_cast<const v4i*>(sl + X_OFF + qm * 256 + qsub * 16);
-      float v[8];
-      const uint32_t mag = unpack_bf16x8(raw, v);
-      uint32_t w0, w1;
-      quant_row16_8(v, mag, w0, w1, scale);
-      v2i packed;
-      packed[0] = (int)w0;
-      packed[1] = (int)w1;
-      *reinterpret_cast<v2i*>(qb + qm * 128 + (((qsub >> 1) ^ (qm & 7)) << 4) + (qsub & 1) * 8) =
-          packed;
-    } else {
-      const v4i raw0 = *reinterpret_cast<const v4i*>(sl + X_OFF + qm * 256 + qsub * 32);
-      const v4i raw1 = *reinterpret_cast<const v4i*>(sl + X_OFF + qm * 256 + qsub * 32 + 16);
-      float v[16];
-      const uint32_t mag = max(unpack_bf16x8(raw0, v), unpack_bf16x8(raw1, v + 8));
-      uint32_t w[4];
-      quant_row8_16(v, mag, w, scale);
-      v4i packed;
-      for (int i = 0; i < 4; ++i) packed[i] = (int)w[i];
-      *reinterpret_cast<v4i*>(qb + qm * 128 + ((qsub ^ (qm & 7)) << 4)) = packed;
-    }
-    if (qsub == 0) qs[qm] = scale;
+    quant_codes<QE>(quant_load<QE>(sl + X_OFF, qm, qsub), qm, qsub, qb, qs);
   };
 
   const int c0 = 2 * (lane >> 4);
@@ -2464,16 +2476,16 @@ __global__ void __launch_bounds__(64 * NW) gemm_tiny_kernel(GemmArgs a) {
 
 // ---------------------------------------------------------------------------
 // Small-grid GEMM with the group-128 act-quant inside it
-// (fp8b_act_quant_matmul on small-grid plans of 32-row tiles, M <= QR <= 8):
-// gemm_tiny_kernel<2, FN, NW, 2>'s grid, K ranges, fold and wave-order sum
-// for the first 16 rows of the tile (rows 8..31 do not exist). Each wave's
+// (fp8b_act_quant_matmul on small-grid plans of 32-row tiles, M <= QR <= 16):
+// gemm_tiny_kernel's grid, K ranges, fold and wave-order sum for the first
+// 16 rows of the tile (rows 16..31 do not exist). Each wave's
 // ring slots carry its TN weight rows (chunk-swizzled), the QR bf16
 // activation rows (unswizzled) and the weight block's scale, and the wave
 // quantises a slot's rows (one task of 2*QR values per lane, the
-// act-quant's arithmetic) into its own fragment and scale buffers right
-// before that slot's MFMAs (LDS operations of one wave complete in order).
-// Same codes, scales and sums as act-quant followed by gemm_tiny_kernel, so
-// the same output bits.
+// act-quant's arithmetic: quant_codes) into its own fragment and scale
+// buffers right before that slot's MFMAs (LDS operations of one wave
+// complete in order). Same codes, scales and sums as act-quant followed by
+// gemm_tiny_kernel, so the same output bits.
 // Preconditions (checked by the host): M <= QR, x 16-byte aligned with a row
 // stride (a.lda, in bytes) that is a multiple of 16; a.tiles_m = 1.
 // ---------------------------------------------------------------------------
@@ -2488,7 +2500,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_tiny_quant_kernel(GemmArgs a) {
   constexpr int S_OFF = X_OFF + QR * 256;      // the weight block's scale
   constexpr int SLOT = S_OFF + 64;
   constexpr int PER_KB = WLOADS + XLOADS + 1;  // DMA instructions per K-block
-  static_assert(QR == 4 || QR == 8, "4 or 8 activation rows");
+  static_assert(QR == 4 || QR == 8 || QR == 16, "4, 8 or 16 activation rows");
   static_assert(NW == 1 || NS * SLOT >= FN * 4 * 64 * 4, "partials reuse the ring");
   __shared__ __attribute__((aligned(1024))) uint8_t ring[NW][NS][SLOT];
   __shared__ __attribute__((aligned(1024))) uint8_t qbuf[NW][16 * 128 + 64];
@@ -2526,30 +2538,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_tiny_quant_kernel(GemmArgs a) {
   uint8_t* qb = &qbuf[wid][0];
   float* qs = reinterpret_cast<float*>(qb + 16 * 128);
   auto quantise = [&](const uint8_t* sl) {
-    float scale;
-    if constexpr (QE == 8) {
-      const v4i raw = *reinterpret_cast<const v4i*>(sl + X_OFF + qm * 256 + qsub * 16);
-      float v[8];
-      const uint32_t mag = unpack_bf16x8(raw, v);
-      uint32_t w0, w1;
-      quant_row16_8(v, mag, w0, w1, scale);
-      v2i packed;
-      packed[0] = (int)w0;
-      packed[1] = (int)w1;
-      *reinterpret_cast<v2i*>(qb + qm * 128 + (((qsub >> 1) ^ (qm & 7)) << 4) + (qsub & 1) * 8) =
-          packed;
-    } else {
-      const v4i raw0 = *reinterpret_cast<const v4i*>(sl + X_OFF + qm * 256 + qsub * 32);
-      const v4i raw1 = *reinterpret_cast<const v4i*>(sl + X_OFF + qm * 256 + qsub * 32 + 16);
-      float v[16];
-      const uint32_t mag = max(unpack_bf16x8(raw0, v), unpack_bf16x8(raw1, v + 8));
-      uint32_t w[4];
-      quant_row8_16(v, mag, w, scale);
-      v4i packed;
-      for (int i = 0; i < 4; ++i) packed[i] = (int)w[i];
-      *reinterpret_cast<v4i*>(qb + qm * 128 + ((qsub ^ (qm & 7)) << 4)) = packed;
-    }
-    if (qsub == 0) qs[qm] = scale;
+    quant_codes<QE>(quant_load<QE>(sl + X_OFF, qm, qsub), qm, qsub, qb, qs);
   };
 
   const int row = lane & 15, c0 = 2 * (lane >> 4), r7 = row & 7;
@@ -3454,11 +3443,18 @@ bool skinny_quant_ok(const Dispatch& d, const void* x, int64_t ldx, int64_t M) {
 }
 
 // ... and gemm_tiny_quant_kernel when the plan is one small grid of 32x16 or
-// 32x32 tiles (no tail launch), M <= 8 and the rows are 16-byte aligned.
-bool tiny_quant_ok(const Dispatch& d, const void* x, int64_t ldx, int64_t M) {
+// 32x32 tiles (no tail launch) and the rows are 16-byte aligned, for M <= 8,
+// or M <= 16 with at most 4 K-blocks per wave: a wave quantises 16 rows in
+// ~200 VALU instructions per K-block, which pays for the saved launch only
+// over a short K range (12x8192x2048, 2 K-blocks per wave: 7.2 against
+// 8.9 us; 16x4096x4096, 4: 8.5 against 8.8; 16x14336x4096, 8: 16.8 against
+// 16.3; 16x28672x4096, 16: level). Measured the same way, the skinny kernel
+// with 16 rows lost (9x2048x8192: 11.9 against 9.7 us).
+bool tiny_quant_ok(const Dispatch& d, const void* x, int64_t ldx, int64_t M, int64_t K) {
+  const int64_t kb_per_wave = (K / 128 + d.waves - 1) / d.waves;
   return use_fused_decode() && d.kernel == FP8B_KERNEL_TINY && d.tail_kernel == FP8B_KERNEL_NONE &&
-         d.bm == 32 && (d.bn == 16 || d.bn == 32) && M <= 8 && ((uintptr_t)x & 15) == 0 &&
-         ldx % 8 == 0;
+         d.bm == 32 && (d.bn == 16 || d.bn == 32) && (M <= 8 || (M <= 16 && kb_per_wave <= 4)) &&
+         ((uintptr_t)x & 15) == 0 && ldx % 8 == 0;
 }
 
 // fp8b_act_quant_matmul takes gemm_decode_quant_kernel when the plan is the
@@ -3641,7 +3637,7 @@ extern "C" int fp8b_act_quant_matmul_plan(int64_t M, int64_t N, int64_t K, int c
     plan->ring = decode_quant_ring(M);
   } else if (skinny_quant_ok(d, nullptr, K, M)) {
     plan->kernel = FP8B_KERNEL_SKINNY_QUANT;
-  } else if (tiny_quant_ok(d, nullptr, K, M)) {
+  } else if (tiny_quant_ok(d, nullptr, K, M, K)) {
     plan->kernel = FP8B_KERNEL_TINY_QUANT;
   }
   plan->workspace_bytes = fp8b_act_quant_matmul_workspace_size(M, N, K);
@@ -3898,7 +3894,7 @@ extern "C" int fp8b_act_quant_matmul(const void* x, int64_t ldx, const void* B, 
   const Dispatch d = resolve(M, N, K, 128, 128, device_cu_count(),
                              call_operands(q, K, B, ldb, s, KB, 1, Bs, bs_sn, bs_sk, M, N, K,
                                            128, 128));
-  if (skinny_quant_ok(d, x, ldx, M) || tiny_quant_ok(d, x, ldx, M)) {
+  if (skinny_quant_ok(d, x, ldx, M) || tiny_quant_ok(d, x, ldx, M, K)) {
     hipStream_t st = (hipStream_t)stream;
     GemmArgs a;
     a.A = (const uint8_t*)x; a.B = (const uint8_t*)B; a.As = nullptr; a.Bs = Bs; a.C = C;
@@ -3916,7 +3912,8 @@ extern "C" int fp8b_act_quant_matmul(const void* x, int64_t ldx, const void* B, 
                            : (ldc % 8 == 0 && ((uintptr_t)C & 15) == 0);
     if (d.kernel == FP8B_KERNEL_TINY) {
       if (M <= 4) launch_tiny_quant<4>(a, d.bn, d.waves, d.grid, st);
-      else launch_tiny_quant<8>(a, d.bn, d.waves, d.grid, st);
+      else if (M <= 8) launch_tiny_quant<8>(a, d.bn, d.waves, d.grid, st);
+      else launch_tiny_quant<16>(a, d.bn, d.waves, d.grid, st);
     } else if (M <= 4) {
       gemm_skinny_quant_kernel<4><<<(unsigned)d.grid, 512, 0, st>>>(a);
     } else {

@@ -73,6 +73,14 @@ __device__ __forceinline__ uint32_t row16_max_u32(uint32_t v) {
   return v;
 }
 
+// Max over the 4 lanes of each DPP quad (lanes 4q..4q+3) of an unsigned
+// value; every lane of the quad receives the result.
+__device__ __forceinline__ uint32_t row4_max_u32(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+  return v;
+}
+
 // Max over the 8 lanes of each DPP half-row (lanes 8h..8h+7) of an unsigned
 // value; every lane of the half-row receives the result.
 __device__ __forceinline__ uint32_t row8_max_u32(uint32_t v) {

@@ -123,6 +123,26 @@ __device__ __forceinline__ void quant_row8_16(const float v[16], uint32_t mag, u
   }
 }
 
+// Quantise 32 values held by one lane of a 4-lane group of 128 (a DPP
+// quad): the arithmetic of quant_row16_8 on four times the values per lane.
+// `mag` is the max over this lane's 32 bf16 magnitude patterns; w[0..7] are
+// the 32 codes, little-endian.
+__device__ __forceinline__ void quant_row4_32(const float v[32], uint32_t mag, uint32_t w[8],
+                                              float& scale) {
+  const uint32_t gmag = row4_max_u32(mag);
+  if (gmag < 0x7F80u) {
+    const float amax = fmaxf(bf16_to_f32(gmag), kAmaxFloor);
+    scale = scale_from_amax(amax);
+    const float recip = recip_of_scale(scale);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) quant8_finite(v + 8 * i, scale, recip, w[2 * i], w[2 * i + 1]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      quant8_nonfinite(v + 8 * i, gmag > 0x7F80u, w[2 * i], w[2 * i + 1], scale);
+  }
+}
+
 // Max over the 8 bf16 magnitude patterns of one 16-byte load: sign bits
 // cleared, then packed 16-bit maxima (v_pk_max_u16).
 __device__ __forceinline__ uint32_t max_mag_bf16x8(const v4i raw) {

@@ -139,7 +139,7 @@ typedef enum fp8b_kernel {
   FP8B_KERNEL_BS128 = 9,        /* two-stage 128x128 / 256x256 tiles (FP8B_PIPE=0, huge leading dims) */
   FP8B_KERNEL_DECODE_QUANT = 10, /* fp8b_act_quant_matmul, M <= 32: act-quant inside the decode kernel */
   FP8B_KERNEL_SKINNY_QUANT = 11, /* fp8b_act_quant_matmul, M <= 8: act-quant inside the skinny kernel */
-  FP8B_KERNEL_TINY_QUANT = 12    /* fp8b_act_quant_matmul, M <= 8: act-quant inside the small-grid kernel */
+  FP8B_KERNEL_TINY_QUANT = 12    /* fp8b_act_quant_matmul, M <= 8 (16 on short K): act-quant inside the small-grid kernel */
 } fp8b_kernel;
 
 /* What fp8b_w8a8_block_matmul launches for one call. */
@@ -209,7 +209,8 @@ int fp8b_w8a8_block_matmul_noalloc(const void* A, int64_t lda,
  * with the Helion kernel of
  * finegrained-fp8-helion/torch-ext/finegrained_fp8_helion/fp8.py:19-39 (the
  * act-quant-into-the-GEMM step for small M). On decode plans with M <= 32
- * and skinny or small-grid plans with M <= 8 (fp8b_act_quant_matmul_plan
+ * and skinny or small-grid plans with M <= 8 (small grids: M <= 16 with at
+ * most 4 K-blocks per wave) (fp8b_act_quant_matmul_plan
  * reports FP8B_KERNEL_DECODE_QUANT / _SKINNY_QUANT / _TINY_QUANT), with x 16-byte
  * aligned and ldx % 8 == 0, one GEMM kernel reads the bf16 rows and
  * quantises them itself (plus the split-K sum when the plan splits K);

@@ -79,10 +79,12 @@ SKINNY_ONE_KERNEL = [(1, 4096, 14336), (3, 1000, 1024), (4, 4096, 4096), (5, 204
 
 
 # Shapes whose plan is the small-grid one-kernel path (gemm_tiny_quant_kernel,
-# M <= 8, 32-row tiles): 8, 4 and 2 waves per tile, one K-block, ragged last
-# 32-column tiles, 4- and 8-row forms.
+# M <= 8, or up to 16 rows with at most 4 K-blocks per wave; 32-row tiles):
+# 8, 4 and 2 waves per tile, one K-block, ragged last 32-column tiles,
+# 32x16 tiles, 4-, 8- and 16-row forms.
 TINY_ONE_KERNEL = [(1, 8192, 128), (3, 8704, 1024), (1, 20992, 4096), (6, 28672, 4096),
-                   (8, 14336, 2048), (5, 8200, 512), (7, 9000, 640)]
+                   (8, 14336, 2048), (5, 8200, 512), (7, 9000, 640), (12, 8192, 2048),
+                   (16, 4096, 4096), (13, 8200, 1024)]
 
 
 def _one_kernel(M, N, K, kernel="gemm_decode_quant_kernel"):

@@ -111,7 +111,8 @@ def test_gate_up_plans(M, I, K, kernel, tile_m):
     (8, 4096, 4096, "gemm_skinny_quant_kernel", 1, 0),
     (9, 2048, 8192, "gemm_skinny_kernel", 1, 0),           # 9+ rows: two launches
     (1, 28672, 4096, "gemm_tiny_quant_kernel", 1, 0),      # small-grid plans, M <= 8
-    (9, 28672, 4096, "gemm_tiny_kernel", 1, 0),
+    (9, 28672, 4096, "gemm_tiny_kernel", 1, 0),            # 9+ rows, 16 K-blocks per wave
+    (12, 8192, 2048, "gemm_tiny_quant_kernel", 1, 0),      # 9..16 rows, 2 K-blocks per wave
     (24, 7168, 8192, "gemm_decode_quant_kernel", 4, 3),
     (33, 4096, 14336, "gemm_decode_kernel", 8, 4),         # 17+ rows of fragments: two launches
     (64, 4096, 14336, "gemm_decode_kernel", 8, 4),
@@ -120,9 +121,10 @@ def test_gate_up_plans(M, I, K, kernel, tile_m):
 def test_act_quant_matmul_plans(M, N, K, kernel, splits, ring):
     """act_quant_w8a8_block_fp8_matmul runs one kernel (act-quant inside the
     GEMM) exactly where the GEMM plan is the one-workgroup-per-CU decode grid
-    and M <= 32, or the skinny or small grid and M <= 8, with that plan's K
-    split, so its result bits equal act-quant + GEMM; elsewhere the GEMM of
-    the two-launch path."""
+    and M <= 32, the skinny grid and M <= 8, or the small grid and M <= 8
+    (M <= 16 with at most 4 K-blocks per wave), with that plan's K split, so
+    its result bits equal act-quant + GEMM; elsewhere the GEMM of the
+    two-launch path."""
     p = _native.act_quant_matmul_plan(M, N, K, cu_count=CUS)
     g = plan(M, N, K)
     assert (p["kernel"], p["splits"], p["ring"]) == (kernel, splits, ring), p
