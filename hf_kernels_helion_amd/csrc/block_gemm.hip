@@ -2629,6 +2629,45 @@ splitk_reduce_kernel(GemmArgs a, int splits) {
   store4(a, m, n, s, false, 0);
 }
 
+// The same sum for the decode grids whose column-tile count is a multiple of
+// 8: workgroup (x, z) of the decode grid runs on XCD x % 8 for every split z
+// (workgroups go round-robin over the 8 XCDs), so the partials of column
+// tile x sit in that XCD's L2. Block b here runs on XCD b % 8 and sums 8
+// rows of a column tile of that XCD: tile x = b % 8 + 8 * ((b / 8) %
+// (tiles_n / 8)), rows 8 * (b / tiles_n) ..; thread t takes row + t / 32,
+// columns 4 * (t % 32) .. of the tile. Placement only changes where the
+// loads hit; the sum and its order are splitk_reduce_kernel's.
+__global__ void __launch_bounds__(256)
+splitk_reduce_xcd_kernel(GemmArgs a, int splits) {
+  const int b = (int)blockIdx.x;
+  const int x = (b & 7) + 8 * ((b >> 3) % (a.tiles_n >> 3));
+  const int m = 8 * (b / a.tiles_n) + (int)(threadIdx.x >> 5);
+  const int n = x * 128 + 4 * (int)(threadIdx.x & 31);
+  if (m >= a.M || n >= a.N) return;
+  v4f s = {0.f, 0.f, 0.f, 0.f};
+  const int64_t plane = (int64_t)a.M * a.N;
+  const float* p = a.ws + (int64_t)m * a.N + n;
+  const bool vec = n + 3 < a.N && a.vec_store;
+  for (int z0 = 0; z0 < splits; z0 += 8) {
+    v4f v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int z = z0 + u;
+      if (z < splits) {
+        if (vec) {
+          v[u] = *reinterpret_cast<const v4f*>(p + z * plane);
+        } else {
+          for (int r = 0; r < 4; ++r) v[u][r] = (n + r < a.N) ? p[z * plane + r] : 0.f;
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (z0 + u < splits) s += v[u];
+  }
+  store4(a, m, n, s, false, 0);
+}
+
 // Generic SIMT kernel: 32x32 outputs per 256-thread block, 2x2 per thread.
 // For each K-block: part = sum_k A*B over the block (fp32 FMA chain in k
 // order), then acc += part * As * Bs, as in fp8.py:31-37.
@@ -2766,7 +2805,8 @@ int device_cu_count() {
 //   FP8B_TILE256X128=0  no 256x128 tiles;
 //   FP8B_FUSED_DECODE=0 fp8b_act_quant_matmul runs act-quant and the GEMM as
 //                   two kernels on decode, skinny and small-grid plans too;
-//   FP8B_TINY16=0   M <= 16 small grids run the 32-row tiles whole.
+//   FP8B_TINY16=0   M <= 16 small grids run the 32-row tiles whole;
+//   FP8B_REDUCE_XCD=0  split-K sums of decode grids in row order.
 bool env_flag_on(const char* name) {
   const char* e = getenv(name);
   return !(e && e[0] == '0');
@@ -2801,6 +2841,10 @@ bool use_tile256x128() {
 }
 bool use_tiny16() {
   static const bool v = env_flag_on("FP8B_TINY16");
+  return v;
+}
+bool use_reduce_xcd() {
+  static const bool v = env_flag_on("FP8B_REDUCE_XCD");
   return v;
 }
 bool use_fused_decode() {
@@ -3422,6 +3466,20 @@ void launch_decode(const GemmArgs& a, int M, int ring, int splits, hipStream_t s
   }
 }
 
+// The split-K sum of a call's partials (a.ws, splits planes of M x N): on
+// decode grids whose column-tile count is a multiple of 8 the XCD-local
+// form (32x4096x14336: act-quant GEMM step 17.0 against 17.4 us, the plain
+// GEMM 16.2 against 16.4), else one thread per 4 outputs in row order.
+void launch_splitk_reduce(const GemmArgs& a, const Dispatch& d, hipStream_t st) {
+  if (d.kernel == FP8B_KERNEL_DECODE && a.tiles_n % 8 == 0 && use_reduce_xcd()) {
+    const int64_t blocks = (int64_t)a.tiles_n * ((a.M + 7) / 8);
+    splitk_reduce_xcd_kernel<<<(unsigned)blocks, 256, 0, st>>>(a, d.splits);
+    return;
+  }
+  const int64_t quads = (int64_t)a.M * ((a.N + 3) / 4);
+  splitk_reduce_kernel<<<(unsigned)((quads + 255) / 256), 256, 0, st>>>(a, d.splits);
+}
+
 // gemm_decode_quant_kernel: the quantiser takes 8 values per lane for 16
 // rows and 16 for 32 (four waves either way). LDS stages of 16 KiB of weights
 // plus 16*FM bf16 rows, by measured step time (graph-replayed, bit-identical
@@ -3739,8 +3797,7 @@ extern "C" int fp8b_w8a8_block_matmul(const void* A, int64_t lda, const void* B,
   if (d.splits > 1) {
     GemmArgs r = a;
     r.vec_store = (ws_vec && c_vec) ? 1 : 0;
-    const int64_t quads = M * ((N + 3) / 4);
-    splitk_reduce_kernel<<<(unsigned)((quads + 255) / 256), 256, 0, st>>>(r, d.splits);
+    launch_splitk_reduce(r, d, st);
     if (hipGetLastError() != hipSuccess) {
       set_error("fp8b_w8a8_block_matmul: split-K reduce launch failed");
       return FP8B_ERR_LAUNCH;
@@ -3951,8 +4008,7 @@ extern "C" int fp8b_act_quant_matmul(const void* x, int64_t ldx, const void* B, 
     if (d.splits > 1) {
       GemmArgs r = a;
       r.vec_store = (ws_vec && c_vec) ? 1 : 0;
-      const int64_t quads = M * ((N + 3) / 4);
-      splitk_reduce_kernel<<<(unsigned)((quads + 255) / 256), 256, 0, st>>>(r, d.splits);
+      launch_splitk_reduce(r, d, st);
       if (hipGetLastError() != hipSuccess) {
         set_error("fp8b_act_quant_matmul: split-K reduce launch failed");
         return FP8B_ERR_LAUNCH;

@@ -160,7 +160,8 @@ def test_gemm_decode_shape(N, dev):
                                           (8, 18432, 8192, 1), (32, 28672, 4096, 1),
                                           (24, 9216, 11264, 3), (48, 28672, 2048, 1),
                                           (48, 16384, 4096, 2), (1, 28672, 2048, 1),
-                                          (16, 32768, 1536, 1)])
+                                          (16, 32768, 1536, 1), (20, 4000, 14336, 8),
+                                          (33, 4096, 14336, 8), (13, 8100, 8192, 4)])
 def test_gemm_decode_split_plans(M, N, K, splits, dev):
     """The decode plan's split counts: as many splits as keep one workgroup
     per CU (56 column tiles x 4; 144 and 224 tiles unsplit, no sum kernel;
@@ -168,8 +169,11 @@ def test_gemm_decode_split_plans(M, N, K, splits, dev):
     ring two workgroups per CU, where that would leave 32 K-blocks per split
     (100 tiles x 3: 300 workgroups); 17..48 rows on 224 and 128 column tiles,
     and 1..16 rows on more than 128 with short K, take it over the
-    small-grid kernel. Every element against torch's fp32
-    dequant-matmul, sampled rows against the oracle."""
+    small-grid kernel. Split sums over column-tile counts that are
+    multiples of 8 run XCD-local (rows past M in a block of 8, a ragged last
+    column tile: 20x4000, 33x4096, 13x8100), the others in row order. Every
+    element against torch's fp32 dequant-matmul, sampled rows against the
+    oracle."""
     from hf_kernels_helion_amd import _native
     print(f"gemm decode split plan M={M} N={N} K={K} splits={splits}", flush=True)
     ws = _native.load().fp8b_gemm_workspace_size(M, N, K, 128, 128)
