@@ -49,7 +49,7 @@ def parse():
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--only", default=None,
                    help="profile helper: run only one workload "
-                        "(gemm|act_quant|decode|decode_graph|decode_graph_two_op|decode_fused|"
+                        "(gemm|act_quant|decode|decode_graph[_m1|_m1_wide][_two_op]|decode_fused|"
                         "weight_quant|"
                         "weight_quant_bf16|mlp|"
                         "mlp_il|mlp_gateup|"
@@ -383,7 +383,7 @@ def secondary(torch, fp8, synthetic, dev):
         return [fp8.act_quant_w8a8_block_fp8_matmul(xd, ws_[i][0], ws_[i][1], [128, 128],
                                                     torch.bfloat16) for i in range(5)]
 
-    def graph_time(fn):
+    def graph_time(fn, ref):
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
@@ -395,14 +395,16 @@ def secondary(torch, fp8, synthetic, dev):
             gouts = fn()
         for _ in range(2):  # every replay equals the eager two-op result
             graph.replay()
-            eager = dec_two_op()
+            eager = ref()
             torch.cuda.synchronize()
             assert all(torch.equal(x_, y_) for x_, y_ in zip(gouts, eager)), "replay differs"
-        t = time_events(graph.replay, 20, 5, torch) / 5
+        # 200 replays (1000 steps) after 40: the step time at a steady clock
+        # (100 steps after 5 replays read ~0.7 us higher), ~20 ms of GPU time
+        t = time_events(graph.replay, 200, 40, torch) / 5
         del graph, gouts
         return t
-    ms_two = graph_time(dec_two_op)
-    ms = graph_time(dec_fused)
+    ms_two = graph_time(dec_two_op, dec_two_op)
+    ms = graph_time(dec_fused, dec_two_op)
     byt = 2.0 * M * K + N * K + 4.0 * (N // 128) * (K // 128) + 2.0 * M * N
     res["decode_32x4096x14336"] = {"us": round(ms * 1e3, 2), "GB/s": round(byt / ms / 1e6, 1),
                                    "pct_hbm_peak": round(100 * byt / ms / 1e6 / PEAK_HBM_GBS, 1),
@@ -414,6 +416,33 @@ def secondary(torch, fp8, synthetic, dev):
                                                "the GEMM; HIP-graph replay of 5 steps over 5 "
                                                "weight copies"}
     log(f"decode: {res['decode_32x4096x14336']}")
+
+    # The same weights at one activation row (batch-1 decode): the op runs the
+    # skinny GEMM with the act-quant inside it; act_quant then the GEMM beside.
+    x1 = _gpu_acts(1, K, 31, dev, torch)
+
+    def one_fused():
+        return [fp8.act_quant_w8a8_block_fp8_matmul(x1, ws_[i][0], ws_[i][1], [128, 128],
+                                                    torch.bfloat16) for i in range(5)]
+
+    def one_two_op():
+        outs = []
+        for i in range(5):
+            q, s = fp8.act_quant(x1, 128)
+            outs.append(fp8.w8a8_block_fp8_matmul(q, ws_[i][0], s, ws_[i][1], [128, 128],
+                                                  torch.bfloat16))
+        return outs
+    ms1 = graph_time(one_fused, one_two_op)
+    ms1_two = graph_time(one_two_op, one_two_op)
+    byt1 = 2.0 * K + N * K + 4.0 * (N // 128) * (K // 128) + 2.0 * N
+    res["decode_1x4096x14336"] = {"us": round(ms1 * 1e3, 2),
+                                  "GB/s": round(byt1 / ms1 / 1e6, 1),
+                                  "pct_hbm_peak": round(100 * byt1 / ms1 / 1e6 / PEAK_HBM_GBS, 1),
+                                  "two_op_us": round(ms1_two * 1e3, 2),
+                                  "includes": "one activation row, quantised in-op (one kernel); "
+                                              "two_op_us = act_quant then the GEMM; HIP-graph "
+                                              "replay of 5 steps over the same 5 weight copies"}
+    log(f"decode M=1: {res['decode_1x4096x14336']}")
     del ws_
 
     for name, (M, N, K) in {"medium_2048x2048x4096": (2048, 2048, 4096),
@@ -589,17 +618,27 @@ def run_only(what, steps, warmup, torch, fp8, synthetic, dev):
         else:
             W, Bs = _gpu_weights(N, K, 40, dev, torch, synthetic)
             fn = lambda: fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [128, 128], torch.bfloat16)
-    elif what in ("decode_graph", "decode_graph_two_op"):
+    elif what.startswith("decode_graph"):
         # the bench leg's decode step (five weight copies) as a HIP graph of
         # five steps, replayed --steps times: the in-op quantising op
         # (one kernel + split-K sum), or act_quant then the GEMM
-        M, N, K = 32, 4096, 14336
+        # (decode_graph[_two_op]); the same at one row
+        # (decode_graph_m1[_two_op], 1x4096x14336: the skinny one-kernel
+        # path) and at one row of a gate/up projection
+        # (decode_graph_m1_wide[_two_op], 1x28672x4096: the small-grid one)
+        two_op = what.endswith("_two_op")
+        base = what[:-len("_two_op")] if two_op else what
+        shapes_ = {"decode_graph": (32, 4096, 14336), "decode_graph_m1": (1, 4096, 14336),
+                   "decode_graph_m1_wide": (1, 28672, 4096)}
+        if base not in shapes_:
+            raise SystemExit(f"unknown --only {what}")
+        M, N, K = shapes_[base]
         ws_ = [_gpu_weights(N, K, 20 + i, dev, torch, synthetic) for i in range(5)]
         xd = _gpu_acts(M, K, 30, dev, torch)
 
         def five():
             for i in range(5):
-                if what == "decode_graph":
+                if not two_op:
                     fp8.act_quant_w8a8_block_fp8_matmul(xd, ws_[i][0], ws_[i][1], [128, 128],
                                                         torch.bfloat16)
                     continue
