@@ -3314,8 +3314,8 @@ void resolve_pipe128(Dispatch& d, int64_t tiles, int tail, int cus) {
 }
 
 // The launches of one GEMM call (see Dispatch) on a device with `cus` CUs.
-Dispatch resolve(int64_t M, int64_t N, int64_t K, int64_t block_n, int64_t block_k, int cus,
-                 const Operands& o) {
+Dispatch resolve_uncached(int64_t M, int64_t N, int64_t K, int64_t block_n, int64_t block_k,
+                          int cus, const Operands& o) {
   Dispatch d;
   const bool per_row = block_n == 1 && block_k == 128;
   d.per_row = per_row;
@@ -3409,6 +3409,34 @@ Dispatch resolve(int64_t M, int64_t N, int64_t K, int64_t block_n, int64_t block
       }
       break;
   }
+  return d;
+}
+
+// resolve() behind a per-thread cache of the last plans: the planner costs
+// ~1-2 us of host time per call (the cost model prices every tile shape),
+// as much as the rest of a small eager call. The key is everything the plan
+// depends on (the environment switches are read once per process); 64
+// direct-mapped entries, no locking, no allocation.
+Dispatch resolve(int64_t M, int64_t N, int64_t K, int64_t block_n, int64_t block_k, int cus,
+                 const Operands& o) {
+  struct Entry {
+    int64_t M = -1, N, K, bn, bk, lda, ldb;
+    int cus;
+    bool mfma, scales;
+    Dispatch d;
+  };
+  thread_local Entry cache[64];
+  uint64_t h = (uint64_t)M * 0x9E3779B97F4A7C15ull ^ (uint64_t)N * 0xC2B2AE3D27D4EB4Full ^
+               (uint64_t)K * 0x165667B19E3779F9ull ^ (uint64_t)block_n * 31 ^ (uint64_t)block_k ^
+               (uint64_t)o.lda * 0x27D4EB2F165667C5ull ^ (uint64_t)o.ldb * 0x85EBCA77C2B2AE63ull ^
+               (uint64_t)cus << 7 ^ (uint64_t)o.mfma << 1 ^ (uint64_t)o.scales;
+  Entry& e = cache[(h ^ (h >> 29)) & 63];
+  if (e.M == M && e.N == N && e.K == K && e.bn == block_n && e.bk == block_k && e.lda == o.lda &&
+      e.ldb == o.ldb && e.cus == cus && e.mfma == o.mfma && e.scales == o.scales)
+    return e.d;
+  const Dispatch d = resolve_uncached(M, N, K, block_n, block_k, cus, o);
+  e.M = M; e.N = N; e.K = K; e.bn = block_n; e.bk = block_k; e.lda = o.lda; e.ldb = o.ldb;
+  e.cus = cus; e.mfma = o.mfma; e.scales = o.scales; e.d = d;
   return d;
 }
 
