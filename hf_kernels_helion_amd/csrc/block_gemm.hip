@@ -3979,23 +3979,30 @@ extern "C" int fp8b_act_quant_matmul(const void* x, int64_t ldx, const void* B, 
   const Dispatch d = resolve(M, N, K, 128, 128, device_cu_count(),
                              call_operands(q, K, B, ldb, s, KB, 1, Bs, bs_sn, bs_sk, M, N, K,
                                            128, 128));
-  if (skinny_quant_ok(d, x, ldx, M) || tiny_quant_ok(d, x, ldx, M, K)) {
+  const bool small_m = skinny_quant_ok(d, x, ldx, M) || tiny_quant_ok(d, x, ldx, M, K);
+  if (small_m || fused_decode_ok(d, x, ldx, ldb, M)) {
+    // One kernel reads the bf16 rows (a.A, row stride a.lda in bytes) and
+    // quantises them itself; decode plans write split-K partials to the
+    // workspace and sum them after.
     hipStream_t st = (hipStream_t)stream;
     GemmArgs a;
     a.A = (const uint8_t*)x; a.B = (const uint8_t*)B; a.As = nullptr; a.Bs = Bs; a.C = C;
-    a.ws = nullptr;
+    a.ws = small_m ? nullptr : (float*)workspace;
     a.lda = 2 * ldx; a.ldb = ldb; a.as_sm = 0; a.as_sk = 0; a.bs_sn = bs_sn; a.bs_sk = bs_sk;
     a.ldc = ldc; a.M = (int)M; a.N = (int)N; a.K = (int)K; a.KB = (int)KB;
-    a.kb_per_split = (int)KB;
+    a.kb_per_split = small_m ? (int)KB : d.kb_per_split;
     a.tiles_m = 1; a.tiles_n = (int)((N + d.bn - 1) / d.bn);
     a.out_dtype = out_dtype;
     a.rem_base = -1; a.rem_tiles_m = 0; a.rem_tiles_n = 0;
     a.Sq = nullptr; a.sq_sm = 0; a.sq_sg = 0;
     a.win4 = 1;
-    const size_t esz = out_dtype == FP8B_F32 ? 4 : 2;
-    a.vec_store = esz == 4 ? (ldc % 4 == 0 && ((uintptr_t)C & 15) == 0)
-                           : (ldc % 8 == 0 && ((uintptr_t)C & 15) == 0);
-    if (d.kernel == FP8B_KERNEL_TINY) {
+    const bool c_vec = out_dtype == FP8B_F32 ? (ldc % 4 == 0 && ((uintptr_t)C & 15) == 0)
+                                             : (ldc % 8 == 0 && ((uintptr_t)C & 15) == 0);
+    const bool ws_vec = (N % 4 == 0);
+    a.vec_store = (!small_m && d.splits > 1) ? (ws_vec ? 1 : 0) : (c_vec ? 1 : 0);
+    if (!small_m) {
+      launch_decode_quant(a, (int)M, d.splits, st);
+    } else if (d.kernel == FP8B_KERNEL_TINY) {
       if (M <= 4) launch_tiny_quant<4>(a, d.bn, d.waves, d.grid, st);
       else if (M <= 8) launch_tiny_quant<8>(a, d.bn, d.waves, d.grid, st);
       else launch_tiny_quant<16>(a, d.bn, d.waves, d.grid, st);
@@ -4005,35 +4012,10 @@ extern "C" int fp8b_act_quant_matmul(const void* x, int64_t ldx, const void* B, 
       gemm_skinny_quant_kernel<8><<<(unsigned)d.grid, 512, 0, st>>>(a);
     }
     if (hipGetLastError() != hipSuccess) {
-      set_error("fp8b_act_quant_matmul: fused small-M kernel launch failed");
+      set_error("fp8b_act_quant_matmul: act-quant GEMM kernel launch failed");
       return FP8B_ERR_LAUNCH;
     }
-    return FP8B_OK;
-  }
-  if (fused_decode_ok(d, x, ldx, ldb, M)) {
-    hipStream_t st = (hipStream_t)stream;
-    GemmArgs a;
-    a.A = (const uint8_t*)x; a.B = (const uint8_t*)B; a.As = nullptr; a.Bs = Bs; a.C = C;
-    a.ws = (float*)workspace;
-    a.lda = 2 * ldx; a.ldb = ldb; a.as_sm = 0; a.as_sk = 0; a.bs_sn = bs_sn; a.bs_sk = bs_sk;
-    a.ldc = ldc; a.M = (int)M; a.N = (int)N; a.K = (int)K; a.KB = (int)KB;
-    a.kb_per_split = d.kb_per_split;
-    a.tiles_m = 1; a.tiles_n = (int)((N + 127) / 128);
-    a.out_dtype = out_dtype;
-    a.rem_base = -1; a.rem_tiles_m = 0; a.rem_tiles_n = 0;
-    a.Sq = nullptr; a.sq_sm = 0; a.sq_sg = 0;
-    a.win4 = 1;
-    const size_t esz = out_dtype == FP8B_F32 ? 4 : 2;
-    const bool c_vec = esz == 4 ? (ldc % 4 == 0 && ((uintptr_t)C & 15) == 0)
-                                : (ldc % 8 == 0 && ((uintptr_t)C & 15) == 0);
-    const bool ws_vec = (N % 4 == 0);
-    a.vec_store = (d.splits > 1) ? (ws_vec ? 1 : 0) : (c_vec ? 1 : 0);
-    launch_decode_quant(a, (int)M, d.splits, st);
-    if (hipGetLastError() != hipSuccess) {
-      set_error("fp8b_act_quant_matmul: fused decode kernel launch failed");
-      return FP8B_ERR_LAUNCH;
-    }
-    if (d.splits > 1) {
+    if (!small_m && d.splits > 1) {
       GemmArgs r = a;
       r.vec_store = (ws_vec && c_vec) ? 1 : 0;
       launch_splitk_reduce(r, d, st);
