@@ -11,7 +11,9 @@
 //   silu_and_mul_quant(x, block_size) -> (q, s)
 //   gate_up_silu_quant(A, B, As, Bs) -> (q, s)   (gate/up weights interleaved)
 //   act_quant_matmul(x, B, Bs, block_n, block_k, ScalarType output_dtype) -> Tensor
-//       (act_quant then w8a8_block_fp8_matmul in one op: two launches)
+//       (act_quant then w8a8_block_fp8_matmul in one op, the same bits: one
+//       kernel that quantises inside the GEMM on small-M plans, else two
+//       launches)
 //   weight_quant(W, block_n, block_k) -> (Wq, Bs)   (128x128 blocks)
 // and, in _deep_gemm_helion_rocm_mi355x (deep-gemm-helion's op,
 // deep-gemm-helion/deep-gemm-helion/torch-ext/deep_gemm_helion/op.py:7-14):

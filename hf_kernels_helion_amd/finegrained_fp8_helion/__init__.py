@@ -84,9 +84,12 @@ def silu_and_mul_quant(x: torch.Tensor, block_size: int = 128):
 def act_quant_w8a8_block_fp8_matmul(x: torch.Tensor, B: torch.Tensor, Bs: torch.Tensor,
                                     block_size=(128, 128), output_dtype=torch.float32):
     """w8a8_block_fp8_matmul(*act_quant(x, 128), B, Bs, block_size, output_dtype),
-    bit for bit, as one op: the quantiser writes (q, s) into the op's
-    workspace and the GEMM reads them (two kernel launches on the current
-    stream). x: [M,K] bfloat16, K % 128 == 0; block_size must be [128, 128]."""
+    bit for bit, as one op. On decode-sized M (up to 32 rows on the split-K
+    decode plan, up to 8 on the skinny and small-grid plans; 16-byte aligned
+    rows) one kernel reads the bf16 rows and quantises them inside the GEMM;
+    otherwise the quantiser writes (q, s) into the op's workspace and the
+    GEMM reads them (two launches on the current stream).
+    x: [M,K] bfloat16, K % 128 == 0; block_size must be [128, 128]."""
     block_n, block_k = int(block_size[0]), int(block_size[1])
     if output_dtype in _DIRECT_OUT:
         if not _compiling():
