@@ -36,6 +36,21 @@ namespace fp8b {
 // bx*16U + r + 16u, u < U, and issues all U loads before converting any.
 // The row is uniform over the block, so its base addresses are scalar and
 // each lane adds a 32-bit offset (no per-lane index division).
+// For U > 1 the block's 16U scales of a row go through LDS and leave as one
+// contiguous store (16U lanes) instead of U four-float stores per wave;
+// two LDS slots alternate between rows, so one barrier per row suffices.
+__device__ __forceinline__ void store_group_scale(float* sc, uint32_t u, float scale) {
+  if ((threadIdx.x & 15u) == 0) sc[(threadIdx.x >> 4) + 16u * u] = scale;
+}
+
+template <int U>
+__device__ __forceinline__ void flush_group_scales(const float* sc, float* sr, int64_t ssg,
+                                                   uint32_t groups_per_row) {
+  __syncthreads();
+  const uint32_t g = blockIdx.x * 16u * U + threadIdx.x;
+  if (threadIdx.x < 16u * U && g < groups_per_row) sr[(int64_t)g * ssg] = sc[threadIdx.x];
+}
+
 template <int U>
 __global__ void __launch_bounds__(256)
 act_quant_g128_kernel(const uint16_t* __restrict__ x, int64_t ldx,
@@ -44,7 +59,9 @@ act_quant_g128_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                       uint32_t rows, uint32_t groups_per_row) {
   const uint32_t sub = threadIdx.x & 15u;
   const uint32_t g0 = blockIdx.x * 16u * U + (threadIdx.x >> 4);
-  for (uint32_t m = blockIdx.y; m < rows; m += gridDim.y) {
+  __shared__ float sc[2][16 * U];
+  uint32_t par = 0;
+  for (uint32_t m = blockIdx.y; m < rows; m += gridDim.y, par ^= 1u) {
     const uint16_t* xr = x + (int64_t)m * ldx;
     v4i raw[U];
 #pragma unroll
@@ -67,8 +84,13 @@ act_quant_g128_kernel(const uint16_t* __restrict__ x, int64_t ldx,
       packed[0] = (int)w0;
       packed[1] = (int)w1;
       __builtin_nontemporal_store(packed, reinterpret_cast<v2i*>(qr + g * 128u + sub * 8u));
-      if (sub == 0) sr[(int64_t)g * ssg] = scale;
+      if constexpr (U == 1) {
+        if (sub == 0) sr[(int64_t)g * ssg] = scale;
+      } else {
+        store_group_scale(sc[par], u, scale);
+      }
     }
+    if constexpr (U > 1) flush_group_scales<U>(sc[par], sr, ssg, groups_per_row);
   }
 }
 
@@ -100,15 +122,24 @@ act_quant_g128_flat_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   if (sub == 0) s[(int64_t)m * ssm + (int64_t)g * ssg] = scale;
 }
 
-// Groups per block column of the fast kernels: 16*U with U in {4, 2, 1},
-// the largest that divides the groups of a row (no idle lanes at the row's
-// end), and 1 when there are few groups in all (decode: spread them over
-// as many CUs as possible).
-inline int g128_unroll(int64_t rows, int64_t gpr) {
+// Groups per block column of the fast kernels: 16*U with U in {4, 2, 1}.
+// 1 when there are few groups in all (decode: spread them over as many CUs
+// as possible); else 4 or 2 when that divides the groups of a row (no idle
+// 16-lane rows at the row's end). Other rows still take 4 or 2: the loads
+// each lane has in flight count for more than the idle rows of the last
+// column. U = 4 when the row fits one 64-group column that U = 2 would need
+// two columns for, 2 otherwise, except where a lane already has two loads
+// per group in flight (loads_per_group = 2, gate and up of the SiLU kernel)
+// and U = 1 leaves no idle rows. Measured (graph replays over 4 input sets,
+// M x K bf16): act-quant 8192 x 7168 29.0 us at U = 4, 30.9 at U = 2, 35.4
+// at U = 1; 4096 x 14336 30.0 us at U = 2, 30.7 at U = 4, 33.3 at U = 1.
+// SiLU-quant 8192 x 2*14336 106.4 us at U = 1, 110.2 at U = 2.
+inline int g128_unroll(int64_t rows, int64_t gpr, int loads_per_group = 1) {
   if (rows * gpr < 16 * 1024) return 1;
   if (gpr % 64 == 0) return 4;
   if (gpr % 32 == 0) return 2;
-  return 1;
+  if (gpr > 32 && gpr < 64) return 4;
+  return loads_per_group > 1 && gpr % 16 == 0 ? 1 : 2;
 }
 
 // Scalar reference-shaped path for any group size, ragged K or unaligned
@@ -358,7 +389,9 @@ silu_mul_quant_g128_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                            uint32_t rows, uint32_t groups_per_row, int64_t d) {
   const uint32_t sub = threadIdx.x & 15u;
   const uint32_t g0 = blockIdx.x * 16u * U + (threadIdx.x >> 4);
-  for (uint32_t m = blockIdx.y; m < rows; m += gridDim.y) {
+  __shared__ float sc[2][16 * U];
+  uint32_t par = 0;
+  for (uint32_t m = blockIdx.y; m < rows; m += gridDim.y, par ^= 1u) {
     const uint16_t* xr = x + (int64_t)m * ldx;
     const uint16_t* ur_ = xr + d;
     v4i gr[U], ur[U];
@@ -383,8 +416,13 @@ silu_mul_quant_g128_kernel(const uint16_t* __restrict__ x, int64_t ldx,
       packed[0] = (int)w0;
       packed[1] = (int)w1;
       __builtin_nontemporal_store(packed, reinterpret_cast<v2i*>(qr + g * 128u + sub * 8u));
-      if (sub == 0) sr[(int64_t)g * ssg] = scale;
+      if constexpr (U == 1) {
+        if (sub == 0) sr[(int64_t)g * ssg] = scale;
+      } else {
+        store_group_scale(sc[par], u, scale);
+      }
     }
+    if constexpr (U > 1) flush_group_scales<U>(sc[par], sr, ssg, groups_per_row);
   }
 }
 
@@ -644,7 +682,7 @@ extern "C" int fp8b_silu_and_mul_quant(const void* x, int64_t ldx, void* q, int6
         (const uint16_t*)x, ldx, (uint8_t*)q, ldq, s, s_stride_m, s_stride_g, (uint32_t)slots,
         (uint32_t)gpr, d);
   } else if (fast) {
-    const int U = g128_unroll(M, gpr);
+    const int U = g128_unroll(M, gpr, 2);
     const dim3 grid((unsigned)((gpr + 16 * U - 1) / (16 * U)), (unsigned)std::min<int64_t>(M, 65535));
     auto launch = [&](auto kernel) {
       kernel<<<grid, 256, 0, st>>>((const uint16_t*)x, ldx, (uint8_t*)q, ldq, s, s_stride_m,

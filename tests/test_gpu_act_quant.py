@@ -45,21 +45,32 @@ def test_act_quant_more_rows_than_grid_y(M, K, dev):
     _assert_exact(x, 128, dev)
 
 
-def _g128_unroll(M, K):
-    """Groups per block column / 16 that fp8b_act_quant picks for group 128
-    (g128_unroll in act_quant.hip)."""
+def _g128_unroll(M, K, loads_per_group=1):
+    """Groups per block column / 16 that fp8b_act_quant (loads_per_group 1)
+    and fp8b_silu_and_mul_quant (2) pick for group 128 (g128_unroll in
+    act_quant.hip)."""
     gpr = K // 128
     if M * gpr < 16 * 1024:
         return 1
-    return 4 if gpr % 64 == 0 else (2 if gpr % 32 == 0 else 1)
+    if gpr % 64 == 0:
+        return 4
+    if gpr % 32 == 0:
+        return 2
+    if 32 < gpr < 64:
+        return 4
+    return 1 if loads_per_group > 1 and gpr % 16 == 0 else 2
 
 
 @pytest.mark.parametrize("M,K,unroll", [(2048, 4096, 2), (3001, 4096, 2), (512, 4096, 2),
-                                        (256, 8192, 4), (300, 14336, 1)])
+                                        (256, 8192, 4), (300, 14336, 2), (600, 7168, 4),
+                                        (1000, 2560, 2), (100, 7168, 1)])
 def test_act_quant_every_unroll_on_config_inputs(M, K, unroll, dev):
     """The BASELINE config inputs (~N(0,1) with 1% outliers x20 per row) on
     each unrolled kernel variant: [2048,4096] (C2) and [3001,4096] (C5) run
-    act_quant_g128_kernel<2>, [256,8192] <4>, [300,14336] <1>."""
+    act_quant_g128_kernel<2>, [256,8192] <4>; rows whose groups 16*U does
+    not divide leave idle 16-lane rows in their last block column:
+    [300,14336] (112 groups) and [1000,2560] (20) at <2>, [600,7168] (56) at
+    <4>; [100,7168] has too few groups in all and runs <1>."""
     assert _g128_unroll(M, K) == unroll
     print(f"act_quant U={unroll} M={M} K={K}", flush=True)
     x = synthetic.activations(M, K, seed=M + 3 * K, outlier_frac=0.01)

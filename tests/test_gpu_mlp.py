@@ -87,15 +87,20 @@ def test_silu_and_mul_strided_layouts(dev):
 @pytest.mark.parametrize("M,d,group", [(3001, 14336, 128), (5, 384, 128), (9, 200, 64),
                                        (4, 256, 256), (70000, 256, 128), (512, 4096, 128),
                                        (256, 8192, 128), (1000, 8192, 128), (4097, 1920, 128),
-                                       (28672, 128, 128)])
+                                       (28672, 128, 128), (600, 7168, 128), (1000, 2560, 128),
+                                       (300, 18944, 128)])
 def test_silu_and_mul_quant_equals_two_ops(M, d, group, dev):
     """Fused kernel == silu_and_mul then act_quant, bit for bit, and its codes
     and scales are oracle.act_quant of the GPU's bf16 silu_and_mul output.
     d = 14336 runs silu_mul_quant_g128_kernel<1>, d = 4096 with 512 rows <2>,
-    d = 8192 with 256 or more rows <4> (16*U groups per block column, U the
-    largest of 4, 2, 1 dividing the row's groups, 1 below 16384 groups);
-    rows of fewer than 16 groups (d = 384, 256, 1920, 128) the flat-mapped
-    kernel."""
+    d = 8192 with 256 or more rows <4> (16*U groups per block column); rows
+    whose groups 16*U does not divide: d = 7168 (56 groups) <4>, d = 2560
+    (20) and d = 18944 (148) <2>; rows of fewer than 16 groups (d = 384,
+    256, 1920, 128) the flat-mapped kernel."""
+    from test_gpu_act_quant import _g128_unroll
+    if group == 128 and d >= 2048:
+        assert _g128_unroll(M, d, 2) == {14336: 1, 4096: 2, 8192: 4, 7168: 4, 2560: 2,
+                                         18944: 2}[d], (M, d)
     print(f"silu_and_mul_quant M={M} d={d} group={group}", flush=True)
     x = (synthetic.activations(M, 2 * d, seed=M + d) * 2).to(dev)
     q, s = fp8.silu_and_mul_quant(x, group)
