@@ -39,16 +39,19 @@ namespace fp8b {
 // For U > 1 the block's 16U scales of a row go through LDS and leave as one
 // contiguous store (16U lanes) instead of U four-float stores per wave;
 // two LDS slots alternate between rows, so one barrier per row suffices.
+// (R: 16-lane rows per block, 16 here and 16, 8 or 4 in the SiLU kernel;
+// a block column holds R*U groups and 16-lane row r takes r + R*u.)
+template <int R>
 __device__ __forceinline__ void store_group_scale(float* sc, uint32_t u, float scale) {
-  if ((threadIdx.x & 15u) == 0) sc[(threadIdx.x >> 4) + 16u * u] = scale;
+  if ((threadIdx.x & 15u) == 0) sc[(threadIdx.x >> 4) + (uint32_t)R * u] = scale;
 }
 
-template <int U>
+template <int N>
 __device__ __forceinline__ void flush_group_scales(const float* sc, float* sr, int64_t ssg,
                                                    uint32_t groups_per_row) {
   __syncthreads();
-  const uint32_t g = blockIdx.x * 16u * U + threadIdx.x;
-  if (threadIdx.x < 16u * U && g < groups_per_row) sr[(int64_t)g * ssg] = sc[threadIdx.x];
+  const uint32_t g = blockIdx.x * (uint32_t)N + threadIdx.x;
+  if (threadIdx.x < (uint32_t)N && g < groups_per_row) sr[(int64_t)g * ssg] = sc[threadIdx.x];
 }
 
 template <int U>
@@ -87,10 +90,10 @@ act_quant_g128_kernel(const uint16_t* __restrict__ x, int64_t ldx,
       if constexpr (U == 1) {
         if (sub == 0) sr[(int64_t)g * ssg] = scale;
       } else {
-        store_group_scale(sc[par], u, scale);
+        store_group_scale<16>(sc[par], u, scale);
       }
     }
-    if constexpr (U > 1) flush_group_scales<U>(sc[par], sr, ssg, groups_per_row);
+    if constexpr (U > 1) flush_group_scales<16 * U>(sc[par], sr, ssg, groups_per_row);
   }
 }
 
@@ -128,18 +131,35 @@ act_quant_g128_flat_kernel(const uint16_t* __restrict__ x, int64_t ldx,
 // 16-lane rows at the row's end). Other rows still take 4 or 2: the loads
 // each lane has in flight count for more than the idle rows of the last
 // column. U = 4 when the row fits one 64-group column that U = 2 would need
-// two columns for, 2 otherwise, except where a lane already has two loads
-// per group in flight (loads_per_group = 2, gate and up of the SiLU kernel)
-// and U = 1 leaves no idle rows. Measured (graph replays over 4 input sets,
-// M x K bf16): act-quant 8192 x 7168 29.0 us at U = 4, 30.9 at U = 2, 35.4
-// at U = 1; 4096 x 14336 30.0 us at U = 2, 30.7 at U = 4, 33.3 at U = 1.
-// SiLU-quant 8192 x 2*14336 106.4 us at U = 1, 110.2 at U = 2.
-inline int g128_unroll(int64_t rows, int64_t gpr, int loads_per_group = 1) {
+// two columns for, 2 otherwise. Measured (graph replays over 4 input sets,
+// M x K bf16): 8192 x 7168 29.0 us at U = 4, 30.9 at U = 2, 35.4 at U = 1;
+// 4096 x 14336 30.0 us at U = 2, 30.7 at U = 4, 33.3 at U = 1. Blocks of 8
+// or 4 16-lane rows that split such rows exactly measured level or slower
+// here (4096 x 14336 30.4 us at 8 rows x 2 or 7 groups, 8192 x 7168 30.4
+// at 8 x 7).
+inline int g128_unroll(int64_t rows, int64_t gpr) {
   if (rows * gpr < 16 * 1024) return 1;
   if (gpr % 64 == 0) return 4;
   if (gpr % 32 == 0) return 2;
-  if (gpr > 32 && gpr < 64) return 4;
-  return loads_per_group > 1 && gpr % 16 == 0 ? 1 : 2;
+  return gpr > 32 && gpr < 64 ? 4 : 2;
+}
+
+// Block shape of silu_mul_quant_g128_kernel: R 16-lane rows of U groups.
+// A lane loads two vectors per group (gate and up), so U = 2 already keeps
+// four loads in flight; rows whose group count is a multiple of 8 (but not
+// of 64) take U = 2 and the largest R of 16, 8, 4 that splits the row
+// exactly, the rest the act-quant shape (R = 16, U from g128_unroll).
+// Measured (graph replays over 4 input sets, M x 2d bf16 in): d = 14336
+// (112 groups) 3001 rows 39.3 us at R = 8 against 40.4 at 16 x 1 (the
+// earlier shape), 4096 rows 51.7 against 54.1; d = 7168 (56 groups) 8192
+// rows 52.3 at R = 4 against 53.2 at 16 x 4 with 8 idle rows, 1024 rows 8.8
+// against 9.5; 16 x 7 and 8 x 7 (one or two blocks per row) level or slower.
+inline void silu_quant_shape(int64_t rows, int64_t gpr, int& R, int& U) {
+  R = 16;
+  U = g128_unroll(rows, gpr);
+  if (rows * gpr < 16 * 1024 || gpr % 64 == 0 || gpr % 8 != 0) return;
+  U = 2;
+  R = (gpr / 2) % 16 == 0 ? 16 : (gpr / 2) % 8 == 0 ? 8 : 4;
 }
 
 // Scalar reference-shaped path for any group size, ragged K or unaligned
@@ -378,18 +398,19 @@ silu_and_mul_typed_kernel(const void* __restrict__ x, int64_t ldx, void* __restr
 
 // Fused silu_and_mul + group-128 quantisation: identical arithmetic to
 // silu_and_mul_vec_kernel followed by act_quant_g128_kernel, without the
-// bf16 round trip through memory. Requires d % 128 == 0. Blocks and 16-lane
-// rows map to (row, group) as in act_quant_g128_kernel; each lane loads its
-// 8 gate and 8 up values of U groups before converting any.
-template <int U>
+// bf16 round trip through memory. Requires d % 128 == 0. Blocks of R 16-lane
+// rows (16R threads) map to (row, group) as in act_quant_g128_kernel with
+// R*U groups per block column; each lane loads its 8 gate and 8 up values
+// of U groups before converting any.
+template <int U, int R>
 __global__ void __launch_bounds__(256)
 silu_mul_quant_g128_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                            uint8_t* __restrict__ q, int64_t ldq,
                            float* __restrict__ s, int64_t ssm, int64_t ssg,
                            uint32_t rows, uint32_t groups_per_row, int64_t d) {
   const uint32_t sub = threadIdx.x & 15u;
-  const uint32_t g0 = blockIdx.x * 16u * U + (threadIdx.x >> 4);
-  __shared__ float sc[2][16 * U];
+  const uint32_t g0 = blockIdx.x * (uint32_t)(R * U) + (threadIdx.x >> 4);
+  __shared__ float sc[2][R * U];
   uint32_t par = 0;
   for (uint32_t m = blockIdx.y; m < rows; m += gridDim.y, par ^= 1u) {
     const uint16_t* xr = x + (int64_t)m * ldx;
@@ -397,7 +418,7 @@ silu_mul_quant_g128_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     v4i gr[U], ur[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const uint32_t g = min(g0 + 16u * u, groups_per_row - 1);  // uniform per 16-lane row
+      const uint32_t g = min(g0 + (uint32_t)R * u, groups_per_row - 1);  // uniform per 16-lane row
       gr[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(xr + g * 128u + sub * 8u));
       ur[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(ur_ + g * 128u + sub * 8u));
     }
@@ -405,7 +426,7 @@ silu_mul_quant_g128_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     float* sr = s + (int64_t)m * ssm;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const uint32_t g = g0 + 16u * u;
+      const uint32_t g = g0 + (uint32_t)R * u;
       if (g >= groups_per_row) break;  // uniform across the 16-lane group
       float v[8];
       const v4i h = silu_mul_bf16x8(gr[u], ur[u], v);
@@ -419,10 +440,10 @@ silu_mul_quant_g128_kernel(const uint16_t* __restrict__ x, int64_t ldx,
       if constexpr (U == 1) {
         if (sub == 0) sr[(int64_t)g * ssg] = scale;
       } else {
-        store_group_scale(sc[par], u, scale);
+        store_group_scale<R>(sc[par], u, scale);
       }
     }
-    if constexpr (U > 1) flush_group_scales<U>(sc[par], sr, ssg, groups_per_row);
+    if constexpr (U > 1) flush_group_scales<R * U>(sc[par], sr, ssg, groups_per_row);
   }
 }
 
@@ -682,15 +703,18 @@ extern "C" int fp8b_silu_and_mul_quant(const void* x, int64_t ldx, void* q, int6
         (const uint16_t*)x, ldx, (uint8_t*)q, ldq, s, s_stride_m, s_stride_g, (uint32_t)slots,
         (uint32_t)gpr, d);
   } else if (fast) {
-    const int U = g128_unroll(M, gpr, 2);
-    const dim3 grid((unsigned)((gpr + 16 * U - 1) / (16 * U)), (unsigned)std::min<int64_t>(M, 65535));
+    int R, U;
+    silu_quant_shape(M, gpr, R, U);
+    const dim3 grid((unsigned)((gpr + R * U - 1) / (R * U)), (unsigned)std::min<int64_t>(M, 65535));
     auto launch = [&](auto kernel) {
-      kernel<<<grid, 256, 0, st>>>((const uint16_t*)x, ldx, (uint8_t*)q, ldq, s, s_stride_m,
-                                   s_stride_g, (uint32_t)M, (uint32_t)gpr, d);
+      kernel<<<grid, 16 * R, 0, st>>>((const uint16_t*)x, ldx, (uint8_t*)q, ldq, s, s_stride_m,
+                                      s_stride_g, (uint32_t)M, (uint32_t)gpr, d);
     };
-    if (U == 4) launch(silu_mul_quant_g128_kernel<4>);
-    else if (U == 2) launch(silu_mul_quant_g128_kernel<2>);
-    else launch(silu_mul_quant_g128_kernel<1>);
+    if (U == 4) launch(silu_mul_quant_g128_kernel<4, 16>);
+    else if (U == 2 && R == 16) launch(silu_mul_quant_g128_kernel<2, 16>);
+    else if (U == 2 && R == 8) launch(silu_mul_quant_g128_kernel<2, 8>);
+    else if (U == 2) launch(silu_mul_quant_g128_kernel<2, 4>);
+    else launch(silu_mul_quant_g128_kernel<1, 16>);
   } else {
     const int64_t groups = M * gpr;
     silu_mul_quant_generic_kernel<<<(unsigned)((groups + 63) / 64), 64, 0, st>>>(

@@ -45,10 +45,9 @@ def test_act_quant_more_rows_than_grid_y(M, K, dev):
     _assert_exact(x, 128, dev)
 
 
-def _g128_unroll(M, K, loads_per_group=1):
-    """Groups per block column / 16 that fp8b_act_quant (loads_per_group 1)
-    and fp8b_silu_and_mul_quant (2) pick for group 128 (g128_unroll in
-    act_quant.hip)."""
+def _g128_unroll(M, K):
+    """Groups per block column / 16 that fp8b_act_quant picks for group 128
+    (g128_unroll in act_quant.hip)."""
     gpr = K // 128
     if M * gpr < 16 * 1024:
         return 1
@@ -56,9 +55,17 @@ def _g128_unroll(M, K, loads_per_group=1):
         return 4
     if gpr % 32 == 0:
         return 2
-    if 32 < gpr < 64:
-        return 4
-    return 1 if loads_per_group > 1 and gpr % 16 == 0 else 2
+    return 4 if 32 < gpr < 64 else 2
+
+
+def _silu_quant_shape(M, d):
+    """(16-lane rows per block, groups per lane) that fp8b_silu_and_mul_quant
+    picks for group 128 (silu_quant_shape in act_quant.hip)."""
+    gpr = d // 128
+    if M * gpr < 16 * 1024 or gpr % 64 == 0 or gpr % 8 != 0:
+        return 16, _g128_unroll(M, d)
+    h = gpr // 2
+    return (16 if h % 16 == 0 else 8 if h % 8 == 0 else 4), 2
 
 
 @pytest.mark.parametrize("M,K,unroll", [(2048, 4096, 2), (3001, 4096, 2), (512, 4096, 2),

@@ -92,15 +92,16 @@ def test_silu_and_mul_strided_layouts(dev):
 def test_silu_and_mul_quant_equals_two_ops(M, d, group, dev):
     """Fused kernel == silu_and_mul then act_quant, bit for bit, and its codes
     and scales are oracle.act_quant of the GPU's bf16 silu_and_mul output.
-    d = 14336 runs silu_mul_quant_g128_kernel<1>, d = 4096 with 512 rows <2>,
-    d = 8192 with 256 or more rows <4> (16*U groups per block column); rows
-    whose groups 16*U does not divide: d = 7168 (56 groups) <4>, d = 2560
-    (20) and d = 18944 (148) <2>; rows of fewer than 16 groups (d = 384,
-    256, 1920, 128) the flat-mapped kernel."""
-    from test_gpu_act_quant import _g128_unroll
+    Block shapes (16-lane rows per block, groups per lane): d = 14336 (112
+    groups) 8 x 2, d = 7168 (56) 4 x 2, d = 4096 with 512 rows 16 x 2,
+    d = 8192 with 256 or more rows 16 x 4; d = 2560 (20 groups) and 18944
+    (148) 16 x 2 with idle 16-lane rows in the last block column; rows of
+    fewer than 16 groups (d = 384, 256, 1920, 128) the flat-mapped kernel."""
+    from test_gpu_act_quant import _silu_quant_shape
     if group == 128 and d >= 2048:
-        assert _g128_unroll(M, d, 2) == {14336: 1, 4096: 2, 8192: 4, 7168: 4, 2560: 2,
-                                         18944: 2}[d], (M, d)
+        assert _silu_quant_shape(M, d) == {14336: (8, 2), 4096: (16, 2), 8192: (16, 4),
+                                           7168: (4, 2), 2560: (16, 2),
+                                           18944: (16, 2)}[d], (M, d)
     print(f"silu_and_mul_quant M={M} d={d} group={group}", flush=True)
     x = (synthetic.activations(M, 2 * d, seed=M + d) * 2).to(dev)
     q, s = fp8.silu_and_mul_quant(x, group)
