@@ -26,6 +26,7 @@ lib.fp8b_w8a8_block_matmul.argtypes = [P, I, P, I, P, I, I, P, I, I, P, I, ctype
 lib.fp8b_gemm_workspace_size.restype = ctypes.c_size_t
 lib.fp8b_gemm_workspace_size.argtypes = [I, I, I, I, I]
 lib.fp8b_act_quant.argtypes = [P, I, P, I, P, I, I, I, I, I, P]
+lib.fp8b_silu_and_mul_quant.argtypes = [P, I, P, I, P, I, I, I, I, I, P]
 lib.fp8b_last_error.restype = ctypes.c_char_p
 
 
@@ -97,3 +98,41 @@ def test_ctypes_binding_reports_errors(dev):
         w8a8_block_fp8_matmul_bf16(overlapping, B, torch.ones(4, 2, device=dev), Bs)
     C = w8a8_block_fp8_matmul_bf16(A[:, :256], B, torch.ones(4, 2, device=dev), Bs)
     assert torch.equal(C.float(), torch.zeros(4, 128, device=dev))
+
+
+def _quant_call(fn, x, ldx, q, ldq, s, s_sm, s_sg, M, K):
+    st = fn(x.data_ptr(), ldx, q.data_ptr(), ldq, s.data_ptr(), s_sm, s_sg, M, K, 128,
+            torch.cuda.current_stream().cuda_stream)
+    if st:
+        raise RuntimeError(lib.fp8b_last_error().decode())
+
+
+@pytest.mark.parametrize("silu", [False, True])
+@pytest.mark.parametrize("K", [7168, 8192, 14336, 4096])
+def test_ctypes_quant_block_shapes_strided(silu, K, dev):
+    """fp8b_act_quant and fp8b_silu_and_mul_quant on padded rows (ldx, ldq
+    past the row), column-major scales and a guard band after every row:
+    the same codes and scales as the packed call, and nothing written past
+    a row's end. K covers each block shape of the group-128 kernels at 600
+    rows: act-quant 16 x 4 with 8 idle 16-lane rows (K = 7168), 16 x 4
+    (8192), 16 x 2 with 16 idle rows (14336), 16 x 2 (4096); SiLU-quant
+    (K = d) 4 x 2, 16 x 4, 8 x 2, 16 x 2."""
+    M = 600
+    fn = lib.fp8b_silu_and_mul_quant if silu else lib.fp8b_act_quant
+    width = 2 * K if silu else K
+    print(f"ctypes quant strided silu={silu} M={M} K={K}", flush=True)
+    x = (synthetic.activations(M, width, seed=K + silu, outlier_frac=0.01) * 2).to(dev)
+    G = K // 128
+    q0 = torch.empty(M, K, dtype=torch.uint8, device=dev)
+    s0 = torch.empty(M, G, dtype=torch.float32, device=dev)
+    _quant_call(fn, x, width, q0, K, s0, G, 1, M, K)
+    xp = torch.zeros(M, width + 256, dtype=torch.bfloat16, device=dev)
+    xp[:, :width] = x
+    qp = torch.full((M, K + 128), 0xA5, dtype=torch.uint8, device=dev)
+    sp = torch.full((G + 1, M), -7.0, dtype=torch.float32, device=dev)  # column-major + a guard row
+    _quant_call(fn, xp, width + 256, qp, K + 128, sp, 1, M, M, K)
+    torch.cuda.synchronize()
+    assert torch.equal(qp[:, :K], q0)
+    assert torch.all(qp[:, K:] == 0xA5)
+    assert torch.equal(sp[:G].t().contiguous().view(torch.int32), s0.view(torch.int32))
+    assert torch.all(sp[G] == -7.0)
