@@ -2085,11 +2085,18 @@ __global__ void __launch_bounds__(512) gemm_decode_quant_kernel(GemmArgs a) {
 // operand: the weight scale is wave-uniform and the activation scale is one
 // register per lane). The 8 partial tiles are summed in wave order through
 // LDS: deterministic, no workspace, no second kernel.
-template <int FM>
+// Only the first 8*XG activation rows (XG = ceil(M/8) groups of 8) are
+// staged: lanes of the MFMA operand past them read a staged row with the
+// same swizzle key, and their outputs (rows >= M) are never stored. Each
+// DMA instruction that is not issued saves the L2 -> LDS traffic of 1 KiB
+// per K-block and wave (1x4096x14336: 2 KiB of activation rows per K-block
+// cost as much time as the 2 KiB of weights beside them).
+template <int FM, int XG>
 __global__ void __launch_bounds__(512) gemm_skinny_kernel(GemmArgs a) {
+  static_assert(XG >= 1 && XG <= 2 * FM, "staged activation row groups");
   constexpr int NWAVE = 8;
   constexpr int SK = FM <= 2 ? 3 : 2;          // K-blocks in flight per wave
-  constexpr int ROWS = 16 + 16 * FM;           // weight rows, then activation rows
+  constexpr int ROWS = 16 + 8 * XG;            // weight rows, then staged activation rows
   constexpr int LOADS = ROWS / 8;              // 1 KiB DMA instructions per K-block
   constexpr int SCALE_OFF = ROWS * 128;        // 64 fp32: sa rows 0..16FM-1, sb at 63
   constexpr int SLOT = SCALE_OFF + 256;
@@ -2149,7 +2156,8 @@ __global__ void __launch_bounds__(512) gemm_skinny_kernel(GemmArgs a) {
         const float sb = *reinterpret_cast<const float*>(sl + SCALE_OFF + 63 * 4);
 #pragma unroll
         for (int f = 0; f < FM; ++f) {
-          const v8i x = lds_frag(sl + (16 + f * 16 + row) * 128, c0, r7);
+          const int xr = f * 16 + row < 8 * XG ? f * 16 + row : 8 * (XG - 1) + r7;
+          const v8i x = lds_frag(sl + (16 + xr) * 128, c0, r7);
           const float sc = *reinterpret_cast<const float*>(sl + SCALE_OFF + (f * 16 + row) * 4) * sb;
           const v4f t = mfma16x16x128(w, x);
 #pragma unroll
@@ -2188,7 +2196,7 @@ __global__ void __launch_bounds__(512) gemm_skinny_kernel(GemmArgs a) {
 
 // ---------------------------------------------------------------------------
 // Skinny GEMM with the group-128 act-quant inside it (fp8b_act_quant_matmul
-// on skinny plans, M <= QR <= 8): gemm_skinny_kernel<1>'s grid, K ranges and
+// on skinny plans, M <= QR <= 8): gemm_skinny_kernel<1, XG>'s grid, K ranges and
 // fold, with the activations read as bf16. Each wave streams its K-blocks
 // through a private ring of LDS slots (its 16 weight rows, chunk-swizzled;
 // the QR bf16 activation rows, unswizzled; the weight block's scale), all by
@@ -3562,9 +3570,15 @@ void launch_dispatch(const Dispatch& d, const GemmArgs& a, hipStream_t st) {
     case FP8B_KERNEL_SKINNY: {
       const int fm = (a.M + 15) / 16;
       if constexpr (!PR) {
-        if (fm <= 1) gemm_skinny_kernel<1><<<(unsigned)d.grid, 512, 0, st>>>(a);
-        else if (fm == 2) gemm_skinny_kernel<2><<<(unsigned)d.grid, 512, 0, st>>>(a);
-        else gemm_skinny_kernel<3><<<(unsigned)d.grid, 512, 0, st>>>(a);
+        // staged activation row groups: ceil(M / 8) (odd counts save a DMA)
+        const int xg = (a.M + 7) / 8;
+        const dim3 g((unsigned)d.grid);
+        if (xg <= 1) gemm_skinny_kernel<1, 1><<<g, 512, 0, st>>>(a);
+        else if (fm <= 1) gemm_skinny_kernel<1, 2><<<g, 512, 0, st>>>(a);
+        else if (xg == 3) gemm_skinny_kernel<2, 3><<<g, 512, 0, st>>>(a);
+        else if (fm == 2) gemm_skinny_kernel<2, 4><<<g, 512, 0, st>>>(a);
+        else if (xg == 5) gemm_skinny_kernel<3, 5><<<g, 512, 0, st>>>(a);
+        else gemm_skinny_kernel<3, 6><<<g, 512, 0, st>>>(a);
       }
       break;
     }

@@ -489,6 +489,35 @@ def test_gemm_zero_k_gives_zeros(dev):
     assert out.shape == (4, 8) and torch.equal(out, torch.zeros_like(out))
 
 
+def test_gemm_skinny_staged_row_groups_bit_equal(dev):
+    """The skinny kernel stages ceil(M/8) groups of 8 activation rows per
+    K-block (1..6 for M up to 48); the lanes past them read a staged row and
+    their outputs are not stored. Its K ranges, fold and wave-order sum do
+    not depend on M, so every row of the 48-row call must equal, bit for
+    bit, the same row computed by calls on 1, 8, 9, 16, 17, 24, 25, 32, 33,
+    40 and 41 rows (each staged row-group count, at its edges), and the
+    48-row call matches the oracle on sampled rows."""
+    from hf_kernels_helion_amd import _native
+    N, K = 2048, 8192
+    print(f"gemm skinny row groups N={N} K={K}", flush=True)
+    x = synthetic.activations(48, K, seed=48, outlier_frac=0.01)
+    q, s = fp8.act_quant(x.to(dev), 128)
+    W, Bs = synthetic.weights(N, K, seed=N + K)
+    W, Bs = W.to(dev), Bs.to(dev)
+    full = fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [128, 128], torch.bfloat16)
+    for M in (1, 8, 9, 16, 17, 24, 25, 32, 33, 40, 41, 48):
+        assert _native.gemm_plan(M, N, K)["kernel"] == "gemm_skinny_kernel", M
+        r0 = 48 - M  # the last M rows, so each call's rows start at a different row
+        part = fp8.w8a8_block_fp8_matmul(q[r0:], W, s[r0:], Bs, [128, 128], torch.bfloat16)
+        torch.testing.assert_close(part, full[r0:], rtol=0, atol=0)
+    rows = torch.tensor([0, 7, 8, 23, 40, 47])
+    orc = oracle.block_gemm(_u8(q.cpu()[rows]), _u8(W.cpu()), s.cpu()[rows].numpy(),
+                            Bs.cpu().numpy())
+    torch.testing.assert_close(full[rows.to(dev)].float().cpu(),
+                               torch.from_numpy(orc).to(torch.bfloat16).float(),
+                               rtol=RTOL, atol=ATOL)
+
+
 @pytest.mark.parametrize("M,N,K,block_n", [(3001, 28672, 4096, 128), (4224, 4096, 1024, 128),
                                            (4096, 4224, 1024, 128), (4100, 4096, 2048, 128),
                                            (4224, 4096, 1024, 1)])
