@@ -74,6 +74,18 @@ def time_events(fn, steps, warmup, torch):
     return e0.elapsed_time(e1) / steps  # ms per call
 
 
+def time_steady(fn, steps, torch, warm_ms=25.0, min_warmup=200):
+    """time_events after a warm-up of at least min_warmup calls and warm_ms
+    of GPU time: the shader clock takes ~10 ms of MFMA load to settle after
+    an HBM-bound leg, which 200 calls of a 5-30 us GEMM do not cover."""
+    done, spent = 0, 0.0
+    batch = min(50, min_warmup)
+    while done < min_warmup or spent < warm_ms:
+        spent += time_events(fn, batch, 0, torch) * batch
+        done += batch
+    return time_events(fn, steps, 0, torch)
+
+
 def gemm_launcher(A, B, As, Bs, out, torch):
     """Direct C-ABI launch of the GEMM on the current stream (no Python-side
     allocation or validation), used to time the kernel itself."""
@@ -342,14 +354,18 @@ def secondary(torch, fp8, synthetic, dev):
     torch.cuda.synchronize()
     assert all(torch.equal(g[0].view(torch.uint8), e[0].view(torch.uint8)) and torch.equal(g[1], e[1])
                for g, e in zip(gouts, eager + eager)), "act_quant replay differs"
-    ms = time_events(graph.replay, 50, 20, torch) / 8
+    # five windows of 50 replays after 20 warm-up replays; the median window
+    windows = [time_events(graph.replay, 50, 20 if w == 0 else 0, torch) / 8 for w in range(5)]
+    ms = sorted(windows)[2]
     del graph, gouts, eager
     byt = 3.0 * M * K + 4.0 * M * K / 128
     res["act_quant_4096x8192"] = {"us": round(ms * 1e3, 2), "GB/s": round(byt / ms / 1e6, 1),
                                   "pct_hbm_peak": round(100 * byt / ms / 1e6 / PEAK_HBM_GBS, 1),
                                   "eager_us": round(ms_eager * 1e3, 2),
+                                  "windows_us": [round(w * 1e3, 2) for w in windows],
                                   "includes": "HIP-graph replay of 8 launches over 4 input "
-                                              "sets (384 MB, past the 256 MB MALL)"}
+                                              "sets (384 MB, past the 256 MB MALL); median of "
+                                              "5 windows of 50 replays"}
     log(f"act_quant: {res['act_quant_4096x8192']}")
     del xs
 
@@ -449,10 +465,10 @@ def secondary(torch, fp8, synthetic, dev):
                             "small_512x512x2048": (512, 512, 2048)}.items():
         W, Bs = _gpu_weights(N, K, 40, dev, torch, synthetic)
         q, s = fp8.act_quant(_gpu_acts(M, K, 41, dev, torch), 128)
-        # 200 warmup launches, as for the harness shapes below: after the
+        # warm-up by GPU time, as for the harness shapes below: after the
         # HBM-bound decode legs the shader clock ramps over ~10 ms of MFMA load
-        ms = time_events(lambda: fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [128, 128],
-                                                           torch.bfloat16), 50, 200, torch)
+        ms = time_steady(lambda: fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [128, 128],
+                                                           torch.bfloat16), 50, torch)
         tf = 2.0 * M * N * K / ms / 1e9
         res[name] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
                      "pct_fp8_peak": round(100 * tf / PEAK_FP8_TFLOPS, 1)}
@@ -469,9 +485,9 @@ def secondary(torch, fp8, synthetic, dev):
     harness = {}
     for (M, N, K), ref_tf in b200.items():
         A, B, As, Bs = [t.to(dev) for t in synthetic.harness_operands(M, N, K, seed=0)]
-        # 200 warmup launches: the shader clock ramps over ~10 ms of MFMA load
-        ms = time_events(lambda: fp8.w8a8_block_fp8_matmul(A, B, As, Bs, [128, 128],
-                                                           torch.bfloat16), 50, 200, torch)
+        # warm-up by GPU time: the shader clock ramps over ~10 ms of MFMA load
+        ms = time_steady(lambda: fp8.w8a8_block_fp8_matmul(A, B, As, Bs, [128, 128],
+                                                           torch.bfloat16), 50, torch)
         tf = 2.0 * M * N * K / ms / 1e9
         harness[f"{M}x{N}x{K}"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
                                    "pct_fp8_peak": round(100 * tf / PEAK_FP8_TFLOPS, 1)}
@@ -495,12 +511,12 @@ def secondary(torch, fp8, synthetic, dev):
         try:
             f_v = lambda: torch._scaled_mm(A_, W_.t(), scale_a=one, scale_b=one,
                                            out_dtype=torch.bfloat16)
-            ms_v = time_events(f_v, 50, 200, torch)
+            ms_v = time_steady(f_v, 50, torch)
         except Exception as e:  # the vendor op is context only
             vendor[f"{M}x{N}x{K}"] = {"error": str(e)[:120]}
             continue
-        ms_b = time_events(lambda: fp8.w8a8_block_fp8_matmul(A_, W_, As_, Bs_, [128, 128],
-                                                             torch.bfloat16), 50, 200, torch)
+        ms_b = time_steady(lambda: fp8.w8a8_block_fp8_matmul(A_, W_, As_, Bs_, [128, 128],
+                                                             torch.bfloat16), 50, torch)
         fl = 2.0 * M * N * K
         vendor[f"{M}x{N}x{K}"] = {"hipblaslt_plain_fp8_us": round(ms_v * 1e3, 2),
                                   "hipblaslt_plain_fp8_TFLOP/s": round(fl / ms_v / 1e9, 1),
@@ -523,7 +539,7 @@ def secondary(torch, fp8, synthetic, dev):
         def dgf():
             i = it[0] = (it[0] + 1) % copies
             return dg.gemm_fp8_fp8_bf16_nt(q, wl[i][0], s, wl[i][1], 128)
-        ms = time_events(dgf, 50, 20, torch)
+        ms = time_steady(dgf, 50, torch, min_warmup=20)
         tf = 2.0 * M * N * K / ms / 1e9
         byt = M * K + N * K + 4.0 * (M + N) * (K // 128) + 2.0 * M * N
         res[name] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
@@ -571,7 +587,8 @@ def secondary(torch, fp8, synthetic, dev):
     w13, s13 = _gpu_weights(2 * I, H, 50, dev, torch, synthetic)
     w2, s2 = _gpu_weights(H, I, 51, dev, torch, synthetic)
     x = _gpu_acts(M, H, 52, dev, torch)
-    ms = time_events(lambda: fp8.fp8_mlp(x, w13, s13, w2, s2), 10, 3, torch)
+    # warm-up by GPU time (the legs before it are HBM-bound; see time_steady)
+    ms = time_steady(lambda: fp8.fp8_mlp(x, w13, s13, w2, s2), 20, torch, min_warmup=10)
     fl = 2.0 * M * (2 * I * H + H * I)
     res["mlp_chain_3001"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(fl / ms / 1e9, 1),
                              "pct_fp8_peak": round(100 * fl / ms / 1e9 / PEAK_FP8_TFLOPS, 1)}
@@ -583,8 +600,8 @@ def secondary(torch, fp8, synthetic, dev):
     y1 = fp8.fp8_mlp(x, wi, si, w2, s2, gate_up_interleaved=True)
     assert torch.equal(y0, y1), "interleaved MLP chain differs from the default chain"
     del w13, s13, y0, y1
-    ms = time_events(lambda: fp8.fp8_mlp(x, wi, si, w2, s2, gate_up_interleaved=True),
-                     10, 3, torch)
+    ms = time_steady(lambda: fp8.fp8_mlp(x, wi, si, w2, s2, gate_up_interleaved=True),
+                     20, torch, min_warmup=10)
     res["mlp_chain_3001_interleaved"] = {
         "us": round(ms * 1e3, 2), "TFLOP/s": round(fl / ms / 1e9, 1),
         "pct_fp8_peak": round(100 * fl / ms / 1e9 / PEAK_FP8_TFLOPS, 1),
