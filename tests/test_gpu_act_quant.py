@@ -39,10 +39,33 @@ def test_act_quant_g128_exact(M, K, dev):
 
 @pytest.mark.parametrize("M,K", [(70000, 256), (66000, 1024)])
 def test_act_quant_more_rows_than_grid_y(M, K, dev):
-    """Rows past the 65535 grid rows: each block walks rows m, m + 65535, ..."""
+    """Many rows of few groups (the flat-mapped kernel, one (row, group)
+    slot per 16-lane row) past the 65535 grid rows."""
     print(f"act_quant rows M={M} K={K}", flush=True)
     x = synthetic.activations(M, K, seed=M + K)
     _assert_exact(x, 128, dev)
+
+
+@pytest.mark.parametrize("silu,K", [(False, 4096), (False, 8192), (False, 7168),
+                                    (True, 14336), (True, 7168), (True, 4096)])
+def test_quant_row_walk_past_grid_y_equals_slices(silu, K, dev):
+    """Past 65535 rows the row-mapped kernels cap the grid and each block
+    walks rows m, m + 65535, ..., alternating its two LDS scale slots from
+    row to row. The result must equal, bit for bit, calls on row slices that
+    fit the grid (one row per block): act-quant at U = 2, 4 and 4 with idle
+    16-lane rows, SiLU-quant in blocks of 8, 4 and 16 rows."""
+    M = 66000
+    print(f"quant row walk silu={silu} M={M} K={K}", flush=True)
+    width = 2 * K if silu else K
+    g = torch.Generator(device=dev).manual_seed(K + silu)
+    x = (torch.randn(M, width, generator=g, device=dev) * 2).to(torch.bfloat16)
+    fn = fp8.silu_and_mul_quant if silu else fp8.act_quant
+    q, s = fn(x, 128)
+    for r0, r1 in ((0, 33000), (33000, M)):
+        qp, sp = fn(x[r0:r1], 128)
+        assert torch.equal(q[r0:r1].view(torch.uint8), qp.view(torch.uint8)), (r0, r1)
+        assert torch.equal(s[r0:r1].view(torch.int32), sp.view(torch.int32)), (r0, r1)
+    del x, q, s
 
 
 def _g128_unroll(M, K):
