@@ -150,8 +150,8 @@ inline int g128_unroll(int64_t rows, int64_t gpr) {
 // of 64) take U = 2 and the largest R of 16, 8, 4 that splits the row
 // exactly, the rest the act-quant shape (R = 16, U from g128_unroll).
 // Measured (graph replays over 4 input sets, M x 2d bf16 in): d = 14336
-// (112 groups) 3001 rows 39.3 us at R = 8 against 40.4 at 16 x 1 (the
-// earlier shape), 4096 rows 51.7 against 54.1; d = 7168 (56 groups) 8192
+// (112 groups) 3001 rows 39.3 us at R = 8 against 40.4 at 16 x 1 (one
+// group per lane, no idle rows), 4096 rows 51.7 against 54.1; d = 7168 (56 groups) 8192
 // rows 52.3 at R = 4 against 53.2 at 16 x 4 with 8 idle rows, 1024 rows 8.8
 // against 9.5; 16 x 7 and 8 x 7 (one or two blocks per row) level or slower.
 inline void silu_quant_shape(int64_t rows, int64_t gpr, int& R, int& U) {
