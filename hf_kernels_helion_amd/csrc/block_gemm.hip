@@ -141,6 +141,38 @@ __device__ __forceinline__ void store4(const GemmArgs& a, int m, int n, const v4
   }
 }
 
+// Split-K partials of a decode workgroup's tile (AR rows x 128 columns at
+// column n0, fp32, 512 threads) staged through LDS: each lane first puts its
+// 16-byte pieces into a [AR][132] tile (rows padded against bank conflicts),
+// then every store instruction writes two whole 512-byte row segments of the
+// workspace (full cache lines) instead of sixteen 64-byte pieces. Called by
+// every thread once the operand stages are dead (each wave has waited for
+// all its DMA); put(tile, pitch) writes the calling lane's accumulators. For
+// whole column tiles (n0 + 128 <= N) with vector stores only.
+template <int AR, typename Put>
+__device__ __forceinline__ void decode_partials_lds(const GemmArgs& a, uint8_t* smem, int n0,
+                                                    int split, Put put) {
+  constexpr int P = 132;
+  static_assert(AR % 16 == 0, "16 rows per pass of 512 threads");
+  float* tile = reinterpret_cast<float*>(smem);
+  __syncthreads();
+  put(tile, P);
+  __syncthreads();
+  const int t = threadIdx.x, c = 4 * (t & 31);
+#pragma unroll
+  for (int p = 0; p < AR / 16; ++p) {
+    const int m = p * 16 + (t >> 5);
+    if (m < a.M)
+      *reinterpret_cast<v4f*>(a.ws + ((int64_t)split * a.M + m) * a.N + n0 + c) =
+          *reinterpret_cast<const v4f*>(tile + m * P + c);
+  }
+}
+
+// Whether a decode workgroup's partial tile can take decode_partials_lds.
+__device__ __forceinline__ bool decode_partials_whole(const GemmArgs& a, int n0) {
+  return gridDim.z > 1 && a.vec_store && (a.N & 3) == 0 && n0 + 128 <= a.N;
+}
+
 __device__ __forceinline__ void lds_dma4(const void* gsrc, uint8_t* ldst) {
   __builtin_amdgcn_global_load_lds(gsrc, (lds_void*)ldst, 4, 0, 0);
 }
@@ -1688,6 +1720,7 @@ __global__ void __launch_bounds__(512) gemm_decode_kernel(GemmArgs a) {
   constexpr int STAGE = Cfg::STAGE, WIN_SA = Cfg::WIN_SA, WIN = Cfg::WIN;
   constexpr int SW_OFF = Cfg::SW_OFF, ACT_LOADS = Cfg::ACT_LOADS;
   static_assert(Cfg::SMEM <= 160 * 1024, "LDS budget");
+  static_assert(Cfg::AR * 132 * 4 <= Cfg::SMEM, "the partial tile fits the dead stages");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[Cfg::SMEM];
 
   const int lane = threadIdx.x & 63;
@@ -1805,6 +1838,15 @@ __global__ void __launch_bounds__(512) gemm_decode_kernel(GemmArgs a) {
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
+  if (decode_partials_whole(a, n0)) {
+    decode_partials_lds<Cfg::AR>(a, smem, n0, split, [&](float* tile, int pitch) {
+#pragma unroll
+      for (int f = 0; f < FM; ++f)
+        *reinterpret_cast<v4f*>(tile + (f * 16 + (lane & 15)) * pitch + wid * 16 +
+                                4 * (lane >> 4)) = acc[f];
+    });
+    return;
+  }
   const bool to_ws = gridDim.z > 1;
 #pragma unroll
   for (int f = 0; f < FM; ++f)
@@ -1921,6 +1963,7 @@ __global__ void __launch_bounds__(512) gemm_decode_quant_kernel(GemmArgs a) {
   static_assert(QE == 8 || QE == 16, "8 or 16 values per lane");
   static_assert(4 * QROWS == AR && QLOADS >= 1, "four quantiser waves cover the rows");
   static_assert(NS >= 2 && Cfg::SMEM <= 160 * 1024, "LDS budget");
+  static_assert(AR * 132 * 4 <= Cfg::SMEM, "the partial tile fits the dead stages");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[Cfg::SMEM];
 
   const int lane = threadIdx.x & 63;
@@ -2062,6 +2105,18 @@ __global__ void __launch_bounds__(512) gemm_decode_quant_kernel(GemmArgs a) {
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
+  if (decode_partials_whole(a, n0)) {
+    decode_partials_lds<AR>(a, smem, n0, split, [&](float* tile, int pitch) {
+      if (!mfma_wave) return;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int f = 0; f < FM; ++f)
+          *reinterpret_cast<v4f*>(tile + (f * 16 + (lane & 15)) * pitch + wid * 32 + j * 16 +
+                                  4 * (lane >> 4)) = acc[j][f];
+    });
+    return;
+  }
   if (mfma_wave) {
     const bool to_ws = gridDim.z > 1;
 #pragma unroll
