@@ -141,17 +141,18 @@ __device__ __forceinline__ void store4(const GemmArgs& a, int m, int n, const v4
   }
 }
 
-// Split-K partials of a decode workgroup's tile (AR rows x 128 columns at
-// column n0, fp32, 512 threads) staged through LDS: each lane first puts its
+// Split-K partials of a workgroup's tile (AR rows from m0 x 128 columns from
+// n0, fp32, 512 threads) staged through LDS: each lane first puts its
 // 16-byte pieces into a [AR][132] tile (rows padded against bank conflicts),
 // then every store instruction writes two whole 512-byte row segments of the
-// workspace (full cache lines) instead of sixteen 64-byte pieces. Called by
-// every thread once the operand stages are dead (each wave has waited for
-// all its DMA); put(tile, pitch) writes the calling lane's accumulators. For
-// whole column tiles (n0 + 128 <= N) with vector stores only.
+// workspace (full cache lines) instead of the 64-byte pieces of four lanes
+// per row. Called by every thread once the operand stages are dead (each
+// wave has waited for all its DMA); put(tile, pitch) writes the calling
+// lane's accumulators at their tile rows and columns. For whole column
+// tiles (n0 + 128 <= N) with vector stores only (partials_whole).
 template <int AR, typename Put>
-__device__ __forceinline__ void decode_partials_lds(const GemmArgs& a, uint8_t* smem, int n0,
-                                                    int split, Put put) {
+__device__ __forceinline__ void partials_lds(const GemmArgs& a, uint8_t* smem, int m0, int n0,
+                                             int split, Put put) {
   constexpr int P = 132;
   static_assert(AR % 16 == 0, "16 rows per pass of 512 threads");
   float* tile = reinterpret_cast<float*>(smem);
@@ -162,14 +163,14 @@ __device__ __forceinline__ void decode_partials_lds(const GemmArgs& a, uint8_t* 
 #pragma unroll
   for (int p = 0; p < AR / 16; ++p) {
     const int m = p * 16 + (t >> 5);
-    if (m < a.M)
-      *reinterpret_cast<v4f*>(a.ws + ((int64_t)split * a.M + m) * a.N + n0 + c) =
+    if (m0 + m < a.M)
+      *reinterpret_cast<v4f*>(a.ws + ((int64_t)split * a.M + m0 + m) * a.N + n0 + c) =
           *reinterpret_cast<const v4f*>(tile + m * P + c);
   }
 }
 
-// Whether a decode workgroup's partial tile can take decode_partials_lds.
-__device__ __forceinline__ bool decode_partials_whole(const GemmArgs& a, int n0) {
+// Whether a split-K workgroup's partial tile can take partials_lds.
+__device__ __forceinline__ bool partials_whole(const GemmArgs& a, int n0) {
   return gridDim.z > 1 && a.vec_store && (a.N & 3) == 0 && n0 + 128 <= a.N;
 }
 
@@ -1656,6 +1657,18 @@ __global__ void __launch_bounds__((128 / WM) * (128 / WN) * 64) gemm_pipe128_ker
   }
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
   __syncthreads();
+  if (partials_whole(a, n0)) {
+    static_assert(BM * 132 * 4 <= SMEM && NW == 8, "the partial tile fits the dead stages");
+    partials_lds<BM>(a, smem, m0, n0, split, [&](float* tile, int pitch) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          *reinterpret_cast<v4f*>(tile + (wm * WM + i * 16 + (lane & 15)) * pitch + wn * WN +
+                                  j * 16 + 4 * (lane >> 4)) = acc[i][j];
+    });
+    return;
+  }
   tile_epilogue<WM, WN>(a, smem, acc, m0 + wm * WM, n0 + wn * WN, wid, lane, split);
 }
 
@@ -1838,8 +1851,8 @@ __global__ void __launch_bounds__(512) gemm_decode_kernel(GemmArgs a) {
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  if (decode_partials_whole(a, n0)) {
-    decode_partials_lds<Cfg::AR>(a, smem, n0, split, [&](float* tile, int pitch) {
+  if (partials_whole(a, n0)) {
+    partials_lds<Cfg::AR>(a, smem, 0, n0, split, [&](float* tile, int pitch) {
 #pragma unroll
       for (int f = 0; f < FM; ++f)
         *reinterpret_cast<v4f*>(tile + (f * 16 + (lane & 15)) * pitch + wid * 16 +
@@ -2105,8 +2118,8 @@ __global__ void __launch_bounds__(512) gemm_decode_quant_kernel(GemmArgs a) {
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  if (decode_partials_whole(a, n0)) {
-    decode_partials_lds<AR>(a, smem, n0, split, [&](float* tile, int pitch) {
+  if (partials_whole(a, n0)) {
+    partials_lds<AR>(a, smem, 0, n0, split, [&](float* tile, int pitch) {
       if (!mfma_wave) return;
 #pragma unroll
       for (int j = 0; j < 2; ++j)
