@@ -147,25 +147,29 @@ __device__ __forceinline__ void store4(const GemmArgs& a, int m, int n, const v4
 // then every store instruction writes two whole 512-byte row segments of the
 // workspace (full cache lines) instead of the 64-byte pieces of four lanes
 // per row. Called by every thread once the operand stages are dead (each
-// wave has waited for all its DMA); put(tile, pitch) writes the calling
-// lane's accumulators at their tile rows and columns. For whole column
+// wave has waited for all its DMA). Rounds of RR rows when the whole tile
+// does not fit the LDS: put(tile, pitch, r0) writes the calling lane's
+// accumulators of tile rows r0..r0+RR-1 at row - r0. For whole column
 // tiles (n0 + 128 <= N) with vector stores only (partials_whole).
-template <int AR, typename Put>
+template <int AR, int RR = AR, typename Put>
 __device__ __forceinline__ void partials_lds(const GemmArgs& a, uint8_t* smem, int m0, int n0,
                                              int split, Put put) {
   constexpr int P = 132;
-  static_assert(AR % 16 == 0, "16 rows per pass of 512 threads");
+  static_assert(RR % 16 == 0 && AR % RR == 0, "16 rows per pass of 512 threads");
   float* tile = reinterpret_cast<float*>(smem);
-  __syncthreads();
-  put(tile, P);
-  __syncthreads();
   const int t = threadIdx.x, c = 4 * (t & 31);
 #pragma unroll
-  for (int p = 0; p < AR / 16; ++p) {
-    const int m = p * 16 + (t >> 5);
-    if (m0 + m < a.M)
-      *reinterpret_cast<v4f*>(a.ws + ((int64_t)split * a.M + m0 + m) * a.N + n0 + c) =
-          *reinterpret_cast<const v4f*>(tile + m * P + c);
+  for (int r0 = 0; r0 < AR; r0 += RR) {
+    __syncthreads();
+    put(tile, P, r0);
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < RR / 16; ++p) {
+      const int m = p * 16 + (t >> 5);
+      if (m0 + r0 + m < a.M)
+        *reinterpret_cast<v4f*>(a.ws + ((int64_t)split * a.M + m0 + r0 + m) * a.N + n0 + c) =
+            *reinterpret_cast<const v4f*>(tile + m * P + c);
+    }
   }
 }
 
@@ -1399,6 +1403,20 @@ __global__ void __launch_bounds__(512) gemm_pipe256x128_kernel(GemmArgs a) {
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
+  if (partials_whole(a, n0)) {
+    // two rounds of 128 rows: the padded 256-row tile exceeds the stages
+    static_assert(128 * 132 * 4 <= SMEM, "half the partial tile fits the dead stages");
+    partials_lds<BM, 128>(a, smem, m0, n0, split, [&](float* tile, int pitch, int r0) {
+      if (wm * WM < r0 || wm * WM >= r0 + 128) return;  // wave-uniform
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          *reinterpret_cast<v4f*>(tile + (wm * WM - r0 + i * 16 + (lane & 15)) * pitch +
+                                  wn * WN + j * 16 + 4 * (lane >> 4)) = acc[i][j];
+    });
+    return;
+  }
   tile_epilogue<WM, WN>(a, smem, acc, m0 + wm * WM, n0 + wn * WN, wid, lane, split);
 }
 
@@ -1659,7 +1677,7 @@ __global__ void __launch_bounds__((128 / WM) * (128 / WN) * 64) gemm_pipe128_ker
   __syncthreads();
   if (partials_whole(a, n0)) {
     static_assert(BM * 132 * 4 <= SMEM && NW == 8, "the partial tile fits the dead stages");
-    partials_lds<BM>(a, smem, m0, n0, split, [&](float* tile, int pitch) {
+    partials_lds<BM>(a, smem, m0, n0, split, [&](float* tile, int pitch, int) {
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -1852,7 +1870,7 @@ __global__ void __launch_bounds__(512) gemm_decode_kernel(GemmArgs a) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   if (partials_whole(a, n0)) {
-    partials_lds<Cfg::AR>(a, smem, 0, n0, split, [&](float* tile, int pitch) {
+    partials_lds<Cfg::AR>(a, smem, 0, n0, split, [&](float* tile, int pitch, int) {
 #pragma unroll
       for (int f = 0; f < FM; ++f)
         *reinterpret_cast<v4f*>(tile + (f * 16 + (lane & 15)) * pitch + wid * 16 +
@@ -2119,7 +2137,7 @@ __global__ void __launch_bounds__(512) gemm_decode_quant_kernel(GemmArgs a) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   if (partials_whole(a, n0)) {
-    partials_lds<AR>(a, smem, 0, n0, split, [&](float* tile, int pitch) {
+    partials_lds<AR>(a, smem, 0, n0, split, [&](float* tile, int pitch, int) {
       if (!mfma_wave) return;
 #pragma unroll
       for (int j = 0; j < 2; ++j)
