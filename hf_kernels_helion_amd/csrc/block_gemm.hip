@@ -141,41 +141,53 @@ __device__ __forceinline__ void store4(const GemmArgs& a, int m, int n, const v4
   }
 }
 
-// Split-K partials of a workgroup's tile (AR rows from m0 x 128 columns from
-// n0, fp32, 512 threads) staged through LDS: each lane first puts its
-// 16-byte pieces into a [AR][132] tile (rows padded against bank conflicts),
-// then every store instruction writes two whole 512-byte row segments of the
-// workspace (full cache lines) instead of the 64-byte pieces of four lanes
-// per row. Called by every thread once the operand stages are dead (each
-// wave has waited for all its DMA). Rounds of RR rows when the whole tile
-// does not fit the LDS: put(tile, pitch, r0) writes the calling lane's
-// accumulators of tile rows r0..r0+RR-1 at row - r0. For whole column
-// tiles (n0 + 128 <= N) with vector stores only (partials_whole).
-template <int AR, int RR = AR, typename Put>
-__device__ __forceinline__ void partials_lds(const GemmArgs& a, uint8_t* smem, int m0, int n0,
-                                             int split, Put put) {
-  constexpr int P = 132;
-  static_assert(RR % 16 == 0 && AR % RR == 0, "16 rows per pass of 512 threads");
+// fp32 tile of a workgroup (AR rows from m0 x BN columns from n0, 512
+// threads) staged through LDS on its way to dst + row * ld + column (the
+// split-K workspace slice, or fp32 C): each lane first puts its 16-byte
+// pieces into a [rows][BN + 4] tile (rows padded against bank conflicts),
+// then every store instruction writes whole row segments of BN * 4 bytes
+// (full cache lines) instead of the 64-byte pieces of four lanes per row.
+// Called by every thread once the operand stages are dead (each wave has
+// waited for all its DMA). Rounds of RR rows when the whole tile does not
+// fit the LDS: put(tile, pitch, r0) writes the calling lane's accumulators
+// of tile rows r0..r0+RR-1 at row - r0.
+template <int AR, int BN, int RR, typename Put>
+__device__ __forceinline__ void f32_tile_lds(const GemmArgs& a, uint8_t* smem, int m0, int n0,
+                                             float* dst, int64_t ld, Put put) {
+  constexpr int P = BN + 4, TPR = BN / 4, RPP = 512 / TPR;
+  static_assert(RR % RPP == 0 && AR % RR == 0, "whole passes of 512 threads per round");
   float* tile = reinterpret_cast<float*>(smem);
-  const int t = threadIdx.x, c = 4 * (t & 31);
+  const int t = threadIdx.x, c = 4 * (t % TPR);
 #pragma unroll
   for (int r0 = 0; r0 < AR; r0 += RR) {
     __syncthreads();
     put(tile, P, r0);
     __syncthreads();
 #pragma unroll
-    for (int p = 0; p < RR / 16; ++p) {
-      const int m = p * 16 + (t >> 5);
+    for (int p = 0; p < RR / RPP; ++p) {
+      const int m = p * RPP + t / TPR;
       if (m0 + r0 + m < a.M)
-        *reinterpret_cast<v4f*>(a.ws + ((int64_t)split * a.M + m0 + r0 + m) * a.N + n0 + c) =
+        *reinterpret_cast<v4f*>(dst + (int64_t)(m0 + r0 + m) * ld + n0 + c) =
             *reinterpret_cast<const v4f*>(tile + m * P + c);
     }
   }
 }
 
-// Whether a split-K workgroup's partial tile can take partials_lds.
-__device__ __forceinline__ bool partials_whole(const GemmArgs& a, int n0) {
-  return gridDim.z > 1 && a.vec_store && (a.N & 3) == 0 && n0 + 128 <= a.N;
+// Where a workgroup's fp32 tile (BN columns from n0) goes through
+// f32_tile_lds: the split-K workspace slice of its split, or fp32 C when
+// the launch is unsplit; nullptr when it keeps per-lane stores (a partial
+// column tile, no vector stores, or 16-bit C).
+__device__ __forceinline__ float* f32_tile_dest(const GemmArgs& a, int n0, int BN, int split,
+                                                int64_t& ld) {
+  if (!a.vec_store || n0 + BN > a.N) return nullptr;
+  if (gridDim.z > 1) {
+    if (a.N & 3) return nullptr;
+    ld = a.N;
+    return a.ws + (int64_t)split * a.M * a.N;
+  }
+  if (a.out_dtype != FP8B_F32) return nullptr;
+  ld = a.ldc;
+  return reinterpret_cast<float*>(a.C);
 }
 
 __device__ __forceinline__ void lds_dma4(const void* gsrc, uint8_t* ldst) {
@@ -875,6 +887,23 @@ __global__ void __launch_bounds__(512) gemm_pipe256_kernel(GemmArgs a) {
   if constexpr (SWIGLU) {
     swiglu_epilogue<BM, WM, WN>(a, smem, acc, m0, tn, wid, lane);
     return;
+  } else {
+    int64_t ld = 0;
+    if (float* dst = f32_tile_dest(a, n0, BN, split, ld)) {
+      // two rounds of 128 rows (waves 0-3, then 4-7): the padded 256 x 256
+      // tile exceeds the dead stages
+      static_assert(128 * (BN + 4) * 4 <= SMEM && WM == 128, "half the fp32 tile fits");
+      f32_tile_lds<BM, BN, 128>(a, smem, m0, n0, dst, ld, [&](float* tile, int pitch, int r0) {
+        if (wm * WM != r0) return;  // wave-uniform
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            *reinterpret_cast<v4f*>(tile + (i * 16 + (lane & 15)) * pitch + wn * WN + j * 16 +
+                                    4 * (lane >> 4)) = acc[i][j];
+      });
+      return;
+    }
   }
   tile_epilogue<WM, WN>(a, smem, acc, m0 + wm * WM, n0 + wn * WN, wid, lane, split);
 }
@@ -1403,10 +1432,11 @@ __global__ void __launch_bounds__(512) gemm_pipe256x128_kernel(GemmArgs a) {
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  if (partials_whole(a, n0)) {
+  int64_t ld = 0;
+  if (float* dst = f32_tile_dest(a, n0, BN, split, ld)) {
     // two rounds of 128 rows: the padded 256-row tile exceeds the stages
-    static_assert(128 * 132 * 4 <= SMEM, "half the partial tile fits the dead stages");
-    partials_lds<BM, 128>(a, smem, m0, n0, split, [&](float* tile, int pitch, int r0) {
+    static_assert(128 * (BN + 4) * 4 <= SMEM, "half the fp32 tile fits the dead stages");
+    f32_tile_lds<BM, BN, 128>(a, smem, m0, n0, dst, ld, [&](float* tile, int pitch, int r0) {
       if (wm * WM < r0 || wm * WM >= r0 + 128) return;  // wave-uniform
 #pragma unroll
       for (int i = 0; i < FM; ++i)
@@ -1675,9 +1705,10 @@ __global__ void __launch_bounds__((128 / WM) * (128 / WN) * 64) gemm_pipe128_ker
   }
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
   __syncthreads();
-  if (partials_whole(a, n0)) {
-    static_assert(BM * 132 * 4 <= SMEM && NW == 8, "the partial tile fits the dead stages");
-    partials_lds<BM>(a, smem, m0, n0, split, [&](float* tile, int pitch, int) {
+  int64_t ld = 0;
+  if (float* dst = f32_tile_dest(a, n0, BN, split, ld)) {
+    static_assert(BM * (BN + 4) * 4 <= SMEM && NW == 8, "the fp32 tile fits the dead stages");
+    f32_tile_lds<BM, BN, BM>(a, smem, m0, n0, dst, ld, [&](float* tile, int pitch, int) {
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -1869,8 +1900,9 @@ __global__ void __launch_bounds__(512) gemm_decode_kernel(GemmArgs a) {
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  if (partials_whole(a, n0)) {
-    partials_lds<Cfg::AR>(a, smem, 0, n0, split, [&](float* tile, int pitch, int) {
+  int64_t ld = 0;
+  if (float* dst = f32_tile_dest(a, n0, BN, split, ld)) {
+    f32_tile_lds<Cfg::AR, BN, Cfg::AR>(a, smem, 0, n0, dst, ld, [&](float* tile, int pitch, int) {
 #pragma unroll
       for (int f = 0; f < FM; ++f)
         *reinterpret_cast<v4f*>(tile + (f * 16 + (lane & 15)) * pitch + wid * 16 +
@@ -2136,8 +2168,9 @@ __global__ void __launch_bounds__(512) gemm_decode_quant_kernel(GemmArgs a) {
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  if (partials_whole(a, n0)) {
-    partials_lds<AR>(a, smem, 0, n0, split, [&](float* tile, int pitch, int) {
+  int64_t ld = 0;
+  if (float* dst = f32_tile_dest(a, n0, BN, split, ld)) {
+    f32_tile_lds<AR, BN, AR>(a, smem, 0, n0, dst, ld, [&](float* tile, int pitch, int) {
       if (!mfma_wave) return;
 #pragma unroll
       for (int j = 0; j < 2; ++j)
