@@ -1095,3 +1095,35 @@ def test_gemm_graph_replays(M, N, K, dev):
         assert torch.equal(out, eager)
         f()  # eager work between replays
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("M,N,K,kernel", [
+    (4096, 4096, 1024, "gemm_pipe256_kernel"), (4224, 4096, 1024, "gemm_pipe256_kernel"),
+    (2048, 2048, 4096, "gemm_pipe128_kernel"), (128, 4096, 11008, "gemm_pipe128_kernel"),
+    (512, 4096, 14336, "gemm_pipe256x128_kernel"), (32, 4096, 14336, "gemm_decode_kernel"),
+    (1000, 4100, 2048, None)])
+def test_gemm_fp32_output_rounds_to_the_bf16_output(M, N, K, kernel, dev):
+    """fp32 C (the public op's default dtype) leaves the tiled and decode
+    kernels through the LDS-staged fp32 tile write, bf16 C through the 16-bit
+    epilogue; split-K plans reduce staged fp32 partials. Both round the same
+    fp32 results, so the fp32 output rounded to bf16 must equal the bf16
+    output bit for bit, on each kernel (4224 rows: 128x128 quarters after the
+    256x256 tiles; 4100 columns: a ragged last column tile on per-lane
+    stores), and it matches the oracle on sampled rows."""
+    from hf_kernels_helion_amd import _native
+    if kernel is not None:
+        assert _native.gemm_plan(M, N, K)["kernel"] == kernel
+    print(f"gemm fp32 vs bf16 output M={M} N={N} K={K}", flush=True)
+    x = synthetic.activations(M, K, seed=M + K, outlier_frac=0.01)
+    q, s = fp8.act_quant(x.to(dev), 128)
+    W, Bs = synthetic.weights(N, K, seed=N + 2 * K)
+    W, Bs = W.to(dev), Bs.to(dev)
+    o32 = fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [128, 128])
+    o16 = fp8.w8a8_block_fp8_matmul(q, W, s, Bs, [128, 128], torch.bfloat16)
+    assert o32.dtype == torch.float32
+    assert torch.equal(o32.to(torch.bfloat16).view(torch.int16), o16.view(torch.int16))
+    rows = torch.tensor([0, M // 2, M - 1])
+    orc = oracle.block_gemm(_u8(q.cpu()[rows]), _u8(W.cpu()), s.cpu()[rows].numpy(),
+                            Bs.cpu().numpy())
+    torch.testing.assert_close(o32[rows.to(dev)].cpu(), torch.from_numpy(orc),
+                               rtol=RTOL, atol=ATOL)
