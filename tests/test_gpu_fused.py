@@ -269,3 +269,33 @@ def test_fused_rejects_bad_inputs(dev):
     W = torch.zeros(128, 256, dtype=torch.float8_e4m3fn, device=dev)
     with pytest.raises(RuntimeError, match="128, 128"):
         fp8.act_quant_w8a8_block_fp8_matmul(x, W, Bs, [64, 128])
+
+
+def _random_small_m(n, seed):
+    g = torch.Generator().manual_seed(seed)
+    out = []
+    for _ in range(n):
+        M = int(torch.randint(1, 65, (1,), generator=g))
+        N = int(torch.randint(1, 12289, (1,), generator=g))
+        K = 128 * int(torch.randint(1, 113, (1,), generator=g))
+        out.append((M, N, K))
+    return out
+
+
+@pytest.mark.parametrize("M,N,K", _random_small_m(24, 2026))
+def test_fused_random_small_m_both_dtypes(M, N, K, dev):
+    """A seeded sweep of decode-sized shapes (M 1-64, N up to 12288, K up to
+    14336) over every act-quant + GEMM path the planner picks (one kernel on
+    decode, skinny and small-grid plans, or two launches): bf16 and fp32
+    outputs each equal the two public ops bit for bit, and the fp32 output
+    rounded to bf16 equals the bf16 output."""
+    print(f"fused random M={M} N={N} K={K}", flush=True)
+    gx = torch.Generator(device=dev).manual_seed(M * 7 + N)
+    x = torch.randn(M, K, generator=gx, device=dev).to(torch.bfloat16)
+    W, Bs = _weights(N, K, seed=N + K, dev=dev)
+    outs = {}
+    for dtype in (torch.bfloat16, torch.float32):
+        out = fp8.act_quant_w8a8_block_fp8_matmul(x, W, Bs, [128, 128], dtype)
+        _same(out, _two_op(x, W, Bs, dtype))
+        outs[dtype] = out
+    _same(outs[torch.float32].to(torch.bfloat16), outs[torch.bfloat16])
